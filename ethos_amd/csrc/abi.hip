@@ -1,0 +1,176 @@
+// C-ABI of the ETHOS expert-layer kernels (declared in include/ethos_hip.h).
+// Every entry point validates its arguments, enqueues on the caller's stream, never
+// allocates, never throws, and returns 0 on success, a negative ETHOS_E* code for an
+// argument error, or a positive hipError_t; ethos_last_error() describes the last
+// failure of the calling thread.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <atomic>
+
+#include "../../include/ethos_hip.h"
+#include "ethos_common.hpp"
+#include "ethos_launch.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(int rc, const char* what) {
+    if (rc == 0) return 0;
+    return fail(rc, "%s: %s", what, hipGetErrorString((hipError_t)rc));
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_num_cus[kMaxDevices];
+
+int num_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = g_num_cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        g_num_cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+int elem_bytes(int dtype) { return dtype == ETHOS_BF16 ? 2 : 4; }
+bool dtype_ok(int dtype) { return dtype == ETHOS_F32 || dtype == ETHOS_BF16; }
+
+}  // namespace
+
+extern "C" {
+
+const char* ethos_last_error(void) { return g_err; }
+
+int ethos_abi_version(void) { return ETHOS_ABI_VERSION; }
+
+int ethos_query_proj(const void* x, const void* wq, const void* bq, const float* bn_alpha, const float* bn_beta,
+                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* q_out,
+                     void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_query_proj: unknown dtype %d", dtype);
+    if (n_tok < 0 || d_model <= 0 || n_heads <= 0 || d_query <= 0)
+        return fail(ETHOS_ESIZE, "ethos_query_proj: bad sizes n_tok=%lld d_model=%d n_heads=%d d_query=%d",
+                    (long long)n_tok, d_model, n_heads, d_query);
+    if (n_tok > INT32_MAX / 2) return fail(ETHOS_ESIZE, "ethos_query_proj: n_tok too large");
+    if (n_tok == 0) return 0;
+    if (!x || !wq || !bq || !bn_alpha || !bn_beta || !q_out)
+        return fail(ETHOS_ENULL, "ethos_query_proj: null pointer");
+    return hip_status(ethos::launch_qproj(x, wq, bq, bn_alpha, bn_beta, n_tok, d_model, n_heads * d_query, dtype,
+                                          q_out, (hipStream_t)stream),
+                      "ethos_query_proj");
+}
+
+int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, int64_t n_rows, int32_t d_query,
+                     int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype, void* out_scores,
+                     int32_t* out_ids, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_route_topk: unknown dtype %d", dtype);
+    if (n_rows < 0 || d_query <= 0 || (d_query & 1) || n_sub_keys <= 0 || top_k <= 0 || k_cand <= 0)
+        return fail(ETHOS_ESIZE, "ethos_route_topk: bad sizes rows=%lld d_query=%d K=%d top_k=%d k_cand=%d",
+                    (long long)n_rows, d_query, n_sub_keys, top_k, k_cand);
+    if (k_cand > n_sub_keys)
+        return fail(ETHOS_ESIZE, "ethos_route_topk: k_cand=%d exceeds the %d sub-keys", k_cand, n_sub_keys);
+    if (top_k > k_cand * k_cand)
+        return fail(ETHOS_ESIZE, "ethos_route_topk: top_k=%d exceeds k_cand^2=%d", top_k, k_cand * k_cand);
+    if (k_cand > 32 || top_k > 32)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_route_topk: k_cand=%d / top_k=%d above 32 are not supported", k_cand,
+                    top_k);
+    if ((int64_t)n_sub_keys * n_sub_keys > INT32_MAX)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_route_topk: %d sub-keys give expert ids beyond int32", n_sub_keys);
+    const int dh2 = d_query / 2;
+    if (ethos::route_tile_keys(n_sub_keys, dh2, elem_bytes(dtype)) < 64)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_route_topk: d_query=%d too wide for the LDS key tile", d_query);
+    if (n_rows == 0) return 0;
+    if (!q || !sub_keys_1 || !sub_keys_2 || !out_scores || !out_ids)
+        return fail(ETHOS_ENULL, "ethos_route_topk: null pointer");
+    return hip_status(ethos::launch_route(q, sub_keys_1, sub_keys_2, n_rows, d_query, n_sub_keys, top_k, k_cand,
+                                          dtype, out_scores, out_ids, (hipStream_t)stream),
+                      "ethos_route_topk");
+}
+
+size_t ethos_sort_workspace_bytes(int64_t n_pairs, int64_t n_experts) {
+    (void)n_experts;
+    if (n_pairs <= 0) return 256;
+    return ethos::sort_workspace_bytes(n_pairs);
+}
+
+int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, void* workspace,
+                       size_t workspace_bytes, int32_t* perm, int32_t* uniq_ids, int32_t* seg_off,
+                       int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique, void* stream) {
+    g_err[0] = 0;
+    if (n_pairs < 0 || n_experts <= 0 || n_experts > INT32_MAX || n_pairs > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_sort_segment: bad sizes n_pairs=%lld n_experts=%lld", (long long)n_pairs,
+                    (long long)n_experts);
+    if (!seg_off || !n_unique) return fail(ETHOS_ENULL, "ethos_sort_segment: null pointer");
+    if (n_pairs == 0)
+        return hip_status(ethos::launch_sort_empty(seg_off, n_unique, (hipStream_t)stream), "ethos_sort_segment");
+    if (!ids || !workspace || !perm || !uniq_ids || !pair_slot || !sorted_slot)
+        return fail(ETHOS_ENULL, "ethos_sort_segment: null pointer");
+    if (workspace_bytes < ethos::sort_workspace_bytes(n_pairs))
+        return fail(ETHOS_EWORKSPACE, "ethos_sort_segment: workspace of %zu bytes, %zu needed", workspace_bytes,
+                    ethos::sort_workspace_bytes(n_pairs));
+    if (!aligned16(workspace)) return fail(ETHOS_EALIGN, "ethos_sort_segment: workspace not 16-byte aligned");
+    return hip_status(ethos::launch_sort_segment(ids, n_pairs, n_experts, workspace, perm, uniq_ids, seg_off,
+                                                 pair_slot, sorted_slot, n_unique, (hipStream_t)stream),
+                      "ethos_sort_segment");
+}
+
+int ethos_generate(const void* latents, int64_t n_experts, const int32_t* uniq_ids, const int32_t* n_unique,
+                   int64_t max_unique, const void* w1, const void* w2, int32_t d_latent, int32_t d_hidden,
+                   int32_t d_model, int32_t dtype, void* uv_out, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_generate: unknown dtype %d", dtype);
+    if (n_experts <= 0 || max_unique < 0 || d_latent <= 0 || d_hidden <= 0 || d_model <= 0)
+        return fail(ETHOS_ESIZE, "ethos_generate: bad sizes");
+    const int kq = dtype == ETHOS_BF16 ? 16 : 2;
+    if (d_latent % kq || d_hidden % 32 || (2 * d_model) % 32 || d_hidden % kq)
+        return fail(ETHOS_EUNSUPPORTED,
+                    "ethos_generate: needs d_latent %% %d == 0, d_hidden %% 32 == 0, d_model %% 16 == 0 "
+                    "(got %d, %d, %d)", kq, d_latent, d_hidden, d_model);
+    if (ethos::generate_smem_bytes(d_latent, d_hidden, dtype) > 160 * 1024)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_generate: d_latent + d_hidden too large for LDS");
+    if (max_unique == 0) return 0;
+    if (!latents || !uniq_ids || !n_unique || !w1 || !w2 || !uv_out)
+        return fail(ETHOS_ENULL, "ethos_generate: null pointer");
+    if (dtype == ETHOS_BF16 && (!aligned16(w1) || !aligned16(w2)))
+        return fail(ETHOS_EALIGN, "ethos_generate: weights not 16-byte aligned");
+    return hip_status(ethos::launch_generate(latents, n_experts, uniq_ids, n_unique, max_unique, w1, w2, d_latent,
+                                             d_hidden, 2 * d_model, dtype, uv_out, num_cus(), (hipStream_t)stream),
+                      "ethos_generate");
+}
+
+int ethos_apply_scatter(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
+                        const int32_t* pair_slot, const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k,
+                        int32_t d_model, int32_t dtype, float* act_workspace, void* out, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_apply_scatter: unknown dtype %d", dtype);
+    if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || d_model <= 0)
+        return fail(ETHOS_ESIZE, "ethos_apply_scatter: bad sizes");
+    const int vec = dtype == ETHOS_BF16 ? 8 : 4;
+    if (d_model % vec || ethos::apply_chunks(d_model, dtype) > 8)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_apply_scatter: d_model=%d must be a multiple of %d and <= %d", d_model,
+                    vec, 8 * 64 * vec);
+    if (n_tok * n_heads * top_k > INT32_MAX) return fail(ETHOS_ESIZE, "ethos_apply_scatter: too many pairs");
+    if (n_tok == 0) return 0;
+    if (!x || !uv || !perm || !sorted_slot || !pair_slot || !scores || !act_workspace || !out)
+        return fail(ETHOS_ENULL, "ethos_apply_scatter: null pointer");
+    if (!aligned16(x) || !aligned16(uv) || !aligned16(out))
+        return fail(ETHOS_EALIGN, "ethos_apply_scatter: x, uv and out must be 16-byte aligned");
+    return hip_status(ethos::launch_apply(x, uv, perm, sorted_slot, pair_slot, scores, n_tok, n_heads, top_k, d_model,
+                                          dtype, act_workspace, out, num_cus(), (hipStream_t)stream),
+                      "ethos_apply_scatter");
+}
+
+}  // extern "C"

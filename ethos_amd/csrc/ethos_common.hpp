@@ -1,0 +1,132 @@
+// Shared device helpers for the ETHOS expert-layer kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ethos {
+
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// float -> bf16 bits, round to nearest even.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t b = __float_as_uint(f);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x40u);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+// double -> float with round-to-odd: truncate, then force the last bit to 1 if inexact.
+// Rounding that float to bf16 (8 significant bits <= 24 - 2) gives the correctly rounded
+// bf16 of the double.
+__device__ __forceinline__ float f64_to_f32_odd(double d) {
+    float f = (float)d;
+    if ((double)f == d) return f;
+    uint32_t b = __float_as_uint(f);
+    if ((b & 1u) == 0u) b = (fabs((double)f) > fabs(d)) ? b - 1u : b + 1u;
+    return __uint_as_float(b);
+}
+
+// Storage-type traits: T is float (fp32) or uint16_t (bf16 bits).
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static constexpr DType kDType = kF32;
+    __device__ __forceinline__ static float to_f32(float v) { return v; }
+    __device__ __forceinline__ static double to_f64(float v) { return (double)v; }
+    __device__ __forceinline__ static float from_f32(float v) { return v; }
+    __device__ __forceinline__ static float from_f64(double v) { return (float)v; }
+    // round a float to T and return the T value as float
+    __device__ __forceinline__ static float round32(float v) { return v; }
+    __device__ __forceinline__ static float round64(double v) { return (float)v; }
+};
+template <> struct Elem<uint16_t> {
+    static constexpr DType kDType = kBF16;
+    __device__ __forceinline__ static float to_f32(uint16_t v) { return bf16_bits_to_f32(v); }
+    __device__ __forceinline__ static double to_f64(uint16_t v) { return (double)bf16_bits_to_f32(v); }
+    __device__ __forceinline__ static uint16_t from_f32(float v) { return f32_to_bf16_bits(v); }
+    __device__ __forceinline__ static uint16_t from_f64(double v) { return f32_to_bf16_bits(f64_to_f32_odd(v)); }
+    __device__ __forceinline__ static float round32(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+    __device__ __forceinline__ static float round64(double v) { return bf16_bits_to_f32(from_f64(v)); }
+};
+
+// Exact GELU (erf form), fp32.
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+// ---------------------------------------------------------------- wave reductions (DPP)
+// dpp_ctrl encodings (GCN/CDNA DPP): quad_perm, row_half_mirror, row_mirror.
+constexpr int kDppXor1 = 0xb1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4e;        // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xf, 0xf, false);
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __uint_as_float(dpp_u32<kCtrl>(__float_as_uint(v)));
+}
+
+// Sum over the 64 lanes; every lane receives the same value (fixed association order).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppRowHalfMirror>(v);
+    v += dpp_f32<kDppRowMirror>(v);
+    float r0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+    float r1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+    float r2 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+    float r3 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ uint64_t u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+template <int kCtrl>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    uint32_t lo = dpp_u32<kCtrl>((uint32_t)v);
+    uint32_t hi = dpp_u32<kCtrl>((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+    uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, lane);
+    uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Max over the 64 lanes; every lane receives it.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = u64_max(v, dpp_u64<kDppXor1>(v));
+    v = u64_max(v, dpp_u64<kDppXor2>(v));
+    v = u64_max(v, dpp_u64<kDppRowHalfMirror>(v));
+    v = u64_max(v, dpp_u64<kDppRowMirror>(v));
+    uint64_t a = u64_max(readlane_u64(v, 0), readlane_u64(v, 16));
+    uint64_t b = u64_max(readlane_u64(v, 32), readlane_u64(v, 48));
+    return u64_max(a, b);
+}
+
+// ---------------------------------------------------------------- canonical keys
+// Order-preserving image of a float (-0 == +0), and a 64-bit selection key whose
+// natural order is (score descending, index ascending).
+__device__ __forceinline__ uint32_t ord32(float f) {
+    uint32_t b = __float_as_uint(f);
+    if (b == 0x80000000u) b = 0u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ uint64_t make_key(float score, uint32_t idx) {
+    return ((uint64_t)ord32(score) << 32) | (uint64_t)(~idx);
+}
+__device__ __forceinline__ uint32_t key_idx(uint64_t k) { return ~(uint32_t)(k & 0xffffffffu); }
+__device__ __forceinline__ float key_score(uint64_t k) {
+    uint32_t o = (uint32_t)(k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+}  // namespace ethos

@@ -1,0 +1,35 @@
+// Internal launch functions of the ETHOS expert-layer kernels (C++ linkage; the
+// public C-ABI lives in abi.hip / include/ethos_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ethos {
+
+int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
+                 int d, int ncols, int dtype, void* q, hipStream_t stream);
+
+int route_tile_keys(int K, int dh2, int elem_bytes);
+size_t route_smem_bytes(int dh2, int KT, int elem_bytes);
+int launch_route(const void* q, const void* k1, const void* k2, int64_t rows, int dq, int K, int top_k, int kc,
+                 int dtype, void* gates, int32_t* ids, hipStream_t stream);
+
+size_t sort_workspace_bytes(int64_t n);
+int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,
+                        int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
+                        hipStream_t stream);
+int launch_sort_empty(int32_t* seg_off, int32_t* n_unique, hipStream_t stream);
+
+size_t generate_smem_bytes(int dl, int dh, int dtype);
+int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
+                    int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, int dtype, void* uv,
+                    int num_cus, hipStream_t stream);
+
+int apply_chunks(int d, int dtype);
+int launch_apply(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
+                 const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k, int d, int dtype, float* act,
+                 void* out, int num_cus, hipStream_t stream);
+
+}  // namespace ethos

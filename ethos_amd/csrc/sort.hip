@@ -1,0 +1,264 @@
+// Reordering of (token, head, k) pairs by expert id: an LSD radix sort of the expert
+// ids carrying the pair index, followed by segmentation into unique experts.
+// (No reference code: the reference loops over pairs in token order, model.py:306-334;
+// the paper's Algorithm 1 reorders by expert, paper/ETHOS.pdf p.10.)
+//
+// Sort: 8-bit digits, ceil(bits / 8) passes over keys < n_experts.  Each pass is
+//   upsweep   per-tile digit histogram            -> hist[digit][tile]
+//   scan      exclusive scan of hist (digit-major) -> global offsets
+//   downsweep stable scatter: rank inside a tile by wave-level multisplit
+// A tile is 4096 keys = 4 waves x 16 chunks of 64 consecutive keys.  Inside a wave,
+// the lanes holding the same digit are found with eight ballots ("peer mask"); the
+// rank of a key is (keys of that digit in earlier waves) + (in earlier chunks of its
+// wave) + (peers in lower lanes), which keeps the order of equal keys.  No global
+// atomics; LDS counters are updated by one leader lane per digit.
+//
+// Segment: flags[i] = (i == 0 || key[i] != key[i-1]); slot = inclusive scan - 1.
+// Outputs: perm (pair ids by expert), uniq (expert id per slot), seg_off (U + 1),
+// pair_slot[p] (slot of pair p), sorted_slot[i] (slot of position i), n_unique.
+#include "ethos_common.hpp"
+#include "ethos_launch.hpp"
+
+namespace ethos {
+
+constexpr int kSortChunks = 16;                 // chunks of 64 keys per wave
+constexpr int kSortTile = 4 * kSortChunks * 64; // 4096 keys
+constexpr int kRadix = 256;
+constexpr int kScanThreads = 1024;
+
+__device__ __forceinline__ uint64_t peer_mask(uint32_t digit, uint64_t valid) {
+    uint64_t peers = valid;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const uint32_t bit = (digit >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        peers &= bit ? bal : ~bal;
+    }
+    return peers;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
+
+__global__ __launch_bounds__(256) void sort_upsweep(const uint32_t* __restrict__ keys, int64_t n, int shift,
+                                                    uint32_t* __restrict__ hist, int n_tiles) {
+    __shared__ uint32_t cnt[4][kRadix];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (int i = tid; i < 4 * kRadix; i += 256) cnt[i / kRadix][i % kRadix] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortChunks * 64);
+    for (int c = 0; c < kSortChunks; ++c) {
+        const int64_t idx = base + c * 64 + lane;
+        const bool v = idx < n;
+        const uint32_t key = v ? keys[idx] : 0u;
+        const uint32_t dg = (key >> shift) & (kRadix - 1);
+        const uint64_t peers = peer_mask(dg, __ballot(v));
+        if (v && lane == 63 - __clzll((long long)peers)) cnt[wave][dg] += (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+    hist[(int64_t)tid * n_tiles + blockIdx.x] = cnt[0][tid] + cnt[1][tid] + cnt[2][tid] + cnt[3][tid];
+}
+
+template <bool kFirst>
+__global__ __launch_bounds__(256) void sort_downsweep(const uint32_t* __restrict__ keys_in,
+                                                      const uint32_t* __restrict__ vals_in,
+                                                      uint32_t* __restrict__ keys_out,
+                                                      uint32_t* __restrict__ vals_out, int64_t n, int shift,
+                                                      const uint32_t* __restrict__ hist, int n_tiles) {
+    __shared__ uint32_t cnt[4][kRadix];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (int i = tid; i < 4 * kRadix; i += 256) cnt[i / kRadix][i % kRadix] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortChunks * 64);
+    uint32_t key[kSortChunks], val[kSortChunks], rank[kSortChunks];
+#pragma unroll
+    for (int c = 0; c < kSortChunks; ++c) {
+        const int64_t idx = base + c * 64 + lane;
+        const bool v = idx < n;
+        key[c] = v ? keys_in[idx] : 0u;
+        val[c] = v ? (kFirst ? (uint32_t)idx : vals_in[idx]) : 0u;
+        const uint32_t dg = (key[c] >> shift) & (kRadix - 1);
+        const uint64_t peers = peer_mask(dg, __ballot(v));
+        const uint32_t below = (uint32_t)__popcll(peers & lanemask_lt(lane));
+        uint32_t start = 0;
+        if (v) start = cnt[wave][dg];
+        __builtin_amdgcn_wave_barrier();
+        rank[c] = start + below;
+        if (v && lane == 63 - __clzll((long long)peers)) cnt[wave][dg] = start + (uint32_t)__popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    {
+        uint32_t run = hist[(int64_t)tid * n_tiles + blockIdx.x];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t c = cnt[w][tid];
+            cnt[w][tid] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kSortChunks; ++c) {
+        const int64_t idx = base + c * 64 + lane;
+        if (idx < n) {
+            const uint32_t dg = (key[c] >> shift) & (kRadix - 1);
+            const uint32_t pos = cnt[wave][dg] + rank[c];
+            keys_out[pos] = key[c];
+            vals_out[pos] = val[c];
+        }
+    }
+}
+
+// Exclusive scan of n uint32 in place by one workgroup; total -> *total (if given).
+__global__ __launch_bounds__(kScanThreads) void scan_exclusive(uint32_t* __restrict__ a, int64_t n,
+                                                               int32_t* __restrict__ total) {
+    __shared__ uint32_t part[kScanThreads];
+    const int tid = threadIdx.x;
+    const int64_t per = (n + kScanThreads - 1) / kScanThreads;
+    const int64_t lo = tid * per, hi = min(n, lo + per);
+    uint32_t s = 0;
+    for (int64_t i = lo; i < hi; ++i) s += a[i];
+    part[tid] = s;
+    __syncthreads();
+    for (int off = 1; off < kScanThreads; off <<= 1) {
+        const uint32_t v = tid >= off ? part[tid - off] : 0u;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    uint32_t run = part[tid] - s;
+    for (int64_t i = lo; i < hi; ++i) {
+        const uint32_t v = a[i];
+        a[i] = run;
+        run += v;
+    }
+    if (tid == kScanThreads - 1 && total) *total = (int32_t)part[tid];
+}
+
+// Head count per tile (items thread-contiguous: thread t owns 16 consecutive keys).
+__global__ __launch_bounds__(256) void seg_count(const uint32_t* __restrict__ keys, int64_t n,
+                                                 uint32_t* __restrict__ tile_cnt) {
+    __shared__ uint32_t red[256];
+    const int tid = threadIdx.x;
+    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * 16;
+    uint32_t c = 0;
+    for (int i = 0; i < 16; ++i) {
+        const int64_t idx = lo + i;
+        if (idx < n && (idx == 0 || keys[idx] != keys[idx - 1])) ++c;
+    }
+    red[tid] = c;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (tid < off) red[tid] += red[tid + off];
+        __syncthreads();
+    }
+    if (tid == 0) tile_cnt[blockIdx.x] = red[0];
+}
+
+__global__ __launch_bounds__(256) void seg_write(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ perm,
+                                                 int64_t n, const uint32_t* __restrict__ tile_base,
+                                                 int32_t* __restrict__ uniq, int32_t* __restrict__ seg_off,
+                                                 int32_t* __restrict__ pair_slot, int32_t* __restrict__ sorted_slot,
+                                                 int32_t* __restrict__ n_unique, int32_t max_unique) {
+    __shared__ uint32_t part[256];
+    const int tid = threadIdx.x;
+    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * 16;
+    uint32_t c = 0;
+    for (int i = 0; i < 16; ++i) {
+        const int64_t idx = lo + i;
+        if (idx < n && (idx == 0 || keys[idx] != keys[idx - 1])) ++c;
+    }
+    part[tid] = c;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t v = tid >= off ? part[tid - off] : 0u;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    // slot of the item just before this thread's first head
+    int32_t slot = (int32_t)(tile_base[blockIdx.x] + part[tid] - c) - 1;
+    for (int i = 0; i < 16; ++i) {
+        const int64_t idx = lo + i;
+        if (idx >= n) break;
+        const uint32_t k = keys[idx];
+        if (idx == 0 || k != keys[idx - 1]) {
+            ++slot;
+            if (slot < max_unique) {
+                uniq[slot] = (int32_t)k;
+                seg_off[slot] = (int32_t)idx;
+            }
+        }
+        // Ids >= n_experts (a caller error) could make more slots than the buffers hold;
+        // clamp so every later kernel stays in bounds.
+        const int32_t s = slot < max_unique ? slot : max_unique - 1;
+        sorted_slot[idx] = s;
+        pair_slot[perm[idx]] = s;
+        if (idx == n - 1) {
+            const int32_t u = *n_unique < max_unique ? *n_unique : max_unique;
+            *n_unique = u;
+            seg_off[u] = (int32_t)n;
+        }
+    }
+}
+
+__global__ void seg_empty(int32_t* __restrict__ seg_off, int32_t* __restrict__ n_unique) {
+    seg_off[0] = 0;
+    *n_unique = 0;
+}
+
+int launch_sort_empty(int32_t* seg_off, int32_t* n_unique, hipStream_t stream) {
+    hipLaunchKernelGGL(seg_empty, dim3(1), dim3(1), 0, stream, seg_off, n_unique);
+    return (int)hipGetLastError();
+}
+
+static int key_bits(int64_t n_experts) {
+    int b = 0;
+    while (b < 32 && ((int64_t)1 << b) < n_experts) ++b;
+    return b;
+}
+
+size_t sort_workspace_bytes(int64_t n) {
+    const int64_t tiles = (n + kSortTile - 1) / kSortTile;
+    const size_t words = (size_t)4 * n + (size_t)kRadix * tiles + (size_t)tiles + 64;
+    return words * sizeof(uint32_t);
+}
+
+int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,
+                        int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
+                        hipStream_t stream) {
+    const int n_tiles = (int)((n + kSortTile - 1) / kSortTile);
+    uint32_t* w = reinterpret_cast<uint32_t*>(ws);
+    uint32_t* kbuf[2] = {w, w + n};
+    uint32_t* vbuf[2] = {w + 2 * n, w + 3 * n};
+    uint32_t* hist = w + 4 * n;
+    uint32_t* tcnt = hist + (size_t)kRadix * n_tiles;
+    const int bits = key_bits(n_experts);
+    const int passes = bits <= 8 ? 1 : (bits + 7) / 8;
+    hipError_t err;
+    for (int p = 0; p < passes; ++p) {
+        const uint32_t* kin = p == 0 ? reinterpret_cast<const uint32_t*>(ids) : kbuf[(p - 1) & 1];
+        const uint32_t* vin = p == 0 ? nullptr : vbuf[(p - 1) & 1];
+        uint32_t* kout = kbuf[p & 1];
+        uint32_t* vout = p == passes - 1 ? reinterpret_cast<uint32_t*>(perm) : vbuf[p & 1];
+        const int shift = 8 * p;
+        hipLaunchKernelGGL(sort_upsweep, dim3(n_tiles), dim3(256), 0, stream, kin, n, shift, hist, n_tiles);
+        hipLaunchKernelGGL(scan_exclusive, dim3(1), dim3(kScanThreads), 0, stream, hist, (int64_t)kRadix * n_tiles,
+                           (int32_t*)nullptr);
+        if (p == 0)
+            hipLaunchKernelGGL(sort_downsweep<true>, dim3(n_tiles), dim3(256), 0, stream, kin, vin, kout, vout, n,
+                               shift, hist, n_tiles);
+        else
+            hipLaunchKernelGGL(sort_downsweep<false>, dim3(n_tiles), dim3(256), 0, stream, kin, vin, kout, vout, n,
+                               shift, hist, n_tiles);
+        if ((err = hipGetLastError()) != hipSuccess) return (int)err;
+    }
+    const uint32_t* sorted = kbuf[(passes - 1) & 1];
+    hipLaunchKernelGGL(seg_count, dim3(n_tiles), dim3(256), 0, stream, sorted, n, tcnt);
+    hipLaunchKernelGGL(scan_exclusive, dim3(1), dim3(kScanThreads), 0, stream, tcnt, (int64_t)n_tiles, n_unique);
+    hipLaunchKernelGGL(seg_write, dim3(n_tiles), dim3(256), 0, stream, sorted, (const uint32_t*)perm, n, tcnt, uniq,
+                       seg_off, pair_slot, sorted_slot, n_unique, (int32_t)(n < n_experts ? n : n_experts));
+    return (int)hipGetLastError();
+}
+
+}  // namespace ethos

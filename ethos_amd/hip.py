@@ -1,0 +1,138 @@
+"""Torch-facing wrappers of the C-ABI: validate, allocate outputs from the caching
+allocator, enqueue on the current stream.  Every function requires CUDA (HIP)
+tensors and raises on anything else -- there is no CPU path.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, dtype_code, load
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtype=None, dim=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be on a HIP device (got {t.device}); the ETHOS kernels have no CPU path")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if dim is not None and t.dim() != dim:
+        raise RuntimeError(f"{name} must have {dim} dims, got shape {tuple(t.shape)}")
+
+
+def workspace(nbytes: int, device) -> tuple[torch.Tensor, int]:
+    """A scratch buffer of at least `nbytes` bytes (int64 storage keeps it 16-byte
+    aligned) and its real size, which is what the ABI is told."""
+    ws = torch.empty((max(1, (nbytes + 7) // 8),), dtype=torch.int64, device=device)
+    size = ws.numel() * ws.element_size()
+    if size < nbytes:
+        raise AssertionError("workspace sizing")
+    return ws, size
+
+
+def query_proj(x: torch.Tensor, wq: torch.Tensor, bq: torch.Tensor, bn_alpha: torch.Tensor, bn_beta: torch.Tensor,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [n, d], wq [H, dq, d], bq [H, dq], bn_alpha/beta [H, dq] fp32 -> q [n, H, dq]."""
+    _need(x, "x", dim=2)
+    _need(wq, "wq", x.dtype, 3)
+    _need(bq, "bq", x.dtype, 2)
+    _need(bn_alpha, "bn_alpha", torch.float32)
+    _need(bn_beta, "bn_beta", torch.float32)
+    n, d = x.shape
+    H, dq, d2 = wq.shape
+    if d2 != d or bq.shape != (H, dq) or bn_alpha.numel() != H * dq or bn_beta.numel() != H * dq:
+        raise RuntimeError("query_proj: inconsistent shapes")
+    if out is None:
+        out = torch.empty((n, H, dq), dtype=x.dtype, device=x.device)
+    rc = load().ethos_query_proj(x.data_ptr(), wq.data_ptr(), bq.data_ptr(), bn_alpha.data_ptr(), bn_beta.data_ptr(),
+                                 n, d, H, dq, dtype_code(x.dtype), out.data_ptr(), _stream())
+    check(rc, "ethos_query_proj")
+    return out
+
+
+def route_topk(q: torch.Tensor, sub_keys_1: torch.Tensor, sub_keys_2: torch.Tensor, top_k: int,
+               k_cand: int | None = None):
+    """q [..., dq] -> (gates [..., top_k] q.dtype, expert ids [..., top_k] int32)."""
+    _need(q, "q")
+    _need(sub_keys_1, "sub_keys_1", q.dtype, 2)
+    _need(sub_keys_2, "sub_keys_2", q.dtype, 2)
+    dq = q.shape[-1]
+    K = sub_keys_1.shape[0]
+    if sub_keys_1.shape != (K, dq // 2) or sub_keys_2.shape != (K, dq // 2):
+        raise RuntimeError("route_topk: sub-key tables must be [K, d_query/2]")
+    kc = 2 * top_k if k_cand is None else k_cand
+    rows = q.numel() // dq
+    gates = torch.empty((*q.shape[:-1], top_k), dtype=q.dtype, device=q.device)
+    ids = torch.empty((*q.shape[:-1], top_k), dtype=torch.int32, device=q.device)
+    rc = load().ethos_route_topk(q.data_ptr(), sub_keys_1.data_ptr(), sub_keys_2.data_ptr(), rows, dq, K, top_k, kc,
+                                 dtype_code(q.dtype), gates.data_ptr(), ids.data_ptr(), _stream())
+    check(rc, "ethos_route_topk")
+    return gates, ids
+
+
+def sort_segment(ids: torch.Tensor, n_experts: int) -> dict:
+    """Reorder pairs by expert id.  Returns perm, uniq, seg_off, pair_slot, sorted_slot,
+    n_unique (device int32[1]) and max_unique (host int, the buffer bound)."""
+    _need(ids, "ids", torch.int32)
+    n = ids.numel()
+    dev = ids.device
+    max_u = max(1, min(n, n_experts))
+    ws, ws_bytes = workspace(load().ethos_sort_workspace_bytes(n, n_experts), dev)
+    r = dict(
+        perm=torch.empty(n, dtype=torch.int32, device=dev),
+        uniq=torch.empty(max_u, dtype=torch.int32, device=dev),
+        seg_off=torch.empty(max_u + 1, dtype=torch.int32, device=dev),
+        pair_slot=torch.empty(n, dtype=torch.int32, device=dev),
+        sorted_slot=torch.empty(n, dtype=torch.int32, device=dev),
+        n_unique=torch.empty(1, dtype=torch.int32, device=dev),
+        max_unique=max_u,
+    )
+    rc = load().ethos_sort_segment(ids.data_ptr(), n, n_experts, ws.data_ptr(), ws_bytes, r["perm"].data_ptr(),
+                                   r["uniq"].data_ptr(), r["seg_off"].data_ptr(), r["pair_slot"].data_ptr(),
+                                   r["sorted_slot"].data_ptr(), r["n_unique"].data_ptr(), _stream())
+    check(rc, "ethos_sort_segment")
+    return r
+
+
+def generate(latents: torch.Tensor, uniq: torch.Tensor, n_unique: torch.Tensor, max_unique: int, w1: torch.Tensor,
+             w2: torch.Tensor) -> torch.Tensor:
+    """[u ; v] rows [max_unique, 2 d] for the unique experts (rows >= U untouched)."""
+    _need(latents, "latents", dim=2)
+    _need(uniq, "uniq", torch.int32)
+    _need(n_unique, "n_unique", torch.int32)
+    _need(w1, "w1", latents.dtype, 2)
+    _need(w2, "w2", latents.dtype, 2)
+    E, dl = latents.shape
+    dh = w1.shape[0]
+    if w1.shape != (dh, dl) or w2.shape[1] != dh or w2.shape[0] % 2:
+        raise RuntimeError("generate: inconsistent weight shapes")
+    d = w2.shape[0] // 2
+    uv = torch.empty((max_unique, 2 * d), dtype=latents.dtype, device=latents.device)
+    rc = load().ethos_generate(latents.data_ptr(), E, uniq.data_ptr(), n_unique.data_ptr(), max_unique, w1.data_ptr(),
+                               w2.data_ptr(), dl, dh, d, dtype_code(latents.dtype), uv.data_ptr(), _stream())
+    check(rc, "ethos_generate")
+    return uv
+
+
+def apply_scatter(x: torch.Tensor, uv: torch.Tensor, seg: dict, gates: torch.Tensor, n_heads: int,
+                  top_k: int) -> torch.Tensor:
+    """out [n, d] = head-averaged weighted sum of the experts' contributions."""
+    _need(x, "x", dim=2)
+    _need(uv, "uv", x.dtype, 2)
+    _need(gates, "gates", x.dtype)
+    n, d = x.shape
+    if uv.shape[1] != 2 * d or gates.numel() != n * n_heads * top_k:
+        raise RuntimeError("apply_scatter: inconsistent shapes")
+    act = torch.empty(n * n_heads * top_k, dtype=torch.float32, device=x.device)
+    out = torch.empty_like(x)
+    rc = load().ethos_apply_scatter(x.data_ptr(), uv.data_ptr(), seg["perm"].data_ptr(), seg["sorted_slot"].data_ptr(),
+                                    seg["pair_slot"].data_ptr(), gates.data_ptr(), n, n_heads, top_k, d,
+                                    dtype_code(x.dtype), act.data_ptr(), out.data_ptr(), _stream())
+    check(rc, "ethos_apply_scatter")
+    return out

@@ -1,0 +1,145 @@
+/*
+ * ethos_hip.h -- C-ABI of the MI355X (gfx950) ETHOS expert-layer forward path.
+ *
+ * The reference (wrmedford/ETHOS) implements the path as a PyTorch nn.Module
+ * (SimplifiedHypernetMoE, model.py:267-343) and a Triton launch per routing head
+ * (FusedLowRankMoE_Reordered.forward, kernels.py:145-221; launch site
+ * kernels.py:179-215).  This library replaces the work below those modules with
+ * four stages, each an entry point here:
+ *
+ *   ethos_query_proj     per-head query projection + eval BatchNorm
+ *   ethos_route_topk     sub-key scoring, top-k_cand per half, combination, top-k, softmax
+ *   ethos_sort_segment   reordering of (token, head, k) pairs by expert id
+ *   ethos_generate       hypernetwork expert generation over the unique experts
+ *   ethos_apply_scatter  per-pair activation and weighted scatter-back into tokens
+ *
+ * Conventions (every entry point):
+ *   - All pointers are device pointers owned by the caller; nothing is allocated.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and the
+ *     call returns without synchronising.
+ *   - Return 0 on success, a negative ETHOS_E* code for an argument error (nothing is
+ *     enqueued), or a positive hipError_t from the launch.  ethos_last_error() gives a
+ *     message for the calling thread's last failure.
+ *   - dtype: ETHOS_F32 or ETHOS_BF16; tensors of "dtype T" hold that type, row-major.
+ *   - Deterministic: the same inputs give bit-identical outputs on every run.
+ */
+#ifndef ETHOS_HIP_H
+#define ETHOS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ETHOS_ABI_VERSION 1
+
+#define ETHOS_F32 0
+#define ETHOS_BF16 1
+
+#define ETHOS_EDTYPE (-1)       /* unknown dtype code */
+#define ETHOS_ESIZE (-2)        /* sizes out of range / inconsistent */
+#define ETHOS_ENULL (-3)        /* a required pointer is NULL */
+#define ETHOS_EALIGN (-4)       /* a pointer is not 16-byte aligned */
+#define ETHOS_EWORKSPACE (-5)   /* workspace too small */
+#define ETHOS_EUNSUPPORTED (-6) /* valid for the reference, outside this build's limits */
+
+/* Message for the calling thread's last failed call ("" after a success). */
+const char* ethos_last_error(void);
+
+/* ETHOS_ABI_VERSION of the loaded library. */
+int ethos_abi_version(void);
+
+/*
+ * Query projection + eval-mode Query BatchNorm for all heads.
+ * Replaces query_projs[h](x_flat) then query_norms[h](.) (model.py:215-216; modules
+ * built at model.py:195-202).
+ *   x        [n_tok, d_model]            dtype T
+ *   wq       [n_heads, d_query, d_model] dtype T  (query_projs[h].weight stacked)
+ *   bq       [n_heads, d_query]          dtype T  (query_projs[h].bias stacked)
+ *   bn_alpha [n_heads, d_query] fp32  weight / sqrt(running_var + eps)
+ *   bn_beta  [n_heads, d_query] fp32  bias - running_mean * bn_alpha
+ *   q_out    [n_tok, n_heads, d_query]   dtype T
+ * q = RN_T(fmaf(RN_T(x . wq[h,o] + bq[h,o]), alpha, beta)); the dot product is
+ * evaluated exactly for bf16 (fp64 accumulation) and in a fixed order for fp32.
+ */
+int ethos_query_proj(const void* x, const void* wq, const void* bq, const float* bn_alpha, const float* bn_beta,
+                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* q_out,
+                     void* stream);
+
+/*
+ * Product-key routing of n_rows independent query rows (row = token * n_heads + head).
+ * Replaces the body of ProductKeyRouter.forward (model.py:217-245) and the head
+ * stacking (model.py:250-252).
+ *   q          [n_rows, d_query]        dtype T
+ *   sub_keys_1 [n_sub_keys, d_query/2]  dtype T  (router.sub_keys_1.weight)
+ *   sub_keys_2 [n_sub_keys, d_query/2]  dtype T  (router.sub_keys_2.weight)
+ *   out_scores [n_rows, top_k]          dtype T  softmax gates (fp32 softmax cast to T)
+ *   out_ids    [n_rows, top_k]          int32    expert ids = i1 * n_sub_keys + i2
+ * k_cand is the per-half candidate count (the reference uses 2 * top_k, model.py:224).
+ * Order: score descending, ties to the lowest index (sub-key index per half, expert id
+ * for the final list).  Limits: k_cand <= 32 (top_k <= 16 at k_cand = 2 top_k).
+ */
+int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, int64_t n_rows, int32_t d_query,
+                     int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype, void* out_scores,
+                     int32_t* out_ids, void* stream);
+
+/* Workspace size for ethos_sort_segment. */
+size_t ethos_sort_workspace_bytes(int64_t n_pairs, int64_t n_experts);
+
+/*
+ * Reordering of pairs by expert id (stable LSD radix sort + segmentation).
+ * No reference code: the reference visits pairs in token order (model.py:306-334;
+ * kernels.py:167-215); the paper's Algorithm 1 reorders by expert (paper p.10).
+ *   ids         [n_pairs] int32 expert id of pair p (out_ids flattened), < n_experts
+ *   workspace   >= ethos_sort_workspace_bytes(n_pairs, n_experts) bytes, 16-byte aligned
+ *   perm        [n_pairs] int32   pair ids ordered by (expert id, pair id)
+ *   uniq_ids    [min(n_pairs, n_experts)] int32  expert id of each unique slot, ascending
+ *   seg_off     [min(n_pairs, n_experts) + 1] int32  pairs of slot u are perm[seg_off[u]..seg_off[u+1])
+ *   pair_slot   [n_pairs] int32   slot of pair p
+ *   sorted_slot [n_pairs] int32   slot of sorted position i
+ *   n_unique    [1] int32         number of unique experts U (written on the device)
+ */
+int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, void* workspace,
+                       size_t workspace_bytes, int32_t* perm, int32_t* uniq_ids, int32_t* seg_off,
+                       int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique, void* stream);
+
+/*
+ * Expert generation for the unique experts: uv[u] = RN_T(W2 gelu(RN_T(W1 z))), with
+ * z = latents[uniq_ids[u]] and gelu in erf form.  Replaces the per-pair
+ * gelu(z @ W1) / h @ W_u / h @ W_v of model.py:320-332 (weights read at
+ * model.py:297-300; ExpertGenerationNetwork model.py:168-179).
+ *   latents  [n_experts, d_latent]          dtype T  (expert_latents.weight)
+ *   uniq_ids [max_unique], n_unique [1]     from ethos_sort_segment (U read on the device)
+ *   w1       [d_hidden, d_latent]           dtype T  (generation_network.net.0.weight)
+ *   w2       [2 * d_model, d_hidden]        dtype T  (generation_network.net.2.weight)
+ *   uv_out   [max_unique, 2 * d_model]      dtype T  rows u < U written: u_e = [:d_model], v_e = [d_model:]
+ * Limits: d_latent % 16 (bf16) or % 2 (fp32) == 0, d_hidden % 32 == 0, d_model % 16 == 0.
+ */
+int ethos_generate(const void* latents, int64_t n_experts, const int32_t* uniq_ids, const int32_t* n_unique,
+                   int64_t max_unique, const void* w1, const void* w2, int32_t d_latent, int32_t d_hidden,
+                   int32_t d_model, int32_t dtype, void* uv_out, void* stream);
+
+/*
+ * Expert apply and weighted scatter-back, averaged over heads.
+ * Replaces the pair loop and head average of model.py:306-341 (and the per-token
+ * Triton program of kernels.py:83-120 with the head loop of kernels.py:167-220).
+ *   x             [n_tok, d_model]                 dtype T, 16-byte aligned
+ *   uv            [>= U, 2 * d_model]              dtype T, from ethos_generate
+ *   perm, sorted_slot, pair_slot                   from ethos_sort_segment
+ *   scores        [n_tok, n_heads, top_k]          dtype T  gates from ethos_route_topk
+ *   act_workspace [n_tok * n_heads * top_k] fp32   per-pair activations (scratch)
+ *   out           [n_tok, d_model]                 dtype T
+ * out[t] = RN_T(sum_h^T RN_T(sum_k RN_T(a_p * v_e)) / n_heads), a_p = RN_T(RN_T(gelu(RN_T(u_e . x_t))) * g_p).
+ * Limits: d_model % 8 (bf16) or % 4 (fp32) == 0 and d_model <= 4096 (bf16) / 2048 (fp32).
+ */
+int ethos_apply_scatter(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
+                        const int32_t* pair_slot, const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k,
+                        int32_t d_model, int32_t dtype, float* act_workspace, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ETHOS_HIP_H */

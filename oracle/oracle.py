@@ -145,14 +145,12 @@ def gelu64(v: np.ndarray) -> np.ndarray:
 
 # ------------------------------------------------------------------ router
 def bn_coeffs(weight, bias, running_mean, running_var, eps: float = 1e-5):
-    """fp32 eval-mode BatchNorm coefficients: alpha = w / sqrt(var + eps),
-    beta = b - mean * alpha (model.py:200-202,216 in .eval())."""
-    w = np.asarray(weight, np.float32)
-    b = np.asarray(bias, np.float32)
-    m = np.asarray(running_mean, np.float32)
-    v = np.asarray(running_var, np.float32)
-    alpha = (w / np.sqrt(v + np.float32(eps))).astype(np.float32)
-    beta = (b - (m * alpha).astype(np.float32)).astype(np.float32)
+    """fp32 eval-mode BatchNorm coefficients (model.py:200-202,216 in .eval()):
+    alpha = fp32(w / sqrt(var + eps)) and beta = fp32(b - mean * alpha), each computed in
+    fp64 from the fp32 parameters and rounded once."""
+    w, b, m, v = (np.asarray(a, np.float32).astype(np.float64) for a in (weight, bias, running_mean, running_var))
+    alpha = (w / np.sqrt(v + float(eps))).astype(np.float32)
+    beta = (b - m * alpha.astype(np.float64)).astype(np.float32)
     return np.ascontiguousarray(alpha), np.ascontiguousarray(beta)
 
 

@@ -1,0 +1,86 @@
+"""The C-ABI library loads and exports every entry point include/ethos_hip.h declares;
+argument errors come back as codes (checked without a GPU: validation runs before
+any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from ethos_amd import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "ethos_hip.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(ethos_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    assert names == sorted(_lib.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version():
+    assert _lib.load().ethos_abi_version() == 1
+
+
+def _rc(fn, *args):
+    return getattr(_lib.load(), fn)(*args)
+
+
+def test_argument_errors_are_codes():
+    L = _lib.load()
+    # unknown dtype
+    assert L.ethos_route_topk(1, 1, 1, 4, 8, 16, 2, 4, 7, 1, 1, None) == -1
+    assert b"dtype" in L.ethos_last_error()
+    # k_cand larger than the sub-key count (the reference's torch.topk would raise)
+    assert L.ethos_route_topk(1, 1, 1, 4, 8, 16, 16, 32, 1, 1, 1, None) == -2
+    # k_cand beyond this build's limit
+    assert L.ethos_route_topk(1, 1, 1, 4, 8, 4096, 32, 64, 1, 1, 1, None) == -6
+    # odd d_query
+    assert L.ethos_route_topk(1, 1, 1, 4, 7, 16, 2, 4, 1, 1, 1, None) == -2
+    # null pointers
+    assert L.ethos_query_proj(None, 1, 1, 1, 1, 4, 8, 2, 8, 1, 1, None) == -3
+    # workspace too small
+    assert L.ethos_sort_segment(1, 100, 16, 16, 8, 16, 16, 16, 16, 16, 16, None) == -5
+    # misaligned apply pointers
+    assert L.ethos_apply_scatter(3, 16, 16, 16, 16, 16, 4, 2, 2, 64, 1, 16, 16, None) == -4
+    # unsupported generator shape
+    assert L.ethos_generate(16, 4, 16, 16, 4, 16, 16, 10, 32, 64, 1, 16, None) == -6
+    # zero-size work is a no-op success
+    assert L.ethos_query_proj(None, None, None, None, None, 0, 8, 2, 8, 1, None, None) == 0
+    assert L.ethos_last_error() == b""
+
+
+def test_workspace_size_grows_with_pairs():
+    L = _lib.load()
+    a = L.ethos_sort_workspace_bytes(1000, 262144)
+    b = L.ethos_sort_workspace_bytes(1_000_000, 262144)
+    assert 16 * 1000 <= a < b and b >= 16 * 1_000_000
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 4097, 524288, 4194304])
+def test_workspace_helper_covers_requested_bytes(n):
+    """The sort workspace handed to the ABI is at least what the library asks for."""
+    import torch
+
+    from ethos_amd import hip
+
+    need = _lib.load().ethos_sort_workspace_bytes(n, 262144)
+    ws, size = hip.workspace(need, torch.device("cpu"))
+    assert size == ws.numel() * ws.element_size() >= need
+
+
+def test_route_rejects_top_k_above_32():
+    L = _lib.load()
+    assert L.ethos_route_topk(1, 1, 1, 4, 8, 4096, 40, 32, 1, 1, 1, None) == -6

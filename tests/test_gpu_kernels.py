@@ -1,0 +1,135 @@
+"""Each HIP stage against the oracle on identical inputs (through the C-ABI).
+
+Bars: query projection, sub-key routing ids, the sort and the segmentation are
+bit-exact; gates equal in bf16 (fp32: rtol 2e-6, the softmax's expf may differ by an
+ulp); generated expert rows and layer outputs within the stated tolerances.
+"""
+import numpy as np
+import pytest
+import torch
+
+from ethos_amd import hip
+from ethos_amd.workloads import SHAPES, make_inputs
+from gpu_util import check_out, to_dev, to_host
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SMALL = ["tiny", "tiny_fp32", "cfg1", "cfg1_dq128"]
+
+
+def _setup(name, n_tok=None, signal=False):
+    sh = SHAPES[name]
+    if n_tok is not None:
+        sh = sh.with_tokens(n_tok)
+    x, sd = make_inputs(sh, signal=signal)
+    P = O.unpack_state(sd, sh.num_heads)
+    return sh, O.from_torch(x), P
+
+
+@pytest.mark.parametrize("name", SMALL + ["cfg3"])
+def test_query_proj_bit_exact(name):
+    sh, x, P = _setup(name)
+    q_ref = O.query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype)
+    q = hip.query_proj(to_dev(x), to_dev(P["Wq"]), to_dev(P["bq"]), to_dev(P["alpha"]), to_dev(P["beta"]))
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(q), q_ref)
+
+
+@pytest.mark.parametrize("name", SMALL + ["cfg3", "yaml"])
+def test_route_bit_exact(name):
+    sh, x, P = _setup(name)
+    q = O.query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype)
+    g_ref, ids_ref = O.route(q, P["K1"], P["K2"], sh.top_k, sh.dtype)
+    g, ids = hip.route_topk(to_dev(q), to_dev(P["K1"]), to_dev(P["K2"]), sh.top_k)
+    torch.cuda.synchronize()
+    ids = to_host(ids)
+    assert np.array_equal(ids, ids_ref), f"{np.sum(np.any(ids != ids_ref, -1))} rows differ"
+    gf, gr = O.to_f32(to_host(g), sh.dtype), O.to_f32(g_ref, sh.dtype)
+    if sh.dtype == "bf16":
+        assert np.array_equal(gf, gr)
+    else:
+        np.testing.assert_allclose(gf, gr, rtol=2e-6, atol=1e-8)
+
+
+def test_route_ties_break_to_lowest_index():
+    """Duplicate sub-key rows force exact score ties in both halves."""
+    sh, x, P = _setup("tiny")
+    K1 = P["K1"].copy()
+    K2 = P["K2"].copy()
+    K1[1::2] = K1[0::2]
+    K2[3] = K2[5]
+    q = O.query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype)
+    g_ref, ids_ref = O.route(q, K1, K2, sh.top_k, sh.dtype)
+    g, ids = hip.route_topk(to_dev(q), to_dev(K1), to_dev(K2), sh.top_k)
+    assert np.array_equal(to_host(ids), ids_ref)
+
+
+@pytest.mark.parametrize("n,E,pattern", [(1, 1, "rand"), (5, 262144, "rand"), (4096, 4096, "rand"),
+                                         (8192, 4096, "rand"), (70000, 262144, "rand"), (524288, 262144, "rand"),
+                                         (30000, 262144, "same"), (50000, 262144, "skew"), (4097, 7, "rand"),
+                                         (12345, 262144, "max")])
+def test_sort_segment_exact(n, E, pattern):
+    rng = np.random.default_rng(n + E)
+    if pattern == "same":
+        ids = np.full(n, 12345, np.int32)
+    elif pattern == "skew":
+        ids = np.minimum((rng.zipf(1.3, n) - 1), E - 1).astype(np.int32)
+    elif pattern == "max":
+        ids = np.where(rng.random(n) < 0.5, E - 1, rng.integers(0, E, n)).astype(np.int32)
+    else:
+        ids = rng.integers(0, E, n).astype(np.int32)
+    perm, uniq, seg, inv = O.sort_segment(ids, E)
+    r = hip.sort_segment(to_dev(ids), E)
+    torch.cuda.synchronize()
+    U = int(r["n_unique"].item())
+    assert U == len(uniq)
+    assert np.array_equal(to_host(r["perm"]), perm)
+    assert np.array_equal(to_host(r["uniq"])[:U], uniq)
+    assert np.array_equal(to_host(r["seg_off"])[: U + 1], seg)
+    assert np.array_equal(to_host(r["pair_slot"]), inv)
+    assert np.array_equal(to_host(r["sorted_slot"]), inv[perm])
+
+
+@pytest.mark.parametrize("name,signal", [("tiny", False), ("tiny", True), ("tiny_fp32", True), ("cfg1", True),
+                                         ("cfg3", False), ("cfg3", True)])
+def test_generate_matches_oracle(name, signal):
+    sh, x, P = _setup(name, signal=signal)
+    rng = np.random.default_rng(0)
+    U = min(sh.num_experts, 777)
+    uniq = np.sort(rng.choice(sh.num_experts, U, replace=False)).astype(np.int32)
+    uv_ref = O.generate(P["latents"], uniq, P["W1"], P["W2"], sh.dtype)
+    n_unique = torch.tensor([U], dtype=torch.int32, device="cuda")
+    uv = hip.generate(to_dev(P["latents"]), to_dev(uniq), n_unique, U + 5, to_dev(P["W1"]), to_dev(P["W2"]))
+    torch.cuda.synchronize()
+    got = O.to_f32(to_host(uv), sh.dtype)[:U].astype(np.float64)
+    ref = uv_ref.astype(np.float64)
+    d = np.abs(got - ref)
+    scale = np.abs(ref).max()
+    if sh.dtype == "fp32":
+        assert np.all(d <= 1e-4 * np.abs(ref) + 1e-5 * scale), d.max()
+    else:
+        # bf16 storage: most elements identical, the rest one rounding apart
+        ulp = np.abs(ref) * 2.0 ** -7 + 1e-30
+        assert np.mean(d > 0) < 0.05, np.mean(d > 0)
+        assert np.all(d <= 2 * ulp + 1e-3 * scale)
+        assert np.linalg.norm(d) / np.linalg.norm(ref) < 2e-3
+
+
+@pytest.mark.parametrize("name,signal", [("tiny", False), ("tiny", True), ("tiny_fp32", True), ("cfg1", False),
+                                         ("cfg3", True)])
+def test_apply_matches_oracle(name, signal):
+    """Given identical routing and generated rows, the scatter-back matches the oracle."""
+    sh, x, P = _setup(name, signal=signal)
+    q = O.query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype)
+    g, ids = O.route(q, P["K1"], P["K2"], sh.top_k, sh.dtype)
+    seg = hip.sort_segment(to_dev(ids.reshape(-1)), sh.num_experts)
+    U = int(seg["n_unique"].item())
+    uv_dev = hip.generate(to_dev(P["latents"]), seg["uniq"], seg["n_unique"], seg["max_unique"], to_dev(P["W1"]),
+                          to_dev(P["W2"]))
+    out = hip.apply_scatter(to_dev(x), uv_dev, seg, to_dev(g), sh.num_heads, sh.top_k)
+    torch.cuda.synchronize()
+    uv = O.to_f32(to_host(uv_dev), sh.dtype)[:U]
+    ref = O.apply(x, uv, to_host(seg["pair_slot"]), g, sh.num_heads, sh.top_k, sh.dtype)
+    got = O.to_f32(to_host(out), sh.dtype)
+    check_out(got, ref, sh.dtype, signal=signal, nerr_max=2e-3)
