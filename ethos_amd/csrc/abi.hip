@@ -44,7 +44,6 @@ int num_cus() {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-int elem_bytes(int dtype) { return dtype == ETHOS_BF16 ? 2 : 4; }
 bool dtype_ok(int dtype) { return dtype == ETHOS_F32 || dtype == ETHOS_BF16; }
 
 }  // namespace
@@ -72,9 +71,9 @@ int ethos_query_proj(const void* x, const void* wq, const void* bq, const float*
                       "ethos_query_proj");
 }
 
-int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, int64_t n_rows, int32_t d_query,
-                     int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype, void* out_scores,
-                     int32_t* out_ids, void* stream) {
+int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, const float* key_norms,
+                     int64_t n_rows, int32_t d_query, int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype,
+                     void* out_scores, int32_t* out_ids, void* stream) {
     g_err[0] = 0;
     if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_route_topk: unknown dtype %d", dtype);
     if (n_rows < 0 || d_query <= 0 || (d_query & 1) || n_sub_keys <= 0 || top_k <= 0 || k_cand <= 0)
@@ -90,13 +89,17 @@ int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys
     if ((int64_t)n_sub_keys * n_sub_keys > INT32_MAX)
         return fail(ETHOS_EUNSUPPORTED, "ethos_route_topk: %d sub-keys give expert ids beyond int32", n_sub_keys);
     const int dh2 = d_query / 2;
-    if (ethos::route_tile_keys(n_sub_keys, dh2, elem_bytes(dtype)) < 64)
-        return fail(ETHOS_EUNSUPPORTED, "ethos_route_topk: d_query=%d too wide for the LDS key tile", d_query);
+    if (!ethos::route_supported(n_sub_keys, dh2, dtype))
+        return fail(ETHOS_EUNSUPPORTED,
+                    "ethos_route_topk: needs n_sub_keys <= 512, d_query/2 <= 256 and d_query/2 %% %d == 0 "
+                    "(got %d, %d)", dtype == ETHOS_BF16 ? 16 : 4, n_sub_keys, d_query);
     if (n_rows == 0) return 0;
     if (!q || !sub_keys_1 || !sub_keys_2 || !out_scores || !out_ids)
         return fail(ETHOS_ENULL, "ethos_route_topk: null pointer");
-    return hip_status(ethos::launch_route(q, sub_keys_1, sub_keys_2, n_rows, d_query, n_sub_keys, top_k, k_cand,
-                                          dtype, out_scores, out_ids, (hipStream_t)stream),
+    if (!aligned16(q) || !aligned16(sub_keys_1) || !aligned16(sub_keys_2))
+        return fail(ETHOS_EALIGN, "ethos_route_topk: q and sub-key tables must be 16-byte aligned");
+    return hip_status(ethos::launch_route(q, sub_keys_1, sub_keys_2, key_norms, n_rows, d_query, n_sub_keys, top_k,
+                                          k_cand, dtype, out_scores, out_ids, (hipStream_t)stream),
                       "ethos_route_topk");
 }
 

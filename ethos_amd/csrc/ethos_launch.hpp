@@ -11,10 +11,10 @@ namespace ethos {
 int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
                  int d, int ncols, int dtype, void* q, hipStream_t stream);
 
-int route_tile_keys(int K, int dh2, int elem_bytes);
-size_t route_smem_bytes(int dh2, int KT, int elem_bytes);
-int launch_route(const void* q, const void* k1, const void* k2, int64_t rows, int dq, int K, int top_k, int kc,
-                 int dtype, void* gates, int32_t* ids, hipStream_t stream);
+size_t route_smem_bytes(int K, int dh2);
+bool route_supported(int K, int dh2, int dtype);
+int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, int64_t rows, int dq, int K,
+                 int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream);
 
 size_t sort_workspace_bytes(int64_t n);
 int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,

@@ -15,38 +15,15 @@
 // maximum and tiles past U are skipped, so no host synchronisation is needed.
 #include "ethos_common.hpp"
 #include "ethos_launch.hpp"
+#include "ethos_mfma.hpp"
 
 namespace ethos {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-template <typename T> struct Mfma;
-template <> struct Mfma<uint16_t> {
-    static constexpr int kK = 16;     // reduction depth per instruction
-    static constexpr int kKL = 8;     // consecutive k per lane; lanes 32..63 hold the upper half
-    static constexpr int kRows = 64;  // experts per tile
-    typedef bf16x8_t frag;
-    __device__ __forceinline__ static frag load(const uint16_t* p) { return *reinterpret_cast<const frag*>(p); }
-    __device__ __forceinline__ static f32x16_t mma(frag a, frag b, f32x16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-    }
-};
-template <> struct Mfma<float> {
-    static constexpr int kK = 2;
-    static constexpr int kKL = 1;
-    static constexpr int kRows = 32;
-    typedef float frag;
-    __device__ __forceinline__ static frag load(const float* p) { return *p; }
-    __device__ __forceinline__ static f32x16_t mma(frag a, frag b, f32x16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-    }
-};
+template <typename T> struct GenTile;
+template <> struct GenTile<uint16_t> { static constexpr int kRows = 64; };  // experts per tile
+template <> struct GenTile<float> { static constexpr int kRows = 32; };
 
 constexpr int kGenPad = 8;  // LDS row padding (elements)
-
-// Row of accumulator element i of a 32x32 MFMA tile held by `lane`; column = lane % 32.
-__device__ __forceinline__ int mfma32_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
 template <typename T>
 __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ latents, int64_t n_experts,
@@ -55,7 +32,7 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
                                                        const T* __restrict__ w2, int dl, int dh, int d2,
                                                        T* __restrict__ uv) {
     using M = Mfma<T>;
-    constexpr int R = M::kRows;
+    constexpr int R = GenTile<T>::kRows;
     constexpr int RB = R / 32;
     extern __shared__ __align__(16) unsigned char smem[];
     const int zp = dl + kGenPad, hp = dh + kGenPad;
@@ -160,7 +137,7 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
 
 template <typename T>
 static size_t gen_smem(int dl, int dh) {
-    return (size_t)Mfma<T>::kRows * ((dl + kGenPad) + (dh + kGenPad)) * sizeof(T);
+    return (size_t)GenTile<T>::kRows * ((dl + kGenPad) + (dh + kGenPad)) * sizeof(T);
 }
 
 size_t generate_smem_bytes(int dl, int dh, int dtype) {
@@ -170,7 +147,7 @@ size_t generate_smem_bytes(int dl, int dh, int dtype) {
 int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                     int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, int dtype, void* uv,
                     int num_cus, hipStream_t stream) {
-    const int R = dtype == kBF16 ? Mfma<uint16_t>::kRows : Mfma<float>::kRows;
+    const int R = dtype == kBF16 ? GenTile<uint16_t>::kRows : GenTile<float>::kRows;
     int64_t tiles = (max_unique + R - 1) / R;
     int64_t cap = (int64_t)num_cus * 2;
     const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);

@@ -5,31 +5,99 @@
 //
 // Numeric contract (identical to the CPU oracle's, written independently):
 //   s[j]   = RN_T(fp64 FMA chain over the half-query and sub-key j, index order)
+//            (for bf16 operands: the correctly rounded dot product)
 //   order  = (score descending, index ascending), -0 == +0; the index is the sub-key
 //            index for the per-half lists and the expert id e = i1*K + i2 for the
 //            combined list -- "ties broken to the lowest index".
 //   c[a,b] = RN_T(fp32(v1[a] + v2[b]))
 //   gate_i = RN_T(expf(c_i - c_0) / sum_i expf(c_i - c_0)), sum in list order.
 //
-// Layout: one workgroup (4 waves) owns 32 consecutive rows.  For each half, the
-// sub-key table is staged into LDS transposed ([dim][key], <= 64 KiB per tile) and
-// every wave scores its 8 rows against it; lane l owns keys l, l+64, ....  A
-// running canonical top-k_cand per (row, half) is merged tile by tile with a
-// DPP wave-max extraction over canonical 64-bit keys (score image << 32 | ~index).
+// Certified filter, exact refinement.  Computing all K sub-key scores exactly is
+// the expensive way; instead:
+//   1. MFMA (fp32 accumulation) gives approximate scores s~ for a 32-row x K tile.
+//      Whatever the accumulation order, |s~ - s| <= e_j = gamma * ||q|| * ||k_j||
+//      with gamma = (dh2 + 16) * 2^-22 (every partial sum rounded at worst like a
+//      truncating fp32 add), by Cauchy-Schwarz on sum |q_i k_ij|.
+//   2. tau_s = the k_cand-th largest of the 64 per-lane maxima of s~ is at most the
+//      k_cand-th largest s~, so at least k_cand keys have s >= tau_s - max_j e_j =: tau.
+//      A key whose upper bound rounds below RN_T(tau) rounds strictly below k_cand
+//      other keys and cannot be selected: it is dropped.
+//   3. The survivors (about 40 of 512) are scored exactly (the fp64 chain) one per
+//      lane and ranked with 64-lane bitonic sort / merge networks on canonical keys.
+// The output therefore equals exhaustive exact scoring bit for bit.
 #pragma clang fp contract(off)
 
 #include "ethos_common.hpp"
 #include "ethos_launch.hpp"
+#include "ethos_mfma.hpp"
 
 namespace ethos {
 
 constexpr int kRtWaves = 4;
-constexpr int kRtRowsPerWave = 8;
-constexpr int kRtRows = kRtWaves * kRtRowsPerWave;
-constexpr int kRtMaxKc = 32;      // k_cand <= 32  (top_k <= 16)
-constexpr int kRtMaxNk = 8;       // keys per lane per tile (tile <= 512 keys)
-constexpr int kRtCombSlots = 16;  // combined pairs per lane (k_cand^2 <= 1024)
-constexpr int kRtTileBytes = 64 * 1024;
+constexpr int kRtRows = 32;                            // rows per workgroup (one MFMA row block)
+constexpr int kRtRowsPerWave = kRtRows / kRtWaves;
+constexpr int kRtMaxKc = 32;                           // k_cand <= 32, top_k <= 32
+constexpr int kRtMaxK = 512;                           // sub-keys per table
+constexpr int kRtSlots = kRtMaxK / kWave;              // approximate scores per lane per row
+constexpr int kRtCombSlots = 16;                       // combined pairs per lane (k_cand^2 <= 1024)
+constexpr int kRtMaxDh2 = 256;
+
+// ---------------------------------------------------------------- wave networks
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
+    const int lo = __shfl_xor((int)(uint32_t)v, mask, kWave);
+    const int hi = __shfl_xor((int)(uint32_t)(v >> 32), mask, kWave);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// Bitonic sort of one value per lane, descending in lane order.
+template <typename V>
+__device__ __forceinline__ V shfl_xor_v(V v, int mask);
+template <>
+__device__ __forceinline__ uint64_t shfl_xor_v<uint64_t>(uint64_t v, int mask) { return shfl_xor_u64(v, mask); }
+template <>
+__device__ __forceinline__ uint32_t shfl_xor_v<uint32_t>(uint32_t v, int mask) {
+    return (uint32_t)__shfl_xor((int)v, mask, kWave);
+}
+
+template <typename V>
+__device__ __forceinline__ V wave_sort_desc(V v, int lane) {
+#pragma unroll
+    for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const V p = shfl_xor_v<V>(v, j);
+            const bool desc = (lane & k) == 0;
+            const bool lower = (lane & j) == 0;
+            const bool keep_max = lower == desc;
+            v = keep_max ? (v > p ? v : p) : (v < p ? v : p);
+        }
+    }
+    return v;
+}
+
+// run and chunk are each sorted descending across the lanes; returns the 64 largest
+// of their union, sorted descending.
+__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t run, uint64_t chunk, int lane) {
+    const uint64_t rev = shfl_xor_u64(chunk, kWave - 1);  // chunk[63 - lane]
+    uint64_t v = run > rev ? run : rev;                    // bitonic top-64
+#pragma unroll
+    for (int j = kWave >> 1; j > 0; j >>= 1) {
+        const uint64_t p = shfl_xor_u64(v, j);
+        const bool lower = (lane & j) == 0;
+        v = lower ? (v > p ? v : p) : (v < p ? v : p);
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<kDppXor1>(v));
+    v = max(v, dpp_u32<kDppXor2>(v));
+    v = max(v, dpp_u32<kDppRowHalfMirror>(v));
+    v = max(v, dpp_u32<kDppRowMirror>(v));
+    const uint32_t a = max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16));
+    const uint32_t b = max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48));
+    return max(a, b);
+}
 
 // Descending compare-exchange sort of a small per-lane array (fully unrolled).
 template <int N>
@@ -60,66 +128,205 @@ __device__ __forceinline__ void wave_extract(uint64_t (&c)[N], int count, uint64
     }
 }
 
+// 16 bytes of a key row -> doubles, in order.
+template <typename T> struct KeyVec;
+template <> struct KeyVec<uint16_t> {
+    static constexpr int kN = 8;
+    __device__ __forceinline__ static void load(const uint16_t* p, double* d) {
+        const uint4 r = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            d[2 * i] = (double)__uint_as_float(w[i] << 16);
+            d[2 * i + 1] = (double)__uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+};
+template <> struct KeyVec<float> {
+    static constexpr int kN = 4;
+    __device__ __forceinline__ static void load(const float* p, double* d) {
+        const float4 r = *reinterpret_cast<const float4*>(p);
+        d[0] = r.x;
+        d[1] = r.y;
+        d[2] = r.z;
+        d[3] = r.w;
+    }
+};
+
+struct RouteSmem {
+    size_t s_off, kn_off, qd_off, cand_off, lists_off, topk_off, total;
+};
+
+__host__ __device__ inline int route_pitch(int K) { return ((K + 31) / 32) * 32 + 4; }
+
+__host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2) {
+    RouteSmem L;
+    size_t off = 0;
+    L.s_off = off;
+    off += (size_t)kRtRows * route_pitch(K) * sizeof(float);
+    L.kn_off = off;
+    off += (size_t)2 * ((K + 31) / 32) * 32 * sizeof(float);
+    off = (off + 15) & ~(size_t)15;
+    L.qd_off = off;
+    off += (size_t)kRtWaves * dh2 * sizeof(double);
+    L.cand_off = off;
+    off += (size_t)kRtWaves * ((K + 31) / 32) * 32 * sizeof(int32_t);
+    off = (off + 15) & ~(size_t)15;
+    L.lists_off = off;
+    off += (size_t)kRtRows * 2 * kRtMaxKc * sizeof(uint64_t);
+    L.topk_off = off;
+    off += (size_t)kRtWaves * kRtMaxKc * sizeof(uint64_t);
+    L.total = off;
+    return L;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
-                                                    const T* __restrict__ keys2, int64_t rows, int dq, int K,
-                                                    int top_k, int kc, int KT, T* __restrict__ out_gates,
-                                                    int32_t* __restrict__ out_ids) {
+                                                    const T* __restrict__ keys2, const float* __restrict__ key_norms,
+                                                    int64_t rows, int dq, int K, int top_k, int kc,
+                                                    T* __restrict__ out_gates, int32_t* __restrict__ out_ids) {
+    using M = Mfma<T>;
     extern __shared__ __align__(16) unsigned char smem[];
     const int dh2 = dq / 2;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    T* keyt = reinterpret_cast<T*>(smem);
-    size_t off = ((size_t)dh2 * KT * sizeof(T) + 15) & ~(size_t)15;
-    double* qs = reinterpret_cast<double*>(smem + off) + (size_t)wave * dh2;
-    off += (size_t)kRtWaves * dh2 * sizeof(double);
-    uint64_t* lists = reinterpret_cast<uint64_t*>(smem + off);  // [kRtRows][2][kRtMaxKc]
-    off += (size_t)kRtRows * 2 * kRtMaxKc * sizeof(uint64_t);
-    uint64_t* topk = reinterpret_cast<uint64_t*>(smem + off) + wave * kRtMaxKc;
+    const int lrow = lane & 31, lk = (lane >> 5) * M::kKL;
+    const RouteSmem L = route_smem_layout(K, dh2);
+    const int pitch = route_pitch(K);
+    const int kpad = ((K + 31) / 32) * 32;
+    float* S = reinterpret_cast<float*>(smem + L.s_off);
+    float* kn = reinterpret_cast<float*>(smem + L.kn_off);
+    double* qd = reinterpret_cast<double*>(smem + L.qd_off) + (size_t)wave * dh2;
+    int32_t* cand = reinterpret_cast<int32_t*>(smem + L.cand_off) + (size_t)wave * kpad;
+    uint64_t* lists = reinterpret_cast<uint64_t*>(smem + L.lists_off);
+    uint64_t* topk = reinterpret_cast<uint64_t*>(smem + L.topk_off) + wave * kRtMaxKc;
 
     const int64_t row0 = (int64_t)blockIdx.x * kRtRows;
-    const int nk = KT / kWave;
+    const int nkb = kpad / 32;
+    const float gamma = (float)(dh2 + 16) * 0x1p-22f * 1.01f;
+
+    // Sub-key norms (upper bounds) for both tables.
+    for (int e = tid; e < 2 * kpad; e += 256) {
+        const int half = e / kpad, j = e - half * kpad;
+        float nrm = 0.0f;
+        if (j < K) {
+            if (key_norms) {
+                nrm = key_norms[half * K + j];
+            } else {
+                const T* kr = (half ? keys2 : keys1) + (int64_t)j * dh2;
+                double s2 = 0.0;
+                for (int i = 0; i < dh2; ++i) {
+                    const double v = Elem<T>::to_f64(kr[i]);
+                    s2 = fma(v, v, s2);
+                }
+                nrm = (float)(sqrt(s2) * (1.0 + 0x1p-20));
+            }
+        }
+        kn[e] = nrm;
+    }
 
     for (int half = 0; half < 2; ++half) {
         const T* keys = half ? keys2 : keys1;
-        for (int j0 = 0; j0 < K; j0 += KT) {
-            const int kt = min(KT, K - j0);
-            __syncthreads();
-            for (int e = tid; e < kt * dh2; e += 256) {
-                const int j = e / dh2, i = e - j * dh2;
-                keyt[i * KT + j] = keys[(int64_t)(j0 + j) * dh2 + i];
+        // 1. approximate scores for the 32-row tile: wave w takes key blocks w, w+4, ...
+        for (int kb0 = wave; kb0 < nkb; kb0 += 4 * kRtWaves) {
+            f32x16_t acc[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = f32x16_zero();
+            const int64_t arow = row0 + lrow;
+            for (int k0 = 0; k0 < dh2; k0 += M::kK) {
+                const typename M::frag a = arow < rows ? M::load(q + arow * dq + half * dh2 + k0 + lk) : M::zero();
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int kb = kb0 + 4 * c;
+                    if (kb < nkb) {
+                        const int j = kb * 32 + lrow;
+                        const typename M::frag b = j < K ? M::load(keys + (int64_t)j * dh2 + k0 + lk) : M::zero();
+                        acc[c] = M::mma(a, b, acc[c]);
+                    }
+                }
             }
-            __syncthreads();
-            for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
-                const int lr = wave * kRtRowsPerWave + rr;
-                const int64_t r = row0 + lr;
-                if (r >= rows) break;
-                for (int i = lane; i < dh2; i += kWave) qs[i] = Elem<T>::to_f64(q[r * dq + half * dh2 + i]);
-                __builtin_amdgcn_wave_barrier();
-                double acc[kRtMaxNk];
 #pragma unroll
-                for (int m = 0; m < kRtMaxNk; ++m) acc[m] = 0.0;
-                for (int i = 0; i < dh2; ++i) {
-                    const double qi = qs[i];
-                    const T* kr = keyt + i * KT + lane;
+            for (int c = 0; c < 4; ++c) {
+                const int kb = kb0 + 4 * c;
+                if (kb < nkb) {
 #pragma unroll
-                    for (int m = 0; m < kRtMaxNk; ++m)
-                        if (m < nk) acc[m] = fma(qi, Elem<T>::to_f64(kr[m * kWave]), acc[m]);
+                    for (int i = 0; i < 16; ++i) S[mfma32_row(i, lane) * pitch + kb * 32 + lrow] = acc[c][i];
                 }
-                __builtin_amdgcn_wave_barrier();
-                uint64_t c[kRtMaxNk + 1];
-#pragma unroll
-                for (int m = 0; m < kRtMaxNk; ++m) {
-                    const int j = lane + m * kWave;
-                    c[m] = (m < nk && j < kt) ? make_key(Elem<T>::round64(acc[m]), (uint32_t)(j0 + j)) : 0ull;
-                }
-                uint64_t* lst = lists + ((size_t)lr * 2 + half) * kRtMaxKc;
-                c[kRtMaxNk] = (j0 > 0 && lane < kc) ? lst[lane] : 0ull;
-                __builtin_amdgcn_wave_barrier();
-                sort_desc(c);
-                wave_extract(c, kc, lst, lane);
-                __builtin_amdgcn_wave_barrier();
             }
         }
+        __syncthreads();
+
+        // 2-3. per row: certified candidate filter, exact scores, canonical top-k_cand
+        for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
+            const int lr = wave * kRtRowsPerWave + rr;
+            const int64_t r = row0 + lr;
+            if (r >= rows) break;
+            float sq = 0.0f;
+            for (int i = lane; i < dh2; i += kWave) {
+                const float v = Elem<T>::to_f32(q[r * dq + half * dh2 + i]);
+                qd[i] = (double)v;
+                sq = __builtin_fmaf(v, v, sq);
+            }
+            const float qn = sqrtf(wave_sum(sq)) * (1.0f + 0x1p-12f);
+            __builtin_amdgcn_wave_barrier();
+
+            float s[kRtSlots], up[kRtSlots];
+            float lane_max = -__builtin_huge_valf();
+            uint32_t emax_bits = 0;
+#pragma unroll
+            for (int m = 0; m < kRtSlots; ++m) {
+                const int j = lane + m * kWave;
+                if (j < K) {
+                    s[m] = S[lr * pitch + j];
+                    const float marg = gamma * qn * kn[half * kpad + j] + fabsf(s[m]) * 0x1p-21f + 0x1p-120f;
+                    up[m] = s[m] + marg;
+                    lane_max = fmaxf(lane_max, s[m]);
+                    emax_bits = max(emax_bits, __float_as_uint(marg));
+                } else {
+                    s[m] = -__builtin_huge_valf();
+                    up[m] = -__builtin_huge_valf();
+                }
+            }
+            const float emax = __uint_as_float(wave_max_u32(emax_bits));
+            const uint32_t sorted = wave_sort_desc<uint32_t>(lane < K ? ord32(lane_max) : 0u, lane);
+            const uint32_t o = __builtin_amdgcn_readlane(sorted, kc - 1);
+            const float tau_s = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+            const float tau = tau_s - emax * (1.0f + 0x1p-20f) - fabsf(tau_s) * 0x1p-21f;
+            const float thr = Elem<T>::round32(tau);
+
+            int n_cand = 0;
+#pragma unroll
+            for (int m = 0; m < kRtSlots; ++m) {
+                const int j = lane + m * kWave;
+                const bool f = j < K && Elem<T>::round32(up[m]) >= thr;
+                const uint64_t bal = __ballot(f);
+                if (f) cand[n_cand + __popcll(bal & ((1ull << lane) - 1ull))] = j;
+                n_cand += (int)__popcll(bal);
+            }
+            __builtin_amdgcn_wave_barrier();
+
+            uint64_t run = 0;
+            for (int c0 = 0; c0 < n_cand; c0 += kWave) {
+                const int idx = c0 + lane;
+                uint64_t key = 0;
+                if (idx < n_cand) {
+                    const int j = cand[idx];
+                    const T* kr = keys + (int64_t)j * dh2;
+                    double acc = 0.0;
+                    for (int i = 0; i < dh2; i += KeyVec<T>::kN) {
+                        double kv[KeyVec<T>::kN];
+                        KeyVec<T>::load(kr + i, kv);
+#pragma unroll
+                        for (int t = 0; t < KeyVec<T>::kN; ++t) acc = fma(qd[i + t], kv[t], acc);
+                    }
+                    key = make_key(Elem<T>::round64(acc), (uint32_t)j);
+                }
+                key = wave_sort_desc<uint64_t>(key, lane);
+                run = c0 == 0 ? key : wave_merge_desc(run, key, lane);
+            }
+            if (lane < kc) lists[((size_t)lr * 2 + half) * kRtMaxKc + lane] = run;
+            __builtin_amdgcn_wave_barrier();
+        }
+        __syncthreads();
     }
 
     // Combine the two candidate lists of each row and take the canonical top-k.
@@ -158,38 +365,25 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
     }
 }
 
-// Keys per LDS tile for a sub-key width and element size (multiple of 64, <= 512).
-int route_tile_keys(int K, int dh2, int elem_bytes) {
-    int kt = kRtTileBytes / (dh2 * elem_bytes);
-    kt = (kt / kWave) * kWave;
-    if (kt > kRtMaxNk * kWave) kt = kRtMaxNk * kWave;
-    const int kround = ((K + kWave - 1) / kWave) * kWave;
-    if (kt > kround) kt = kround;
-    return kt;
+size_t route_smem_bytes(int K, int dh2) { return route_smem_layout(K, dh2).total; }
+
+bool route_supported(int K, int dh2, int dtype) {
+    const int kq = dtype == kBF16 ? 16 : 4;
+    return K <= kRtMaxK && dh2 <= kRtMaxDh2 && dh2 % kq == 0 && route_smem_bytes(K, dh2) <= 160 * 1024;
 }
 
-size_t route_smem_bytes(int dh2, int KT, int elem_bytes) {
-    size_t off = ((size_t)dh2 * KT * elem_bytes + 15) & ~(size_t)15;
-    off += (size_t)kRtWaves * dh2 * sizeof(double);
-    off += (size_t)kRtRows * 2 * kRtMaxKc * sizeof(uint64_t);
-    off += (size_t)kRtWaves * kRtMaxKc * sizeof(uint64_t);
-    return off;
-}
-
-int launch_route(const void* q, const void* k1, const void* k2, int64_t rows, int dq, int K, int top_k, int kc,
-                 int dtype, void* gates, int32_t* ids, hipStream_t stream) {
-    const int eb = dtype == kBF16 ? 2 : 4;
+int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, int64_t rows, int dq, int K,
+                 int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream) {
     const int dh2 = dq / 2;
-    const int KT = route_tile_keys(K, dh2, eb);
-    const size_t smem = route_smem_bytes(dh2, KT, eb);
+    const size_t smem = route_smem_bytes(K, dh2);
     dim3 grid((unsigned)((rows + kRtRows - 1) / kRtRows));
     if (dtype == kBF16)
         hipLaunchKernelGGL(route_kernel<uint16_t>, grid, dim3(256), smem, stream, (const uint16_t*)q,
-                           (const uint16_t*)k1, (const uint16_t*)k2, rows, dq, K, top_k, kc, KT,
+                           (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
                            (uint16_t*)gates, ids);
     else
         hipLaunchKernelGGL(route_kernel<float>, grid, dim3(256), smem, stream, (const float*)q, (const float*)k1,
-                           (const float*)k2, rows, dq, K, top_k, kc, KT, (float*)gates, ids);
+                           (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
     return (int)hipGetLastError();
 }
 

@@ -36,6 +36,18 @@ def workspace(nbytes: int, device) -> tuple[torch.Tensor, int]:
     return ws, size
 
 
+def key_norm_bounds(sub_keys_1: torch.Tensor, sub_keys_2: torch.Tensor) -> torch.Tensor:
+    """fp32 [2, K] upper bounds of the sub-key row norms: fp64 norms of the stored
+    values, inflated by 2^-20 and rounded, on the host (once per parameter version)."""
+    import numpy as np
+
+    rows = []
+    for t in (sub_keys_1, sub_keys_2):
+        v = t.detach().float().cpu().numpy().astype(np.float64)
+        rows.append((np.sqrt((v * v).sum(axis=1)) * (1.0 + 2.0 ** -20)).astype(np.float32))
+    return torch.from_numpy(np.stack(rows)).contiguous()
+
+
 def query_proj(x: torch.Tensor, wq: torch.Tensor, bq: torch.Tensor, bn_alpha: torch.Tensor, bn_beta: torch.Tensor,
                out: torch.Tensor | None = None) -> torch.Tensor:
     """x [n, d], wq [H, dq, d], bq [H, dq], bn_alpha/beta [H, dq] fp32 -> q [n, H, dq]."""
@@ -57,8 +69,9 @@ def query_proj(x: torch.Tensor, wq: torch.Tensor, bq: torch.Tensor, bn_alpha: to
 
 
 def route_topk(q: torch.Tensor, sub_keys_1: torch.Tensor, sub_keys_2: torch.Tensor, top_k: int,
-               k_cand: int | None = None):
-    """q [..., dq] -> (gates [..., top_k] q.dtype, expert ids [..., top_k] int32)."""
+               k_cand: int | None = None, key_norms: torch.Tensor | None = None):
+    """q [..., dq] -> (gates [..., top_k] q.dtype, expert ids [..., top_k] int32).
+    key_norms: optional fp32 [2, K] upper bounds of the sub-key row norms."""
     _need(q, "q")
     _need(sub_keys_1, "sub_keys_1", q.dtype, 2)
     _need(sub_keys_2, "sub_keys_2", q.dtype, 2)
@@ -70,7 +83,12 @@ def route_topk(q: torch.Tensor, sub_keys_1: torch.Tensor, sub_keys_2: torch.Tens
     rows = q.numel() // dq
     gates = torch.empty((*q.shape[:-1], top_k), dtype=q.dtype, device=q.device)
     ids = torch.empty((*q.shape[:-1], top_k), dtype=torch.int32, device=q.device)
-    rc = load().ethos_route_topk(q.data_ptr(), sub_keys_1.data_ptr(), sub_keys_2.data_ptr(), rows, dq, K, top_k, kc,
+    if key_norms is not None:
+        _need(key_norms, "key_norms", torch.float32)
+        if key_norms.numel() != 2 * K:
+            raise RuntimeError("route_topk: key_norms must hold 2 * K values")
+    rc = load().ethos_route_topk(q.data_ptr(), sub_keys_1.data_ptr(), sub_keys_2.data_ptr(),
+                                 key_norms.data_ptr() if key_norms is not None else None, rows, dq, K, top_k, kc,
                                  dtype_code(q.dtype), gates.data_ptr(), ids.data_ptr(), _stream())
     check(rc, "ethos_route_topk")
     return gates, ids

@@ -83,6 +83,7 @@ class ProductKeyRouter(nn.Module):
         self.sub_keys_2 = nn.Embedding(self.num_sub_keys, self.d_query // 2)
         self._cache_key = None
         self._cache = None
+        self._key_norms = None
 
     # -- parameter packing (cached until a parameter changes) ---------------------
     def _packed(self, dtype: torch.dtype, device: torch.device):
@@ -102,6 +103,7 @@ class ProductKeyRouter(nn.Module):
                 beta.append(b)
             alpha = torch.from_numpy(np.stack(alpha)).contiguous().to(device)
             beta = torch.from_numpy(np.stack(beta)).contiguous().to(device)
+            self._key_norms = hip.key_norm_bounds(k1, k2).to(device)
             self._cache = (wq, bq, k1, k2, alpha, beta)
             self._cache_key = key
         return self._cache
@@ -134,7 +136,7 @@ class ProductKeyRouter(nn.Module):
         """(gates [n, H, k] x.dtype, expert ids [n, H, k] int32)."""
         _, _, k1, k2, _, _ = self._packed(x_flat.dtype, x_flat.device)
         q = self.queries(x_flat)
-        return hip.route_topk(q, k1, k2, self.top_k)
+        return hip.route_topk(q, k1, k2, self.top_k, key_norms=self._key_norms)
 
     def forward(self, x_flat: torch.Tensor):
         with torch.no_grad():

@@ -75,15 +75,20 @@ int ethos_query_proj(const void* x, const void* wq, const void* bq, const float*
  *   q          [n_rows, d_query]        dtype T
  *   sub_keys_1 [n_sub_keys, d_query/2]  dtype T  (router.sub_keys_1.weight)
  *   sub_keys_2 [n_sub_keys, d_query/2]  dtype T  (router.sub_keys_2.weight)
+ *   key_norms  [2, n_sub_keys] fp32 or NULL: upper bounds of the Euclidean norms of the
+ *              rows of sub_keys_1 then sub_keys_2 (they size the error bound of the
+ *              MFMA pre-filter; NULL = computed by the kernel, slower)
  *   out_scores [n_rows, top_k]          dtype T  softmax gates (fp32 softmax cast to T)
  *   out_ids    [n_rows, top_k]          int32    expert ids = i1 * n_sub_keys + i2
  * k_cand is the per-half candidate count (the reference uses 2 * top_k, model.py:224).
+ * Sub-key scores are the correctly rounded (bf16) / fp64-accumulated (fp32) dot products.
  * Order: score descending, ties to the lowest index (sub-key index per half, expert id
- * for the final list).  Limits: k_cand <= 32 (top_k <= 16 at k_cand = 2 top_k).
+ * for the final list).  Limits: k_cand, top_k <= 32; n_sub_keys <= 512;
+ * d_query / 2 <= 256 and a multiple of 16 (bf16) or 4 (fp32); q, sub-keys 16-byte aligned.
  */
-int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, int64_t n_rows, int32_t d_query,
-                     int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype, void* out_scores,
-                     int32_t* out_ids, void* stream);
+int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, const float* key_norms,
+                     int64_t n_rows, int32_t d_query, int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype,
+                     void* out_scores, int32_t* out_ids, void* stream);
 
 /* Workspace size for ethos_sort_segment. */
 size_t ethos_sort_workspace_bytes(int64_t n_pairs, int64_t n_experts);

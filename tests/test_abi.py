@@ -41,14 +41,14 @@ def _rc(fn, *args):
 def test_argument_errors_are_codes():
     L = _lib.load()
     # unknown dtype
-    assert L.ethos_route_topk(1, 1, 1, 4, 8, 16, 2, 4, 7, 1, 1, None) == -1
+    assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 16, 2, 4, 7, 16, 16, None) == -1
     assert b"dtype" in L.ethos_last_error()
     # k_cand larger than the sub-key count (the reference's torch.topk would raise)
-    assert L.ethos_route_topk(1, 1, 1, 4, 8, 16, 16, 32, 1, 1, 1, None) == -2
+    assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 16, 16, 32, 1, 16, 16, None) == -2
     # k_cand beyond this build's limit
-    assert L.ethos_route_topk(1, 1, 1, 4, 8, 4096, 32, 64, 1, 1, 1, None) == -6
+    assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 4096, 32, 64, 1, 16, 16, None) == -6
     # odd d_query
-    assert L.ethos_route_topk(1, 1, 1, 4, 7, 16, 2, 4, 1, 1, 1, None) == -2
+    assert L.ethos_route_topk(16, 16, 16, None, 4, 7, 16, 2, 4, 1, 16, 16, None) == -2
     # null pointers
     assert L.ethos_query_proj(None, 1, 1, 1, 1, 4, 8, 2, 8, 1, 1, None) == -3
     # workspace too small
@@ -83,4 +83,7 @@ def test_workspace_helper_covers_requested_bytes(n):
 
 def test_route_rejects_top_k_above_32():
     L = _lib.load()
-    assert L.ethos_route_topk(1, 1, 1, 4, 8, 4096, 40, 32, 1, 1, 1, None) == -6
+    # more than 512 sub-keys and misaligned tables are rejected as well
+    assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 1024, 4, 8, 1, 16, 16, None) == -6
+    assert L.ethos_route_topk(18, 16, 16, None, 4, 32, 64, 4, 8, 1, 16, 16, None) == -4
+    assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 4096, 40, 32, 1, 16, 16, None) == -6

@@ -133,3 +133,47 @@ def test_apply_matches_oracle(name, signal):
     ref = O.apply(x, uv, to_host(seg["pair_slot"]), g, sh.num_heads, sh.top_k, sh.dtype)
     got = O.to_f32(to_host(out), sh.dtype)
     check_out(got, ref, sh.dtype, signal=signal, nerr_max=2e-3)
+
+
+def _stress_case(kind, rng, rows, K, dh2, dt):
+    """Adversarial query / sub-key sets for the certified routing filter."""
+    q = rng.standard_normal((rows, 2 * dh2)).astype(np.float32)
+    k1 = rng.standard_normal((K, dh2)).astype(np.float32) / np.sqrt(dh2)
+    k2 = rng.standard_normal((K, dh2)).astype(np.float32) / np.sqrt(dh2)
+    if kind == "all_equal":        # every sub-key identical: all K scores tie
+        k1[:] = k1[0]
+        k2[:] = k2[3]
+    elif kind == "near_ties":      # keys differ by tiny perturbations -> scores within a few ulps
+        k1 = k1[:1] + 1e-3 * k1
+        k2 = k2[:1] + 1e-3 * k2
+    elif kind == "cancellation":   # large terms cancelling: |s| << ||q|| ||k||
+        k1[:, dh2 // 2:] = -k1[:, : dh2 // 2] if dh2 % 2 == 0 else k1[:, dh2 // 2:]
+        q[:, dh2 // 2: dh2] = q[:, : dh2 // 2] * (1 + 1e-3 * rng.standard_normal((rows, dh2 // 2)))
+    elif kind == "zipf":           # sub-key rows scaled by (r+1)^-1.1
+        z = (np.arange(K) + 1.0) ** -1.1
+        k1 *= z[:, None]
+        k2 *= z[:, None]
+    elif kind == "dynamic_range":  # magnitudes spread over many binades
+        q *= np.exp2(rng.integers(-20, 20, q.shape)).astype(np.float32)
+        k1 *= np.exp2(rng.integers(-10, 10, k1.shape)).astype(np.float32)
+    enc = (lambda a: O.f32_to_bf16_bits(a)) if dt == "bf16" else (lambda a: a.astype(np.float32))
+    return enc(q), enc(k1), enc(k2)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp32"])
+@pytest.mark.parametrize("kind", ["all_equal", "near_ties", "cancellation", "zipf", "dynamic_range"])
+def test_route_stress_bit_exact(kind, dt):
+    rng = np.random.default_rng(hash((kind, dt)) % 2**32)
+    rows, K, dh2, top_k = 96, 512, 128, 16
+    q, k1, k2 = _stress_case(kind, rng, rows, K, dh2, dt)
+    g_ref, ids_ref = O.route(q, k1, k2, top_k, dt)
+    for norms in (None, "host"):
+        kn = None
+        if norms == "host":
+            from ethos_amd import hip as H
+
+            kn = H.key_norm_bounds(to_dev(k1), to_dev(k2)).cuda()
+        g, ids = hip.route_topk(to_dev(q), to_dev(k1), to_dev(k2), top_k, key_norms=kn)
+        torch.cuda.synchronize()
+        got = to_host(ids)
+        assert np.array_equal(got, ids_ref), f"{kind}/{dt}/{norms}: {np.sum(np.any(got != ids_ref, -1))} rows differ"
