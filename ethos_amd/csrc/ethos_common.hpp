@@ -13,12 +13,22 @@ constexpr int kWave = 64;
 // ---------------------------------------------------------------- conversions
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-// float -> bf16 bits, round to nearest even.
+// float -> bf16 bits, round to nearest even (NaN stays a quiet NaN); branch-free.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    uint32_t b = __float_as_uint(f);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x40u);
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return (uint16_t)(b >> 16);
+    const uint32_t b = __float_as_uint(f);
+    const uint32_t r = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+    const uint32_t n = (b >> 16) | 0x40u;
+    return (uint16_t)(((b & 0x7fffffffu) > 0x7f800000u) ? n : r);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair (a in the low half), round to nearest even, one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    const f32x2_t f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
 // double -> float with round-to-odd: truncate, then force the last bit to 1 if inexact.
@@ -56,6 +66,28 @@ template <> struct Elem<uint16_t> {
 
 // Exact GELU (erf form), fp32.
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+// Branch-free erf-form GELU for results that are rounded to bf16.  erfc(z), z >= 0, is
+// the Chebyshev fit of Press et al., Numerical Recipes, "erfcc" (fractional error
+// below 1.2e-7 for all z), so Phi(x) = erfc(-x / sqrt 2) / 2 keeps relative accuracy
+// on the negative tail as well -- far inside half a bf16 ulp (2^-9).
+__device__ __forceinline__ float gelu_erfc_fit(float x) {
+    const float z = fabsf(x) * 0.70710678118654752f;
+    const float t = __frcp_rn(1.0f + 0.5f * z);
+    float p = 0.17087277f;
+    p = __builtin_fmaf(p, t, -0.82215223f);
+    p = __builtin_fmaf(p, t, 1.48851587f);
+    p = __builtin_fmaf(p, t, -1.13520398f);
+    p = __builtin_fmaf(p, t, 0.27886807f);
+    p = __builtin_fmaf(p, t, -0.18628806f);
+    p = __builtin_fmaf(p, t, 0.09678418f);
+    p = __builtin_fmaf(p, t, 0.37409196f);
+    p = __builtin_fmaf(p, t, 1.00002368f);
+    p = __builtin_fmaf(p, t, -1.26551223f);
+    const float erfc_z = t * __expf(p - z * z);          // erfc(|x| / sqrt 2)
+    const float phi = x >= 0.0f ? 1.0f - 0.5f * erfc_z : 0.5f * erfc_z;
+    return x * phi;
+}
 
 // ---------------------------------------------------------------- wave reductions (DPP)
 // dpp_ctrl encodings (GCN/CDNA DPP): quad_perm, row_half_mirror, row_mirror.

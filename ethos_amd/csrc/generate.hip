@@ -135,6 +135,226 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
     }
 }
 
+// ---------------------------------------------------------------------------------
+// bf16 generator for the common shapes: 4 waves x MB*32 experts per workgroup, the
+// hidden activations never leave registers.
+//
+// GEMM1 is computed transposed, hid^T = W1 . Z^T (A = W1 rows, B = gathered latent
+// rows).  Lane l reads W1 row pi(l % 32) of each 32-row block, pi swapping bits 2 and
+// 3 of the row index, so that accumulator elements 8p..8p+7 of lane half h hold the
+// eight consecutive hidden values 16p + 8h .. 16p + 8h + 7 of expert l % 32.  After
+// erf-GELU and bf16 rounding they are exactly the k-slots of GEMM2's operand for
+// k-step s = 2t + p.  GEMM2 is also transposed, uv^T = W2 . hid^T, reading W2 from an
+// LDS chunk of 64 output columns laid out [16-byte group g][column]; each lane then
+// owns one expert row and four consecutive output columns per accumulator group,
+// stored as 8-byte writes.  Two independent accumulators per column block (even and
+// odd k-steps) keep the MFMA pipeline fed.
+// ---------------------------------------------------------------------------------
+constexpr int kG2Waves = 4;
+constexpr int kG2Cols = 64;  // output columns per staged W2 chunk
+
+__device__ __forceinline__ float round_bf16_hw(float x) { return __uint_as_float(pack_bf16x2(x, 0.0f) << 16); }
+
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
+    uint4 r;
+    r.x = pack_bf16x2(v[0], v[1]);
+    r.y = pack_bf16x2(v[2], v[3]);
+    r.z = pack_bf16x2(v[4], v[5]);
+    r.w = pack_bf16x2(v[6], v[7]);
+    return __builtin_bit_cast(bf16x8_t, r);
+}
+
+template <int DL, int DH, int MB>
+__global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void generate_bf16_kernel(
+    const uint16_t* __restrict__ latents, int64_t n_experts, const int32_t* __restrict__ uniq,
+    const int32_t* __restrict__ n_unique, const uint16_t* __restrict__ w1, const uint16_t* __restrict__ w2, int d2,
+    uint16_t* __restrict__ uv) {
+    constexpr int ROWS = kG2Waves * MB * 32;  // experts per tile
+    constexpr int KS1 = DL / 16;              // GEMM1 k-steps
+    constexpr int NB1 = DH / 32;              // hidden blocks of 32
+    constexpr int KS2 = DH / 16;              // GEMM2 k-steps
+    constexpr int GPR = DH / 8;               // 16-byte groups per W2 row
+    static_assert(GPR % kG2Waves == 0, "chunk staging shape");
+    // W2 chunks, double buffered: [buffer][16-byte group g = 2 s + h][column]
+    __shared__ uint4 bs[2][GPR * kG2Cols];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int prow = (l32 & ~0xc) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);  // bits 2 <-> 3
+    const int U = *n_unique;
+    const int n_tiles = (U + ROWS - 1) / ROWS;
+    const int n_chunks = d2 / kG2Cols;
+
+    for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int ubase = tile * ROWS + wave * MB * 32 + l32;
+        // W1 and W2 are the same for every tile; opaque copies of their pointers keep
+        // the compiler from hoisting all their loads out of the tile loop.
+        const uint16_t* w1t = w1;
+        const uint16_t* w2t = w2;
+        asm volatile("" : "+s"(w1t), "+s"(w2t));
+
+        // Direct global -> LDS copy of W2 chunk c: wave w moves groups w, w+4, ...;
+        // lane = column, 16 bytes each, landing contiguously at bs[buf][g][0..63].
+        auto issue_chunk = [&](int c, int buf) {
+            const uint16_t* src = w2t + (int64_t)(c * kG2Cols + lane) * DH;
+#pragma unroll
+            for (int g = wave; g < GPR; g += kG2Waves)
+                __builtin_amdgcn_global_load_lds(src + 8 * g,
+                                                 (__attribute__((address_space(3))) void*)&bs[buf][g * kG2Cols], 16,
+                                                 0, 0);
+        };
+        issue_chunk(0, 0);
+
+        // gathered latent rows (GEMM1 B operand)
+        bf16x8_t zf[MB][KS1];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int u = ubase + mb * 32;
+            const int64_t id = u < U ? (int64_t)uniq[u] : -1;
+            const bool ok = id >= 0 && id < n_experts;
+            const uint16_t* zr = latents + (ok ? id : 0) * DL + 8 * h;
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks)
+                zf[mb][ks] = ok ? *reinterpret_cast<const bf16x8_t*>(zr + ks * 16) : bf16x8_t{};
+        }
+
+        // GEMM1^T + GELU -> hidden k-slots hf[mb][s]; W1 fragments of block t + 1 are
+        // fetched while block t computes.
+        bf16x8_t hf[MB][KS2];
+        bf16x8_t wa[KS1], wn[KS1];
+#pragma unroll
+        for (int ks = 0; ks < KS1; ++ks)
+            wa[ks] = *reinterpret_cast<const bf16x8_t*>(w1t + prow * DL + ks * 16 + 8 * h);
+#pragma clang loop unroll(full)
+        for (int t = 0; t < NB1; ++t) {
+            if (t + 1 < NB1) {
+#pragma unroll
+                for (int ks = 0; ks < KS1; ++ks)
+                    wn[ks] = *reinterpret_cast<const bf16x8_t*>(w1t + ((t + 1) * 32 + prow) * DL + ks * 16 + 8 * h);
+            }
+            f32x16_t acc[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16_zero();
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[ks], zf[mb][ks], acc[mb], 0, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = gelu_erfc_fit(round_bf16_hw(acc[mb][8 * p + j]));
+                    hf[mb][2 * t + p] = pack_bf16x8(v);
+                }
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks) wa[ks] = wn[ks];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // GEMM2^T.  Results of chunk c are stored while chunk c + 1 computes, right
+        // after the loads of chunk c + 2 are issued, so the per-chunk wait for the
+        // LDS copies never waits on fresh stores.
+        uint2 pend[MB][2][4];
+        int pend_c = -1;
+        auto flush = [&]() {
+            if (pend_c < 0) return;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int u = ubase + mb * 32;
+                if (u < U) {
+                    uint16_t* row = uv + (int64_t)u * d2 + pend_c * kG2Cols + 4 * h;
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) *reinterpret_cast<uint2*>(row + cb * 32 + 8 * g) = pend[mb][cb][g];
+                }
+            }
+        };
+        for (int c = 0; c < n_chunks; ++c) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (c + 1 < n_chunks) issue_chunk(c + 1, (c + 1) & 1);
+            flush();
+            const uint4* cur = bs[c & 1];
+            constexpr int KI = MB == 1 ? 2 : 1;  // independent chains per (expert block, column block)
+            f32x16_t acc[MB][2][KI];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int ki = 0; ki < KI; ++ki) acc[mb][cb][ki] = f32x16_zero();
+            // B fragments are software-pipelined in groups of SG k-steps: the group after
+            // next is read from LDS while the current group's MFMAs issue.
+            constexpr int SG = 4;
+            static_assert(KS2 % SG == 0, "k-step grouping");
+            const uint4* bp = cur + h * kG2Cols + l32;
+            bf16x8_t bcur[SG][2], bnxt[SG][2];
+#pragma unroll
+            for (int q = 0; q < SG; ++q)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) bcur[q][cb] = __builtin_bit_cast(bf16x8_t, bp[2 * q * kG2Cols + cb * 32]);
+#pragma clang loop unroll(full)
+            for (int s0 = 0; s0 < KS2; s0 += SG) {
+                if (s0 + SG < KS2) {
+#pragma unroll
+                    for (int q = 0; q < SG; ++q)
+#pragma unroll
+                        for (int cb = 0; cb < 2; ++cb)
+                            bnxt[q][cb] = __builtin_bit_cast(bf16x8_t, bp[2 * (s0 + SG + q) * kG2Cols + cb * 32]);
+                }
+#pragma unroll
+                for (int q = 0; q < SG; ++q)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb) {
+                            const int s = s0 + q;
+                            acc[mb][cb][s % KI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bcur[q][cb], hf[mb][s],
+                                                                                          acc[mb][cb][s % KI], 0, 0, 0);
+                        }
+#pragma unroll
+                for (int q = 0; q < SG; ++q)
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) bcur[q][cb] = bnxt[q][cb];
+            }
+            // acc[mb][cb][*][i]: column c*64 + cb*32 + 8*(i/4) + 4h + i%4 of expert ubase + 32 mb
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+                    for (int ki = 1; ki < KI; ++ki) acc[mb][cb][0] += acc[mb][cb][ki];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        pend[mb][cb][g] = make_uint2(pack_bf16x2(acc[mb][cb][0][4 * g], acc[mb][cb][0][4 * g + 1]),
+                                                     pack_bf16x2(acc[mb][cb][0][4 * g + 2], acc[mb][cb][0][4 * g + 3]));
+                }
+            pend_c = c;
+        }
+        flush();
+        __syncthreads();
+    }
+}
+
+template <int DL, int DH, int MB>
+static bool launch_generate_bf16(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
+                                 int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* uv,
+                                 int num_cus, hipStream_t stream) {
+    constexpr int ROWS = kG2Waves * MB * 32;
+    if (dl != DL || dh != DH || d2 % kG2Cols) return false;
+    const int64_t tiles = (max_unique + ROWS - 1) / ROWS;
+    const int64_t cap = num_cus;
+    const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
+    hipLaunchKernelGGL((generate_bf16_kernel<DL, DH, MB>), dim3(grid), dim3(kG2Waves * 64), 0, stream,
+                       (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)w2,
+                       d2, (uint16_t*)uv);
+    return true;
+}
+
 template <typename T>
 static size_t gen_smem(int dl, int dh) {
     return (size_t)GenTile<T>::kRows * ((dl + kGenPad) + (dh + kGenPad)) * sizeof(T);
@@ -147,6 +367,13 @@ size_t generate_smem_bytes(int dl, int dh, int dtype) {
 int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                     int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, int dtype, void* uv,
                     int num_cus, hipStream_t stream) {
+    if (dtype == kBF16) {
+        if (launch_generate_bf16<128, 512, 1>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
+                                              num_cus, stream) ||
+            launch_generate_bf16<128, 256, 1>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
+                                              num_cus, stream))
+            return (int)hipGetLastError();
+    }
     const int R = dtype == kBF16 ? GenTile<uint16_t>::kRows : GenTile<float>::kRows;
     int64_t tiles = (max_unique + R - 1) / R;
     int64_t cap = (int64_t)num_cus * 2;

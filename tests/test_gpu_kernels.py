@@ -177,3 +177,25 @@ def test_route_stress_bit_exact(kind, dt):
         torch.cuda.synchronize()
         got = to_host(ids)
         assert np.array_equal(got, ids_ref), f"{kind}/{dt}/{norms}: {np.sum(np.any(got != ids_ref, -1))} rows differ"
+
+
+@pytest.mark.parametrize("dl,dh,d,U", [(128, 256, 1024, 1000), (128, 512, 512, 300), (128, 512, 1024, 129),
+                                        (128, 512, 1024, 1)])
+def test_generate_shapes(dl, dh, d, U):
+    """Generator over shapes the configs do not hit (hidden 256, a 512-wide model, tile
+    remainders and a single expert)."""
+    rng = np.random.default_rng(dl + dh + d + U)
+    E = 5000
+    lat = O.f32_to_bf16_bits(rng.standard_normal((E, dl)).astype(np.float32))
+    w1 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (dh, dl)) * 4 / np.sqrt(dl)).astype(np.float32))
+    w2 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(dh)).astype(np.float32))
+    uniq = np.sort(rng.choice(E, U, replace=False)).astype(np.int32)
+    ref = O.generate(lat, uniq, w1, w2, "bf16").astype(np.float64)
+    n_unique = torch.tensor([U], dtype=torch.int32, device="cuda")
+    uv = hip.generate(to_dev(lat), to_dev(uniq), n_unique, U + 3, to_dev(w1), to_dev(w2))
+    torch.cuda.synchronize()
+    got = O.to_f32(to_host(uv), "bf16")[:U].astype(np.float64)
+    d_ = np.abs(got - ref)
+    assert np.mean(d_ > 0) < 0.05
+    assert np.all(d_ <= 2 * np.abs(ref) * 2.0 ** -7 + 1e-3 * np.abs(ref).max())
+    assert np.linalg.norm(d_) / np.linalg.norm(ref) < 2e-3
