@@ -26,7 +26,8 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "ethos_last_error": (ctypes.c_char_p, []),
     "ethos_abi_version": (ctypes.c_int, []),
-    "ethos_query_proj": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "ethos_query_proj_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "ethos_query_proj": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _vp]),
     "ethos_route_topk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "ethos_sort_workspace_bytes": (_sz, [_i64, _i64]),
     "ethos_sort_segment": (ctypes.c_int, [_vp, _i64, _i64, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

@@ -54,20 +54,37 @@ const char* ethos_last_error(void) { return g_err; }
 
 int ethos_abi_version(void) { return ETHOS_ABI_VERSION; }
 
+size_t ethos_query_proj_workspace_bytes(int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query,
+                                        int32_t dtype) {
+    (void)d_model;
+    if (n_tok <= 0 || n_heads <= 0 || d_query <= 0) return 256;
+    const size_t b = ethos::qproj_workspace_bytes(n_tok, n_heads * d_query, dtype);
+    return b < 256 ? 256 : b;
+}
+
 int ethos_query_proj(const void* x, const void* wq, const void* bq, const float* bn_alpha, const float* bn_beta,
-                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* q_out,
-                     void* stream) {
+                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace,
+                     size_t workspace_bytes, void* q_out, void* stream) {
     g_err[0] = 0;
     if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_query_proj: unknown dtype %d", dtype);
     if (n_tok < 0 || d_model <= 0 || n_heads <= 0 || d_query <= 0)
         return fail(ETHOS_ESIZE, "ethos_query_proj: bad sizes n_tok=%lld d_model=%d n_heads=%d d_query=%d",
                     (long long)n_tok, d_model, n_heads, d_query);
-    if (n_tok > INT32_MAX / 2) return fail(ETHOS_ESIZE, "ethos_query_proj: n_tok too large");
+    if ((int64_t)n_heads * d_query > INT32_MAX / 2 || n_tok * (int64_t)n_heads * d_query > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_query_proj: n_tok * n_heads * d_query exceeds int32");
     if (n_tok == 0) return 0;
     if (!x || !wq || !bq || !bn_alpha || !bn_beta || !q_out)
         return fail(ETHOS_ENULL, "ethos_query_proj: null pointer");
+    const size_t need = ethos_query_proj_workspace_bytes(n_tok, d_model, n_heads, d_query, dtype);
+    if (dtype == ETHOS_BF16) {
+        if (!workspace || workspace_bytes < need)
+            return fail(ETHOS_EWORKSPACE, "ethos_query_proj: workspace of %zu bytes, %zu needed", workspace_bytes,
+                        need);
+        if (!aligned16(workspace) || !aligned16(x) || !aligned16(wq) || (d_model % 8))
+            return fail(ETHOS_EALIGN, "ethos_query_proj: x, wq, workspace 16-byte aligned and d_model %% 8 == 0");
+    }
     return hip_status(ethos::launch_qproj(x, wq, bq, bn_alpha, bn_beta, n_tok, d_model, n_heads * d_query, dtype,
-                                          q_out, (hipStream_t)stream),
+                                          workspace, q_out, num_cus(), (hipStream_t)stream),
                       "ethos_query_proj");
 }
 

@@ -8,8 +8,9 @@
 
 namespace ethos {
 
+size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int dtype);
 int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
-                 int d, int ncols, int dtype, void* q, hipStream_t stream);
+                 int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream);
 
 size_t route_smem_bytes(int K, int dh2);
 bool route_supported(int K, int dh2, int dtype);

@@ -198,10 +198,12 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
         auto issue_chunk = [&](int c, int buf) {
             const uint16_t* src = w2t + (int64_t)(c * kG2Cols + lane) * DH;
 #pragma unroll
-            for (int g = wave; g < GPR; g += kG2Waves)
+            for (int it = 0; it < GPR / kG2Waves; ++it) {
+                const int g = wave + it * kG2Waves;
                 __builtin_amdgcn_global_load_lds(src + 8 * g,
                                                  (__attribute__((address_space(3))) void*)&bs[buf][g * kG2Cols], 16,
                                                  0, 0);
+            }
         };
         issue_chunk(0, 0);
 

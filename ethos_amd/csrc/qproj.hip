@@ -12,6 +12,7 @@
 
 #include "ethos_common.hpp"
 #include "ethos_launch.hpp"
+#include "ethos_mfma.hpp"
 
 namespace ethos {
 
@@ -76,8 +77,249 @@ __global__ __launch_bounds__(256) void qproj_kernel(const T* __restrict__ x, con
     }
 }
 
+// ---------------------------------------------------------------------------------
+// bf16: certified MFMA projection with exact refinement.
+//
+// Every 16-term slice of the dot product is one 32x32x16 MFMA on a zero accumulator;
+// bf16 x bf16 products are exact in fp32, so however the MFMA orders its 15
+// additions, each rounded at worst like a truncating fp32 add, the slice is within
+// 15 * 2^-23 of the sum of its |x_i w_i|.  Slices are added in fp64 (error <= 2^-46 of
+// the same sum over 1024 terms), and A = sum |x_i w_i| itself comes from a second MFMA
+// on sign-cleared operands (fp32, relative error < 2^-12).  Hence
+//     |S~ - S| <= E = (15 * 2^-23 + 2^-46) * 1.001 * A * (1 + 2^-12) + 2^-50 (|S~| + |b|),
+// and when RN_T(S~ + b - E) == RN_T(S~ + b + E) the correctly rounded projection is
+// known; the rest (about 1% on random data) is queued and recomputed exactly.
+// ---------------------------------------------------------------------------------
+constexpr int kQmRows = 64;    // tokens per workgroup tile (2 waves x 32)
+constexpr int kQmCols = 128;   // output columns per workgroup tile (2 waves x 64)
+constexpr int kQmKC = 64;      // reduction chunk staged in LDS
+constexpr int kQmPitch = kQmKC + 8;
+
+struct QprojWs {
+    int32_t* count;   // [1]   uncertain elements
+    int32_t* list;    // [n_tok * ncols]
+};
+
+__host__ __device__ inline size_t qproj_ws_bytes(int64_t n_tok, int ncols) {
+    return 256 + 4 * (size_t)n_tok * ncols + 64;
+}
+
+__host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols) {
+    (void)n_tok;
+    (void)ncols;
+    unsigned char* p = reinterpret_cast<unsigned char*>(ws);
+    QprojWs w;
+    w.count = reinterpret_cast<int32_t*>(p);
+    w.list = reinterpret_cast<int32_t*>(p + 256);
+    return w;
+}
+
+__global__ void qproj_clear_kernel(int32_t* __restrict__ count) { *count = 0; }
+
+__device__ __forceinline__ bf16x8_t abs_bf16x8(bf16x8_t v) {
+    uint4 u = __builtin_bit_cast(uint4, v);
+    u.x &= 0x7fff7fffu;
+    u.y &= 0x7fff7fffu;
+    u.z &= 0x7fff7fffu;
+    u.w &= 0x7fff7fffu;
+    return __builtin_bit_cast(bf16x8_t, u);
+}
+
+constexpr int kQmLocal = 1024;  // uncertain elements a workgroup resolves itself (4 per thread)
+
+__global__ __launch_bounds__(256) void qproj_mfma_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ bias,
+                                                         const float* __restrict__ alpha,
+                                                         const float* __restrict__ beta, int n_tok, int d, int ncols,
+                                                         int32_t* __restrict__ count, int32_t* __restrict__ list,
+                                                         uint16_t* __restrict__ q) {
+    __shared__ __align__(16) uint16_t xs[kQmRows * kQmPitch];
+    __shared__ __align__(16) uint16_t ws[kQmCols * kQmPitch];
+    __shared__ uint32_t local[kQmLocal];  // (row << 16) | column within the tile
+    __shared__ int n_local;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int wr = wave >> 1, wc = wave & 1;
+    const int t0 = blockIdx.y * kQmRows, c0 = blockIdx.x * kQmCols;
+    if (tid == 0) n_local = 0;
+
+    auto stage = [&](int k0) {
+        // x [64 x 64] and w [128 x 64] in 16-byte pieces; rows past the end are zero
+        for (int e = tid; e < (kQmRows + kQmCols) * (kQmKC / 8); e += 256) {
+            const int r = e / (kQmKC / 8), kq = (e % (kQmKC / 8)) * 8;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (r < kQmRows) {
+                if (t0 + r < n_tok) v = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * d + k0 + kq);
+                *reinterpret_cast<uint4*>(&xs[r * kQmPitch + kq]) = v;
+            } else {
+                const int rc = r - kQmRows;
+                if (c0 + rc < ncols) v = *reinterpret_cast<const uint4*>(w + (int64_t)(c0 + rc) * d + k0 + kq);
+                *reinterpret_cast<uint4*>(&ws[rc * kQmPitch + kq]) = v;
+            }
+        }
+    };
+
+    double acc64[2][16];
+    f32x16_t accA[2] = {f32x16_zero(), f32x16_zero()};
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc64[cb][i] = 0.0;
+
+    for (int k0 = 0; k0 < d; k0 += kQmKC) {
+        __syncthreads();
+        stage(k0);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kQmKC; kk += 16) {
+            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&xs[(wr * 32 + l32) * kQmPitch + kk + 8 * h]);
+            const bf16x8_t aa = abs_bf16x8(a);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const bf16x8_t b =
+                    *reinterpret_cast<const bf16x8_t*>(&ws[(wc * 64 + cb * 32 + l32) * kQmPitch + kk + 8 * h]);
+                const f32x16_t c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, f32x16_zero(), 0, 0, 0);
+                accA[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aa, abs_bf16x8(b), accA[cb], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc64[cb][i] += (double)c[i];
+            }
+        }
+    }
+
+    // certify each element; store it, or queue it: first in LDS, past kQmLocal globally
+    const double kBound = (15.0 * 0x1p-23 + 0x1p-46) * 1.001 * (1.0 + 0x1p-12);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const int cl = wc * 64 + cb * 32 + l32;
+        const int c = c0 + cl;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int tl = wr * 32 + mfma32_row(i, lane);
+            const int t = t0 + tl;
+            const bool live = t < n_tok && c < ncols;
+            bool sure = true;
+            if (live) {
+                const double s = acc64[cb][i];
+                const double b = (double)bf16_bits_to_f32(bias[c]);
+                const double e = kBound * (double)accA[cb][i] + 0x1p-50 * (fabs(s) + fabs(b)) + 0x1p-1000;
+                const uint16_t lo = Elem<uint16_t>::from_f64((s - e) + b);
+                const uint16_t hi = Elem<uint16_t>::from_f64((s + e) + b);
+                sure = lo == hi;
+                if (sure) {
+                    const float qb = __builtin_fmaf(bf16_bits_to_f32(lo), alpha[c], beta[c]);
+                    q[(int64_t)t * ncols + c] = f32_to_bf16_bits(qb);
+                }
+            }
+            const bool queue = live && !sure;
+            const uint64_t bal = __ballot(queue);
+            if (bal) {
+                const int leader = __builtin_ctzll(bal);
+                const int rank = (int)__popcll(bal & ((1ull << lane) - 1ull));
+                int base = 0;
+                if (lane == leader) base = atomicAdd(&n_local, (int)__popcll(bal));
+                base = __shfl(base, leader, 64);
+                if (queue) {
+                    const int slot = base + rank;
+                    if (slot < kQmLocal) {
+                        local[slot] = ((uint32_t)tl << 16) | (uint32_t)cl;
+                    } else {
+                        const int g = atomicAdd(count, 1);
+                        list[g] = t * ncols + c;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int nl = n_local < kQmLocal ? n_local : kQmLocal;
+    if (nl == 0) return;
+
+    // exact fp64 chains for the queued elements, re-streaming the same K tiles
+    constexpr int R = kQmLocal / 256;
+    double ex[R];
+    int er[R], ec[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        ex[r] = 0.0;
+        const int j = tid + 256 * r;
+        const uint32_t v = j < nl ? local[j] : 0u;
+        er[r] = (int)(v >> 16);
+        ec[r] = (int)(v & 0xffffu);
+    }
+    for (int k0 = 0; k0 < d; k0 += kQmKC) {
+        __syncthreads();
+        stage(k0);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (tid + 256 * r < nl) {
+                const uint16_t* xr = &xs[er[r] * kQmPitch];
+                const uint16_t* wrp = &ws[ec[r] * kQmPitch];
+                for (int kk = 0; kk < kQmKC; ++kk)
+                    ex[r] = fma((double)bf16_bits_to_f32(xr[kk]), (double)bf16_bits_to_f32(wrp[kk]), ex[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (tid + 256 * r < nl) {
+            const int t = t0 + er[r], c = c0 + ec[r];
+            const float ql = Elem<uint16_t>::round64(ex[r] + (double)bf16_bits_to_f32(bias[c]));
+            q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
+        }
+    }
+}
+
+// Exact fp64 chain for the queued elements (index order, as the contract defines).
+__global__ __launch_bounds__(256) void qproj_fixup_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ bias,
+                                                          const float* __restrict__ alpha,
+                                                          const float* __restrict__ beta, int d, int ncols,
+                                                          const int32_t* __restrict__ count,
+                                                          const int32_t* __restrict__ list, uint16_t* __restrict__ q) {
+    const int n = *count;
+    for (int idx = blockIdx.x * 256 + threadIdx.x; idx < n; idx += gridDim.x * 256) {
+        const int e = list[idx];
+        const int t = e / ncols, c = e - t * ncols;
+        const uint16_t* xr = x + (int64_t)t * d;
+        const uint16_t* wr = w + (int64_t)c * d;
+        double acc = 0.0;
+        for (int i = 0; i < d; i += 8) {
+            const uint4 xa = *reinterpret_cast<const uint4*>(xr + i);
+            const uint4 wa = *reinterpret_cast<const uint4*>(wr + i);
+            const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
+            const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc = fma((double)__uint_as_float(xv[j] << 16), (double)__uint_as_float(wv[j] << 16), acc);
+                acc = fma((double)__uint_as_float(xv[j] & 0xffff0000u), (double)__uint_as_float(wv[j] & 0xffff0000u),
+                          acc);
+            }
+        }
+        const float ql = Elem<uint16_t>::round64(acc + (double)bf16_bits_to_f32(bias[c]));
+        q[e] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
+    }
+}
+
+size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int dtype) {
+    return dtype == kBF16 ? qproj_ws_bytes(n_tok, ncols) : 0;
+}
+
 int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
-                 int d, int ncols, int dtype, void* q, hipStream_t stream) {
+                 int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream) {
+    if (dtype == kBF16 && d % kQmKC == 0) {
+        const QprojWs W = qproj_ws(ws, n_tok, ncols);
+        hipLaunchKernelGGL(qproj_clear_kernel, dim3(1), dim3(1), 0, stream, W.count);
+        dim3 grid((ncols + kQmCols - 1) / kQmCols, (unsigned)((n_tok + kQmRows - 1) / kQmRows));
+        hipLaunchKernelGGL(qproj_mfma_kernel, grid, dim3(256), 0, stream, (const uint16_t*)x, (const uint16_t*)w,
+                           (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q);
+        hipLaunchKernelGGL(qproj_fixup_kernel, dim3((unsigned)num_cus * 4), dim3(256), 0, stream, (const uint16_t*)x,
+                           (const uint16_t*)w, (const uint16_t*)b, alpha, beta, d, ncols, W.count, W.list,
+                           (uint16_t*)q);
+        return (int)hipGetLastError();
+    }
     dim3 grid((ncols + kQpTN - 1) / kQpTN, (unsigned)((n_tok + kQpTM - 1) / kQpTM));
     if (dtype == kBF16)
         hipLaunchKernelGGL(qproj_kernel<uint16_t>, grid, dim3(256), 0, stream, (const uint16_t*)x,

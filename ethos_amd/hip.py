@@ -62,8 +62,9 @@ def query_proj(x: torch.Tensor, wq: torch.Tensor, bq: torch.Tensor, bn_alpha: to
         raise RuntimeError("query_proj: inconsistent shapes")
     if out is None:
         out = torch.empty((n, H, dq), dtype=x.dtype, device=x.device)
+    ws, ws_bytes = workspace(load().ethos_query_proj_workspace_bytes(n, d, H, dq, dtype_code(x.dtype)), x.device)
     rc = load().ethos_query_proj(x.data_ptr(), wq.data_ptr(), bq.data_ptr(), bn_alpha.data_ptr(), bn_beta.data_ptr(),
-                                 n, d, H, dq, dtype_code(x.dtype), out.data_ptr(), _stream())
+                                 n, d, H, dq, dtype_code(x.dtype), ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
     check(rc, "ethos_query_proj")
     return out
 

@@ -60,13 +60,19 @@ int ethos_abi_version(void);
  *   bq       [n_heads, d_query]          dtype T  (query_projs[h].bias stacked)
  *   bn_alpha [n_heads, d_query] fp32  weight / sqrt(running_var + eps)
  *   bn_beta  [n_heads, d_query] fp32  bias - running_mean * bn_alpha
+ *   workspace                        >= ethos_query_proj_workspace_bytes(...) bytes, 16-byte
+ *                                    aligned (bf16 uses it; fp32 may pass NULL / 0)
  *   q_out    [n_tok, n_heads, d_query]   dtype T
- * q = RN_T(fmaf(RN_T(x . wq[h,o] + bq[h,o]), alpha, beta)); the dot product is
- * evaluated exactly for bf16 (fp64 accumulation) and in a fixed order for fp32.
+ * q = RN_T(fmaf(RN_T(x . wq[h,o] + bq[h,o]), alpha, beta)); the dot product is the
+ * correctly rounded one for bf16 (certified MFMA accumulation, exact fp64 recomputation of
+ * the elements the certificate cannot settle) and an fp64 chain in index order for fp32.
  */
+size_t ethos_query_proj_workspace_bytes(int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query,
+                                        int32_t dtype);
+
 int ethos_query_proj(const void* x, const void* wq, const void* bq, const float* bn_alpha, const float* bn_beta,
-                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* q_out,
-                     void* stream);
+                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace,
+                     size_t workspace_bytes, void* q_out, void* stream);
 
 /*
  * Product-key routing of n_rows independent query rows (row = token * n_heads + head).

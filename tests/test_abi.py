@@ -50,7 +50,9 @@ def test_argument_errors_are_codes():
     # odd d_query
     assert L.ethos_route_topk(16, 16, 16, None, 4, 7, 16, 2, 4, 1, 16, 16, None) == -2
     # null pointers
-    assert L.ethos_query_proj(None, 1, 1, 1, 1, 4, 8, 2, 8, 1, 1, None) == -3
+    assert L.ethos_query_proj(None, 16, 16, 16, 16, 4, 8, 2, 8, 1, 16, 4096, 16, None) == -3
+    # bf16 needs its workspace
+    assert L.ethos_query_proj(16, 16, 16, 16, 16, 4, 64, 2, 8, 1, 16, 8, 16, None) == -5
     # workspace too small
     assert L.ethos_sort_segment(1, 100, 16, 16, 8, 16, 16, 16, 16, 16, 16, None) == -5
     # misaligned apply pointers
@@ -58,7 +60,7 @@ def test_argument_errors_are_codes():
     # unsupported generator shape
     assert L.ethos_generate(16, 4, 16, 16, 4, 16, 16, 10, 32, 64, 1, 16, None) == -6
     # zero-size work is a no-op success
-    assert L.ethos_query_proj(None, None, None, None, None, 0, 8, 2, 8, 1, None, None) == 0
+    assert L.ethos_query_proj(None, None, None, None, None, 0, 8, 2, 8, 1, None, 0, None, None) == 0
     assert L.ethos_last_error() == b""
 
 

@@ -199,3 +199,29 @@ def test_generate_shapes(dl, dh, d, U):
     assert np.mean(d_ > 0) < 0.05
     assert np.all(d_ <= 2 * np.abs(ref) * 2.0 ** -7 + 1e-3 * np.abs(ref).max())
     assert np.linalg.norm(d_) / np.linalg.norm(ref) < 2e-3
+
+
+@pytest.mark.parametrize("kind", ["cancellation", "midpoints"])
+def test_query_proj_certified_fallback_bit_exact(kind):
+    """Inputs where the MFMA certificate cannot settle most elements, forcing the exact
+    fp64 recomputation path; the result must still equal the oracle bit for bit."""
+    rng = np.random.default_rng(11)
+    n, d, H, dq = 96, 512, 2, 64
+    if kind == "cancellation":
+        half = rng.standard_normal((n, d // 2)).astype(np.float32)
+        x = np.concatenate([half, half], axis=1)
+        a = rng.uniform(-1, 1, (H, dq, d // 2)).astype(np.float32) / np.sqrt(d)
+        w = np.concatenate([a, -a + 1e-3 * rng.standard_normal(a.shape).astype(np.float32)], axis=2)
+        b = np.zeros((H, dq), np.float32)
+    else:
+        # small integers make many exact products and sums land on bf16 rounding ties
+        x = rng.integers(-8, 9, (n, d)).astype(np.float32)
+        w = rng.integers(-8, 9, (H, dq, d)).astype(np.float32) / 64
+        b = rng.integers(-4, 5, (H, dq)).astype(np.float32) / 128
+    x, w, b = (O.f32_to_bf16_bits(v) for v in (x, w, b))
+    alpha = rng.uniform(0.5, 1.5, (H, dq)).astype(np.float32)
+    beta = rng.uniform(-0.1, 0.1, (H, dq)).astype(np.float32)
+    q_ref = O.query_proj(x, w, b, alpha, beta, "bf16")
+    q = hip.query_proj(to_dev(x), to_dev(w), to_dev(b), to_dev(alpha), to_dev(beta))
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(q), q_ref), f"{np.sum(to_host(q) != q_ref)} elements differ"
