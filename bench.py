@@ -58,34 +58,68 @@ def stage_work(sh, U: int) -> dict:
     }
 
 
-def time_stages(m, x_flat, reps: int) -> tuple[dict, int]:
-    """Mean per-stage time (ms) over `reps` forwards, HIP events on the current stream."""
+STAGES = ["query_proj", "route", "sort_segment", "generate", "apply_scatter"]
+
+
+def timed_steps(m, x_flat, steps: int) -> tuple[float, dict]:
+    """Run `steps` layer forwards; return wall ms/step and the mean per-stage ms.
+
+    Stage boundaries are HIP events recorded on the stream every kernel is launched on
+    (torch's current stream, which the library is handed), inside the same timed region.
+    """
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        e = evs[i]
+        e[0].record()
+        pos = iter(range(1, len(STAGES) + 1))
+
+        def mark(stage, e=e, pos=pos):
+            e[next(pos)].record()
+
+        m.forward_flat(x_flat, mark)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    per = {k: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, k in enumerate(STAGES)}
+    return elapsed / steps * 1e3, per
+
+
+def unique_experts(m, x_flat) -> int:
     from ethos_amd import hip
 
-    sh_names = ["query_proj", "route", "sort_segment", "generate", "apply_scatter"]
-    acc = {k: 0.0 for k in sh_names}
-    U = 0
-    r = m.router
-    for _ in range(reps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
-        wq, bq, k1, k2, alpha, beta = r._packed(x_flat.dtype, x_flat.device)
-        lat, w1, w2 = m._generator_params(x_flat.dtype, x_flat.device)
-        ev[0].record()
-        q = hip.query_proj(x_flat, wq, bq, alpha, beta)
-        ev[1].record()
-        gates, ids = hip.route_topk(q, k1, k2, m.top_k)
-        ev[2].record()
+    with torch.no_grad():
+        _, ids = m.router.route(x_flat)
         seg = hip.sort_segment(ids.view(-1), m.num_experts)
-        ev[3].record()
-        uv = hip.generate(lat, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2)
-        ev[4].record()
-        hip.apply_scatter(x_flat, uv, seg, gates, m.num_heads, m.top_k)
-        ev[5].record()
-        torch.cuda.synchronize()
-        for i, k in enumerate(sh_names):
-            acc[k] += ev[i].elapsed_time(ev[i + 1])
-        U = int(seg["n_unique"].item())
-    return {k: v / reps for k, v in acc.items()}, U
+        return int(seg["n_unique"].item())
+
+
+def load_traffic(config: str, stage: str):
+    """HBM bytes per launch of `stage` from the committed rocprofv3 --pmc summary (FETCH_SIZE +
+    WRITE_SIZE, scaled by the same counters on a plain copy of known size), or None."""
+    path = os.path.join(REPO, "profiles", f"hbm_traffic_{config}.md")
+    if not os.path.exists(path):
+        return None
+    text = open(path).read()
+    try:
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block)["stages"][stage]["traffic_bytes"]
+    except (IndexError, KeyError, ValueError):
+        return None
+
+
+def copy_probe(mib: int) -> None:
+    """A plain device copy of `mib` MiB (read mib, write mib): the calibration kernel for the
+    FETCH_SIZE / WRITE_SIZE counters."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log(f"[bench] copy probe: neg over {mib} MiB fp32 ({n * 4} bytes read, {n * 4} bytes written) x3")
+    del src, dst
 
 
 def cpu_baseline(sh, x_cpu, sd_cpu, n_tokens: int) -> dict:
@@ -114,8 +148,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2")
-    ap.add_argument("--cpu-tokens", type=int, default=96, help="token sample for the CPU baseline (0 = skip)")
-    ap.add_argument("--stage-reps", type=int, default=10)
+    ap.add_argument("--cpu-tokens", type=int, default=1024, help="token sample for the CPU baseline (0 = skip)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run a plain copy of this many MiB (counter calibration for profiling)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -134,21 +169,17 @@ def main():
     m = m.cuda().eval()
     x = x_cpu.cuda().view(sh.batch, sh.n_tok // sh.batch, sh.d_model)
 
+    if args.copy_probe_mib > 0:
+        copy_probe(args.copy_probe_mib)
+    x_flat = x.view(-1, sh.d_model)
     with torch.no_grad():
         log("[bench] warmup")
         for _ in range(args.warmup):
             m(x)
         torch.cuda.synchronize()
         log(f"[bench] timing {args.steps} steps")
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            m(x)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        log("[bench] per-stage timing")
-        st, U = time_stages(m, x.view(-1, sh.d_model), args.stage_reps)
-
-    ms = elapsed / args.steps * 1e3
+        ms, st = timed_steps(m, x_flat, args.steps)
+        U = unique_experts(m, x_flat)
     work = stage_work(sh, U)
     kernels = {}
     for k, ms_k in st.items():
@@ -165,7 +196,7 @@ def main():
     dom = max(graded, key=lambda k: graded[k]["us"])
     kd = kernels[dom]
     roofline = dict(kernel=dom, bound=kd["bound"], achieved=kd["achieved"], peak=kd["peak"], unit=kd["unit"],
-                    frac=kd["frac"], traffic=None)
+                    frac=kd["frac"], traffic=load_traffic(args.config, dom))
 
     cpu = None
     if args.cpu_tokens > 0:

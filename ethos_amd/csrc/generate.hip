@@ -174,8 +174,9 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
     constexpr int NB1 = DH / 32;              // hidden blocks of 32
     constexpr int KS2 = DH / 16;              // GEMM2 k-steps
     constexpr int GPR = DH / 8;               // 16-byte groups per W2 row
-    static_assert(GPR % kG2Waves == 0, "chunk staging shape");
-    // W2 chunks, double buffered: [buffer][16-byte group g = 2 s + h][column]
+    constexpr int kCopies = GPR * kG2Cols / 64;  // 64-lane copy instructions per chunk
+    static_assert(kG2Waves == 4 && kG2Cols == 64 && GPR % 8 == 0 && kCopies % kG2Waves == 0, "chunk staging shape");
+    // W2 chunks, double buffered, swizzled (see issue_chunk)
     __shared__ uint4 bs[2][GPR * kG2Cols];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -193,16 +194,21 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
         const uint16_t* w2t = w2;
         asm volatile("" : "+s"(w1t), "+s"(w2t));
 
-        // Direct global -> LDS copy of W2 chunk c: wave w moves groups w, w+4, ...;
-        // lane = column, 16 bytes each, landing contiguously at bs[buf][g][0..63].
+        // Direct global -> LDS copy of W2 chunk c (64 rows of W2 = 64 output columns).
+        // Copy instruction i moves eight whole 128-byte lines: rows 8 (i % 8) + j / 8 of
+        // the chunk, line i / 8; lane j lands at bs[buf][64 i + j] and carries 16-byte
+        // group x = (j % 8) ^ (j / 8) ^ (i % 2) of its line, so that the B-fragment reads
+        // below (fixed group, 16 consecutive columns) hit 16 distinct bank groups.
+        // With i = wave + 4 it, the rows are 8 wave + jr (+ 32 for odd it), the line is
+        // it / 2 and i % 2 = wave % 2: one lane base plus immediate offsets.
         auto issue_chunk = [&](int c, int buf) {
-            const uint16_t* src = w2t + (int64_t)(c * kG2Cols + lane) * DH;
+            const int jr = lane >> 3, jx = lane & 7;
+            const uint16_t* src = w2t + (int64_t)(c * kG2Cols + 8 * wave + jr) * DH + 8 * (jx ^ jr ^ (wave & 1));
 #pragma unroll
-            for (int it = 0; it < GPR / kG2Waves; ++it) {
-                const int g = wave + it * kG2Waves;
-                __builtin_amdgcn_global_load_lds(src + 8 * g,
-                                                 (__attribute__((address_space(3))) void*)&bs[buf][g * kG2Cols], 16,
-                                                 0, 0);
+            for (int it = 0; it < kCopies / kG2Waves; ++it) {
+                const int i = wave + it * kG2Waves;
+                __builtin_amdgcn_global_load_lds(src + (it & 1) * 32 * DH + 64 * (it >> 1),
+                                                 (__attribute__((address_space(3))) void*)&bs[buf][i * 64], 16, 0, 0);
             }
         };
         issue_chunk(0, 0);
@@ -292,13 +298,22 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
             // B fragments are software-pipelined in groups of SG k-steps: the group after
             // next is read from LDS while the current group's MFMAs issue.
             constexpr int SG = 4;
-            static_assert(KS2 % SG == 0, "k-step grouping");
-            const uint4* bp = cur + h * kG2Cols + l32;
+            static_assert(KS2 % SG == 0 && SG == 4, "k-step grouping");
+            // column col = 32 cb + l32, group g = 2 s + h sits at 64 i + 8 (col % 8) + x with
+            // i = 8 (g / 8) + col / 8 and x = (g % 8) ^ (col % 8) ^ (col / 8 % 2); only
+            // s % 4 changes x, so four lane bases cover every k-step.
+            const uint4* bq[SG];
+#pragma unroll
+            for (int q = 0; q < SG; ++q)
+                bq[q] = cur + (l32 >> 3) * 64 + (l32 & 7) * 8 + ((2 * q + h) ^ (l32 & 7) ^ ((l32 >> 3) & 1));
+            auto bfrag = [&](int s, int cb) {
+                return __builtin_bit_cast(bf16x8_t, bq[s & 3][(s >> 2) * 512 + cb * 256]);
+            };
             bf16x8_t bcur[SG][2], bnxt[SG][2];
 #pragma unroll
             for (int q = 0; q < SG; ++q)
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb) bcur[q][cb] = __builtin_bit_cast(bf16x8_t, bp[2 * q * kG2Cols + cb * 32]);
+                for (int cb = 0; cb < 2; ++cb) bcur[q][cb] = bfrag(q, cb);
 #pragma clang loop unroll(full)
             for (int s0 = 0; s0 < KS2; s0 += SG) {
                 if (s0 + SG < KS2) {
@@ -306,7 +321,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
                     for (int q = 0; q < SG; ++q)
 #pragma unroll
                         for (int cb = 0; cb < 2; ++cb)
-                            bnxt[q][cb] = __builtin_bit_cast(bf16x8_t, bp[2 * (s0 + SG + q) * kG2Cols + cb * 32]);
+                            bnxt[q][cb] = bfrag(s0 + SG + q, cb);
                 }
 #pragma unroll
                 for (int q = 0; q < SG; ++q)

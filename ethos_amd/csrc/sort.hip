@@ -110,29 +110,72 @@ __global__ __launch_bounds__(256) void sort_downsweep(const uint32_t* __restrict
 }
 
 // Exclusive scan of n uint32 in place by one workgroup; total -> *total (if given).
+// Exclusive scan of a[0..n) in place, one workgroup.  Each thread holds 16 consecutive
+// values in registers (four 16-byte loads issued together); thread sums are scanned
+// across the wave with shuffles and across the 16 waves through LDS; chunks of 16384
+// values are chained by a carry.  *total (if given) receives the sum of all values.
+constexpr int kScanPer = 16;
+constexpr int kScanChunk = kScanThreads * kScanPer;
+
 __global__ __launch_bounds__(kScanThreads) void scan_exclusive(uint32_t* __restrict__ a, int64_t n,
                                                                int32_t* __restrict__ total) {
-    __shared__ uint32_t part[kScanThreads];
-    const int tid = threadIdx.x;
-    const int64_t per = (n + kScanThreads - 1) / kScanThreads;
-    const int64_t lo = tid * per, hi = min(n, lo + per);
-    uint32_t s = 0;
-    for (int64_t i = lo; i < hi; ++i) s += a[i];
-    part[tid] = s;
-    __syncthreads();
-    for (int off = 1; off < kScanThreads; off <<= 1) {
-        const uint32_t v = tid >= off ? part[tid - off] : 0u;
+    __shared__ uint32_t wsum[kScanThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool vec = ((uintptr_t)a & 15) == 0;
+    uint32_t carry = 0;
+    for (int64_t base = 0; base < n; base += kScanChunk) {
+        const int64_t lo = base + (int64_t)tid * kScanPer;
+        const bool full = vec && lo + kScanPer <= n;
+        uint32_t v[kScanPer];
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < kScanPer / 4; ++j) {
+                const uint4 q = reinterpret_cast<const uint4*>(a + lo)[j];
+                v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j) v[j] = lo + j < n ? a[lo + j] : 0u;
+        }
+        uint32_t s = 0;
+#pragma unroll
+        for (int j = 0; j < kScanPer; ++j) s += v[j];
+        // inclusive wave scan of the thread sums
+        uint32_t inc = s;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t t = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += t;
+        }
+        if (lane == 63) wsum[wave] = inc;
         __syncthreads();
-        part[tid] += v;
-        __syncthreads();
+        uint32_t wpre = 0, chunk_total = 0;
+#pragma unroll
+        for (int w = 0; w < kScanThreads / 64; ++w) {
+            const uint32_t t = wsum[w];
+            wpre += w < wave ? t : 0u;
+            chunk_total += t;
+        }
+        __syncthreads();  // wsum is rewritten by the next chunk
+        uint32_t run = carry + wpre + inc - s;
+#pragma unroll
+        for (int j = 0; j < kScanPer; ++j) {
+            const uint32_t t = v[j];
+            v[j] = run;
+            run += t;
+        }
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < kScanPer / 4; ++j)
+                reinterpret_cast<uint4*>(a + lo)[j] = make_uint4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j)
+                if (lo + j < n) a[lo + j] = v[j];
+        }
+        carry += chunk_total;
     }
-    uint32_t run = part[tid] - s;
-    for (int64_t i = lo; i < hi; ++i) {
-        const uint32_t v = a[i];
-        a[i] = run;
-        run += v;
-    }
-    if (tid == kScanThreads - 1 && total) *total = (int32_t)part[tid];
+    if (tid == 0 && total) *total = (int32_t)carry;
 }
 
 // Head count per tile (items thread-contiguous: thread t owns 16 consecutive keys).

@@ -132,11 +132,17 @@ class ProductKeyRouter(nn.Module):
                 m.num_batches_tracked.add_(1)
         return torch.stack(outs, dim=1).contiguous()
 
-    def route(self, x_flat: torch.Tensor):
-        """(gates [n, H, k] x.dtype, expert ids [n, H, k] int32)."""
+    def route(self, x_flat: torch.Tensor, mark=None):
+        """(gates [n, H, k] x.dtype, expert ids [n, H, k] int32).  `mark(stage)`, if given,
+        is called after each stage is enqueued (used to place timing events)."""
         _, _, k1, k2, _, _ = self._packed(x_flat.dtype, x_flat.device)
         q = self.queries(x_flat)
-        return hip.route_topk(q, k1, k2, self.top_k, key_norms=self._key_norms)
+        if mark is not None:
+            mark("query_proj")
+        out = hip.route_topk(q, k1, k2, self.top_k, key_norms=self._key_norms)
+        if mark is not None:
+            mark("route")
+        return out
 
     def forward(self, x_flat: torch.Tensor):
         with torch.no_grad():
@@ -179,15 +185,26 @@ class EthosExpertLayer(nn.Module):
             raise RuntimeError(f"expected x of shape [batch, seq, {self.d_model}], got {tuple(x.shape)}")
         b, s, d = x.shape
         x_flat = _as_input(x, 3).view(-1, d)
+        if x_flat.shape[0] == 0:
+            return torch.zeros_like(x)
+        return self.forward_flat(x_flat).view(b, s, d)
+
+    def forward_flat(self, x_flat: torch.Tensor, mark=None) -> torch.Tensor:
+        """The layer on [n_tok, d_model] rows (model.py:288-343).  `mark(stage)`, if given, is
+        called after each of the five stages is enqueued on the current stream."""
         with torch.no_grad():
-            if x_flat.shape[0] == 0:
-                return torch.zeros_like(x)
-            gates, ids = self.router.route(x_flat)
+            gates, ids = self.router.route(x_flat, mark)
             seg = hip.sort_segment(ids.view(-1), self.num_experts)
-            latents, w1, w2 = self._generator_params(x.dtype, x.device)
+            if mark is not None:
+                mark("sort_segment")
+            latents, w1, w2 = self._generator_params(x_flat.dtype, x_flat.device)
             uv = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2)
+            if mark is not None:
+                mark("generate")
             out = hip.apply_scatter(x_flat, uv, seg, gates, self.num_heads, self.top_k)
-        return out.view(b, s, d)
+            if mark is not None:
+                mark("apply_scatter")
+        return out
 
 
 def _as_input(x: torch.Tensor, dim: int) -> torch.Tensor:

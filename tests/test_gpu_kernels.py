@@ -68,7 +68,8 @@ def test_route_ties_break_to_lowest_index():
 @pytest.mark.parametrize("n,E,pattern", [(1, 1, "rand"), (5, 262144, "rand"), (4096, 4096, "rand"),
                                          (8192, 4096, "rand"), (70000, 262144, "rand"), (524288, 262144, "rand"),
                                          (30000, 262144, "same"), (50000, 262144, "skew"), (4097, 7, "rand"),
-                                         (12345, 262144, "max")])
+                                         (12345, 262144, "max"), (300000, 262144, "rand"),
+                                         (2000003, 262144, "rand")])
 def test_sort_segment_exact(n, E, pattern):
     rng = np.random.default_rng(n + E)
     if pattern == "same":
