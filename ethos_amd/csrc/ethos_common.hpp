@@ -73,7 +73,7 @@ __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + e
 // on the negative tail as well -- far inside half a bf16 ulp (2^-9).
 __device__ __forceinline__ float gelu_erfc_fit(float x) {
     const float z = fabsf(x) * 0.70710678118654752f;
-    const float t = __frcp_rn(1.0f + 0.5f * z);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.5f * z);  // v_rcp_f32, 1 ulp
     float p = 0.17087277f;
     p = __builtin_fmaf(p, t, -0.82215223f);
     p = __builtin_fmaf(p, t, 1.48851587f);

@@ -136,22 +136,24 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
 }
 
 // ---------------------------------------------------------------------------------
-// bf16 generator for the common shapes: 4 waves x MB*32 experts per workgroup, the
-// hidden activations never leave registers.
+// bf16 generator for the common shapes: tiles of 128 experts, 4 waves x 32 experts,
+// two workgroups per CU (at most 256 registers per lane and 64 KiB of LDS each), so
+// that one workgroup's GELU (VALU work) runs under the other's MFMAs.  The hidden
+// activations never leave registers.
 //
 // GEMM1 is computed transposed, hid^T = W1 . Z^T (A = W1 rows, B = gathered latent
 // rows).  Lane l reads W1 row pi(l % 32) of each 32-row block, pi swapping bits 2 and
 // 3 of the row index, so that accumulator elements 8p..8p+7 of lane half h hold the
 // eight consecutive hidden values 16p + 8h .. 16p + 8h + 7 of expert l % 32.  After
 // erf-GELU and bf16 rounding they are exactly the k-slots of GEMM2's operand for
-// k-step s = 2t + p.  GEMM2 is also transposed, uv^T = W2 . hid^T, reading W2 from an
-// LDS chunk of 64 output columns laid out [16-byte group g][column]; each lane then
-// owns one expert row and four consecutive output columns per accumulator group,
-// stored as 8-byte writes.  Two independent accumulators per column block (even and
-// odd k-steps) keep the MFMA pipeline fed.
+// k-step s = 2t + p.  GEMM2 is also transposed, uv^T = W2 . hid^T, over chunks of 32
+// output columns: the chunk's 32 rows of W2 are copied global -> LDS (double
+// buffered) and each lane owns one expert and four groups of four consecutive output
+// columns of the chunk, stored as 8-byte writes one chunk later.
 // ---------------------------------------------------------------------------------
 constexpr int kG2Waves = 4;
-constexpr int kG2Cols = 64;  // output columns per staged W2 chunk
+constexpr int kG2Cols = 32;                // output columns per staged W2 chunk
+constexpr int kG2Rows = kG2Waves * 32;     // experts per tile
 
 __device__ __forceinline__ float round_bf16_hw(float x) { return __uint_as_float(pack_bf16x2(x, 0.0f) << 16); }
 
@@ -164,18 +166,17 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
-template <int DL, int DH, int MB>
-__global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void generate_bf16_kernel(
+template <int DL, int DH>
+__global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void generate_bf16_kernel(
     const uint16_t* __restrict__ latents, int64_t n_experts, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_unique, const uint16_t* __restrict__ w1, const uint16_t* __restrict__ w2, int d2,
     uint16_t* __restrict__ uv) {
-    constexpr int ROWS = kG2Waves * MB * 32;  // experts per tile
-    constexpr int KS1 = DL / 16;              // GEMM1 k-steps
-    constexpr int NB1 = DH / 32;              // hidden blocks of 32
-    constexpr int KS2 = DH / 16;              // GEMM2 k-steps
-    constexpr int GPR = DH / 8;               // 16-byte groups per W2 row
-    constexpr int kCopies = GPR * kG2Cols / 64;  // 64-lane copy instructions per chunk
-    static_assert(kG2Waves == 4 && kG2Cols == 64 && GPR % 8 == 0 && kCopies % kG2Waves == 0, "chunk staging shape");
+    constexpr int KS1 = DL / 16;                  // GEMM1 k-steps
+    constexpr int NB1 = DH / 32;                  // hidden blocks of 32
+    constexpr int KS2 = DH / 16;                  // GEMM2 k-steps
+    constexpr int GPR = DH / 8;                   // 16-byte groups per W2 row
+    constexpr int kCopies = GPR * kG2Cols / 64;   // 64-lane copy instructions per chunk
+    static_assert(GPR % 8 == 0 && kCopies % kG2Waves == 0 && KS2 % 4 == 0, "chunk staging shape");
     // W2 chunks, double buffered, swizzled (see issue_chunk)
     __shared__ uint4 bs[2][GPR * kG2Cols];
 
@@ -183,103 +184,103 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
     const int h = lane >> 5, l32 = lane & 31;
     const int prow = (l32 & ~0xc) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);  // bits 2 <-> 3
     const int U = *n_unique;
-    const int n_tiles = (U + ROWS - 1) / ROWS;
+    const int n_tiles = (U + kG2Rows - 1) / kG2Rows;
     const int n_chunks = d2 / kG2Cols;
+    // W2 as a buffer resource (raw, byte-addressed; loads beyond its size return 0)
+    const __amdgpu_buffer_rsrc_t w2r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(w2), (short)0, d2 * DH * (int)sizeof(uint16_t), 0x00020000);
+    // Copy instruction i = wave + 4 it of a chunk moves eight whole 128-byte lines: rows
+    // 8 wave + j / 8 of the chunk, line it.  Lane j lands at bs[buf][64 i + j] and
+    // carries 16-byte group x = (j % 8) ^ (j / 8) ^ (wave % 2) of its line, so that the
+    // B-fragment reads (one group, 16 consecutive rows) hit 16 distinct bank groups.
+    const int w2_voff = ((8 * wave + (lane >> 3)) * DH + 8 * ((lane & 7) ^ (lane >> 3) ^ (wave & 1))) * 2;
+    // W2 row (output column) r = l32 of a chunk, group g = 2 s + h, sits at
+    // 64 (4 (g / 8) + r / 8) + 8 (r % 8) + ((g % 8) ^ (r % 8) ^ (r / 8 % 2)); only s % 4
+    // changes the last term, so four lane bases cover every k-step.
+    int bq_off[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        bq_off[q] = (l32 >> 3) * 64 + (l32 & 7) * 8 + ((2 * q + h) ^ (l32 & 7) ^ ((l32 >> 3) & 1));
 
     for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-        const int ubase = tile * ROWS + wave * MB * 32 + l32;
-        // W1 and W2 are the same for every tile; opaque copies of their pointers keep
-        // the compiler from hoisting all their loads out of the tile loop.
-        const uint16_t* w1t = w1;
-        const uint16_t* w2t = w2;
-        asm volatile("" : "+s"(w1t), "+s"(w2t));
+        const int u_own = tile * kG2Rows + wave * 32 + l32;
+        // W1 is the same for every tile; an opaque copy of its pointer keeps the compiler
+        // from hoisting all its loads out of the tile loop.
+        const uint16_t* w1o = w1;
+        asm volatile("" : "+s"(w1o));
+        const __attribute__((address_space(1))) uint16_t* w1t =
+            (const __attribute__((address_space(1))) uint16_t*)w1o;
 
-        // Direct global -> LDS copy of W2 chunk c (64 rows of W2 = 64 output columns).
-        // Copy instruction i moves eight whole 128-byte lines: rows 8 (i % 8) + j / 8 of
-        // the chunk, line i / 8; lane j lands at bs[buf][64 i + j] and carries 16-byte
-        // group x = (j % 8) ^ (j / 8) ^ (i % 2) of its line, so that the B-fragment reads
-        // below (fixed group, 16 consecutive columns) hit 16 distinct bank groups.
-        // With i = wave + 4 it, the rows are 8 wave + jr (+ 32 for odd it), the line is
-        // it / 2 and i % 2 = wave % 2: one lane base plus immediate offsets.
+        // The copies are buffer loads (not global ones) so that the compiler keeps
+        // counting LDS reads precisely while they are in flight.
         auto issue_chunk = [&](int c, int buf) {
-            const int jr = lane >> 3, jx = lane & 7;
-            const uint16_t* src = w2t + (int64_t)(c * kG2Cols + 8 * wave + jr) * DH + 8 * (jx ^ jr ^ (wave & 1));
 #pragma unroll
             for (int it = 0; it < kCopies / kG2Waves; ++it) {
-                const int i = wave + it * kG2Waves;
-                __builtin_amdgcn_global_load_lds(src + (it & 1) * 32 * DH + 64 * (it >> 1),
-                                                 (__attribute__((address_space(3))) void*)&bs[buf][i * 64], 16, 0, 0);
+                const int soff = (c * kG2Cols * DH + 64 * it) * 2;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    w2r, (__attribute__((address_space(3))) void*)&bs[buf][(wave + it * kG2Waves) * 64], 16, w2_voff,
+                    soff, 0, 0);
             }
         };
         issue_chunk(0, 0);
 
-        // gathered latent rows (GEMM1 B operand)
-        bf16x8_t zf[MB][KS1];
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-            const int u = ubase + mb * 32;
-            const int64_t id = u < U ? (int64_t)uniq[u] : -1;
+        // gathered latent row of this lane's expert (GEMM1 B operand)
+        bf16x8_t zf[KS1];
+        {
+            const int64_t id = u_own < U ? (int64_t)uniq[u_own] : -1;
             const bool ok = id >= 0 && id < n_experts;
             const uint16_t* zr = latents + (ok ? id : 0) * DL + 8 * h;
 #pragma unroll
-            for (int ks = 0; ks < KS1; ++ks)
-                zf[mb][ks] = ok ? *reinterpret_cast<const bf16x8_t*>(zr + ks * 16) : bf16x8_t{};
+            for (int ks = 0; ks < KS1; ++ks) zf[ks] = ok ? *reinterpret_cast<const bf16x8_t*>(zr + ks * 16) : bf16x8_t{};
         }
 
-        // GEMM1^T + GELU -> hidden k-slots hf[mb][s]; W1 fragments of block t + 1 are
-        // fetched while block t computes.
-        bf16x8_t hf[MB][KS2];
-        bf16x8_t wa[KS1], wn[KS1];
+        // GEMM1^T + GELU -> hidden k-slots hf[s].  An MFMA reads its operands when it
+        // issues, so the W1 fragments of block t + 1 are loaded into the same registers
+        // right after block t's MFMAs and arrive while block t's GELU runs.
+        bf16x8_t hf[KS2];
+        bf16x8_t wa[KS1];
 #pragma unroll
-        for (int ks = 0; ks < KS1; ++ks)
-            wa[ks] = *reinterpret_cast<const bf16x8_t*>(w1t + prow * DL + ks * 16 + 8 * h);
+        for (int ks = 0; ks < KS1; ++ks) wa[ks] = *reinterpret_cast<const __attribute__((address_space(1))) bf16x8_t*>(w1t + prow * DL + ks * 16 + 8 * h);
 #pragma clang loop unroll(full)
         for (int t = 0; t < NB1; ++t) {
+            f32x16_t acc = f32x16_zero();
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[ks], zf[ks], acc, 0, 0, 0);
             if (t + 1 < NB1) {
 #pragma unroll
                 for (int ks = 0; ks < KS1; ++ks)
-                    wn[ks] = *reinterpret_cast<const bf16x8_t*>(w1t + ((t + 1) * 32 + prow) * DL + ks * 16 + 8 * h);
+                    wa[ks] = *reinterpret_cast<const __attribute__((address_space(1))) bf16x8_t*>(
+                        w1t + ((t + 1) * 32 + prow) * DL + ks * 16 + 8 * h);
             }
-            f32x16_t acc[MB];
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16_zero();
+            for (int p = 0; p < 2; ++p) {
+                float v[8];
 #pragma unroll
-            for (int ks = 0; ks < KS1; ++ks)
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[ks], zf[mb][ks], acc[mb], 0, 0, 0);
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    float v[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = gelu_erfc_fit(round_bf16_hw(acc[mb][8 * p + j]));
-                    hf[mb][2 * t + p] = pack_bf16x8(v);
+                for (int j = 0; j < 8; ++j) {
+                    // one GELU chain at a time: VALU throughput is the same and the
+                    // temporaries of sixteen interleaved chains would not fit
+                    v[j] = gelu_erfc_fit(round_bf16_hw(acc[8 * p + j]));
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-#pragma unroll
-            for (int ks = 0; ks < KS1; ++ks) wa[ks] = wn[ks];
+                hf[2 * t + p] = pack_bf16x8(v);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
+        // Materialise every k-slot here: left alone, the compiler sinks the GELUs past
+        // the chunk-loop entry and keeps all GEMM1 accumulators live at once.
+#pragma unroll
+        for (int s = 0; s < KS2; ++s) asm volatile("" : "+v"(hf[s]));
 
         // GEMM2^T.  Results of chunk c are stored while chunk c + 1 computes, right
-        // after the loads of chunk c + 2 are issued, so the per-chunk wait for the
-        // LDS copies never waits on fresh stores.
-        uint2 pend[MB][2][4];
+        // after the copies of chunk c + 2 are issued, so the per-chunk wait for the
+        // copies never waits on fresh stores.
+        uint2 pend[4];
         int pend_c = -1;
         auto flush = [&]() {
-            if (pend_c < 0) return;
+            if (pend_c < 0 || u_own >= U) return;
+            uint16_t* row = uv + (int64_t)u_own * d2 + pend_c * kG2Cols + 4 * h;
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-                const int u = ubase + mb * 32;
-                if (u < U) {
-                    uint16_t* row = uv + (int64_t)u * d2 + pend_c * kG2Cols + 4 * h;
-#pragma unroll
-                    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) *reinterpret_cast<uint2*>(row + cb * 32 + 8 * g) = pend[mb][cb][g];
-                }
-            }
+            for (int g = 0; g < 4; ++g) *reinterpret_cast<uint2*>(row + 8 * g) = pend[g];
         };
         for (int c = 0; c < n_chunks; ++c) {
             __builtin_amdgcn_s_waitcnt(0);
@@ -287,69 +288,30 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
             if (c + 1 < n_chunks) issue_chunk(c + 1, (c + 1) & 1);
             flush();
             const uint4* cur = bs[c & 1];
-            constexpr int KI = MB == 1 ? 2 : 1;  // independent chains per (expert block, column block)
-            f32x16_t acc[MB][2][KI];
+            auto bfrag = [&](int s) { return __builtin_bit_cast(bf16x8_t, cur[bq_off[s & 3] + (s >> 2) * 256]); };
+            // B fragments run LA k-steps ahead of the MFMAs in a ring of LA + 1 slots.
+            constexpr int LA = 6;
+            bf16x8_t bfr[LA + 1];
+            f32x16_t acc = f32x16_zero();
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
+            for (int s = 0; s < LA; ++s) bfr[s] = bfrag(s);
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                    for (int ki = 0; ki < KI; ++ki) acc[mb][cb][ki] = f32x16_zero();
-            // B fragments are software-pipelined in groups of SG k-steps: the group after
-            // next is read from LDS while the current group's MFMAs issue.
-            constexpr int SG = 4;
-            static_assert(KS2 % SG == 0 && SG == 4, "k-step grouping");
-            // column col = 32 cb + l32, group g = 2 s + h sits at 64 i + 8 (col % 8) + x with
-            // i = 8 (g / 8) + col / 8 and x = (g % 8) ^ (col % 8) ^ (col / 8 % 2); only
-            // s % 4 changes x, so four lane bases cover every k-step.
-            const uint4* bq[SG];
-#pragma unroll
-            for (int q = 0; q < SG; ++q)
-                bq[q] = cur + (l32 >> 3) * 64 + (l32 & 7) * 8 + ((2 * q + h) ^ (l32 & 7) ^ ((l32 >> 3) & 1));
-            auto bfrag = [&](int s, int cb) {
-                return __builtin_bit_cast(bf16x8_t, bq[s & 3][(s >> 2) * 512 + cb * 256]);
-            };
-            bf16x8_t bcur[SG][2], bnxt[SG][2];
-#pragma unroll
-            for (int q = 0; q < SG; ++q)
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb) bcur[q][cb] = bfrag(q, cb);
-#pragma clang loop unroll(full)
-            for (int s0 = 0; s0 < KS2; s0 += SG) {
-                if (s0 + SG < KS2) {
-#pragma unroll
-                    for (int q = 0; q < SG; ++q)
-#pragma unroll
-                        for (int cb = 0; cb < 2; ++cb)
-                            bnxt[q][cb] = bfrag(s0 + SG + q, cb);
-                }
-#pragma unroll
-                for (int q = 0; q < SG; ++q)
-#pragma unroll
-                    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                        for (int mb = 0; mb < MB; ++mb) {
-                            const int s = s0 + q;
-                            acc[mb][cb][s % KI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bcur[q][cb], hf[mb][s],
-                                                                                          acc[mb][cb][s % KI], 0, 0, 0);
-                        }
-#pragma unroll
-                for (int q = 0; q < SG; ++q)
-#pragma unroll
-                    for (int cb = 0; cb < 2; ++cb) bcur[q][cb] = bnxt[q][cb];
+            for (int s = 0; s < KS2; ++s) {
+                if (s + LA < KS2) bfr[(s + LA) % (LA + 1)] = bfrag(s + LA);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[s % (LA + 1)], hf[s], acc, 0, 0, 0);
             }
-            // acc[mb][cb][*][i]: column c*64 + cb*32 + 8*(i/4) + 4h + i%4 of expert ubase + 32 mb
+            // Pin that interleave in the schedule: the first LA reads, then for each
+            // k-step its MFMA followed by the read of k-step s + LA.
+            __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
+            for (int s = 0; s < KS2; ++s) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            // acc[i]: column c*32 + 8*(i/4) + 4h + i%4 of expert u_own
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb) {
-#pragma unroll
-                    for (int ki = 1; ki < KI; ++ki) acc[mb][cb][0] += acc[mb][cb][ki];
-#pragma unroll
-                    for (int g = 0; g < 4; ++g)
-                        pend[mb][cb][g] = make_uint2(pack_bf16x2(acc[mb][cb][0][4 * g], acc[mb][cb][0][4 * g + 1]),
-                                                     pack_bf16x2(acc[mb][cb][0][4 * g + 2], acc[mb][cb][0][4 * g + 3]));
-                }
+            for (int g = 0; g < 4; ++g)
+                pend[g] = make_uint2(pack_bf16x2(acc[4 * g], acc[4 * g + 1]), pack_bf16x2(acc[4 * g + 2], acc[4 * g + 3]));
             pend_c = c;
         }
         flush();
@@ -357,16 +319,15 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
     }
 }
 
-template <int DL, int DH, int MB>
+template <int DL, int DH>
 static bool launch_generate_bf16(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                                  int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* uv,
                                  int num_cus, hipStream_t stream) {
-    constexpr int ROWS = kG2Waves * MB * 32;
     if (dl != DL || dh != DH || d2 % kG2Cols) return false;
-    const int64_t tiles = (max_unique + ROWS - 1) / ROWS;
-    const int64_t cap = num_cus;
+    const int64_t tiles = (max_unique + kG2Rows - 1) / kG2Rows;
+    const int64_t cap = 2 * (int64_t)num_cus;  // two workgroups per CU
     const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
-    hipLaunchKernelGGL((generate_bf16_kernel<DL, DH, MB>), dim3(grid), dim3(kG2Waves * 64), 0, stream,
+    hipLaunchKernelGGL((generate_bf16_kernel<DL, DH>), dim3(grid), dim3(kG2Waves * 64), 0, stream,
                        (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)w2,
                        d2, (uint16_t*)uv);
     return true;
@@ -385,9 +346,9 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
                     int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, int dtype, void* uv,
                     int num_cus, hipStream_t stream) {
     if (dtype == kBF16) {
-        if (launch_generate_bf16<128, 512, 1>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
+        if (launch_generate_bf16<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
                                               num_cus, stream) ||
-            launch_generate_bf16<128, 256, 1>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
+            launch_generate_bf16<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
                                               num_cus, stream))
             return (int)hipGetLastError();
     }
