@@ -23,6 +23,8 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Two floats -> packed bf16 pair (a in the low half), round to nearest even, one
 // v_cvt_pk_bf16_f32.

@@ -179,6 +179,9 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
     static_assert(GPR % 8 == 0 && kCopies % kG2Waves == 0 && KS2 % 4 == 0, "chunk staging shape");
     // W2 chunks, double buffered, swizzled (see issue_chunk)
     __shared__ uint4 bs[2][GPR * kG2Cols];
+    // Output staging, per wave: 32 experts x 64 columns (two chunks) of bf16; expert r's
+    // 128-byte row holds its 16-byte group q at slot q ^ (r % 8).
+    __shared__ u32x4_t stg[kG2Waves][32 * 8];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
@@ -202,7 +205,25 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
     for (int q = 0; q < 4; ++q)
         bq_off[q] = (l32 >> 3) * 64 + (l32 & 7) * 8 + ((2 * q + h) ^ (l32 & 7) ^ ((l32 >> 3) & 1));
 
-    for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    // Work units: tiles that fill whole rounds of the grid are done whole; the
+    // remaining rem tiles are split by column range into parts so that the last round
+    // spreads over the grid (each part recomputes the tile's GEMM1 and GELU).
+    const int G = gridDim.x;
+    const int n_full = n_tiles - n_tiles % G;
+    const int rem = n_tiles - n_full;
+    int parts = rem > 0 ? G / rem : 1;
+    parts = parts < 1 ? 1 : (parts > n_chunks ? n_chunks : parts);
+    const int cpp = ((n_chunks + parts - 1) / parts + 1) & ~1;  // chunks per part, even
+    const int n_units = n_full + rem * parts;
+
+    for (int w = blockIdx.x; w < n_units; w += G) {
+        int tile = w, c_begin = 0, c_end = n_chunks;
+        if (w >= n_full) {
+            tile = n_full + (w - n_full) / parts;
+            c_begin = ((w - n_full) % parts) * cpp;
+            c_end = c_begin + cpp < n_chunks ? c_begin + cpp : n_chunks;
+            if (c_begin >= c_end) continue;
+        }
         const int u_own = tile * kG2Rows + wave * 32 + l32;
         // W1 is the same for every tile; an opaque copy of its pointer keeps the compiler
         // from hoisting all its loads out of the tile loop.
@@ -222,7 +243,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
                     soff, 0, 0);
             }
         };
-        issue_chunk(0, 0);
+        issue_chunk(c_begin, c_begin & 1);
 
         // gathered latent row of this lane's expert (GEMM1 B operand)
         bf16x8_t zf[KS1];
@@ -231,7 +252,10 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
             const bool ok = id >= 0 && id < n_experts;
             const uint16_t* zr = latents + (ok ? id : 0) * DL + 8 * h;
 #pragma unroll
-            for (int ks = 0; ks < KS1; ++ks) zf[ks] = ok ? *reinterpret_cast<const bf16x8_t*>(zr + ks * 16) : bf16x8_t{};
+            for (int ks = 0; ks < KS1; ++ks)
+                zf[ks] = ok ? __builtin_bit_cast(bf16x8_t, __builtin_nontemporal_load(
+                                                               reinterpret_cast<const u32x4_t*>(zr + ks * 16)))
+                            : bf16x8_t{};
         }
 
         // GEMM1^T + GELU -> hidden k-slots hf[s].  An MFMA reads its operands when it
@@ -271,21 +295,28 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
         for (int s = 0; s < KS2; ++s) asm volatile("" : "+v"(hf[s]));
 
-        // GEMM2^T.  Results of chunk c are stored while chunk c + 1 computes, right
-        // after the copies of chunk c + 2 are issued, so the per-chunk wait for the
-        // copies never waits on fresh stores.
-        uint2 pend[4];
-        int pend_c = -1;
+        // GEMM2^T.  Each chunk's results go to the wave's staging rows; a pair of chunks
+        // (one 128-byte line per expert) is stored while the next chunk computes, right
+        // after the copies of the chunk after it are issued, as whole lines with
+        // non-temporal stores (the uv stream must not evict W2 from L2).
+        u32x4_t* my = stg[wave];
+        int pend_pair = -1;
         auto flush = [&]() {
-            if (pend_c < 0 || u_own >= U) return;
-            uint16_t* row = uv + (int64_t)u_own * d2 + pend_c * kG2Cols + 4 * h;
+            if (pend_pair < 0) return;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) *reinterpret_cast<uint2*>(row + 8 * g) = pend[g];
+            for (int k = 0; k < 4; ++k) {
+                const int r = 8 * k + (lane >> 3), q = lane & 7;
+                const u32x4_t v = my[r * 8 + (q ^ (r & 7))];
+                const int u = tile * kG2Rows + wave * 32 + r;
+                if (u < U)
+                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(uv + (int64_t)u * d2 + 64 * pend_pair + 8 * q));
+            }
+            pend_pair = -1;
         };
-        for (int c = 0; c < n_chunks; ++c) {
+        for (int c = c_begin; c < c_end; ++c) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (c + 1 < n_chunks) issue_chunk(c + 1, (c + 1) & 1);
+            if (c + 1 < c_end) issue_chunk(c + 1, (c + 1) & 1);
             flush();
             const uint4* cur = bs[c & 1];
             auto bfrag = [&](int s) { return __builtin_bit_cast(bf16x8_t, cur[bq_off[s & 3] + (s >> 2) * 256]); };
@@ -308,11 +339,16 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-            // acc[i]: column c*32 + 8*(i/4) + 4h + i%4 of expert u_own
+            // acc[i]: column c*32 + 8*(i/4) + 4h + i%4 of expert l32 of this wave, i.e.
+            // 8-byte half h of 16-byte group 4 (c % 2) + i/4 of the staged row
+            u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                pend[g] = make_uint2(pack_bf16x2(acc[4 * g], acc[4 * g + 1]), pack_bf16x2(acc[4 * g + 2], acc[4 * g + 3]));
-            pend_c = c;
+            for (int a4 = 0; a4 < 4; ++a4) {
+                const int q = 4 * (c & 1) + a4;
+                my2[l32 * 16 + (q ^ (l32 & 7)) * 2 + h] =
+                    u32x2_t{pack_bf16x2(acc[4 * a4], acc[4 * a4 + 1]), pack_bf16x2(acc[4 * a4 + 2], acc[4 * a4 + 3])};
+            }
+            if (c & 1) pend_pair = c >> 1;
         }
         flush();
         __syncthreads();
@@ -323,7 +359,7 @@ template <int DL, int DH>
 static bool launch_generate_bf16(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                                  int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* uv,
                                  int num_cus, hipStream_t stream) {
-    if (dl != DL || dh != DH || d2 % kG2Cols) return false;
+    if (dl != DL || dh != DH || d2 % (2 * kG2Cols)) return false;
     const int64_t tiles = (max_unique + kG2Rows - 1) / kG2Rows;
     const int64_t cap = 2 * (int64_t)num_cus;  // two workgroups per CU
     const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
