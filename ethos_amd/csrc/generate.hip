@@ -136,24 +136,27 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
 }
 
 // ---------------------------------------------------------------------------------
-// bf16 generator for the common shapes: tiles of 128 experts, 4 waves x 32 experts,
-// two workgroups per CU (at most 256 registers per lane and 64 KiB of LDS each), so
-// that one workgroup's GELU (VALU work) runs under the other's MFMAs.  The hidden
-// activations never leave registers.
+// bf16 generator for the common shapes: tiles of 256 experts, one workgroup of 4 waves
+// per CU, 64 experts (two blocks of 32) per wave.  The hidden activations never leave
+// registers: 64 experts x DH bf16 is 256 registers per lane, held in AGPRs, which the
+// MFMAs read directly.  Every W2 fragment read from LDS feeds two MFMAs (one per
+// expert block), which halves the LDS traffic per flop against 32 experts per wave.
 //
 // GEMM1 is computed transposed, hid^T = W1 . Z^T (A = W1 rows, B = gathered latent
 // rows).  Lane l reads W1 row pi(l % 32) of each 32-row block, pi swapping bits 2 and
 // 3 of the row index, so that accumulator elements 8p..8p+7 of lane half h hold the
 // eight consecutive hidden values 16p + 8h .. 16p + 8h + 7 of expert l % 32.  After
 // erf-GELU and bf16 rounding they are exactly the k-slots of GEMM2's operand for
-// k-step s = 2t + p.  GEMM2 is also transposed, uv^T = W2 . hid^T, over chunks of 32
-// output columns: the chunk's 32 rows of W2 are copied global -> LDS (double
-// buffered) and each lane owns one expert and four groups of four consecutive output
-// columns of the chunk, stored as 8-byte writes one chunk later.
+// k-step s = 2t + p.  GEMM2 is also transposed, uv^T = W2 . hid^T, over chunks of 64
+// output columns: the chunk's 64 rows of W2 are copied global -> LDS (double
+// buffered) and each lane owns, per expert block, one expert and eight groups of
+// four consecutive output columns of the chunk.  Results go through a per-wave LDS
+// staging area and are stored one chunk later as whole 128-byte lines.
 // ---------------------------------------------------------------------------------
 constexpr int kG2Waves = 4;
-constexpr int kG2Cols = 32;                // output columns per staged W2 chunk
-constexpr int kG2Rows = kG2Waves * 32;     // experts per tile
+constexpr int kG2MB = 2;                          // expert blocks of 32 per wave
+constexpr int kG2Cols = 64;                       // output columns per staged W2 chunk
+constexpr int kG2Rows = kG2Waves * kG2MB * 32;    // experts per tile
 
 __device__ __forceinline__ float round_bf16_hw(float x) { return __uint_as_float(pack_bf16x2(x, 0.0f) << 16); }
 
@@ -166,22 +169,45 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (byte-addressed, stride 0, 32-bit num_records) for a global array.
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    return i32x4_t{(int32_t)(uint32_t)a, (int32_t)(uint32_t)((a >> 32) & 0xffffu), (int32_t)bytes, 0x00020000};
+}
+
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (lds is the
+// wave-uniform LDS byte address).  Issued as inline asm so that the compiler does not
+// make later LDS reads of other buffers wait for the copy; the caller waits (vmcnt)
+// and synchronises before the copied data is read.
+__device__ __forceinline__ void lds_dma16(i32x4_t rsrc, int voff, int soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
+                 "s"(soff)
+                 : "memory");
+}
+
+template <typename P>
+__device__ __forceinline__ uint32_t lds_addr(P* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) P*)p);
+}
+
 template <int DL, int DH>
-__global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void generate_bf16_kernel(
+__global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void generate_bf16_kernel(
     const uint16_t* __restrict__ latents, int64_t n_experts, const int32_t* __restrict__ uniq,
-    const int32_t* __restrict__ n_unique, const uint16_t* __restrict__ w1, const uint16_t* __restrict__ w2, int d2,
-    uint16_t* __restrict__ uv) {
+    const int32_t* __restrict__ n_unique, int64_t max_unique, const uint16_t* __restrict__ w1,
+    const uint16_t* __restrict__ w2, int d2, uint16_t* __restrict__ uv) {
     constexpr int KS1 = DL / 16;                  // GEMM1 k-steps
     constexpr int NB1 = DH / 32;                  // hidden blocks of 32
     constexpr int KS2 = DH / 16;                  // GEMM2 k-steps
     constexpr int GPR = DH / 8;                   // 16-byte groups per W2 row
     constexpr int kCopies = GPR * kG2Cols / 64;   // 64-lane copy instructions per chunk
     static_assert(GPR % 8 == 0 && kCopies % kG2Waves == 0 && KS2 % 4 == 0, "chunk staging shape");
-    // W2 chunks, double buffered, swizzled (see issue_chunk)
+    // W2 chunks, double buffered, swizzled (see w2_voff)
     __shared__ uint4 bs[2][GPR * kG2Cols];
-    // Output staging, per wave: 32 experts x 64 columns (two chunks) of bf16; expert r's
-    // 128-byte row holds its 16-byte group q at slot q ^ (r % 8).
-    __shared__ u32x4_t stg[kG2Waves][32 * 8];
+    // Output staging, per wave: 64 experts x 64 columns of bf16; expert r's 128-byte
+    // row holds its 16-byte group q at slot q ^ (r % 8).
+    __shared__ u32x4_t stg[kG2Waves][kG2MB * 32 * 8];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
@@ -190,15 +216,15 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
     const int n_tiles = (U + kG2Rows - 1) / kG2Rows;
     const int n_chunks = d2 / kG2Cols;
     // W2 as a buffer resource (raw, byte-addressed; loads beyond its size return 0)
-    const __amdgpu_buffer_rsrc_t w2r = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(w2), (short)0, d2 * DH * (int)sizeof(uint16_t), 0x00020000);
+    const i32x4_t w2r = buffer_rsrc(w2, (uint32_t)d2 * DH * (uint32_t)sizeof(uint16_t));
     // Copy instruction i = wave + 4 it of a chunk moves eight whole 128-byte lines: rows
-    // 8 wave + j / 8 of the chunk, line it.  Lane j lands at bs[buf][64 i + j] and
-    // carries 16-byte group x = (j % 8) ^ (j / 8) ^ (wave % 2) of its line, so that the
-    // B-fragment reads (one group, 16 consecutive rows) hit 16 distinct bank groups.
+    // 8 (i % 8) + j / 8 = 8 wave + 32 (it % 2) + j / 8 of the chunk, line i / 8 = it / 2.
+    // Lane j lands at bs[buf][64 i + j] and carries 16-byte group
+    // x = (j % 8) ^ (j / 8) ^ (i % 2) of its line, so that the B-fragment reads (one
+    // group, 16 consecutive rows) hit 16 distinct bank groups.
     const int w2_voff = ((8 * wave + (lane >> 3)) * DH + 8 * ((lane & 7) ^ (lane >> 3) ^ (wave & 1))) * 2;
-    // W2 row (output column) r = l32 of a chunk, group g = 2 s + h, sits at
-    // 64 (4 (g / 8) + r / 8) + 8 (r % 8) + ((g % 8) ^ (r % 8) ^ (r / 8 % 2)); only s % 4
+    // W2 row (output column) r = 32 cb + l32 of a chunk, group g = 2 s + h, sits at
+    // 64 (8 (g / 8) + r / 8) + 8 (r % 8) + ((g % 8) ^ (r % 8) ^ (r / 8 % 2)); only s % 4
     // changes the last term, so four lane bases cover every k-step.
     int bq_off[4];
 #pragma unroll
@@ -213,7 +239,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
     const int rem = n_tiles - n_full;
     int parts = rem > 0 ? G / rem : 1;
     parts = parts < 1 ? 1 : (parts > n_chunks ? n_chunks : parts);
-    const int cpp = ((n_chunks + parts - 1) / parts + 1) & ~1;  // chunks per part, even
+    const int cpp = (n_chunks + parts - 1) / parts;  // chunks per part
     const int n_units = n_full + rem * parts;
 
     for (int w = blockIdx.x; w < n_units; w += G) {
@@ -224,7 +250,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
             c_end = c_begin + cpp < n_chunks ? c_begin + cpp : n_chunks;
             if (c_begin >= c_end) continue;
         }
-        const int u_own = tile * kG2Rows + wave * 32 + l32;
+        const int u_wave = tile * kG2Rows + wave * kG2MB * 32;  // first expert of this wave
         // W1 is the same for every tile; an opaque copy of its pointer keeps the compiler
         // from hoisting all its loads out of the tile loop.
         const uint16_t* w1o = w1;
@@ -232,44 +258,47 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
         const __attribute__((address_space(1))) uint16_t* w1t =
             (const __attribute__((address_space(1))) uint16_t*)w1o;
 
-        // The copies are buffer loads (not global ones) so that the compiler keeps
-        // counting LDS reads precisely while they are in flight.
-        auto issue_chunk = [&](int c, int buf) {
-#pragma unroll
-            for (int it = 0; it < kCopies / kG2Waves; ++it) {
-                const int soff = (c * kG2Cols * DH + 64 * it) * 2;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    w2r, (__attribute__((address_space(3))) void*)&bs[buf][(wave + it * kG2Waves) * 64], 16, w2_voff,
-                    soff, 0, 0);
-            }
+        // copy instruction it of chunk c into buffer buf
+        auto copy = [&](int c, int buf, int it) {
+            const int soff = ((c * kG2Cols + 32 * (it & 1)) * DH + 64 * (it >> 1)) * 2;
+            lds_dma16(w2r, w2_voff, soff, lds_addr(&bs[buf][(wave + it * kG2Waves) * 64]));
         };
-        issue_chunk(c_begin, c_begin & 1);
+#pragma unroll
+        for (int it = 0; it < kCopies / kG2Waves; ++it) copy(c_begin, c_begin & 1, it);
 
-        // gathered latent row of this lane's expert (GEMM1 B operand)
-        bf16x8_t zf[KS1];
-        {
-            const int64_t id = u_own < U ? (int64_t)uniq[u_own] : -1;
+        // gathered latent rows of this lane's two experts (GEMM1 B operands)
+        bf16x8_t zf[kG2MB][KS1];
+#pragma unroll
+        for (int mb = 0; mb < kG2MB; ++mb) {
+            const int u = u_wave + mb * 32 + l32;
+            const int64_t id = u < U ? (int64_t)uniq[u] : -1;
             const bool ok = id >= 0 && id < n_experts;
             const uint16_t* zr = latents + (ok ? id : 0) * DL + 8 * h;
 #pragma unroll
             for (int ks = 0; ks < KS1; ++ks)
-                zf[ks] = ok ? __builtin_bit_cast(bf16x8_t, __builtin_nontemporal_load(
-                                                               reinterpret_cast<const u32x4_t*>(zr + ks * 16)))
-                            : bf16x8_t{};
+                zf[mb][ks] = ok ? __builtin_bit_cast(bf16x8_t, __builtin_nontemporal_load(
+                                                                   reinterpret_cast<const u32x4_t*>(zr + ks * 16)))
+                                : bf16x8_t{};
         }
 
-        // GEMM1^T + GELU -> hidden k-slots hf[s].  An MFMA reads its operands when it
+        // GEMM1^T + GELU -> hidden k-slots hf[mb][s].  An MFMA reads its operands when it
         // issues, so the W1 fragments of block t + 1 are loaded into the same registers
         // right after block t's MFMAs and arrive while block t's GELU runs.
-        bf16x8_t hf[KS2];
+        bf16x8_t hf[kG2MB][KS2];
         bf16x8_t wa[KS1];
 #pragma unroll
-        for (int ks = 0; ks < KS1; ++ks) wa[ks] = *reinterpret_cast<const __attribute__((address_space(1))) bf16x8_t*>(w1t + prow * DL + ks * 16 + 8 * h);
+        for (int ks = 0; ks < KS1; ++ks)
+            wa[ks] = *reinterpret_cast<const __attribute__((address_space(1))) bf16x8_t*>(w1t + prow * DL + ks * 16 + 8 * h);
 #pragma clang loop unroll(full)
         for (int t = 0; t < NB1; ++t) {
-            f32x16_t acc = f32x16_zero();
+            f32x16_t acc[kG2MB];
 #pragma unroll
-            for (int ks = 0; ks < KS1; ++ks) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[ks], zf[ks], acc, 0, 0, 0);
+            for (int mb = 0; mb < kG2MB; ++mb) acc[mb] = f32x16_zero();
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks)
+#pragma unroll
+                for (int mb = 0; mb < kG2MB; ++mb)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[ks], zf[mb][ks], acc[mb], 0, 0, 0);
             if (t + 1 < NB1) {
 #pragma unroll
                 for (int ks = 0; ks < KS1; ++ks)
@@ -277,80 +306,128 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(2
                         w1t + ((t + 1) * 32 + prow) * DL + ks * 16 + 8 * h);
             }
 #pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                float v[8];
+            for (int mb = 0; mb < kG2MB; ++mb)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    // one GELU chain at a time: VALU throughput is the same and the
-                    // temporaries of sixteen interleaved chains would not fit
-                    v[j] = gelu_erfc_fit(round_bf16_hw(acc[8 * p + j]));
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int p = 0; p < 2; ++p) {
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = gelu_bf16_fit(round_bf16_hw(acc[mb][8 * p + j]));
+                    hf[mb][2 * t + p] = pack_bf16x8(v);
+                    // park the k-slot in AGPRs (the MFMAs read it from there), which also
+                    // keeps the compiler from sinking the GELUs into the chunk loop
+                    asm volatile("" : "+a"(hf[mb][2 * t + p]));
                 }
-                hf[2 * t + p] = pack_bf16x8(v);
-            }
             __builtin_amdgcn_sched_barrier(0);
         }
-        // Materialise every k-slot here: left alone, the compiler sinks the GELUs past
-        // the chunk-loop entry and keeps all GEMM1 accumulators live at once.
-#pragma unroll
-        for (int s = 0; s < KS2; ++s) asm volatile("" : "+v"(hf[s]));
 
-        // GEMM2^T.  Each chunk's results go to the wave's staging rows; a pair of chunks
-        // (one 128-byte line per expert) is stored while the next chunk computes, right
-        // after the copies of the chunk after it are issued, as whole lines with
-        // non-temporal stores (the uv stream must not evict W2 from L2).
+        // GEMM2^T.  Each chunk's results go to the wave's staging rows; they are read
+        // back at the start of the next chunk and stored between its first MFMAs as
+        // whole 128-byte lines with non-temporal stores (the uv stream must not evict W2
+        // from L2).  The stores go through a buffer resource covering this tile's rows
+        // below max_unique, so rows past the allocation are dropped by the hardware and
+        // no store needs a branch; rows in [U, max_unique) receive the (zero) rows of
+        // absent experts.
+        const int64_t row0 = (int64_t)tile * kG2Rows;
+        const int64_t rows_left = max_unique - row0;
+        const int tile_rows = rows_left < kG2Rows ? (int)(rows_left > 0 ? rows_left : 0) : kG2Rows;
+        const __amdgpu_buffer_rsrc_t uvr = __builtin_amdgcn_make_buffer_rsrc(
+            uv + row0 * d2, (short)0, tile_rows * d2 * (int)sizeof(uint16_t), 0x00020000);
+        // lane's store k covers row 8 k + lane / 8 of the wave, 16-byte group lane % 8
+        const int st_voff = ((wave * kG2MB * 32 + (lane >> 3)) * d2 + 8 * (lane & 7)) * 2;
+        constexpr int kOOB = 0x7fff0000;  // a byte offset past any tile's rows
         u32x4_t* my = stg[wave];
-        int pend_pair = -1;
-        auto flush = [&]() {
-            if (pend_pair < 0) return;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int r = 8 * k + (lane >> 3), q = lane & 7;
-                const u32x4_t v = my[r * 8 + (q ^ (r & 7))];
-                const int u = tile * kG2Rows + wave * 32 + r;
-                if (u < U)
-                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(uv + (int64_t)u * d2 + 64 * pend_pair + 8 * q));
-            }
-            pend_pair = -1;
-        };
+        u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
+        int pend_c = -1;
         for (int c = c_begin; c < c_end; ++c) {
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (c + 1 < c_end) issue_chunk(c + 1, (c + 1) & 1);
-            flush();
+            // the previous chunk's staged rows
+            u32x4_t outv[kG2MB * 4];
+#pragma unroll
+            for (int k = 0; k < kG2MB * 4; ++k) {
+                const int r = 8 * k + (lane >> 3);
+                outv[k] = my[r * 8 + ((lane & 7) ^ (r & 7))];
+            }
+            const int st_base = pend_c >= 0 ? st_voff + kG2Cols * 2 * pend_c : kOOB;
             const uint4* cur = bs[c & 1];
-            auto bfrag = [&](int s) { return __builtin_bit_cast(bf16x8_t, cur[bq_off[s & 3] + (s >> 2) * 256]); };
+            auto bfrag = [&](int s, int cb) {
+                return __builtin_bit_cast(bf16x8_t, cur[bq_off[s & 3] + (s >> 2) * 512 + cb * 256]);
+            };
             // B fragments run LA k-steps ahead of the MFMAs in a ring of LA + 1 slots.
-            constexpr int LA = 6;
-            bf16x8_t bfr[LA + 1];
-            f32x16_t acc = f32x16_zero();
+            constexpr int LA = 4;
+            constexpr int kCopiesW = kCopies / kG2Waves;  // copies per wave, 4 per k-step
+            static_assert(kCopiesW % 4 == 0 && kCopiesW / 4 <= KS2 && kG2MB * 4 <= KS2, "interleave shape");
+            bf16x8_t bfr[LA + 1][2];
+            f32x16_t acc[kG2MB][2];
 #pragma unroll
-            for (int s = 0; s < LA; ++s) bfr[s] = bfrag(s);
+            for (int mb = 0; mb < kG2MB; ++mb)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) acc[mb][cb] = f32x16_zero();
+#pragma unroll
+            for (int s = 0; s < LA; ++s)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) bfr[s][cb] = bfrag(s, cb);
 #pragma unroll
             for (int s = 0; s < KS2; ++s) {
-                if (s + LA < KS2) bfr[(s + LA) % (LA + 1)] = bfrag(s + LA);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[s % (LA + 1)], hf[s], acc, 0, 0, 0);
+                if (s + LA < KS2) {
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) bfr[(s + LA) % (LA + 1)][cb] = bfrag(s + LA, cb);
+                }
+                // the k-slots stay in AGPRs: the MFMAs take them from there directly
+#pragma unroll
+                for (int mb = 0; mb < kG2MB; ++mb) asm volatile("" : "+a"(hf[mb][s]));
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int mb = 0; mb < kG2MB; ++mb)
+                        acc[mb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[s % (LA + 1)][cb], hf[mb][s],
+                                                                             acc[mb][cb], 0, 0, 0);
+                // copies of the next chunk (past the last chunk they read zeros into the
+                // idle buffer), four per k-step
+                if (s < kCopiesW / 4) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) copy(c + 1, (c + 1) & 1, 4 * s + j);
+                }
+                // the previous chunk's rows, one store per k-step
+                if (s < kG2MB * 4)
+                    __builtin_amdgcn_raw_buffer_store_b128(outv[s], uvr, st_base + s * 8 * d2 * 2, 0, 2);
             }
-            // Pin that interleave in the schedule: the first LA reads, then for each
-            // k-step its MFMA followed by the read of k-step s + LA.
-            __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
+            // Pin that interleave in the schedule: the staged-row reads and the first LA
+            // fragment reads, then per k-step its four MFMAs, the two fragment reads of
+            // k-step s + LA and the store (the copies keep their place in program order).
+            __builtin_amdgcn_sched_group_barrier(0x100, kG2MB * 4 + 2 * LA, 0);
 #pragma unroll
             for (int s = 0; s < KS2; ++s) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2 * kG2MB, 0);
+                if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                if (s < kG2MB * 4) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
             }
-            // acc[i]: column c*32 + 8*(i/4) + 4h + i%4 of expert l32 of this wave, i.e.
-            // 8-byte half h of 16-byte group 4 (c % 2) + i/4 of the staged row
-            u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
+            // acc[mb][cb][i]: column c*64 + 32 cb + 8 (i/4) + 4h + i%4 of expert
+            // u_wave + 32 mb + l32, i.e. 8-byte half h of 16-byte group 4 cb + i/4 of the
+            // staged row 32 mb + l32
 #pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                const int q = 4 * (c & 1) + a4;
-                my2[l32 * 16 + (q ^ (l32 & 7)) * 2 + h] =
-                    u32x2_t{pack_bf16x2(acc[4 * a4], acc[4 * a4 + 1]), pack_bf16x2(acc[4 * a4 + 2], acc[4 * a4 + 3])};
+            for (int mb = 0; mb < kG2MB; ++mb) {
+                const int r = mb * 32 + l32;
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int a4 = 0; a4 < 4; ++a4) {
+                        const int q = 4 * cb + a4;
+                        my2[r * 16 + (q ^ (r & 7)) * 2 + h] =
+                            u32x2_t{pack_bf16x2(acc[mb][cb][4 * a4], acc[mb][cb][4 * a4 + 1]),
+                                    pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3])};
+                    }
             }
-            if (c & 1) pend_pair = c >> 1;
+            pend_c = c;
         }
-        flush();
+        // the last chunk's rows
+        __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+        for (int k = 0; k < kG2MB * 4; ++k) {
+            const int r = 8 * k + (lane >> 3);
+            __builtin_amdgcn_raw_buffer_store_b128(my[r * 8 + ((lane & 7) ^ (r & 7))], uvr,
+                                                   st_voff + kG2Cols * 2 * pend_c + k * 8 * d2 * 2, 0, 2);
+        }
         __syncthreads();
     }
 }
@@ -359,13 +436,13 @@ template <int DL, int DH>
 static bool launch_generate_bf16(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                                  int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* uv,
                                  int num_cus, hipStream_t stream) {
-    if (dl != DL || dh != DH || d2 % (2 * kG2Cols)) return false;
+    if (dl != DL || dh != DH || d2 % kG2Cols) return false;
     const int64_t tiles = (max_unique + kG2Rows - 1) / kG2Rows;
-    const int64_t cap = 2 * (int64_t)num_cus;  // two workgroups per CU
+    const int64_t cap = num_cus;  // one workgroup per CU
     const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
     hipLaunchKernelGGL((generate_bf16_kernel<DL, DH>), dim3(grid), dim3(kG2Waves * 64), 0, stream,
-                       (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)w2,
-                       d2, (uint16_t*)uv);
+                       (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
+                       (const uint16_t*)w2, d2, (uint16_t*)uv);
     return true;
 }
 
