@@ -68,6 +68,20 @@ __device__ __forceinline__ void load_row(const T* __restrict__ row, int d, int l
     }
 }
 
+// Raw (undecoded) row slices of one lane: element e = c*64*N + lane*N + v.
+template <typename T, int CH>
+__device__ __forceinline__ void load_raw(const T* __restrict__ row, int d, int lane,
+                                         typename Vec16<T>::raw (&r)[CH]) {
+    constexpr int N = Vec16<T>::kN;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int e = c * 64 * N + lane * N;
+        r[c] = e < d ? *reinterpret_cast<const typename Vec16<T>::raw*>(row + e) : typename Vec16<T>::raw{};
+    }
+}
+
+constexpr int kActGroup = 4;  // pairs whose loads are in flight together
+
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ x, const T* __restrict__ uv,
                                                         const int32_t* __restrict__ perm,
@@ -75,40 +89,58 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ x,
                                                         const T* __restrict__ gates, int64_t n_pairs, int hk, int d,
                                                         float* __restrict__ act) {
     constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
     const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     const int64_t n_chunks = (n_pairs + 63) / 64;
     const int64_t d2 = 2 * (int64_t)d;
-    float u[CH * N], xv[CH * N];
     for (int64_t chunk = wave_id; chunk < n_chunks; chunk += n_waves) {
         const int64_t i0 = chunk * 64;
         const int cnt = (int)min((int64_t)64, n_pairs - i0);
         const int my_p = lane < cnt ? perm[i0 + lane] : 0;
         const int my_s = lane < cnt ? sorted_slot[i0 + lane] : 0;
-        int cur = -1;
-        for (int j = 0; j < cnt; ++j) {
-            const int s = __builtin_amdgcn_readlane(my_s, j);
-            const int p = __builtin_amdgcn_readlane(my_p, j);
-            if (s != cur) {
-                load_row<T, CH>(uv + (int64_t)s * d2, d, lane, u);
-                cur = s;
-            }
-            load_row<T, CH>(x + (int64_t)(p / hk) * d, d, lane, xv);
-            float part = 0.0f;
+        // Groups of kActGroup consecutive sorted pairs: every u and x row of a group is
+        // requested before the first dot product (repeated u rows of one expert hit in
+        // the cache), then the group's wave reductions run interleaved.
+        for (int j0 = 0; j0 < cnt; j0 += kActGroup) {
+            Raw ur[kActGroup][CH], xr[kActGroup][CH];
+            int pq[kActGroup];
 #pragma unroll
-            for (int e = 0; e < CH * N; ++e) part = __builtin_fmaf(u[e], xv[e], part);
-            const float dot = wave_sum(part);
-            if (lane == 0) {
-                const float g = Elem<T>::to_f32(gates[p]);
-                const float a = Elem<T>::round32(gelu_erf(Elem<T>::round32(dot)));
-                act[p] = Elem<T>::round32(a * g);
+            for (int q = 0; q < kActGroup; ++q) {
+                const int j = j0 + q < cnt ? j0 + q : cnt - 1;  // a tail group repeats the last pair
+                const int s = __builtin_amdgcn_readlane(my_s, j);
+                pq[q] = __builtin_amdgcn_readlane(my_p, j);
+                load_raw<T, CH>(uv + (int64_t)s * d2, d, lane, ur[q]);
+                load_raw<T, CH>(x + (int64_t)(pq[q] / hk) * d, d, lane, xr[q]);
+            }
+            float part[kActGroup];
+#pragma unroll
+            for (int q = 0; q < kActGroup; ++q) {
+                part[q] = 0.0f;
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    float uf[N], xf[N];
+                    Vec16<T>::unpack(ur[q][c], uf);
+                    Vec16<T>::unpack(xr[q][c], xf);
+#pragma unroll
+                    for (int v = 0; v < N; ++v) part[q] = __builtin_fmaf(uf[v], xf[v], part[q]);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kActGroup; ++q) {
+                const float dot = wave_sum(part[q]);
+                if (lane == q && j0 + q < cnt) {
+                    const float g = Elem<T>::to_f32(gates[pq[q]]);
+                    const float a = Elem<T>::round32(gelu_erf(Elem<T>::round32(dot)));
+                    act[pq[q]] = Elem<T>::round32(a * g);
+                }
             }
         }
     }
 }
 
-constexpr int kScatterUnroll = 4;
+constexpr int kScatterUnroll = 8;  // v rows in flight per wave
 
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict__ uv,
@@ -116,6 +148,7 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
                                                             const float* __restrict__ act, int64_t n_tok, int H,
                                                             int k, int d, T* __restrict__ out) {
     constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
     const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
@@ -131,21 +164,26 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
             for (int e = 0; e < CH * N; ++e) hacc[e] = 0.0f;
             const int64_t pbase = (t * H + h) * k;
             for (int j0 = 0; j0 < k; j0 += kScatterUnroll) {
-                float vv[kScatterUnroll][CH * N];
+                Raw vr[kScatterUnroll][CH];
                 float a[kScatterUnroll];
 #pragma unroll
                 for (int q = 0; q < kScatterUnroll; ++q) {
                     if (j0 + q < k) {
                         const int s = pair_slot[pbase + j0 + q];
                         a[q] = act[pbase + j0 + q];
-                        load_row<T, CH>(uv + (int64_t)s * d2 + d, d, lane, vv[q]);
+                        load_raw<T, CH>(uv + (int64_t)s * d2 + d, d, lane, vr[q]);
                     }
                 }
 #pragma unroll
                 for (int q = 0; q < kScatterUnroll; ++q) {
                     if (j0 + q < k) {
 #pragma unroll
-                        for (int e = 0; e < CH * N; ++e) hacc[e] += Elem<T>::round32(a[q] * vv[q][e]);
+                        for (int c = 0; c < CH; ++c) {
+                            float vf[N];
+                            Vec16<T>::unpack(vr[q][c], vf);
+#pragma unroll
+                            for (int v = 0; v < N; ++v) hacc[c * N + v] += Elem<T>::round32(a[q] * vf[v]);
+                        }
                     }
                 }
             }

@@ -78,7 +78,9 @@ __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + e
 // in exact arithmetic; evaluated in fp32 with v_rcp_f32 / v_exp_f32 the result stays
 // within 4.5e-6 relative over [-9, 9] (worst in the far negative tail, where it is
 // ~1e-17 in magnitude), far inside half a bf16 ulp (2^-9).  |x| is clamped in the
-// product so that GELU(+inf) = +inf.
+// product so that GELU(+inf) = +inf.  max(x, 0) and the clamp are integer operations
+// on the bit patterns (same results for all non-NaN inputs; a NaN input still yields
+// NaN through hc), which spares the IEEE-mode canonicalisation of float min / max.
 __device__ __forceinline__ float gelu_bf16_fit(float x) {
     const float ax = fabsf(x);
     const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.32f, ax, 1.0f));
@@ -91,7 +93,9 @@ __device__ __forceinline__ float gelu_bf16_fit(float x) {
     q = __builtin_fmaf(q, t, 1.41815186f);
     q = __builtin_fmaf(q, t, -2.96816778f);
     const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x * -0.72134752f, x, q));  // -log2(e)/2
-    return __builtin_fmaf(-fminf(ax, 3.0e38f), t * e, fmaxf(x, 0.0f));
+    const float pos = __int_as_float(max(__float_as_int(x), 0));                         // max(x, 0)
+    const float axc = __int_as_float(min(__float_as_int(ax), 0x7f61b1e6));              // min(|x|, 3e38)
+    return __builtin_fmaf(-axc, t * e, pos);
 }
 
 // ---------------------------------------------------------------- wave reductions (DPP)

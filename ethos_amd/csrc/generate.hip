@@ -311,7 +311,12 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
                 for (int p = 0; p < 2; ++p) {
                     float v[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = gelu_bf16_fit(round_bf16_hw(acc[mb][8 * p + j]));
+                    for (int j = 0; j < 8; j += 2) {
+                        // bf16-round two pre-activations with one conversion
+                        const uint32_t pk = pack_bf16x2(acc[mb][8 * p + j], acc[mb][8 * p + j + 1]);
+                        v[j] = gelu_bf16_fit(__uint_as_float(pk << 16));
+                        v[j + 1] = gelu_bf16_fit(__uint_as_float(pk & 0xffff0000u));
+                    }
                     hf[mb][2 * t + p] = pack_bf16x8(v);
                     // park the k-slot in AGPRs (the MFMAs read it from there), which also
                     // keeps the compiler from sinking the GELUs into the chunk loop
