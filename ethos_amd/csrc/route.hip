@@ -33,13 +33,14 @@
 
 namespace ethos {
 
-constexpr int kRtWaves = 4;
+constexpr int kRtWaves = 8;                            // two waves per SIMD
 constexpr int kRtRows = 32;                            // rows per workgroup (one MFMA row block)
 constexpr int kRtRowsPerWave = kRtRows / kRtWaves;
 constexpr int kRtMaxKc = 32;                           // k_cand <= 32, top_k <= 32
 constexpr int kRtMaxK = 512;                           // sub-keys per table
 constexpr int kRtSlots = kRtMaxK / kWave;              // approximate scores per lane per row
 constexpr int kRtCombSlots = 16;                       // combined pairs per lane (k_cand^2 <= 1024)
+constexpr int kRtStSlots = 2;                          // staircase pairs per lane (<= 119 for top_k <= 32)
 constexpr int kRtMaxDh2 = 256;
 
 // ---------------------------------------------------------------- wave networks
@@ -169,9 +170,7 @@ __host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2) {
     off = (off + 15) & ~(size_t)15;
     L.qd_off = off;
     off += (size_t)kRtWaves * dh2 * sizeof(double);
-    L.cand_off = off;
-    off += (size_t)kRtWaves * ((K + 31) / 32) * 32 * sizeof(int32_t);
-    off = (off + 15) & ~(size_t)15;
+    L.cand_off = 0;  // candidates reuse the row's own score storage
     L.lists_off = off;
     off += (size_t)kRtRows * 2 * kRtMaxKc * sizeof(uint64_t);
     L.topk_off = off;
@@ -181,7 +180,7 @@ __host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
+__global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
                                                     const T* __restrict__ keys2, const float* __restrict__ key_norms,
                                                     int64_t rows, int dq, int K, int top_k, int kc,
                                                     T* __restrict__ out_gates, int32_t* __restrict__ out_ids) {
@@ -196,7 +195,6 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
     float* S = reinterpret_cast<float*>(smem + L.s_off);
     float* kn = reinterpret_cast<float*>(smem + L.kn_off);
     double* qd = reinterpret_cast<double*>(smem + L.qd_off) + (size_t)wave * dh2;
-    int32_t* cand = reinterpret_cast<int32_t*>(smem + L.cand_off) + (size_t)wave * kpad;
     uint64_t* lists = reinterpret_cast<uint64_t*>(smem + L.lists_off);
     uint64_t* topk = reinterpret_cast<uint64_t*>(smem + L.topk_off) + wave * kRtMaxKc;
 
@@ -205,7 +203,7 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
     const float gamma = (float)(dh2 + 16) * 0x1p-22f * 1.01f;
 
     // Sub-key norms (upper bounds) for both tables.
-    for (int e = tid; e < 2 * kpad; e += 256) {
+    for (int e = tid; e < 2 * kpad; e += kRtWaves * 64) {
         const int half = e / kpad, j = e - half * kpad;
         float nrm = 0.0f;
         if (j < K) {
@@ -226,7 +224,7 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
 
     for (int half = 0; half < 2; ++half) {
         const T* keys = half ? keys2 : keys1;
-        // 1. approximate scores for the 32-row tile: wave w takes key blocks w, w+4, ...
+        // 1. approximate scores for the 32-row tile: wave w takes key blocks w, w + 8, ...
         for (int kb0 = wave; kb0 < nkb; kb0 += 4 * kRtWaves) {
             f32x16_t acc[4];
 #pragma unroll
@@ -236,7 +234,7 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
                 const typename M::frag a = arow < rows ? M::load(q + arow * dq + half * dh2 + k0 + lk) : M::zero();
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const int kb = kb0 + 4 * c;
+                    const int kb = kb0 + kRtWaves * c;
                     if (kb < nkb) {
                         const int j = kb * 32 + lrow;
                         const typename M::frag b = j < K ? M::load(keys + (int64_t)j * dh2 + k0 + lk) : M::zero();
@@ -246,7 +244,7 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
             }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int kb = kb0 + 4 * c;
+                const int kb = kb0 + kRtWaves * c;
                 if (kb < nkb) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) S[mfma32_row(i, lane) * pitch + kb * 32 + lrow] = acc[c][i];
@@ -293,6 +291,9 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
             const float tau = tau_s - emax * (1.0f + 0x1p-20f) - fabsf(tau_s) * 0x1p-21f;
             const float thr = Elem<T>::round32(tau);
 
+            // the row's scores are in registers now: its LDS row holds the candidates
+            int32_t* cand = reinterpret_cast<int32_t*>(S + lr * pitch);
+            __builtin_amdgcn_wave_barrier();
             int n_cand = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
@@ -330,38 +331,71 @@ __global__ __launch_bounds__(256) void route_kernel(const T* __restrict__ q, con
     }
 
     // Combine the two candidate lists of each row and take the canonical top-k.
+    // Both lists are sorted (score descending), so c[a][b] = RN_T(v1[a] + v2[b]) does
+    // not increase in a or b, and a pair with (a+1)(b+1) > top_k is dominated by at
+    // least top_k pairs of the staircase {(a+1)(b+1) <= top_k} (at most 119 pairs).
+    // Hence theta, the top_k-th largest staircase value, bounds every pair outside the
+    // staircase, and an outside pair can enter the top-k only by tying theta (it may
+    // win the tie on its expert id).  So: rank the staircase, then merge in the rare
+    // outside pairs equal to theta.
+    int st_a[kRtStSlots], st_b[kRtStSlots];
+#pragma unroll
+    for (int t = 0; t < kRtStSlots; ++t) {
+        int idx = lane + t * kWave, a = 0;
+        st_a[t] = -1;
+        st_b[t] = 0;
+        for (; a < kc; ++a) {
+            int nb = top_k / (a + 1);
+            nb = nb < kc ? nb : kc;
+            if (nb == 0) break;
+            if (idx < nb) {
+                st_a[t] = a;
+                st_b[t] = idx;
+                break;
+            }
+            idx -= nb;
+        }
+    }
     for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
         const int lr = wave * kRtRowsPerWave + rr;
         const int64_t r = row0 + lr;
         if (r >= rows) break;
         const uint64_t* l1 = lists + ((size_t)lr * 2 + 0) * kRtMaxKc;
         const uint64_t* l2 = lists + ((size_t)lr * 2 + 1) * kRtMaxKc;
-        uint64_t c[kRtCombSlots];
+        auto pair_key = [&](int a, int b) {
+            const uint64_t ka = l1[a], kb = l2[b];
+            const float v = Elem<T>::round32(key_score(ka) + key_score(kb));
+            return make_key(v, key_idx(ka) * (uint32_t)K + key_idx(kb));
+        };
+        uint64_t run = 0;
 #pragma unroll
-        for (int s = 0; s < kRtCombSlots; ++s) {
-            const int p = lane * kRtCombSlots + s;
-            const int a = p / kc, b = p - a * kc;
-            if (p < kc * kc) {
-                const uint64_t ka = l1[a], kb = l2[b];
-                const float v = Elem<T>::round32(key_score(ka) + key_score(kb));
-                c[s] = make_key(v, key_idx(ka) * (uint32_t)K + key_idx(kb));
-            } else {
-                c[s] = 0ull;
-            }
+        for (int t = 0; t < kRtStSlots; ++t) {
+            uint64_t key = st_a[t] >= 0 ? pair_key(st_a[t], st_b[t]) : 0ull;
+            key = wave_sort_desc<uint64_t>(key, lane);
+            run = t == 0 ? key : wave_merge_desc(run, key, lane);
         }
-        sort_desc(c);
-        wave_extract(c, top_k, topk, lane);
-        __builtin_amdgcn_wave_barrier();
-        const float m = key_score(topk[0]);
+        const float theta = key_score(readlane_u64(run, top_k - 1));
+        for (int s0 = 0; s0 < kRtCombSlots; ++s0) {
+            const int p = lane * kRtCombSlots + s0;
+            const int a = p / kc, b = p - a * kc;
+            bool tie = false;
+            uint64_t key = 0;
+            if (p < kc * kc && (a + 1) * (b + 1) > top_k) {
+                key = pair_key(a, b);
+                tie = key_score(key) == theta;
+            }
+            if (__ballot(tie) == 0) continue;
+            key = wave_sort_desc<uint64_t>(tie ? key : 0ull, lane);
+            run = wave_merge_desc(run, key, lane);
+        }
+        const float m = key_score(readlane_u64(run, 0));
         float sum = 0.0f;
-        for (int i = 0; i < top_k; ++i) sum += expf(key_score(topk[i]) - m);
+        for (int i = 0; i < top_k; ++i) sum += expf(key_score(readlane_u64(run, i)) - m);
         if (lane < top_k) {
-            const uint64_t k = topk[lane];
-            const float ex = expf(key_score(k) - m);
-            out_ids[r * top_k + lane] = (int32_t)key_idx(k);
+            const float ex = expf(key_score(run) - m);
+            out_ids[r * top_k + lane] = (int32_t)key_idx(run);
             out_gates[r * top_k + lane] = Elem<T>::from_f32(ex / sum);
         }
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -378,11 +412,11 @@ int launch_route(const void* q, const void* k1, const void* k2, const float* key
     const size_t smem = route_smem_bytes(K, dh2);
     dim3 grid((unsigned)((rows + kRtRows - 1) / kRtRows));
     if (dtype == kBF16)
-        hipLaunchKernelGGL(route_kernel<uint16_t>, grid, dim3(256), smem, stream, (const uint16_t*)q,
+        hipLaunchKernelGGL(route_kernel<uint16_t>, grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
                            (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
                            (uint16_t*)gates, ids);
     else
-        hipLaunchKernelGGL(route_kernel<float>, grid, dim3(256), smem, stream, (const float*)q, (const float*)k1,
+        hipLaunchKernelGGL(route_kernel<float>, grid, dim3(kRtWaves * 64), smem, stream, (const float*)q, (const float*)k1,
                            (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
     return (int)hipGetLastError();
 }
