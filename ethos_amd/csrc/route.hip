@@ -370,17 +370,23 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
         uint64_t run = 0;
 #pragma unroll
         for (int t = 0; t < kRtStSlots; ++t) {
+            if (t > 0 && __ballot(st_a[t] >= 0) == 0) break;
             uint64_t key = st_a[t] >= 0 ? pair_key(st_a[t], st_b[t]) : 0ull;
             key = wave_sort_desc<uint64_t>(key, lane);
             run = t == 0 ? key : wave_merge_desc(run, key, lane);
         }
         const float theta = key_score(readlane_u64(run, top_k - 1));
-        for (int s0 = 0; s0 < kRtCombSlots; ++s0) {
-            const int p = lane * kRtCombSlots + s0;
-            const int a = p / kc, b = p - a * kc;
+        // A tie with theta needs c[a][0] >= theta and c[0][b] >= theta: a < na, b < nb.
+        const float v1_0 = key_score(l1[0]), v2_0 = key_score(l2[0]);
+        const bool in_a = lane < kc && Elem<T>::round32(key_score(l1[lane < kc ? lane : 0]) + v2_0) >= theta;
+        const bool in_b = lane < kc && Elem<T>::round32(v1_0 + key_score(l2[lane < kc ? lane : 0])) >= theta;
+        const int na = (int)__popcll(__ballot(in_a)), nb = (int)__popcll(__ballot(in_b));
+        for (int p0 = 0; p0 < na * nb; p0 += kWave) {
+            const int p = p0 + lane;
+            const int a = p / nb, b = p - a * nb;
             bool tie = false;
             uint64_t key = 0;
-            if (p < kc * kc && (a + 1) * (b + 1) > top_k) {
+            if (p < na * nb && (a + 1) * (b + 1) > top_k) {
                 key = pair_key(a, b);
                 tie = key_score(key) == theta;
             }
@@ -388,11 +394,12 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
             key = wave_sort_desc<uint64_t>(tie ? key : 0ull, lane);
             run = wave_merge_desc(run, key, lane);
         }
+        // gates: exponentials in parallel, their sum in list order
         const float m = key_score(readlane_u64(run, 0));
+        const float ex = lane < top_k ? expf(key_score(run) - m) : 0.0f;
         float sum = 0.0f;
-        for (int i = 0; i < top_k; ++i) sum += expf(key_score(readlane_u64(run, i)) - m);
+        for (int i = 0; i < top_k; ++i) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ex), i));
         if (lane < top_k) {
-            const float ex = expf(key_score(run) - m);
             out_ids[r * top_k + lane] = (int32_t)key_idx(run);
             out_gates[r * top_k + lane] = Elem<T>::from_f32(ex / sum);
         }
