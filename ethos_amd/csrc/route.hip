@@ -39,11 +39,16 @@ constexpr int kRtRowsPerWave = kRtRows / kRtWaves;
 constexpr int kRtMaxKc = 32;                           // k_cand <= 32, top_k <= 32
 constexpr int kRtMaxK = 512;                           // sub-keys per table
 constexpr int kRtSlots = kRtMaxK / kWave;              // approximate scores per lane per row
-constexpr int kRtCombSlots = 16;                       // combined pairs per lane (k_cand^2 <= 1024)
 constexpr int kRtStSlots = 2;                          // staircase pairs per lane (<= 119 for top_k <= 32)
 constexpr int kRtMaxDh2 = 256;
 
 // ---------------------------------------------------------------- wave networks
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    const int lo = __shfl((int)(uint32_t)v, src, kWave);
+    const int hi = __shfl((int)(uint32_t)(v >> 32), src, kWave);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
     const int lo = __shfl_xor((int)(uint32_t)v, mask, kWave);
     const int hi = __shfl_xor((int)(uint32_t)(v >> 32), mask, kWave);
@@ -100,35 +105,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return max(a, b);
 }
 
-// Descending compare-exchange sort of a small per-lane array (fully unrolled).
-template <int N>
-__device__ __forceinline__ void sort_desc(uint64_t (&c)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-#pragma unroll
-        for (int j = N - 1; j > i; --j) {
-            const uint64_t a = c[j - 1], b = c[j];
-            const bool sw = b > a;
-            c[j - 1] = sw ? b : a;
-            c[j] = sw ? a : b;
-        }
-}
-
-// Extract the `count` largest keys over the wave (each lane's array sorted
-// descending, 0 = empty) into out[0..count), descending.  Keys are distinct.
-template <int N>
-__device__ __forceinline__ void wave_extract(uint64_t (&c)[N], int count, uint64_t* out, int lane) {
-    for (int r = 0; r < count; ++r) {
-        const uint64_t m = wave_max_u64(c[0]);
-        if (m != 0 && c[0] == m) {
-#pragma unroll
-            for (int i = 0; i < N - 1; ++i) c[i] = c[i + 1];
-            c[N - 1] = 0;
-        }
-        if (lane == 0) out[r] = m;
-    }
-}
-
 // 16 bytes of a key row -> doubles, in order.
 template <typename T> struct KeyVec;
 template <> struct KeyVec<uint16_t> {
@@ -170,11 +146,9 @@ __host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2) {
     off = (off + 15) & ~(size_t)15;
     L.qd_off = off;
     off += (size_t)kRtWaves * dh2 * sizeof(double);
-    L.cand_off = 0;  // candidates reuse the row's own score storage
-    L.lists_off = off;
-    off += (size_t)kRtRows * 2 * kRtMaxKc * sizeof(uint64_t);
-    L.topk_off = off;
-    off += (size_t)kRtWaves * kRtMaxKc * sizeof(uint64_t);
+    L.cand_off = 0;   // candidates reuse the row's own score storage
+    L.lists_off = 0;  // the candidate lists stay in registers
+    L.topk_off = 0;
     L.total = off;
     return L;
 }
@@ -195,8 +169,11 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
     float* S = reinterpret_cast<float*>(smem + L.s_off);
     float* kn = reinterpret_cast<float*>(smem + L.kn_off);
     double* qd = reinterpret_cast<double*>(smem + L.qd_off) + (size_t)wave * dh2;
-    uint64_t* lists = reinterpret_cast<uint64_t*>(smem + L.lists_off);
-    uint64_t* topk = reinterpret_cast<uint64_t*>(smem + L.topk_off) + wave * kRtMaxKc;
+    // lst[rr][half]: the canonical top-k_cand list of this wave's row rr and query half,
+    // entry i held by lane i
+    uint64_t lst[kRtRowsPerWave][2];
+#pragma unroll
+    for (int rr = 0; rr < kRtRowsPerWave; ++rr) lst[rr][0] = lst[rr][1] = 0;
 
     const int64_t row0 = (int64_t)blockIdx.x * kRtRows;
     const int nkb = kpad / 32;
@@ -225,15 +202,15 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
     for (int half = 0; half < 2; ++half) {
         const T* keys = half ? keys2 : keys1;
         // 1. approximate scores for the 32-row tile: wave w takes key blocks w, w + 8, ...
-        for (int kb0 = wave; kb0 < nkb; kb0 += 4 * kRtWaves) {
-            f32x16_t acc[4];
+        for (int kb0 = wave; kb0 < nkb; kb0 += 2 * kRtWaves) {
+            f32x16_t acc[2];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[c] = f32x16_zero();
+            for (int c = 0; c < 2; ++c) acc[c] = f32x16_zero();
             const int64_t arow = row0 + lrow;
             for (int k0 = 0; k0 < dh2; k0 += M::kK) {
                 const typename M::frag a = arow < rows ? M::load(q + arow * dq + half * dh2 + k0 + lk) : M::zero();
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
+                for (int c = 0; c < 2; ++c) {
                     const int kb = kb0 + kRtWaves * c;
                     if (kb < nkb) {
                         const int j = kb * 32 + lrow;
@@ -243,7 +220,7 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
                 }
             }
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int c = 0; c < 2; ++c) {
                 const int kb = kb0 + kRtWaves * c;
                 if (kb < nkb) {
 #pragma unroll
@@ -254,6 +231,7 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
         __syncthreads();
 
         // 2-3. per row: certified candidate filter, exact scores, canonical top-k_cand
+#pragma unroll
         for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
             const int lr = wave * kRtRowsPerWave + rr;
             const int64_t r = row0 + lr;
@@ -324,7 +302,8 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
                 key = wave_sort_desc<uint64_t>(key, lane);
                 run = c0 == 0 ? key : wave_merge_desc(run, key, lane);
             }
-            if (lane < kc) lists[((size_t)lr * 2 + half) * kRtMaxKc + lane] = run;
+            if (half == 0) lst[rr][0] = run;
+            else lst[rr][1] = run;
             __builtin_amdgcn_wave_barrier();
         }
         __syncthreads();
@@ -356,14 +335,15 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
             idx -= nb;
         }
     }
+#pragma unroll
     for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
         const int lr = wave * kRtRowsPerWave + rr;
         const int64_t r = row0 + lr;
         if (r >= rows) break;
-        const uint64_t* l1 = lists + ((size_t)lr * 2 + 0) * kRtMaxKc;
-        const uint64_t* l2 = lists + ((size_t)lr * 2 + 1) * kRtMaxKc;
+        const uint64_t L1 = lst[rr][0], L2 = lst[rr][1];
+        // (lane shuffles: call with every lane active, then select)
         auto pair_key = [&](int a, int b) {
-            const uint64_t ka = l1[a], kb = l2[b];
+            const uint64_t ka = shfl_u64(L1, a), kb = shfl_u64(L2, b);
             const float v = Elem<T>::round32(key_score(ka) + key_score(kb));
             return make_key(v, key_idx(ka) * (uint32_t)K + key_idx(kb));
         };
@@ -371,25 +351,23 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
 #pragma unroll
         for (int t = 0; t < kRtStSlots; ++t) {
             if (t > 0 && __ballot(st_a[t] >= 0) == 0) break;
-            uint64_t key = st_a[t] >= 0 ? pair_key(st_a[t], st_b[t]) : 0ull;
+            const uint64_t pk = pair_key(st_a[t] >= 0 ? st_a[t] : 0, st_b[t]);
+            uint64_t key = st_a[t] >= 0 ? pk : 0ull;
             key = wave_sort_desc<uint64_t>(key, lane);
             run = t == 0 ? key : wave_merge_desc(run, key, lane);
         }
         const float theta = key_score(readlane_u64(run, top_k - 1));
         // A tie with theta needs c[a][0] >= theta and c[0][b] >= theta: a < na, b < nb.
-        const float v1_0 = key_score(l1[0]), v2_0 = key_score(l2[0]);
-        const bool in_a = lane < kc && Elem<T>::round32(key_score(l1[lane < kc ? lane : 0]) + v2_0) >= theta;
-        const bool in_b = lane < kc && Elem<T>::round32(v1_0 + key_score(l2[lane < kc ? lane : 0])) >= theta;
+        const float v1_0 = key_score(readlane_u64(L1, 0)), v2_0 = key_score(readlane_u64(L2, 0));
+        const bool in_a = lane < kc && Elem<T>::round32(key_score(L1) + v2_0) >= theta;
+        const bool in_b = lane < kc && Elem<T>::round32(v1_0 + key_score(L2)) >= theta;
         const int na = (int)__popcll(__ballot(in_a)), nb = (int)__popcll(__ballot(in_b));
         for (int p0 = 0; p0 < na * nb; p0 += kWave) {
             const int p = p0 + lane;
-            const int a = p / nb, b = p - a * nb;
-            bool tie = false;
-            uint64_t key = 0;
-            if (p < na * nb && (a + 1) * (b + 1) > top_k) {
-                key = pair_key(a, b);
-                tie = key_score(key) == theta;
-            }
+            const bool in = p < na * nb;
+            const int a = in ? p / nb : 0, b = in ? p - (p / nb) * nb : 0;
+            uint64_t key = pair_key(a, b);
+            const bool tie = in && (a + 1) * (b + 1) > top_k && key_score(key) == theta;
             if (__ballot(tie) == 0) continue;
             key = wave_sort_desc<uint64_t>(tie ? key : 0ull, lane);
             run = wave_merge_desc(run, key, lane);
