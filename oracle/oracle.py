@@ -30,7 +30,7 @@ import os
 import subprocess
 
 import numpy as np
-from scipy.special import erf
+from scipy.special import erfc
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(HERE, "libethos_oracle.so")
@@ -139,8 +139,10 @@ def storage(a_f32: np.ndarray, dt: str) -> np.ndarray:
 
 
 def gelu64(v: np.ndarray) -> np.ndarray:
-    """Exact (erf) GELU in fp64 -- F.gelu's default, model.py:174,323,329."""
-    return 0.5 * v * (1.0 + erf(v / np.sqrt(2.0)))
+    """Exact (erf) GELU in fp64 -- F.gelu's default, model.py:174,323,329:
+    0.5 v (1 + erf(v / sqrt 2)), evaluated as 0.5 v erfc(-v / sqrt 2), the same function
+    without the cancellation of 1 + erf(.) for negative v."""
+    return 0.5 * v * erfc(-v / np.sqrt(2.0))
 
 
 # ------------------------------------------------------------------ router
