@@ -387,9 +387,9 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
                     for (int mb = 0; mb < kG2MB; ++mb)
                         acc[mb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[s % (LA + 1)][cb], hf[mb][s],
                                                                              acc[mb][cb], 0, 0, 0);
-                // copies of the next chunk (past the last chunk they read zeros into the
-                // idle buffer), four per k-step
-                if (s < kCopiesW / 4) {
+                // copies of the next chunk, four per k-step (never past the unit's last
+                // chunk: the buffer range check does not cover the scalar chunk offset)
+                if (s < kCopiesW / 4 && c + 1 < c_end) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) copy(c + 1, (c + 1) & 1, 4 * s + j);
                 }

@@ -202,6 +202,30 @@ def test_generate_shapes(dl, dh, d, U):
     assert np.linalg.norm(d_) / np.linalg.norm(ref) < 2e-3
 
 
+@pytest.mark.parametrize("dh", [512, 256])
+def test_generate_many_tiles(dh):
+    """Enough experts that each workgroup runs several whole tiles back to back (their
+    hidden activations prepared during the previous tile) plus the column-split last
+    round; sampled rows against the oracle."""
+    rng = np.random.default_rng(dh)
+    E, dl, d, U = 262144, 128, 1024, 200070
+    lat = O.f32_to_bf16_bits(rng.standard_normal((E, dl)).astype(np.float32))
+    w1 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (dh, dl)) * 4 / np.sqrt(dl)).astype(np.float32))
+    w2 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(dh)).astype(np.float32))
+    uniq = np.sort(rng.choice(E, U, replace=False)).astype(np.int32)
+    n_unique = torch.tensor([U], dtype=torch.int32, device="cuda")
+    uv = hip.generate(to_dev(lat), to_dev(uniq), n_unique, U + 5, to_dev(w1), to_dev(w2))
+    torch.cuda.synchronize()
+    edges = [0, 1, 255, 256, 257, 65535, 65536, 131071, 131072, 196607, 196608, U - 2, U - 1]
+    rows = np.unique(np.concatenate([edges, rng.choice(U, 587, replace=False)])).astype(np.int64)
+    ref = O.generate(lat, uniq[rows], w1, w2, "bf16").astype(np.float64)
+    got = O.to_f32(to_host(uv)[rows], "bf16").astype(np.float64)
+    d_ = np.abs(got - ref)
+    assert np.mean(d_ > 0) < 0.05
+    assert np.all(d_ <= 2 * np.abs(ref) * 2.0 ** -7 + 1e-3 * np.abs(ref).max())
+    assert np.linalg.norm(d_) / np.linalg.norm(ref) < 2e-3
+
+
 @pytest.mark.parametrize("kind", ["cancellation", "midpoints"])
 def test_query_proj_certified_fallback_bit_exact(kind):
     """Inputs where the MFMA certificate cannot settle most elements, forcing the exact
