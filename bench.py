@@ -50,11 +50,11 @@ def stage_work(sh, U: int) -> dict:
         "route": dict(bound="hbm", work=(sh.n_tok * H * dq + 2 * K * dq // 2) * eb + N * (eb + 4), unit="GB/s"),
         # 16 B per pair (key + value in and out) + slots
         "sort_segment": dict(bound="hbm", work=16 * N + 4 * (U + 1), unit="GB/s"),
-        # 2 U (dl dh + dh 2d) flops
-        "generate": dict(bound="mfma", work=2 * U * (sh.d_latent * sh.d_hidden + sh.d_hidden * 2 * d), unit="TFLOP/s"),
-        # u and v once per unique expert, x in, y out, id + score + pair per pair
-        "apply_scatter": dict(bound="hbm", work=U * 2 * d * eb + 2 * sh.n_tok * d * eb + N * (4 + eb + 4),
-                              unit="GB/s"),
+        # 2 U (dl dh + dh d) flops: hidden rows and v rows of the unique experts
+        "generate": dict(bound="mfma", work=2 * U * (sh.d_latent * sh.d_hidden + sh.d_hidden * d), unit="TFLOP/s"),
+        # h and v once per unique expert, x in, W_u in, y out, id + score + pair per pair
+        "apply_scatter": dict(bound="hbm", work=U * (sh.d_hidden + d) * eb + 2 * sh.n_tok * d * eb
+                              + d * sh.d_hidden * eb + N * (4 + eb + 4), unit="GB/s"),
     }
 
 

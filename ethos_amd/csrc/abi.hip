@@ -149,47 +149,61 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
 
 int ethos_generate(const void* latents, int64_t n_experts, const int32_t* uniq_ids, const int32_t* n_unique,
                    int64_t max_unique, const void* w1, const void* w2, int32_t d_latent, int32_t d_hidden,
-                   int32_t d_model, int32_t dtype, void* uv_out, void* stream) {
+                   int32_t d_model, int32_t dtype, void* h_out, void* v_out, void* stream) {
     g_err[0] = 0;
     if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_generate: unknown dtype %d", dtype);
     if (n_experts <= 0 || max_unique < 0 || d_latent <= 0 || d_hidden <= 0 || d_model <= 0)
         return fail(ETHOS_ESIZE, "ethos_generate: bad sizes");
     const int kq = dtype == ETHOS_BF16 ? 16 : 2;
-    if (d_latent % kq || d_hidden % 32 || (2 * d_model) % 32 || d_hidden % kq)
+    if (d_latent % kq || d_hidden % 32 || d_model % 32)
         return fail(ETHOS_EUNSUPPORTED,
-                    "ethos_generate: needs d_latent %% %d == 0, d_hidden %% 32 == 0, d_model %% 16 == 0 "
+                    "ethos_generate: needs d_latent %% %d == 0, d_hidden %% 32 == 0, d_model %% 32 == 0 "
                     "(got %d, %d, %d)", kq, d_latent, d_hidden, d_model);
     if (ethos::generate_smem_bytes(d_latent, d_hidden, dtype) > 160 * 1024)
         return fail(ETHOS_EUNSUPPORTED, "ethos_generate: d_latent + d_hidden too large for LDS");
     if (max_unique == 0) return 0;
-    if (!latents || !uniq_ids || !n_unique || !w1 || !w2 || !uv_out)
+    if (!latents || !uniq_ids || !n_unique || !w1 || !w2 || !h_out || !v_out)
         return fail(ETHOS_ENULL, "ethos_generate: null pointer");
-    if (dtype == ETHOS_BF16 && (!aligned16(w1) || !aligned16(w2)))
-        return fail(ETHOS_EALIGN, "ethos_generate: weights not 16-byte aligned");
+    if (dtype == ETHOS_BF16 && (!aligned16(w1) || !aligned16(w2) || !aligned16(h_out) || !aligned16(v_out)))
+        return fail(ETHOS_EALIGN, "ethos_generate: weights and outputs must be 16-byte aligned");
     return hip_status(ethos::launch_generate(latents, n_experts, uniq_ids, n_unique, max_unique, w1, w2, d_latent,
-                                             d_hidden, 2 * d_model, dtype, uv_out, num_cus(), (hipStream_t)stream),
+                                             d_hidden, d_model, dtype, h_out, v_out, num_cus(), (hipStream_t)stream),
                       "ethos_generate");
 }
 
-int ethos_apply_scatter(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
-                        const int32_t* pair_slot, const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k,
-                        int32_t d_model, int32_t dtype, float* act_workspace, void* out, void* stream) {
+size_t ethos_apply_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden, int32_t dtype) {
+    if (n_tok <= 0 || n_heads <= 0 || top_k <= 0 || d_hidden <= 0) return 256;
+    return ethos::apply_workspace_bytes(n_tok, n_heads, top_k, d_hidden, dtype);
+}
+
+int ethos_apply_scatter(const void* x, const void* w2, const void* h, const void* v, const int32_t* perm,
+                        const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores, int64_t n_tok,
+                        int32_t n_heads, int32_t top_k, int32_t d_model, int32_t d_hidden, int32_t dtype,
+                        void* workspace, size_t workspace_bytes, void* out, void* stream) {
     g_err[0] = 0;
     if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_apply_scatter: unknown dtype %d", dtype);
-    if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || d_model <= 0)
+    if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || d_model <= 0 || d_hidden <= 0)
         return fail(ETHOS_ESIZE, "ethos_apply_scatter: bad sizes");
     const int vec = dtype == ETHOS_BF16 ? 8 : 4;
-    if (d_model % vec || ethos::apply_chunks(d_model, dtype) > 8)
-        return fail(ETHOS_EUNSUPPORTED, "ethos_apply_scatter: d_model=%d must be a multiple of %d and <= %d", d_model,
-                    vec, 8 * 64 * vec);
-    if (n_tok * n_heads * top_k > INT32_MAX) return fail(ETHOS_ESIZE, "ethos_apply_scatter: too many pairs");
+    if (d_model % vec || d_hidden % vec || ethos::apply_chunks(d_model, dtype) > 8 ||
+        ethos::apply_chunks(d_hidden, dtype) > 8)
+        return fail(ETHOS_EUNSUPPORTED,
+                    "ethos_apply_scatter: d_model=%d and d_hidden=%d must be multiples of %d and <= %d", d_model,
+                    d_hidden, vec, 8 * 64 * vec);
+    if (n_tok * n_heads * top_k > INT32_MAX || n_tok > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_apply_scatter: too many pairs");
     if (n_tok == 0) return 0;
-    if (!x || !uv || !perm || !sorted_slot || !pair_slot || !scores || !act_workspace || !out)
+    if (!x || !w2 || !h || !v || !perm || !sorted_slot || !pair_slot || !scores || !workspace || !out)
         return fail(ETHOS_ENULL, "ethos_apply_scatter: null pointer");
-    if (!aligned16(x) || !aligned16(uv) || !aligned16(out))
-        return fail(ETHOS_EALIGN, "ethos_apply_scatter: x, uv and out must be 16-byte aligned");
-    return hip_status(ethos::launch_apply(x, uv, perm, sorted_slot, pair_slot, scores, n_tok, n_heads, top_k, d_model,
-                                          dtype, act_workspace, out, num_cus(), (hipStream_t)stream),
+    const size_t need = ethos::apply_workspace_bytes(n_tok, n_heads, top_k, d_hidden, dtype);
+    if (workspace_bytes < need)
+        return fail(ETHOS_EWORKSPACE, "ethos_apply_scatter: workspace of %zu bytes, %zu needed", workspace_bytes,
+                    need);
+    if (!aligned16(x) || !aligned16(w2) || !aligned16(h) || !aligned16(v) || !aligned16(workspace) ||
+        !aligned16(out))
+        return fail(ETHOS_EALIGN, "ethos_apply_scatter: x, w2, h, v, workspace and out must be 16-byte aligned");
+    return hip_status(ethos::launch_apply(x, w2, h, v, perm, sorted_slot, pair_slot, scores, n_tok, n_heads, top_k,
+                                          d_model, d_hidden, dtype, workspace, out, num_cus(), (hipStream_t)stream),
                       "ethos_apply_scatter");
 }
 

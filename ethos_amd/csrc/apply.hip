@@ -1,21 +1,25 @@
-// Expert apply and weighted scatter-back (reference: model.py:326-341).
+// Expert apply and weighted scatter-back (reference: model.py:320-341).
 //
+// Token projection, once per token (the reference forms it inside the pair loop,
+// model.py:326, but it depends only on the token):
+//   xp_t = RN_T( x_t W_u )          W_u = net.2.weight[:d]^T  ([d, dh])
 // Per pair p = (t, h, j) with expert slot s:
-//   a_p = RN_T( RN_T(gelu_erf( RN_T(u_s . x_t) )) * g_p )                  (phase 1)
+//   a_p = RN_T( RN_T(gelu_erf( RN_T(h_s . xp_t) )) * g_p )                 (phase 1)
 //   y_t = RN_T( sum_h^T RN_T( sum_j RN_T(a_p * v_s) ) / H )                (phase 2)
 // where the inner sum is fp32 in j order, the head sum is taken in T one head at a
 // time, and RN_T is rounding to the layer dtype -- the reference's rounding points
-// (fp32 token accumulator model.py:312,334, per-head cast :336, dtype head sum :338,
-// dtype divide :341).
+// (x_proj and torch.dot in T model.py:326-329, fp32 token accumulator model.py:312,334,
+// per-head cast :336, dtype head sum :338, dtype divide :341).
 //
 // Phase 1 walks the pairs in expert order (the sorted permutation): a wave takes 64
-// consecutive sorted positions and reloads u_s only when the slot changes, so each
-// expert's u row is read about once.  Phase 2 is token-major: one wave per token
-// gathers the v rows of its H*k pairs and reduces them in registers; every output
-// element is written by exactly one lane, so no atomics are needed and the result
-// is deterministic.
+// consecutive sorted positions, so each expert's h row is read about once and the
+// token projections (n_tok x dh, a few MB) are gathered from the caches.  Phase 2 is
+// token-major: one wave per token gathers the v rows of its H*k pairs and reduces
+// them in registers; every output element is written by exactly one lane, so no
+// atomics are needed and the result is deterministic.
 #include "ethos_common.hpp"
 #include "ethos_launch.hpp"
+#include "ethos_mfma.hpp"
 
 namespace ethos {
 
@@ -80,13 +84,126 @@ __device__ __forceinline__ void load_raw(const T* __restrict__ row, int d, int l
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Token projection xp = RN_T(x W_u), W_u[i][j] = w2[i * dh + j] for i < d.
+// ---------------------------------------------------------------------------------
+constexpr int kTpT = 64;     // tokens per tile
+constexpr int kTpC = 64;     // hidden columns per tile
+constexpr int kTpK = 64;     // reduction chunk staged in LDS
+constexpr int kTpPitch = kTpK + 8;
+
+// bf16: 32x32x16 MFMA with fp32 accumulation, rounded once.  Computed transposed
+// (xp^T = W_u^T x^T) so that each lane ends with four consecutive hidden columns of
+// one token: 8-byte stores.  W_u is staged transposed (hidden column major) so both
+// operands are read from LDS as 16-byte k-runs.
+__global__ __launch_bounds__(256) void token_proj_bf16_kernel(const uint16_t* __restrict__ x,
+                                                              const uint16_t* __restrict__ wu, int n_tok, int d,
+                                                              int dh, uint16_t* __restrict__ xp) {
+    __shared__ __align__(16) uint16_t xs[kTpT * kTpPitch];
+    __shared__ __align__(16) uint16_t wt[kTpC * kTpPitch];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int wr = wave >> 1, wc = wave & 1;
+    const int c0 = blockIdx.x * kTpC;
+    const int t0 = blockIdx.y * kTpT;
+    f32x16_t acc = f32x16_zero();
+    for (int k0 = 0; k0 < d; k0 += kTpK) {
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int e = tid + 256 * it;  // 512 16-byte pieces per operand
+            const int r = e >> 3, q8 = (e & 7) * 8;
+            uint4 xv = make_uint4(0, 0, 0, 0);
+            if (t0 + r < n_tok) xv = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * d + k0 + q8);
+            *reinterpret_cast<uint4*>(&xs[r * kTpPitch + q8]) = xv;
+            // W_u row k0 + r, columns c0 + q8 .. + 7 -> wt[column][k]
+            const uint4 wv = *reinterpret_cast<const uint4*>(wu + (int64_t)(k0 + r) * dh + c0 + q8);
+            const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                wt[(q8 + 2 * j) * kTpPitch + r] = (uint16_t)(w4[j] & 0xffffu);
+                wt[(q8 + 2 * j + 1) * kTpPitch + r] = (uint16_t)(w4[j] >> 16);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kTpK; kk += 16) {
+            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&wt[(wc * 32 + l32) * kTpPitch + kk + 8 * h]);
+            const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(&xs[(wr * 32 + l32) * kTpPitch + kk + 8 * h]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+        }
+    }
+    // acc[i]: hidden column c0 + 32 wc + mfma32_row(i, lane) of token t0 + 32 wr + l32
+    const int t = t0 + wr * 32 + l32;
+    if (t < n_tok) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c = c0 + wc * 32 + 8 * g + 4 * h;
+            *reinterpret_cast<uint2*>(xp + (int64_t)t * dh + c) =
+                make_uint2(pack_bf16x2(acc[4 * g], acc[4 * g + 1]), pack_bf16x2(acc[4 * g + 2], acc[4 * g + 3]));
+        }
+    }
+}
+
+// Any shape and dtype: fp64 accumulation in index order, rounded once to T.
+template <typename T>
+__global__ __launch_bounds__(256) void token_proj_kernel(const T* __restrict__ x, const T* __restrict__ wu, int n_tok,
+                                                         int d, int dh, T* __restrict__ xp) {
+    constexpr int KC = 32;
+    __shared__ double xs[KC][kTpT];
+    __shared__ double ws[KC][kTpC];
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const int c0 = blockIdx.x * kTpC;
+    const int t0 = blockIdx.y * kTpT;
+    double acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    for (int k0 = 0; k0 < d; k0 += KC) {
+        const int kc = min(KC, d - k0);
+        for (int e = tid; e < kTpT * KC; e += 256) {
+            const int r = e / KC, kk = e % KC;
+            xs[kk][r] = (kk < kc && t0 + r < n_tok) ? Elem<T>::to_f64(x[(int64_t)(t0 + r) * d + k0 + kk]) : 0.0;
+        }
+        for (int e = tid; e < kTpC * KC; e += 256) {
+            const int kk = e / kTpC, r = e % kTpC;
+            ws[kk][r] = (kk < kc && c0 + r < dh) ? Elem<T>::to_f64(wu[(int64_t)(k0 + kk) * dh + c0 + r]) : 0.0;
+        }
+        __syncthreads();
+        for (int kk = 0; kk < kc; ++kk) {
+            double a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = xs[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = ws[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fma(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = t0 + ty * 4 + i;
+        if (t >= n_tok) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = c0 + tx * 4 + j;
+            if (c < dh) xp[(int64_t)t * dh + c] = Elem<T>::from_f32(Elem<T>::round64(acc[i][j]));
+        }
+    }
+}
+
 constexpr int kActGroup = 4;  // pairs whose loads are in flight together
 
 template <typename T, int CH>
-__global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ x, const T* __restrict__ uv,
+__global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
                                                         const int32_t* __restrict__ perm,
                                                         const int32_t* __restrict__ sorted_slot,
-                                                        const T* __restrict__ gates, int64_t n_pairs, int hk, int d,
+                                                        const T* __restrict__ gates, int64_t n_pairs, int hk, int dh,
                                                         float* __restrict__ act) {
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
@@ -94,14 +211,13 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ x,
     const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     const int64_t n_chunks = (n_pairs + 63) / 64;
-    const int64_t d2 = 2 * (int64_t)d;
     for (int64_t chunk = wave_id; chunk < n_chunks; chunk += n_waves) {
         const int64_t i0 = chunk * 64;
         const int cnt = (int)min((int64_t)64, n_pairs - i0);
         const int my_p = lane < cnt ? perm[i0 + lane] : 0;
         const int my_s = lane < cnt ? sorted_slot[i0 + lane] : 0;
-        // Groups of kActGroup consecutive sorted pairs: every u and x row of a group is
-        // requested before the first dot product (repeated u rows of one expert hit in
+        // Groups of kActGroup consecutive sorted pairs: every h and xp row of a group is
+        // requested before the first dot product (repeated h rows of one expert hit in
         // the cache), then the group's wave reductions run interleaved.
         for (int j0 = 0; j0 < cnt; j0 += kActGroup) {
             Raw ur[kActGroup][CH], xr[kActGroup][CH];
@@ -111,8 +227,8 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ x,
                 const int j = j0 + q < cnt ? j0 + q : cnt - 1;  // a tail group repeats the last pair
                 const int s = __builtin_amdgcn_readlane(my_s, j);
                 pq[q] = __builtin_amdgcn_readlane(my_p, j);
-                load_raw<T, CH>(uv + (int64_t)s * d2, d, lane, ur[q]);
-                load_raw<T, CH>(x + (int64_t)(pq[q] / hk) * d, d, lane, xr[q]);
+                load_raw<T, CH>(hid + (int64_t)s * dh, dh, lane, ur[q]);
+                load_raw<T, CH>(xp + (int64_t)(pq[q] / hk) * dh, dh, lane, xr[q]);
             }
             float part[kActGroup];
 #pragma unroll
@@ -143,7 +259,7 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ x,
 constexpr int kScatterUnroll = 8;  // v rows in flight per wave
 
 template <typename T, int CH>
-__global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict__ uv,
+__global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict__ vr_,
                                                             const int32_t* __restrict__ pair_slot,
                                                             const float* __restrict__ act, int64_t n_tok, int H,
                                                             int k, int d, T* __restrict__ out) {
@@ -152,7 +268,6 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
     const int lane = threadIdx.x & 63;
     const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
-    const int64_t d2 = 2 * (int64_t)d;
     const float inv_h_div = (float)H;
     for (int64_t t = wave_id; t < n_tok; t += n_waves) {
         float o[CH * N];
@@ -171,7 +286,7 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
                     if (j0 + q < k) {
                         const int s = pair_slot[pbase + j0 + q];
                         a[q] = act[pbase + j0 + q];
-                        load_raw<T, CH>(uv + (int64_t)s * d2 + d, d, lane, vr[q]);
+                        load_raw<T, CH>(vr_ + (int64_t)s * d, d, lane, vr[q]);
                     }
                 }
 #pragma unroll
@@ -203,22 +318,22 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
     }
 }
 
-template <typename T, int CH>
-static int launch_apply_t(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
-                          const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k, int d, float* act,
-                          void* out, int num_cus, hipStream_t stream) {
+template <typename T, int CH1, int CH2>
+static int launch_apply_t(const void* xp, const void* hid, const void* v, const int32_t* perm,
+                          const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,
+                          int k, int d, int dh, float* act, void* out, int num_cus, hipStream_t stream) {
     const int64_t n_pairs = n_tok * H * k;
     const int64_t chunks = (n_pairs + 63) / 64;
     int64_t g1 = (chunks + 3) / 4;
     const int64_t cap = (int64_t)num_cus * 16;
     if (g1 > cap) g1 = cap;
     if (g1 < 1) g1 = 1;
-    hipLaunchKernelGGL((apply_act_kernel<T, CH>), dim3((unsigned)g1), dim3(256), 0, stream, (const T*)x,
-                       (const T*)uv, perm, sorted_slot, (const T*)gates, n_pairs, H * k, d, act);
+    hipLaunchKernelGGL((apply_act_kernel<T, CH1>), dim3((unsigned)g1), dim3(256), 0, stream, (const T*)xp,
+                       (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, H * k, dh, act);
     int64_t g2 = (n_tok + 3) / 4;
     if (g2 > cap) g2 = cap;
     if (g2 < 1) g2 = 1;
-    hipLaunchKernelGGL((apply_scatter_kernel<T, CH>), dim3((unsigned)g2), dim3(256), 0, stream, (const T*)uv,
+    hipLaunchKernelGGL((apply_scatter_kernel<T, CH2>), dim3((unsigned)g2), dim3(256), 0, stream, (const T*)v,
                        pair_slot, (const float*)act, n_tok, H, k, d, (T*)out);
     return (int)hipGetLastError();
 }
@@ -228,24 +343,51 @@ int apply_chunks(int d, int dtype) {
     return (d + per - 1) / per;
 }
 
-int launch_apply(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
-                 const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k, int d, int dtype, float* act,
-                 void* out, int num_cus, hipStream_t stream) {
-    const int ch = apply_chunks(d, dtype);
-#define ETHOS_APPLY_CASE(TT, C)                                                                                   \
-    if (ch <= C)                                                                                                  \
-        return launch_apply_t<TT, C>(x, uv, perm, sorted_slot, pair_slot, gates, n_tok, H, k, d, act, out, num_cus, \
-                                     stream);
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    return align256((size_t)n_tok * dh * eb) + (size_t)n_tok * H * k * sizeof(float);
+}
+
+int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
+                 const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k,
+                 int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    void* xp = ws;
+    float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
+    // token projection (W_u^T = the first d rows of net.2.weight, row length dh)
+    const dim3 tgrid((unsigned)((dh + kTpC - 1) / kTpC), (unsigned)((n_tok + kTpT - 1) / kTpT));
+    if (dtype == kBF16 && d % kTpK == 0 && dh % kTpC == 0)
+        hipLaunchKernelGGL(token_proj_bf16_kernel, tgrid, dim3(256), 0, stream, (const uint16_t*)x,
+                           (const uint16_t*)w2, (int)n_tok, d, dh, (uint16_t*)xp);
+    else if (dtype == kBF16)
+        hipLaunchKernelGGL(token_proj_kernel<uint16_t>, tgrid, dim3(256), 0, stream, (const uint16_t*)x,
+                           (const uint16_t*)w2, (int)n_tok, d, dh, (uint16_t*)xp);
+    else
+        hipLaunchKernelGGL(token_proj_kernel<float>, tgrid, dim3(256), 0, stream, (const float*)x, (const float*)w2,
+                           (int)n_tok, d, dh, (float*)xp);
+    const int c1 = apply_chunks(dh, dtype), c2 = apply_chunks(d, dtype);
+#define ETHOS_APPLY_CASE(TT, C1, C2)                                                                             \
+    if (c1 <= C1 && c2 <= C2)                                                                                    \
+        return launch_apply_t<TT, C1, C2>(xp, hid, v, perm, sorted_slot, pair_slot, gates, n_tok, H, k, d, dh, act, \
+                                          out, num_cus, stream);
     if (dtype == kBF16) {
-        ETHOS_APPLY_CASE(uint16_t, 1)
-        ETHOS_APPLY_CASE(uint16_t, 2)
-        ETHOS_APPLY_CASE(uint16_t, 4)
-        ETHOS_APPLY_CASE(uint16_t, 8)
+        ETHOS_APPLY_CASE(uint16_t, 1, 1)
+        ETHOS_APPLY_CASE(uint16_t, 1, 2)
+        ETHOS_APPLY_CASE(uint16_t, 2, 2)
+        ETHOS_APPLY_CASE(uint16_t, 2, 4)
+        ETHOS_APPLY_CASE(uint16_t, 4, 4)
+        ETHOS_APPLY_CASE(uint16_t, 4, 8)
+        ETHOS_APPLY_CASE(uint16_t, 8, 8)
     } else {
-        ETHOS_APPLY_CASE(float, 1)
-        ETHOS_APPLY_CASE(float, 2)
-        ETHOS_APPLY_CASE(float, 4)
-        ETHOS_APPLY_CASE(float, 8)
+        ETHOS_APPLY_CASE(float, 1, 1)
+        ETHOS_APPLY_CASE(float, 1, 2)
+        ETHOS_APPLY_CASE(float, 2, 2)
+        ETHOS_APPLY_CASE(float, 2, 4)
+        ETHOS_APPLY_CASE(float, 4, 4)
+        ETHOS_APPLY_CASE(float, 4, 8)
+        ETHOS_APPLY_CASE(float, 8, 8)
     }
 #undef ETHOS_APPLY_CASE
     return -1;

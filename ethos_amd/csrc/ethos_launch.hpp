@@ -25,12 +25,13 @@ int launch_sort_empty(int32_t* seg_off, int32_t* n_unique, hipStream_t stream);
 
 size_t generate_smem_bytes(int dl, int dh, int dtype);
 int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
-                    int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, int dtype, void* uv,
-                    int num_cus, hipStream_t stream);
+                    int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d, int dtype, void* hout,
+                    void* vout, int num_cus, hipStream_t stream);
 
 int apply_chunks(int d, int dtype);
-int launch_apply(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
-                 const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k, int d, int dtype, float* act,
-                 void* out, int num_cus, hipStream_t stream);
+size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype);
+int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
+                 const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k,
+                 int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream);
 
 }  // namespace ethos

@@ -1,12 +1,15 @@
-// Expert generation over the unique-expert set: [u_e ; v_e] = W2 gelu(W1 z_e)
-// (reference: ExpertGenerationNetwork, model.py:168-179; the weights are read
-// directly at model.py:297-300 and applied per pair at model.py:320-332 -- here
-// each unique expert is generated once).
+// Expert generation over the unique-expert set (reference: ExpertGenerationNetwork,
+// model.py:168-179; the weights are read directly at model.py:297-300 and applied per
+// pair at model.py:320-332 -- here each unique expert is generated once).
 //
 //   z   = latents[uniq[u]]                      gathered rows  [U, dl]
 //   pre = RN_T(z W1^T)      (fp32 MFMA accumulation)          [U, dh]
-//   hid = RN_T(gelu_erf(pre))                                  [U, dh]   (LDS only)
-//   uv  = RN_T(hid W2^T)                                       [U, 2 d]  u = first d, v = last d
+//   h   = RN_T(gelu_erf(pre))                                  [U, dh]   h_i of model.py:323
+//   v   = RN_T(h W_v^T)                                        [U, d]    h_i @ W_v of model.py:332
+//
+// W_v^T is rows d .. 2d-1 of net.2.weight ([2d, dh]); the first d rows (W_u^T) are not
+// used here: the reference contracts them with the token (x_proj = x W_u, model.py:326),
+// which the apply stage does once per token.
 //
 // One workgroup (4 waves) owns a tile of experts; the latent tile and the hidden
 // tile live in LDS.  Wave w computes 32-column blocks w*4.., w*4+16.. of each GEMM
@@ -30,7 +33,7 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
                                                        const int32_t* __restrict__ uniq,
                                                        const int32_t* __restrict__ n_unique, const T* __restrict__ w1,
                                                        const T* __restrict__ w2, int dl, int dh, int d2,
-                                                       T* __restrict__ uv) {
+                                                       T* __restrict__ hout, T* __restrict__ uv) {
     using M = Mfma<T>;
     constexpr int R = GenTile<T>::kRows;
     constexpr int RB = R / 32;
@@ -91,13 +94,15 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
                     for (int i = 0; i < 16; ++i) {
                         const int row = rb * 32 + mfma32_row(i, lane);
                         const float pre = Elem<T>::round32(acc[rb][cb][i]);
-                        hs[row * hp + col] = Elem<T>::from_f32(gelu_erf(pre));
+                        const T hv = Elem<T>::from_f32(gelu_erf(pre));
+                        hs[row * hp + col] = hv;
+                        if (u0 + row < U) hout[(int64_t)(u0 + row) * dh + col] = hv;
                     }
             }
         }
         __syncthreads();
 
-        // GEMM2 -> [u ; v] rows
+        // GEMM2 -> v rows
         for (int g = wave * 4; g < nb2; g += 16) {
             f32x16_t acc[RB][4];
 #pragma unroll
@@ -196,7 +201,7 @@ template <int DL, int DH>
 __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void generate_bf16_kernel(
     const uint16_t* __restrict__ latents, int64_t n_experts, const int32_t* __restrict__ uniq,
     const int32_t* __restrict__ n_unique, int64_t max_unique, const uint16_t* __restrict__ w1,
-    const uint16_t* __restrict__ w2, int d2, uint16_t* __restrict__ uv) {
+    const uint16_t* __restrict__ w2, int d2, uint16_t* __restrict__ hout, uint16_t* __restrict__ uv) {
     constexpr int KS1 = DL / 16;                  // GEMM1 k-steps
     constexpr int NB1 = DH / 32;                  // hidden blocks of 32
     constexpr int KS2 = DH / 16;                  // GEMM2 k-steps
@@ -266,6 +271,17 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
         for (int it = 0; it < kCopies / kG2Waves; ++it) copy(c_begin, c_begin & 1, it);
 
+        // The hidden rows are stored by the unit that starts at column 0, through a
+        // buffer resource over this tile's rows below max_unique (rows past it are
+        // dropped by the range check; a unit that does not store aims past every row).
+        constexpr int kOOB = 0x7fff0000;  // a byte offset past any tile's rows
+        const int64_t row0 = (int64_t)tile * kG2Rows;
+        const int64_t rows_left = max_unique - row0;
+        const int tile_rows = rows_left < kG2Rows ? (int)(rows_left > 0 ? rows_left : 0) : kG2Rows;
+        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+            hout + row0 * DH, (short)0, tile_rows * DH * (int)sizeof(uint16_t), 0x00020000);
+        const int h_voff = c_begin == 0 ? ((wave * kG2MB * 32 + l32) * DH + 8 * h) * 2 : kOOB;
+
         // gathered latent rows of this lane's two experts (GEMM1 B operands)
         bf16x8_t zf[kG2MB][KS1];
 #pragma unroll
@@ -318,6 +334,8 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
                         v[j + 1] = gelu_bf16_fit(__uint_as_float(pk & 0xffff0000u));
                     }
                     hf[mb][2 * t + p] = pack_bf16x8(v);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, hf[mb][2 * t + p]), hr,
+                                                           h_voff + (32 * mb * DH + 16 * (2 * t + p)) * 2, 0, 0);
                     // park the k-slot in AGPRs (the MFMAs read it from there), which also
                     // keeps the compiler from sinking the GELUs into the chunk loop
                     asm volatile("" : "+a"(hf[mb][2 * t + p]));
@@ -332,14 +350,10 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
         // below max_unique, so rows past the allocation are dropped by the hardware and
         // no store needs a branch; rows in [U, max_unique) receive the (zero) rows of
         // absent experts.
-        const int64_t row0 = (int64_t)tile * kG2Rows;
-        const int64_t rows_left = max_unique - row0;
-        const int tile_rows = rows_left < kG2Rows ? (int)(rows_left > 0 ? rows_left : 0) : kG2Rows;
         const __amdgpu_buffer_rsrc_t uvr = __builtin_amdgcn_make_buffer_rsrc(
             uv + row0 * d2, (short)0, tile_rows * d2 * (int)sizeof(uint16_t), 0x00020000);
         // lane's store k covers row 8 k + lane / 8 of the wave, 16-byte group lane % 8
         const int st_voff = ((wave * kG2MB * 32 + (lane >> 3)) * d2 + 8 * (lane & 7)) * 2;
-        constexpr int kOOB = 0x7fff0000;  // a byte offset past any tile's rows
         u32x4_t* my = stg[wave];
         u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
         int pend_c = -1;
@@ -439,15 +453,15 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
 
 template <int DL, int DH>
 static bool launch_generate_bf16(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
-                                 int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* uv,
-                                 int num_cus, hipStream_t stream) {
+                                 int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* hout,
+                                 void* uv, int num_cus, hipStream_t stream) {
     if (dl != DL || dh != DH || d2 % kG2Cols) return false;
     const int64_t tiles = (max_unique + kG2Rows - 1) / kG2Rows;
     const int64_t cap = num_cus;  // one workgroup per CU
     const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
     hipLaunchKernelGGL((generate_bf16_kernel<DL, DH>), dim3(grid), dim3(kG2Waves * 64), 0, stream,
                        (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
-                       (const uint16_t*)w2, d2, (uint16_t*)uv);
+                       (const uint16_t*)w2, d2, (uint16_t*)hout, (uint16_t*)uv);
     return true;
 }
 
@@ -461,13 +475,16 @@ size_t generate_smem_bytes(int dl, int dh, int dtype) {
 }
 
 int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
-                    int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, int dtype, void* uv,
-                    int num_cus, hipStream_t stream) {
+                    int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d, int dtype, void* hout,
+                    void* vout, int num_cus, hipStream_t stream) {
+    // W_v^T: rows d .. 2d-1 of net.2.weight
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    const void* wv = static_cast<const unsigned char*>(w2) + (size_t)d * dh * eb;
     if (dtype == kBF16) {
-        if (launch_generate_bf16<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
-                                              num_cus, stream) ||
-            launch_generate_bf16<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d2, uv,
-                                              num_cus, stream))
+        if (launch_generate_bf16<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout,
+                                              vout, num_cus, stream) ||
+            launch_generate_bf16<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout,
+                                              vout, num_cus, stream))
             return (int)hipGetLastError();
     }
     const int R = dtype == kBF16 ? GenTile<uint16_t>::kRows : GenTile<float>::kRows;
@@ -477,11 +494,12 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
     const size_t smem = generate_smem_bytes(dl, dh, dtype);
     if (dtype == kBF16)
         hipLaunchKernelGGL(generate_kernel<uint16_t>, dim3(grid), dim3(256), smem, stream, (const uint16_t*)latents,
-                           n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)w2, dl, dh, d2,
-                           (uint16_t*)uv);
+                           n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)wv, dl, dh, d,
+                           (uint16_t*)hout, (uint16_t*)vout);
     else
         hipLaunchKernelGGL(generate_kernel<float>, dim3(grid), dim3(256), smem, stream, (const float*)latents,
-                           n_experts, uniq, n_unique, (const float*)w1, (const float*)w2, dl, dh, d2, (float*)uv);
+                           n_experts, uniq, n_unique, (const float*)w1, (const float*)wv, dl, dh, d, (float*)hout,
+                           (float*)vout);
     return (int)hipGetLastError();
 }
 

@@ -120,8 +120,9 @@ def sort_segment(ids: torch.Tensor, n_experts: int) -> dict:
 
 
 def generate(latents: torch.Tensor, uniq: torch.Tensor, n_unique: torch.Tensor, max_unique: int, w1: torch.Tensor,
-             w2: torch.Tensor) -> torch.Tensor:
-    """[u ; v] rows [max_unique, 2 d] for the unique experts (rows >= U untouched)."""
+             w2: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Hidden rows h [max_unique, d_hidden] and v rows [max_unique, d] of the unique experts
+    (rows >= U unspecified)."""
     _need(latents, "latents", dim=2)
     _need(uniq, "uniq", torch.int32)
     _need(n_unique, "n_unique", torch.int32)
@@ -132,26 +133,32 @@ def generate(latents: torch.Tensor, uniq: torch.Tensor, n_unique: torch.Tensor, 
     if w1.shape != (dh, dl) or w2.shape[1] != dh or w2.shape[0] % 2:
         raise RuntimeError("generate: inconsistent weight shapes")
     d = w2.shape[0] // 2
-    uv = torch.empty((max_unique, 2 * d), dtype=latents.dtype, device=latents.device)
+    h = torch.empty((max_unique, dh), dtype=latents.dtype, device=latents.device)
+    v = torch.empty((max_unique, d), dtype=latents.dtype, device=latents.device)
     rc = load().ethos_generate(latents.data_ptr(), E, uniq.data_ptr(), n_unique.data_ptr(), max_unique, w1.data_ptr(),
-                               w2.data_ptr(), dl, dh, d, dtype_code(latents.dtype), uv.data_ptr(), _stream())
+                               w2.data_ptr(), dl, dh, d, dtype_code(latents.dtype), h.data_ptr(), v.data_ptr(),
+                               _stream())
     check(rc, "ethos_generate")
-    return uv
+    return h, v
 
 
-def apply_scatter(x: torch.Tensor, uv: torch.Tensor, seg: dict, gates: torch.Tensor, n_heads: int,
-                  top_k: int) -> torch.Tensor:
+def apply_scatter(x: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, v: torch.Tensor, seg: dict,
+                  gates: torch.Tensor, n_heads: int, top_k: int) -> torch.Tensor:
     """out [n, d] = head-averaged weighted sum of the experts' contributions."""
     _need(x, "x", dim=2)
-    _need(uv, "uv", x.dtype, 2)
+    _need(w2, "w2", x.dtype, 2)
+    _need(h, "h", x.dtype, 2)
+    _need(v, "v", x.dtype, 2)
     _need(gates, "gates", x.dtype)
     n, d = x.shape
-    if uv.shape[1] != 2 * d or gates.numel() != n * n_heads * top_k:
+    dh = h.shape[1]
+    if w2.shape != (2 * d, dh) or v.shape[1] != d or gates.numel() != n * n_heads * top_k:
         raise RuntimeError("apply_scatter: inconsistent shapes")
-    act = torch.empty(n * n_heads * top_k, dtype=torch.float32, device=x.device)
+    code = dtype_code(x.dtype)
+    ws, ws_bytes = workspace(load().ethos_apply_workspace_bytes(n, n_heads, top_k, dh, code), x.device)
     out = torch.empty_like(x)
-    rc = load().ethos_apply_scatter(x.data_ptr(), uv.data_ptr(), seg["perm"].data_ptr(), seg["sorted_slot"].data_ptr(),
-                                    seg["pair_slot"].data_ptr(), gates.data_ptr(), n, n_heads, top_k, d,
-                                    dtype_code(x.dtype), act.data_ptr(), out.data_ptr(), _stream())
+    rc = load().ethos_apply_scatter(x.data_ptr(), w2.data_ptr(), h.data_ptr(), v.data_ptr(), seg["perm"].data_ptr(),
+                                    seg["sorted_slot"].data_ptr(), seg["pair_slot"].data_ptr(), gates.data_ptr(), n,
+                                    n_heads, top_k, d, dh, code, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
     check(rc, "ethos_apply_scatter")
     return out

@@ -198,10 +198,10 @@ class EthosExpertLayer(nn.Module):
             if mark is not None:
                 mark("sort_segment")
             latents, w1, w2 = self._generator_params(x_flat.dtype, x_flat.device)
-            uv = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2)
+            h, v = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2)
             if mark is not None:
                 mark("generate")
-            out = hip.apply_scatter(x_flat, uv, seg, gates, self.num_heads, self.top_k)
+            out = hip.apply_scatter(x_flat, w2, h, v, seg, gates, self.num_heads, self.top_k)
             if mark is not None:
                 mark("apply_scatter")
         return out

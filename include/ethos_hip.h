@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define ETHOS_ABI_VERSION 1
+#define ETHOS_ABI_VERSION 2
 
 #define ETHOS_F32 0
 #define ETHOS_BF16 1
@@ -117,37 +117,50 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
                        int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique, void* stream);
 
 /*
- * Expert generation for the unique experts: uv[u] = RN_T(W2 gelu(RN_T(W1 z))), with
- * z = latents[uniq_ids[u]] and gelu in erf form.  Replaces the per-pair
- * gelu(z @ W1) / h @ W_u / h @ W_v of model.py:320-332 (weights read at
- * model.py:297-300; ExpertGenerationNetwork model.py:168-179).
+ * Expert generation for the unique experts, u = 0 .. U-1, z = latents[uniq_ids[u]]:
+ *   h[u] = RN_T(gelu(RN_T(W1 z)))        the hidden row h_i (model.py:323), erf-form GELU
+ *   v[u] = RN_T(W_v h[u])                h_i @ W_v (model.py:332), W_v^T = w2 rows d_model .. 2 d_model - 1
+ * Replaces the per-pair gelu(z @ W1) and h @ W_v of model.py:320-332 (weights read at
+ * model.py:297-300; ExpertGenerationNetwork model.py:168-179); each unique expert is
+ * generated once.
  *   latents  [n_experts, d_latent]          dtype T  (expert_latents.weight)
  *   uniq_ids [max_unique], n_unique [1]     from ethos_sort_segment (U read on the device)
  *   w1       [d_hidden, d_latent]           dtype T  (generation_network.net.0.weight)
  *   w2       [2 * d_model, d_hidden]        dtype T  (generation_network.net.2.weight)
- *   uv_out   [max_unique, 2 * d_model]      dtype T  rows u < U written: u_e = [:d_model], v_e = [d_model:]
- * Limits: d_latent % 16 (bf16) or % 2 (fp32) == 0, d_hidden % 32 == 0, d_model % 16 == 0.
+ *   h_out    [max_unique, d_hidden]         dtype T  rows u < U written
+ *   v_out    [max_unique, d_model]          dtype T  rows u < U written
+ * Limits: d_latent % 16 (bf16) or % 2 (fp32) == 0, d_hidden % 32 == 0, d_model % 32 == 0;
+ * bf16 weights and outputs 16-byte aligned.
  */
 int ethos_generate(const void* latents, int64_t n_experts, const int32_t* uniq_ids, const int32_t* n_unique,
                    int64_t max_unique, const void* w1, const void* w2, int32_t d_latent, int32_t d_hidden,
-                   int32_t d_model, int32_t dtype, void* uv_out, void* stream);
+                   int32_t d_model, int32_t dtype, void* h_out, void* v_out, void* stream);
+
+/* Workspace size for ethos_apply_scatter (token projections + per-pair activations). */
+size_t ethos_apply_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden, int32_t dtype);
 
 /*
  * Expert apply and weighted scatter-back, averaged over heads.
  * Replaces the pair loop and head average of model.py:306-341 (and the per-token
  * Triton program of kernels.py:83-120 with the head loop of kernels.py:167-220).
- *   x             [n_tok, d_model]                 dtype T, 16-byte aligned
- *   uv            [>= U, 2 * d_model]              dtype T, from ethos_generate
+ *   x             [n_tok, d_model]                 dtype T
+ *   w2            [2 * d_model, d_hidden]          dtype T  (generation_network.net.2.weight;
+ *                                                  its first d_model rows are W_u^T)
+ *   h, v          [>= U, d_hidden], [>= U, d_model] dtype T, from ethos_generate
  *   perm, sorted_slot, pair_slot                   from ethos_sort_segment
  *   scores        [n_tok, n_heads, top_k]          dtype T  gates from ethos_route_topk
- *   act_workspace [n_tok * n_heads * top_k] fp32   per-pair activations (scratch)
+ *   workspace     >= ethos_apply_workspace_bytes(...) bytes (scratch)
  *   out           [n_tok, d_model]                 dtype T
- * out[t] = RN_T(sum_h^T RN_T(sum_k RN_T(a_p * v_e)) / n_heads), a_p = RN_T(RN_T(gelu(RN_T(u_e . x_t))) * g_p).
- * Limits: d_model % 8 (bf16) or % 4 (fp32) == 0 and d_model <= 4096 (bf16) / 2048 (fp32).
+ * xp_t = RN_T(x_t W_u) (x_proj, model.py:326, formed once per token);
+ * a_p = RN_T(RN_T(gelu(RN_T(h_e . xp_t))) * g_p) (model.py:329);
+ * out[t] = RN_T(sum_h^T RN_T(sum_k RN_T(a_p * v_e)) / n_heads) (model.py:332-341).
+ * Limits: d_model and d_hidden multiples of 8 (bf16) or 4 (fp32) and <= 4096 (bf16) /
+ * 2048 (fp32); x, w2, h, v, workspace and out 16-byte aligned.
  */
-int ethos_apply_scatter(const void* x, const void* uv, const int32_t* perm, const int32_t* sorted_slot,
-                        const int32_t* pair_slot, const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k,
-                        int32_t d_model, int32_t dtype, float* act_workspace, void* out, void* stream);
+int ethos_apply_scatter(const void* x, const void* w2, const void* h, const void* v, const int32_t* perm,
+                        const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores, int64_t n_tok,
+                        int32_t n_heads, int32_t top_k, int32_t d_model, int32_t d_hidden, int32_t dtype,
+                        void* workspace, size_t workspace_bytes, void* out, void* stream);
 
 #ifdef __cplusplus
 }

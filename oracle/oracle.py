@@ -16,12 +16,13 @@ Layout of the oracle:
 Reference algorithm (wrmedford/ETHOS):
   router            model.py:208-254
   generation net    model.py:168-179 (weights read directly at model.py:297-300)
-  expert loop       model.py:306-341 (per pair: h = gelu(z W1); a = gelu(h . x W_u) g;
-                    y += a * (h W_v); per-head fp32 accumulate, cast, head sum in
-                    dtype, divide by H)
-The identity [u_e ; v_e] = W2 gelu(W1 z_e) (u = first d_model outputs, v = last
-d_model) gives h . (x W_u) = u_e . x and h W_v = v_e, which is how every function
-below is written.
+  expert loop       model.py:306-341 (per pair: h = gelu(z W1); x_proj = x W_u;
+                    a = gelu(h . x_proj) g; y += a * (h W_v); per-head fp32
+                    accumulate, cast, head sum in dtype, divide by H)
+The functions below keep the reference's intermediates: the hidden row h_e of each
+unique expert, the token projection x_proj = x W_u (W_u = W2[:d_model]^T, the same for
+every pair of a token) and v_e = h_e W_v (W_v = W2[d_model:]^T), each rounded to the
+layer dtype where the reference rounds it.
 """
 from __future__ import annotations
 
@@ -234,48 +235,62 @@ def sort_segment(ids, n_experts: int):
 
 # ------------------------------------------------------------------ generator / apply
 def generate(latents, uniq, W1, W2, dt: str):
-    """[u_e ; v_e] for each expert id in ``uniq`` (model.py:168-179, 297-300, 320-323).
+    """(h_e, v_e) for each expert id in ``uniq`` (model.py:168-179, 297-300, 320-323, 332).
 
     Rounding points mirror the reference's dtype flow: the pre-activation z W1 is
-    rounded to T (a dtype matmul), GELU's output is rounded to T, and the generated
-    row is rounded to T.  Returns float32 [U, 2 d_model] holding T values.
+    rounded to T (a dtype matmul), GELU's output h is rounded to T, and v = h W_v
+    (W_v = W2[d_model:]^T, model.py:300) is rounded to T.  Returns float32 arrays
+    h [U, d_hidden] and v [U, d_model] holding T values.
     """
+    d = W2.shape[0] // 2
     z = to_f32(latents[uniq], dt).astype(np.float64)
     w1 = to_f32(W1, dt).astype(np.float64)
-    w2 = to_f32(W2, dt).astype(np.float64)
+    wv = to_f32(W2[d:], dt).astype(np.float64)
     pre = round_T(z @ w1.T, dt).astype(np.float64)
-    hid = round_T(gelu64(pre), dt).astype(np.float64)
-    return round_T(hid @ w2.T, dt)
+    hid = round_T(gelu64(pre), dt)
+    return hid, round_T(hid.astype(np.float64) @ wv.T, dt)
 
 
-def apply(x, uv, pair_slot, gates, n_heads: int, top_k: int, dt: str, tokens=None):
+def token_proj(x, W2, dt: str):
+    """x_proj = RN_T(x W_u) [n_tok, d_hidden], W_u = W2[:d_model]^T (model.py:299, 326).
+
+    The reference forms it inside the pair loop; it depends only on the token.
+    """
+    d = x.shape[1]
+    xs = to_f32(x, dt).astype(np.float64)
+    wu = to_f32(W2[:d], dt).astype(np.float64)                          # [d, d_hidden]
+    return round_T(xs @ wu, dt)
+
+
+def apply(xp, h, v, pair_slot, gates, n_heads: int, top_k: int, dt: str, tokens=None):
     """Weighted scatter-back (model.py:326-341) for the listed tokens (default all).
 
-    Per pair p = (t, h, j): a_p = RN(RN(gelu(RN(u . x_t))) * g_p); per head
-    y = RN(sum_j RN(a_p * v)) with the sum in high precision; the heads are summed
-    in T one at a time and the result divided by H in T.  Returns float32 [len(tokens), d]
-    holding T values.
+    Per pair p = (t, head, j) with expert slot s: a_p = RN(RN(gelu(RN(h_s . xp_t))) * g_p);
+    per head y = RN(sum_j RN(a_p * v_s)) with the sum in high precision; the heads are
+    summed in T one at a time and the result divided by H in T.  ``xp`` is
+    token_proj(x).  Returns float32 [len(tokens), d] holding T values.
     """
-    xf = to_f32(x, dt)
-    n_tok, d = xf.shape
+    xpf = np.asarray(xp, np.float32)
+    n_tok = xpf.shape[0]
+    d = v.shape[1]
     g = to_f32(gates, dt).reshape(n_tok, n_heads, top_k)
     slot = np.asarray(pair_slot).reshape(n_tok, n_heads, top_k)
     toks = np.arange(n_tok) if tokens is None else np.asarray(tokens)
-    u = uv[:, :d].astype(np.float64)
-    v = uv[:, d:].astype(np.float64)
+    hh = np.asarray(h).astype(np.float64)
+    vv = np.asarray(v).astype(np.float64)
     out = np.empty((len(toks), d), np.float32)
     for i0 in range(0, len(toks), 32):
         tk = toks[i0:i0 + 32]
-        xs = xf[tk].astype(np.float64)                                  # [b, d]
+        xs = xpf[tk].astype(np.float64)                                 # [b, d_hidden]
         s = slot[tk]                                                      # [b, H, k]
-        dots = np.einsum("bd,bhkd->bhk", xs, u[s])                      # u_e . x_t
+        dots = np.einsum("bj,bhkj->bhk", xs, hh[s])                     # h_s . xp_t
         act = round_T(gelu64(round_T(dots, dt).astype(np.float64)), dt)
         a = round_T((act * g[tk]).astype(np.float32), dt)               # T * T product
-        contrib = round_T((a[..., None].astype(np.float64) * v[s]), dt)  # RN(a * v)
+        contrib = round_T((a[..., None].astype(np.float64) * vv[s]), dt)  # RN(a * v)
         head = round_T(contrib.astype(np.float64).sum(axis=2), dt)       # [b, H, d]
         acc = np.zeros((len(tk), d), np.float32)
-        for h in range(n_heads):
-            acc = round_T((acc + head[:, h]).astype(np.float32), dt)
+        for hd in range(n_heads):
+            acc = round_T((acc + head[:, hd]).astype(np.float32), dt)
         out[i0:i0 + len(tk)] = round_T((acc / np.float32(n_heads)).astype(np.float32), dt)
     return out
 
@@ -317,14 +332,16 @@ def layer_forward(x, P: dict, n_heads: int, top_k: int, dt: str, tokens=None, q=
     E = P["latents"].shape[0]
     sel_ids = ids if tokens is None else ids[np.asarray(tokens)]
     perm, uniq, seg, inv = sort_segment(ids.reshape(-1), E)
+    xp = token_proj(x, P["W2"], dt)
     if tokens is None:
-        uv = generate(P["latents"], uniq, P["W1"], P["W2"], dt)
-        out = apply(x, uv, inv, gates, n_heads, top_k, dt)
+        h, v = generate(P["latents"], uniq, P["W1"], P["W2"], dt)
+        out = apply(xp, h, v, inv, gates, n_heads, top_k, dt)
     else:
         # generate only the experts the listed tokens use; remap slots
         sub_uniq = np.unique(sel_ids.reshape(-1))
-        uv_sub = generate(P["latents"], sub_uniq, P["W1"], P["W2"], dt)
+        h_sub, v_sub = generate(P["latents"], sub_uniq, P["W1"], P["W2"], dt)
         full_slot = np.searchsorted(sub_uniq, ids.reshape(-1)).clip(0, len(sub_uniq) - 1)
-        out = apply(x, uv_sub, full_slot, gates, n_heads, top_k, dt, tokens=tokens)
-        uv = None
-    return dict(q=q, gates=gates, ids=ids, perm=perm, uniq=uniq, seg_off=seg, pair_slot=inv, uv=uv, out=out)
+        out = apply(xp, h_sub, v_sub, full_slot, gates, n_heads, top_k, dt, tokens=tokens)
+        h = v = None
+    return dict(q=q, gates=gates, ids=ids, perm=perm, uniq=uniq, seg_off=seg, pair_slot=inv, xp=xp, h=h, v=v,
+                out=out)

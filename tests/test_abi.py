@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ethos_abi_version() == 1
+    assert _lib.load().ethos_abi_version() == 2
 
 
 def _rc(fn, *args):
@@ -56,9 +56,11 @@ def test_argument_errors_are_codes():
     # workspace too small
     assert L.ethos_sort_segment(1, 100, 16, 16, 8, 16, 16, 16, 16, 16, 16, None) == -5
     # misaligned apply pointers
-    assert L.ethos_apply_scatter(3, 16, 16, 16, 16, 16, 4, 2, 2, 64, 1, 16, 16, None) == -4
+    assert L.ethos_apply_scatter(3, 16, 16, 16, 16, 16, 16, 16, 4, 2, 2, 64, 32, 1, 16, 4096, 16, None) == -4
+    # apply workspace too small
+    assert L.ethos_apply_scatter(16, 16, 16, 16, 16, 16, 16, 16, 4, 2, 2, 64, 32, 1, 16, 8, 16, None) == -5
     # unsupported generator shape
-    assert L.ethos_generate(16, 4, 16, 16, 4, 16, 16, 10, 32, 64, 1, 16, None) == -6
+    assert L.ethos_generate(16, 4, 16, 16, 4, 16, 16, 10, 32, 64, 1, 16, 16, None) == -6
     # zero-size work is a no-op success
     assert L.ethos_query_proj(None, None, None, None, None, 0, 8, 2, 8, 1, None, 0, None, None) == 0
     assert L.ethos_last_error() == b""

@@ -92,6 +92,29 @@ def test_sort_segment_exact(n, E, pattern):
     assert np.array_equal(to_host(r["sorted_slot"]), inv[perm])
 
 
+def _check_rows(got, ref, dt):
+    """Generated rows against the oracle: fp32 to 1e-4; bf16 mostly identical, the rest
+    one or two roundings apart (the GPU accumulates in fp32, the oracle rounds exact sums)."""
+    got = got.astype(np.float64)
+    ref = ref.astype(np.float64)
+    d = np.abs(got - ref)
+    scale = np.abs(ref).max()
+    if dt == "fp32":
+        assert np.all(d <= 1e-4 * np.abs(ref) + 1e-5 * scale), d.max()
+    else:
+        ulp = np.abs(ref) * 2.0 ** -7 + 1e-30
+        assert np.mean(d > 0) < 0.05, np.mean(d > 0)
+        assert np.all(d <= 2 * ulp + 1e-3 * scale)
+        assert np.linalg.norm(d) / np.linalg.norm(ref) < 2e-3
+
+
+def _generate(lat, uniq, w1, w2, max_unique, dt):
+    n_unique = torch.tensor([len(uniq)], dtype=torch.int32, device="cuda")
+    h, v = hip.generate(to_dev(lat), to_dev(uniq), n_unique, max_unique, to_dev(w1), to_dev(w2))
+    torch.cuda.synchronize()
+    return O.to_f32(to_host(h), dt), O.to_f32(to_host(v), dt)
+
+
 @pytest.mark.parametrize("name,signal", [("tiny", False), ("tiny", True), ("tiny_fp32", True), ("cfg1", True),
                                          ("cfg3", False), ("cfg3", True)])
 def test_generate_matches_oracle(name, signal):
@@ -99,22 +122,10 @@ def test_generate_matches_oracle(name, signal):
     rng = np.random.default_rng(0)
     U = min(sh.num_experts, 777)
     uniq = np.sort(rng.choice(sh.num_experts, U, replace=False)).astype(np.int32)
-    uv_ref = O.generate(P["latents"], uniq, P["W1"], P["W2"], sh.dtype)
-    n_unique = torch.tensor([U], dtype=torch.int32, device="cuda")
-    uv = hip.generate(to_dev(P["latents"]), to_dev(uniq), n_unique, U + 5, to_dev(P["W1"]), to_dev(P["W2"]))
-    torch.cuda.synchronize()
-    got = O.to_f32(to_host(uv), sh.dtype)[:U].astype(np.float64)
-    ref = uv_ref.astype(np.float64)
-    d = np.abs(got - ref)
-    scale = np.abs(ref).max()
-    if sh.dtype == "fp32":
-        assert np.all(d <= 1e-4 * np.abs(ref) + 1e-5 * scale), d.max()
-    else:
-        # bf16 storage: most elements identical, the rest one rounding apart
-        ulp = np.abs(ref) * 2.0 ** -7 + 1e-30
-        assert np.mean(d > 0) < 0.05, np.mean(d > 0)
-        assert np.all(d <= 2 * ulp + 1e-3 * scale)
-        assert np.linalg.norm(d) / np.linalg.norm(ref) < 2e-3
+    h_ref, v_ref = O.generate(P["latents"], uniq, P["W1"], P["W2"], sh.dtype)
+    h, v = _generate(P["latents"], uniq, P["W1"], P["W2"], U + 5, sh.dtype)
+    _check_rows(h[:U], h_ref, sh.dtype)
+    _check_rows(v[:U], v_ref, sh.dtype)
 
 
 @pytest.mark.parametrize("name,signal", [("tiny", False), ("tiny", True), ("tiny_fp32", True), ("cfg1", False),
@@ -126,14 +137,41 @@ def test_apply_matches_oracle(name, signal):
     g, ids = O.route(q, P["K1"], P["K2"], sh.top_k, sh.dtype)
     seg = hip.sort_segment(to_dev(ids.reshape(-1)), sh.num_experts)
     U = int(seg["n_unique"].item())
-    uv_dev = hip.generate(to_dev(P["latents"]), seg["uniq"], seg["n_unique"], seg["max_unique"], to_dev(P["W1"]),
-                          to_dev(P["W2"]))
-    out = hip.apply_scatter(to_dev(x), uv_dev, seg, to_dev(g), sh.num_heads, sh.top_k)
+    w2 = to_dev(P["W2"])
+    h_dev, v_dev = hip.generate(to_dev(P["latents"]), seg["uniq"], seg["n_unique"], seg["max_unique"],
+                                to_dev(P["W1"]), w2)
+    out = hip.apply_scatter(to_dev(x), w2, h_dev, v_dev, seg, to_dev(g), sh.num_heads, sh.top_k)
     torch.cuda.synchronize()
-    uv = O.to_f32(to_host(uv_dev), sh.dtype)[:U]
-    ref = O.apply(x, uv, to_host(seg["pair_slot"]), g, sh.num_heads, sh.top_k, sh.dtype)
+    h = O.to_f32(to_host(h_dev), sh.dtype)[:U]
+    v = O.to_f32(to_host(v_dev), sh.dtype)[:U]
+    xp = O.token_proj(x, P["W2"], sh.dtype)
+    ref = O.apply(xp, h, v, to_host(seg["pair_slot"]), g, sh.num_heads, sh.top_k, sh.dtype)
     got = O.to_f32(to_host(out), sh.dtype)
     check_out(got, ref, sh.dtype, signal=signal, nerr_max=2e-3)
+
+
+@pytest.mark.parametrize("n_tok,d,dh,dt", [(100, 1024, 512, "bf16"), (37, 256, 128, "bf16"), (70, 96, 64, "bf16"),
+                                           (33, 128, 96, "fp32")])
+def test_apply_shapes(n_tok, d, dh, dt):
+    """Apply over shapes the configs do not hit: token counts that are not a multiple of
+    the projection tile, widths that take the generic projection, random experts."""
+    rng = np.random.default_rng(n_tok + d + dh)
+    H, k, E = 2, 4, 300
+    enc = (lambda a: O.f32_to_bf16_bits(a)) if dt == "bf16" else (lambda a: a.astype(np.float32))
+    x = enc(rng.standard_normal((n_tok, d)).astype(np.float32))
+    w2 = enc((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(d)).astype(np.float32))
+    ids = rng.integers(0, E, (n_tok, H, k)).astype(np.int32)
+    g = enc(rng.uniform(0, 1, (n_tok, H, k)).astype(np.float32))
+    seg = hip.sort_segment(to_dev(ids.reshape(-1)), E)
+    U = int(seg["n_unique"].item())
+    h = enc(rng.standard_normal((seg["max_unique"], dh)).astype(np.float32) * 0.3)
+    v = enc(rng.standard_normal((seg["max_unique"], d)).astype(np.float32))
+    out = hip.apply_scatter(to_dev(x), to_dev(w2), to_dev(h), to_dev(v), seg, to_dev(g), H, k)
+    torch.cuda.synchronize()
+    xp = O.token_proj(x, w2, dt)
+    ref = O.apply(xp, O.to_f32(h, dt)[:U], O.to_f32(v, dt)[:U], to_host(seg["pair_slot"]), g, H, k, dt)
+    got = O.to_f32(to_host(out), dt)
+    check_out(got, ref, dt, signal=True, nerr_max=2e-3)
 
 
 def _stress_case(kind, rng, rows, K, dh2, dt):
@@ -191,39 +229,29 @@ def test_generate_shapes(dl, dh, d, U):
     w1 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (dh, dl)) * 4 / np.sqrt(dl)).astype(np.float32))
     w2 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(dh)).astype(np.float32))
     uniq = np.sort(rng.choice(E, U, replace=False)).astype(np.int32)
-    ref = O.generate(lat, uniq, w1, w2, "bf16").astype(np.float64)
-    n_unique = torch.tensor([U], dtype=torch.int32, device="cuda")
-    uv = hip.generate(to_dev(lat), to_dev(uniq), n_unique, U + 3, to_dev(w1), to_dev(w2))
-    torch.cuda.synchronize()
-    got = O.to_f32(to_host(uv), "bf16")[:U].astype(np.float64)
-    d_ = np.abs(got - ref)
-    assert np.mean(d_ > 0) < 0.05
-    assert np.all(d_ <= 2 * np.abs(ref) * 2.0 ** -7 + 1e-3 * np.abs(ref).max())
-    assert np.linalg.norm(d_) / np.linalg.norm(ref) < 2e-3
+    h_ref, v_ref = O.generate(lat, uniq, w1, w2, "bf16")
+    h, v = _generate(lat, uniq, w1, w2, U + 3, "bf16")
+    _check_rows(h[:U], h_ref, "bf16")
+    _check_rows(v[:U], v_ref, "bf16")
 
 
 @pytest.mark.parametrize("dh", [512, 256])
 def test_generate_many_tiles(dh):
-    """Enough experts that each workgroup runs several whole tiles back to back (their
-    hidden activations prepared during the previous tile) plus the column-split last
-    round; sampled rows against the oracle."""
+    """Enough experts that each workgroup runs several whole tiles back to back plus the
+    column-split last round (whose first part alone stores the hidden rows); sampled
+    rows against the oracle."""
     rng = np.random.default_rng(dh)
     E, dl, d, U = 262144, 128, 1024, 200070
     lat = O.f32_to_bf16_bits(rng.standard_normal((E, dl)).astype(np.float32))
     w1 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (dh, dl)) * 4 / np.sqrt(dl)).astype(np.float32))
     w2 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(dh)).astype(np.float32))
     uniq = np.sort(rng.choice(E, U, replace=False)).astype(np.int32)
-    n_unique = torch.tensor([U], dtype=torch.int32, device="cuda")
-    uv = hip.generate(to_dev(lat), to_dev(uniq), n_unique, U + 5, to_dev(w1), to_dev(w2))
-    torch.cuda.synchronize()
+    h, v = _generate(lat, uniq, w1, w2, U + 5, "bf16")
     edges = [0, 1, 255, 256, 257, 65535, 65536, 131071, 131072, 196607, 196608, U - 2, U - 1]
     rows = np.unique(np.concatenate([edges, rng.choice(U, 587, replace=False)])).astype(np.int64)
-    ref = O.generate(lat, uniq[rows], w1, w2, "bf16").astype(np.float64)
-    got = O.to_f32(to_host(uv)[rows], "bf16").astype(np.float64)
-    d_ = np.abs(got - ref)
-    assert np.mean(d_ > 0) < 0.05
-    assert np.all(d_ <= 2 * np.abs(ref) * 2.0 ** -7 + 1e-3 * np.abs(ref).max())
-    assert np.linalg.norm(d_) / np.linalg.norm(ref) < 2e-3
+    h_ref, v_ref = O.generate(lat, uniq[rows], w1, w2, "bf16")
+    _check_rows(h[rows], h_ref, "bf16")
+    _check_rows(v[rows], v_ref, "bf16")
 
 
 @pytest.mark.parametrize("kind", ["cancellation", "midpoints"])

@@ -68,9 +68,10 @@ def test_layer_against_reference_outputs(name):
         assert np.mean(np.any(ours != theirs, -1)) <= 0.01
         # expert stage with the reference's routing
         seg = hip.sort_segment(to_dev(ref_ids.reshape(-1).astype(np.int32)), sh.num_experts)
-        uv = hip.generate(m.expert_latents.weight.detach(), seg["uniq"], seg["n_unique"], seg["max_unique"],
-                          m.generation_network.net[0].weight.detach(), m.generation_network.net[2].weight.detach())
-        out = hip.apply_scatter(xd, uv, seg, to_dev(f["ref_scores"]), sh.num_heads, sh.top_k)
+        w2 = m.generation_network.net[2].weight.detach()
+        h, v = hip.generate(m.expert_latents.weight.detach(), seg["uniq"], seg["n_unique"], seg["max_unique"],
+                            m.generation_network.net[0].weight.detach(), w2)
+        out = hip.apply_scatter(xd, w2, h, v, seg, to_dev(f["ref_scores"]), sh.num_heads, sh.top_k)
         check_out(O.to_f32(to_host(out), "bf16"), O.to_f32(f["ref_out"], "bf16"), "bf16", signal=meta["signal"])
 
 

@@ -121,8 +121,9 @@ def test_expert_stage_with_reference_routing(name):
     dt = sh.dtype
     P = O.unpack_state(sd, sh.num_heads)
     perm, uniq, seg, inv = O.sort_segment(f["ref_indices"].reshape(-1), sh.num_experts)
-    uv = O.generate(P["latents"], uniq, P["W1"], P["W2"], dt)
-    out = O.apply(O.from_torch(x), uv, inv, f["ref_scores"], sh.num_heads, sh.top_k, dt)
+    h, v = O.generate(P["latents"], uniq, P["W1"], P["W2"], dt)
+    xp = O.token_proj(O.from_torch(x), P["W2"], dt)
+    out = O.apply(xp, h, v, inv, f["ref_scores"], sh.num_heads, sh.top_k, dt)
     _check_output(out, O.to_f32(f["ref_out"], dt).astype(np.float64), dt, meta["signal"])
 
 
