@@ -98,6 +98,80 @@ __device__ __forceinline__ float gelu_bf16_fit(float x) {
     return __builtin_fmaf(-axc, t * e, pos);
 }
 
+// erf-form GELU of two packed bf16 values (low and high half), correctly rounded to
+// bf16, from a table of the 3328 inputs that are not a closed form (gelu_bf16_lut.inc,
+// written by gelu_lut.py): table entry d for x = +bf16(0x3a80 + d), d < 1536
+// (2^-10 <= x < 4), and entry 1536 + d for x = -bf16(0x3a80 + d), d < 1792
+// (2^-10 <= |x| < 16).  Elsewhere RN(GELU(x)) = x for x >= 4, -0 for -inf < x <= -16,
+// NaN for -inf and NaN, and RN(x / 2) for |x| < 2^-10.  The lane arithmetic works on
+// both 16-bit halves at once; the per-half masks (all ones where a condition holds) come
+// from arithmetic shifts, written as inline asm so that the compiler keeps them packed
+// instead of splitting them into per-half compares and selects.  `lut_bytes` is the
+// table's LDS byte address.
+constexpr int kGeluLutSize = 3328;
+
+// each half: v < 0 (as i16) ? 0xffff : 0.  The shift count is the packed pair (15, 15):
+// an inline constant would give the high half a count of 0.
+__device__ __forceinline__ uint32_t pk_sign_mask(uint32_t v) {
+    uint32_t r;
+    asm("v_pk_ashrrev_i16 %0, %1, %2" : "=v"(r) : "s"(0x000f000fu), "v"(v));
+    return r;
+}
+// b is wave-uniform (a constant): held in an SGPR, since packed instructions take no
+// literal operands
+__device__ __forceinline__ uint32_t pk_add_u16(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_pk_add_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_add_u16_vv(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_pk_add_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_pk_sub_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_rsub_u16(uint32_t a, uint32_t b) {  // b - a per half
+    uint32_t r;
+    asm("v_pk_sub_u16 %0, %2, %1" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b) {  // (m & a) | (~m & b)
+    return (m & a) | (~m & b);
+}
+
+__device__ __forceinline__ uint32_t gelu_bf16x2_lut(uint32_t pk, uint32_t lut_bytes) {
+    const uint32_t a = pk & 0x7fff7fffu;
+    const uint32_t negm = pk_sign_mask(pk);
+    const uint32_t d = pk_sub_u16(a, 0x3a803a80u);  // wraps below the table: |x| < 2^-10
+    const uint32_t smallm = pk_sign_mask(d);
+    // table index: d (+ 1536 for negative x), clamped; lanes outside the table are
+    // replaced below
+    const uint32_t idx = pk_min_u16(pk_add_u16_vv(d, negm & 0x06000600u), 0x0cff0cffu);
+    // big: d >= 0x600 (x >= 4) or d >= 0x700 (x <= -16), i.e. thr - d < 0 with
+    // thr = 0x5ff or 0x6ff
+    const uint32_t bigm = pk_sign_mask(pk_rsub_u16(d, pk_add_u16(negm & 0x01000100u, 0x05ff05ffu)));
+    // big result: x itself for x > 0; -0 for negative x, or a NaN for -inf / NaN (a >= 0x7f80)
+    const uint32_t bigneg = 0x80008000u | (pk_sign_mask(pk_add_u16(a, 0x00800080u)) & 0x7fc07fc0u);
+    const uint32_t bigv = bit_select(negm, bigneg, pk);
+    const uint32_t off = pk_add_u16_vv(idx, idx);  // byte offsets
+    typedef const __attribute__((address_space(3))) uint16_t* lds_u16_ptr;
+    const uint32_t tlo = *(lds_u16_ptr)(size_t)(lut_bytes + (off & 0xffffu));
+    const uint32_t thi = *(lds_u16_ptr)(size_t)(lut_bytes + (off >> 16));
+    const uint32_t tv = tlo | (thi << 16);
+    // small result: RN(x / 2), exact arithmetic in fp32 (also for bf16 subnormals)
+    const uint32_t half = pack_bf16x2(__uint_as_float(pk << 16) * 0.5f, __uint_as_float(pk & 0xffff0000u) * 0.5f);
+    return bit_select(smallm, half, bit_select(bigm, bigv, tv));
+}
+
 // ---------------------------------------------------------------- wave reductions (DPP)
 // dpp_ctrl encodings (GCN/CDNA DPP): quad_perm, row_half_mirror, row_mirror.
 constexpr int kDppXor1 = 0xb1;        // quad_perm [1,0,3,2]

@@ -141,29 +141,15 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
 }
 
 // ---------------------------------------------------------------------------------
-// bf16 generator for the common shapes: tiles of 256 experts, one workgroup of 4 waves
-// per CU, 64 experts (two blocks of 32) per wave.  The hidden activations never leave
-// registers: 64 experts x DH bf16 is 256 registers per lane, held in AGPRs, which the
-// MFMAs read directly.  Every W2 fragment read from LDS feeds two MFMAs (one per
-// expert block), which halves the LDS traffic per flop against 32 experts per wave.
-//
-// GEMM1 is computed transposed, hid^T = W1 . Z^T (A = W1 rows, B = gathered latent
-// rows).  Lane l reads W1 row pi(l % 32) of each 32-row block, pi swapping bits 2 and
-// 3 of the row index, so that accumulator elements 8p..8p+7 of lane half h hold the
-// eight consecutive hidden values 16p + 8h .. 16p + 8h + 7 of expert l % 32.  After
-// erf-GELU and bf16 rounding they are exactly the k-slots of GEMM2's operand for
-// k-step s = 2t + p.  GEMM2 is also transposed, uv^T = W2 . hid^T, over chunks of 64
-// output columns: the chunk's 64 rows of W2 are copied global -> LDS (double
-// buffered) and each lane owns, per expert block, one expert and eight groups of
-// four consecutive output columns of the chunk.  Results go through a per-wave LDS
-// staging area and are stored one chunk later as whole 128-byte lines.
+// bf16 generator for the common shapes (d_latent 128, d_hidden 256 or 512), two kernels:
+// hidden_bf16_kernel writes h (GEMM1 + GELU, VALU heavy, high occupancy) and
+// expand_bf16_kernel reads it back into registers for v = h W_v^T (MFMA bound, one
+// wave per SIMD holding 64 experts' hidden rows).
 // ---------------------------------------------------------------------------------
 constexpr int kG2Waves = 4;
 constexpr int kG2MB = 2;                          // expert blocks of 32 per wave
 constexpr int kG2Cols = 64;                       // output columns per staged W2 chunk
 constexpr int kG2Rows = kG2Waves * kG2MB * 32;    // experts per tile
-
-__device__ __forceinline__ float round_bf16_hw(float x) { return __uint_as_float(pack_bf16x2(x, 0.0f) << 16); }
 
 __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
     uint4 r;
@@ -197,14 +183,97 @@ __device__ __forceinline__ uint32_t lds_addr(P* p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) P*)p);
 }
 
+// Hidden rows, bf16: h = RN(gelu(RN(z W1^T))) for the unique experts, a workgroup of
+// 16 waves per CU with W1 resident in LDS (loaded once) and 32 experts per wave and
+// pass.  GEMM1 is computed transposed, hid^T = W1 . Z^T (A = W1 rows, B = gathered
+// latent rows).  Lane l reads W1 row pi(l % 32) of each 32-row block, pi swapping bits
+// 2 and 3 of the row index, so that accumulator elements 8p..8p+7 of lane half h hold
+// the eight consecutive hidden values 16p + 8h .. 16p + 8h + 7 of expert l % 32: one
+// 16-byte store each.  GELU comes from a 6.5 KB table in LDS (the pre-activation is a
+// bf16 value); four waves per SIMD overlap one wave's GELU with the others' MFMAs,
+// latent gathers and stores.
+constexpr int kHWaves = 16;
+
+__device__ const uint16_t kGeluLut[kGeluLutSize] = {
+#include "gelu_bf16_lut.inc"
+};
+
 template <int DL, int DH>
-__global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void generate_bf16_kernel(
-    const uint16_t* __restrict__ latents, int64_t n_experts, const int32_t* __restrict__ uniq,
-    const int32_t* __restrict__ n_unique, int64_t max_unique, const uint16_t* __restrict__ w1,
-    const uint16_t* __restrict__ w2, int d2, uint16_t* __restrict__ hout, uint16_t* __restrict__ uv) {
-    constexpr int KS1 = DL / 16;                  // GEMM1 k-steps
-    constexpr int NB1 = DH / 32;                  // hidden blocks of 32
-    constexpr int KS2 = DH / 16;                  // GEMM2 k-steps
+__global__ __launch_bounds__(kHWaves * 64) void hidden_bf16_kernel(const uint16_t* __restrict__ latents,
+                                                                   int64_t n_experts, const int32_t* __restrict__ uniq,
+                                                                   const int32_t* __restrict__ n_unique,
+                                                                   const uint16_t* __restrict__ w1,
+                                                                   uint16_t* __restrict__ hout) {
+    constexpr int KS1 = DL / 16;  // GEMM1 k-steps
+    constexpr int NB1 = DH / 32;  // hidden blocks of 32
+    constexpr int kPitch = DL + 8;  // W1 row pitch in LDS (elements): rows 16 apart share banks
+    // the GELU table first (LDS byte 0 upward), then W1
+    __shared__ __align__(16) uint16_t smem[kGeluLutSize + DH * kPitch];
+    uint16_t* lut = smem;
+    uint16_t* w1s = smem + kGeluLutSize;
+    static_assert(kGeluLutSize % 8 == 0, "W1 rows stay 16-byte aligned");
+    const uint32_t lut_bytes = (uint32_t)(size_t)(__attribute__((address_space(3))) uint16_t*)smem;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int prow = (l32 & ~0xc) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);  // bits 2 <-> 3
+    const int U = *n_unique;
+    for (int e = tid; e < DH * DL / 8; e += kHWaves * 64) {
+        const int r = e / (DL / 8), g = e % (DL / 8);
+        *reinterpret_cast<uint4*>(&w1s[r * kPitch + 8 * g]) = *reinterpret_cast<const uint4*>(w1 + r * DL + 8 * g);
+    }
+    for (int e = tid; e < kGeluLutSize; e += kHWaves * 64) lut[e] = kGeluLut[e];
+    __syncthreads();
+    // blocks go round-robin over the workgroups first, so every CU gets the same count
+    // to within one
+    const int n_blocks = (U + 31) / 32;
+    for (int b = blockIdx.x + gridDim.x * wave; b < n_blocks; b += gridDim.x * kHWaves) {
+        const int u = b * 32 + l32;
+        const int64_t id = u < U ? (int64_t)uniq[u] : -1;
+        const bool ok = id >= 0 && id < n_experts;
+        const uint16_t* zr = latents + (ok ? id : 0) * DL + 8 * h;
+        bf16x8_t zf[KS1];
+#pragma unroll
+        for (int ks = 0; ks < KS1; ++ks)
+            zf[ks] = ok ? __builtin_bit_cast(bf16x8_t, __builtin_nontemporal_load(
+                                                           reinterpret_cast<const u32x4_t*>(zr + ks * 16)))
+                        : bf16x8_t{};
+        uint16_t* hr = hout + (int64_t)u * DH + 8 * h;
+#pragma unroll 2
+        for (int t = 0; t < NB1; ++t) {
+            f32x16_t acc = f32x16_zero();
+#pragma unroll
+            for (int ks = 0; ks < KS1; ++ks) {
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&w1s[(t * 32 + prow) * kPitch + ks * 16 + 8 * h]);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, zf[ks], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                uint32_t g[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)  // bf16-round two pre-activations, then the table
+                    g[j] = gelu_bf16x2_lut(pack_bf16x2(acc[8 * p + 2 * j], acc[8 * p + 2 * j + 1]), lut_bytes);
+                if (u < U) *reinterpret_cast<uint4*>(hr + 32 * t + 16 * p) = make_uint4(g[0], g[1], g[2], g[3]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// v rows, bf16: v = RN(h W_v^T) over tiles of 256 experts, one workgroup of 4 waves per
+// CU, 64 experts (two blocks of 32) per wave.  The wave's hidden rows (64 x DH bf16,
+// 256 registers per lane) are loaded into AGPRs, which the MFMAs read directly; every
+// W2 fragment read from LDS feeds two MFMAs (one per expert block).  The product is
+// computed transposed, v^T = W_v . h^T, over chunks of 64 output columns: the chunk's
+// 64 rows of W_v are copied global -> LDS (double buffered) and each lane owns, per
+// expert block, one expert and eight groups of four consecutive output columns of the
+// chunk.  Results go through a per-wave LDS staging area and are stored one chunk
+// later as whole 128-byte lines.
+// ---------------------------------------------------------------------------------
+template <int DH>
+__global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void expand_bf16_kernel(
+    const int32_t* __restrict__ n_unique, int64_t max_unique, const uint16_t* __restrict__ hin,
+    const uint16_t* __restrict__ w2, int d2, uint16_t* __restrict__ uv) {
+    constexpr int KS2 = DH / 16;                  // k-steps
     constexpr int GPR = DH / 8;                   // 16-byte groups per W2 row
     constexpr int kCopies = GPR * kG2Cols / 64;   // 64-lane copy instructions per chunk
     static_assert(GPR % 8 == 0 && kCopies % kG2Waves == 0 && KS2 % 4 == 0, "chunk staging shape");
@@ -216,7 +285,6 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
-    const int prow = (l32 & ~0xc) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);  // bits 2 <-> 3
     const int U = *n_unique;
     const int n_tiles = (U + kG2Rows - 1) / kG2Rows;
     const int n_chunks = d2 / kG2Cols;
@@ -238,7 +306,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
 
     // Work units: tiles that fill whole rounds of the grid are done whole; the
     // remaining rem tiles are split by column range into parts so that the last round
-    // spreads over the grid (each part recomputes the tile's GEMM1 and GELU).
+    // spreads over the grid (each part loads the tile's hidden rows).
     const int G = gridDim.x;
     const int n_full = n_tiles - n_tiles % G;
     const int rem = n_tiles - n_full;
@@ -246,6 +314,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
     parts = parts < 1 ? 1 : (parts > n_chunks ? n_chunks : parts);
     const int cpp = (n_chunks + parts - 1) / parts;  // chunks per part
     const int n_units = n_full + rem * parts;
+    constexpr int kOOB = 0x7fff0000;  // a byte offset past any tile's rows
 
     for (int w = blockIdx.x; w < n_units; w += G) {
         int tile = w, c_begin = 0, c_end = n_chunks;
@@ -255,14 +324,6 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
             c_end = c_begin + cpp < n_chunks ? c_begin + cpp : n_chunks;
             if (c_begin >= c_end) continue;
         }
-        const int u_wave = tile * kG2Rows + wave * kG2MB * 32;  // first expert of this wave
-        // W1 is the same for every tile; an opaque copy of its pointer keeps the compiler
-        // from hoisting all its loads out of the tile loop.
-        const uint16_t* w1o = w1;
-        asm volatile("" : "+s"(w1o));
-        const __attribute__((address_space(1))) uint16_t* w1t =
-            (const __attribute__((address_space(1))) uint16_t*)w1o;
-
         // copy instruction it of chunk c into buffer buf
         auto copy = [&](int c, int buf, int it) {
             const int soff = ((c * kG2Cols + 32 * (it & 1)) * DH + 64 * (it >> 1)) * 2;
@@ -271,99 +332,61 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
         for (int it = 0; it < kCopies / kG2Waves; ++it) copy(c_begin, c_begin & 1, it);
 
-        // The hidden rows are stored by the unit that starts at column 0, through a
-        // buffer resource over this tile's rows below max_unique (rows past it are
-        // dropped by the range check; a unit that does not store aims past every row).
-        constexpr int kOOB = 0x7fff0000;  // a byte offset past any tile's rows
+        // the wave's hidden rows, k-slot s of expert block mb = h[u][16 s + 8 h ..] with
+        // u = 64 wave + 32 mb + l32 (rows at or past U read as zero)
         const int64_t row0 = (int64_t)tile * kG2Rows;
+        const int64_t live = U - row0;
+        const int h_rows = live < kG2Rows ? (int)(live > 0 ? live : 0) : kG2Rows;
+        const __amdgpu_buffer_rsrc_t hrd = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(hin) + row0 * DH, (short)0, h_rows * DH * (int)sizeof(uint16_t), 0x00020000);
+        bf16x8_t hf[kG2MB][KS2];
+#pragma unroll
+        for (int mb = 0; mb < kG2MB; ++mb)
+#pragma unroll
+            for (int s = 0; s < KS2; ++s)
+                hf[mb][s] = __builtin_bit_cast(
+                    bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                  hrd, ((wave * kG2MB * 32 + mb * 32 + l32) * DH + 16 * s + 8 * h) * 2, 0, 0));
         const int64_t rows_left = max_unique - row0;
         const int tile_rows = rows_left < kG2Rows ? (int)(rows_left > 0 ? rows_left : 0) : kG2Rows;
-        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
-            hout + row0 * DH, (short)0, tile_rows * DH * (int)sizeof(uint16_t), 0x00020000);
-        const int h_voff = c_begin == 0 ? ((wave * kG2MB * 32 + l32) * DH + 8 * h) * 2 : kOOB;
-
-        // gathered latent rows of this lane's two experts (GEMM1 B operands)
-        bf16x8_t zf[kG2MB][KS1];
-#pragma unroll
-        for (int mb = 0; mb < kG2MB; ++mb) {
-            const int u = u_wave + mb * 32 + l32;
-            const int64_t id = u < U ? (int64_t)uniq[u] : -1;
-            const bool ok = id >= 0 && id < n_experts;
-            const uint16_t* zr = latents + (ok ? id : 0) * DL + 8 * h;
-#pragma unroll
-            for (int ks = 0; ks < KS1; ++ks)
-                zf[mb][ks] = ok ? __builtin_bit_cast(bf16x8_t, __builtin_nontemporal_load(
-                                                                   reinterpret_cast<const u32x4_t*>(zr + ks * 16)))
-                                : bf16x8_t{};
-        }
-
-        // GEMM1^T + GELU -> hidden k-slots hf[mb][s].  An MFMA reads its operands when it
-        // issues, so the W1 fragments of block t + 1 are loaded into the same registers
-        // right after block t's MFMAs and arrive while block t's GELU runs.
-        bf16x8_t hf[kG2MB][KS2];
-        bf16x8_t wa[KS1];
-#pragma unroll
-        for (int ks = 0; ks < KS1; ++ks)
-            wa[ks] = *reinterpret_cast<const __attribute__((address_space(1))) bf16x8_t*>(w1t + prow * DL + ks * 16 + 8 * h);
-#pragma clang loop unroll(full)
-        for (int t = 0; t < NB1; ++t) {
-            f32x16_t acc[kG2MB];
-#pragma unroll
-            for (int mb = 0; mb < kG2MB; ++mb) acc[mb] = f32x16_zero();
-#pragma unroll
-            for (int ks = 0; ks < KS1; ++ks)
-#pragma unroll
-                for (int mb = 0; mb < kG2MB; ++mb)
-                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[ks], zf[mb][ks], acc[mb], 0, 0, 0);
-            if (t + 1 < NB1) {
-#pragma unroll
-                for (int ks = 0; ks < KS1; ++ks)
-                    wa[ks] = *reinterpret_cast<const __attribute__((address_space(1))) bf16x8_t*>(
-                        w1t + ((t + 1) * 32 + prow) * DL + ks * 16 + 8 * h);
-            }
-#pragma unroll
-            for (int mb = 0; mb < kG2MB; ++mb)
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    float v[8];
-#pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        // bf16-round two pre-activations with one conversion
-                        const uint32_t pk = pack_bf16x2(acc[mb][8 * p + j], acc[mb][8 * p + j + 1]);
-                        v[j] = gelu_bf16_fit(__uint_as_float(pk << 16));
-                        v[j + 1] = gelu_bf16_fit(__uint_as_float(pk & 0xffff0000u));
-                    }
-                    hf[mb][2 * t + p] = pack_bf16x8(v);
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, hf[mb][2 * t + p]), hr,
-                                                           h_voff + (32 * mb * DH + 16 * (2 * t + p)) * 2, 0, 0);
-                    // park the k-slot in AGPRs (the MFMAs read it from there), which also
-                    // keeps the compiler from sinking the GELUs into the chunk loop
-                    asm volatile("" : "+a"(hf[mb][2 * t + p]));
-                }
-            __builtin_amdgcn_sched_barrier(0);
-        }
 
         // GEMM2^T.  Each chunk's results go to the wave's staging rows; they are read
-        // back at the start of the next chunk and stored between its first MFMAs as
-        // whole 128-byte lines with non-temporal stores (the uv stream must not evict W2
-        // from L2).  The stores go through a buffer resource covering this tile's rows
-        // below max_unique, so rows past the allocation are dropped by the hardware and
-        // no store needs a branch; rows in [U, max_unique) receive the (zero) rows of
-        // absent experts.
+        // back at the start of the next chunk and stored between its MFMAs as whole
+        // 128-byte lines with non-temporal stores (the v stream must not evict W2 from
+        // L2).  The stores go through a buffer resource covering this tile's rows below
+        // max_unique, so rows past the allocation are dropped by the hardware and no
+        // store needs a branch; rows in [U, max_unique) receive the rows of absent
+        // experts.
+        //
+        // Within a chunk the copies of the next chunk (k-steps 0 .. kCS-1) are issued
+        // before its eight stores, so the next chunk only waits for vmcnt(8): its copies
+        // have landed, the stores stay in flight across the boundary.  The first chunk
+        // waits the same way: the 64 hidden-row loads follow its copies (and the MFMAs
+        // wait for each of those loads themselves).
         const __amdgpu_buffer_rsrc_t uvr = __builtin_amdgcn_make_buffer_rsrc(
             uv + row0 * d2, (short)0, tile_rows * d2 * (int)sizeof(uint16_t), 0x00020000);
         // lane's store k covers row 8 k + lane / 8 of the wave, 16-byte group lane % 8
         const int st_voff = ((wave * kG2MB * 32 + (lane >> 3)) * d2 + 8 * (lane & 7)) * 2;
         u32x4_t* my = stg[wave];
         u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
+        // B fragments run LA k-steps ahead of the MFMAs in a ring of LA + 1 slots.
+        constexpr int LA = 4;
+        constexpr int kCopiesW = kCopies / kG2Waves;  // copies per wave, 4 per k-step
+        constexpr int kCS = kCopiesW / 4;             // k-steps that issue copies
+        constexpr int kNSt = kG2MB * 4;               // v-row stores per chunk
+        static_assert(kCopiesW % 4 == 0 && kCS + kNSt <= KS2 && kG2MB * KS2 >= kNSt, "interleave shape");
+        // s_waitcnt vmcnt(8) (gfx9 immediate: vmcnt [3:0] and [15:14], expcnt [6:4],
+        // lgkmcnt [11:8]; expcnt 7 and lgkmcnt 15 do not wait)
+        constexpr int kWaitVm8 = 0x0f78;
+        static_assert(kNSt == 8, "kWaitVm8 assumes eight stores after the copies");
         int pend_c = -1;
         for (int c = c_begin; c < c_end; ++c) {
-            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_s_waitcnt(kWaitVm8);
             __syncthreads();
             // the previous chunk's staged rows
-            u32x4_t outv[kG2MB * 4];
+            u32x4_t outv[kNSt];
 #pragma unroll
-            for (int k = 0; k < kG2MB * 4; ++k) {
+            for (int k = 0; k < kNSt; ++k) {
                 const int r = 8 * k + (lane >> 3);
                 outv[k] = my[r * 8 + ((lane & 7) ^ (r & 7))];
             }
@@ -372,10 +395,6 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
             auto bfrag = [&](int s, int cb) {
                 return __builtin_bit_cast(bf16x8_t, cur[bq_off[s & 3] + (s >> 2) * 512 + cb * 256]);
             };
-            // B fragments run LA k-steps ahead of the MFMAs in a ring of LA + 1 slots.
-            constexpr int LA = 4;
-            constexpr int kCopiesW = kCopies / kG2Waves;  // copies per wave, 4 per k-step
-            static_assert(kCopiesW % 4 == 0 && kCopiesW / 4 <= KS2 && kG2MB * 4 <= KS2, "interleave shape");
             bf16x8_t bfr[LA + 1][2];
             f32x16_t acc[kG2MB][2];
 #pragma unroll
@@ -403,23 +422,24 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
                                                                              acc[mb][cb], 0, 0, 0);
                 // copies of the next chunk, four per k-step (never past the unit's last
                 // chunk: the buffer range check does not cover the scalar chunk offset)
-                if (s < kCopiesW / 4 && c + 1 < c_end) {
+                if (s < kCS && c + 1 < c_end) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) copy(c + 1, (c + 1) & 1, 4 * s + j);
                 }
                 // the previous chunk's rows, one store per k-step
-                if (s < kG2MB * 4)
-                    __builtin_amdgcn_raw_buffer_store_b128(outv[s], uvr, st_base + s * 8 * d2 * 2, 0, 2);
+                if (s >= kCS && s < kCS + kNSt)
+                    __builtin_amdgcn_raw_buffer_store_b128(outv[s - kCS], uvr, st_base + (s - kCS) * 8 * d2 * 2, 0,
+                                                           2);
             }
             // Pin that interleave in the schedule: the staged-row reads and the first LA
             // fragment reads, then per k-step its four MFMAs, the two fragment reads of
             // k-step s + LA and the store (the copies keep their place in program order).
-            __builtin_amdgcn_sched_group_barrier(0x100, kG2MB * 4 + 2 * LA, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, kNSt + 2 * LA, 0);
 #pragma unroll
             for (int s = 0; s < KS2; ++s) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 2 * kG2MB, 0);
                 if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                if (s < kG2MB * 4) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
+                if (s >= kCS && s < kCS + kNSt) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
             }
             // acc[mb][cb][i]: column c*64 + 32 cb + 8 (i/4) + 4h + i%4 of expert
             // u_wave + 32 mb + l32, i.e. 8-byte half h of 16-byte group 4 cb + i/4 of the
@@ -439,10 +459,10 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
             }
             pend_c = c;
         }
-        // the last chunk's rows
-        __builtin_amdgcn_s_waitcnt(0);
+        // the last chunk's rows (the staging writes above are this wave's own LDS
+        // operations, which complete in order)
 #pragma unroll
-        for (int k = 0; k < kG2MB * 4; ++k) {
+        for (int k = 0; k < kNSt; ++k) {
             const int r = 8 * k + (lane >> 3);
             __builtin_amdgcn_raw_buffer_store_b128(my[r * 8 + ((lane & 7) ^ (r & 7))], uvr,
                                                    st_voff + kG2Cols * 2 * pend_c + k * 8 * d2 * 2, 0, 2);
@@ -456,12 +476,15 @@ static bool launch_generate_bf16(const void* latents, int64_t n_experts, const i
                                  int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* hout,
                                  void* uv, int num_cus, hipStream_t stream) {
     if (dl != DL || dh != DH || d2 % kG2Cols) return false;
+    const int64_t blocks = (max_unique + 32 * kHWaves - 1) / (32 * kHWaves);
+    const unsigned g1 = (unsigned)(blocks < num_cus ? (blocks > 0 ? blocks : 1) : num_cus);
+    hipLaunchKernelGGL((hidden_bf16_kernel<DL, DH>), dim3(g1), dim3(kHWaves * 64), 0, stream,
+                       (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (uint16_t*)hout);
     const int64_t tiles = (max_unique + kG2Rows - 1) / kG2Rows;
     const int64_t cap = num_cus;  // one workgroup per CU
     const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
-    hipLaunchKernelGGL((generate_bf16_kernel<DL, DH>), dim3(grid), dim3(kG2Waves * 64), 0, stream,
-                       (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
-                       (const uint16_t*)w2, d2, (uint16_t*)hout, (uint16_t*)uv);
+    hipLaunchKernelGGL((expand_bf16_kernel<DH>), dim3(grid), dim3(kG2Waves * 64), 0, stream, n_unique, max_unique,
+                       (const uint16_t*)hout, (const uint16_t*)w2, d2, (uint16_t*)uv);
     return true;
 }
 

@@ -128,6 +128,26 @@ def test_generate_matches_oracle(name, signal):
     _check_rows(v[:U], v_ref, sh.dtype)
 
 
+def test_generate_gelu_every_bf16_input():
+    """Every finite bf16 value as a pre-activation, through the generator: expert u has the
+    one-hot latent e_(u % 128) and W1[j, k] is value 512 k + j, so pre = W1[j, u] exactly
+    and h[u, j] must be the oracle's RN(GELU(value)) bit for bit."""
+    dl, dh, d, U = 128, 512, 64, 128
+    vals = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = (vals & 0x7F80) != 0x7F80
+    vals = np.where(finite, vals, 0).astype(np.uint16)
+    w1 = np.ascontiguousarray(vals.reshape(dl, dh).T)              # W1[j, k] = vals[512 k + j]
+    lat = np.zeros((U, dl), np.uint16)
+    lat[np.arange(U), np.arange(U) % dl] = O.f32_to_bf16_bits(np.ones(1, np.float32))[0]
+    w2 = O.f32_to_bf16_bits(np.full((2 * d, dh), 1e-3, np.float32))
+    uniq = np.arange(U, dtype=np.int32)
+    h, _ = _generate(lat, uniq, w1, w2, U, "bf16")
+    ref, _ = O.generate(lat, uniq, w1, w2, "bf16")
+    got_bits = O.f32_to_bf16_bits(h[:U].astype(np.float32))
+    ref_bits = O.f32_to_bf16_bits(ref.astype(np.float32))
+    assert np.array_equal(got_bits, ref_bits), int(np.sum(got_bits != ref_bits))
+
+
 @pytest.mark.parametrize("name,signal", [("tiny", False), ("tiny", True), ("tiny_fp32", True), ("cfg1", False),
                                          ("cfg3", True)])
 def test_apply_matches_oracle(name, signal):
