@@ -3,15 +3,17 @@
 // (No reference code: the reference loops over pairs in token order, model.py:306-334;
 // the paper's Algorithm 1 reorders by expert, paper/ETHOS.pdf p.10.)
 //
-// Sort: 8-bit digits, ceil(bits / 8) passes over keys < n_experts.  Each pass is
-//   upsweep   per-tile digit histogram            -> hist[digit][tile]
-//   scan      exclusive scan of hist (digit-major) -> global offsets
-//   downsweep stable scatter: rank inside a tile by wave-level multisplit
-// A tile is 4096 keys = 4 waves x 16 chunks of 64 consecutive keys.  Inside a wave,
-// the lanes holding the same digit are found with eight ballots ("peer mask"); the
-// rank of a key is (keys of that digit in earlier waves) + (in earlier chunks of its
-// wave) + (peers in lower lanes), which keeps the order of equal keys.  No global
-// atomics; LDS counters are updated by one leader lane per digit.
+// Sort: 9-bit digits, ceil(bits / 9) passes over keys < n_experts (two for 262,144
+// experts).  Each pass is
+//   upsweep     per-tile digit histogram                 -> hist[digit][tile]
+//   scan_tiles  per digit, exclusive scan over the tiles  -> hist[digit][tile], total[digit]
+//   downsweep   stable scatter: digit base (scan of the totals, in LDS) + tile prefix +
+//               rank inside the tile by wave-level multisplit
+// A tile is 1024 keys = 4 waves x 4 chunks of 64 consecutive keys.  Inside a wave, the
+// lanes holding the same digit are found with nine ballots ("peer mask"); the rank of a
+// key is (keys of that digit in earlier waves) + (in earlier chunks of its wave) + (peers
+// in lower lanes), which keeps the order of equal keys.  No global atomics; LDS counters
+// are updated by one leader lane per digit.
 //
 // Segment: flags[i] = (i == 0 || key[i] != key[i-1]); slot = inclusive scan - 1.
 // Outputs: perm (pair ids by expert), uniq (expert id per slot), seg_off (U + 1),
@@ -21,15 +23,16 @@
 
 namespace ethos {
 
-constexpr int kSortChunks = 16;                 // chunks of 64 keys per wave
-constexpr int kSortTile = 4 * kSortChunks * 64; // 4096 keys
-constexpr int kRadix = 256;
+constexpr int kSortChunks = 4;                  // chunks of 64 keys per wave
+constexpr int kSortTile = 4 * kSortChunks * 64; // 1024 keys
+constexpr int kRadixBits = 9;
+constexpr int kRadix = 1 << kRadixBits;
 constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ uint64_t peer_mask(uint32_t digit, uint64_t valid) {
     uint64_t peers = valid;
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < kRadixBits; ++b) {
         const uint32_t bit = (digit >> b) & 1u;
         const uint64_t bal = __ballot(bit);
         peers &= bit ? bal : ~bal;
@@ -46,6 +49,7 @@ __global__ __launch_bounds__(256) void sort_upsweep(const uint32_t* __restrict__
     for (int i = tid; i < 4 * kRadix; i += 256) cnt[i / kRadix][i % kRadix] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortChunks * 64);
+#pragma unroll
     for (int c = 0; c < kSortChunks; ++c) {
         const int64_t idx = base + c * 64 + lane;
         const bool v = idx < n;
@@ -55,7 +59,43 @@ __global__ __launch_bounds__(256) void sort_upsweep(const uint32_t* __restrict__
         if (v && lane == 63 - __clzll((long long)peers)) cnt[wave][dg] += (uint32_t)__popcll(peers);
     }
     __syncthreads();
-    hist[(int64_t)tid * n_tiles + blockIdx.x] = cnt[0][tid] + cnt[1][tid] + cnt[2][tid] + cnt[3][tid];
+    for (int d = tid; d < kRadix; d += 256)
+        hist[(int64_t)d * n_tiles + blockIdx.x] = cnt[0][d] + cnt[1][d] + cnt[2][d] + cnt[3][d];
+}
+
+// One wave per digit: exclusive scan of hist[digit][0 .. n_tiles) in place, the digit's
+// total to total[digit].
+__global__ __launch_bounds__(256) void sort_scan_tiles(uint32_t* __restrict__ hist, int n_tiles,
+                                                       uint32_t* __restrict__ total) {
+    const int lane = threadIdx.x & 63;
+    const int d = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (d >= kRadix) return;
+    uint32_t* row = hist + (int64_t)d * n_tiles;
+    uint32_t carry = 0;
+    for (int t0 = 0; t0 < n_tiles; t0 += 64 * 8) {
+        uint32_t v[8], s = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int t = t0 + lane * 8 + j;
+            v[j] = t < n_tiles ? row[t] : 0u;
+            s += v[j];
+        }
+        uint32_t inc = s;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t u = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += u;
+        }
+        uint32_t run = carry + inc - s;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int t = t0 + lane * 8 + j;
+            if (t < n_tiles) row[t] = run;
+            run += v[j];
+        }
+        carry += __shfl(inc, 63, 64);
+    }
+    if (lane == 0) total[d] = carry;
 }
 
 template <bool kFirst>
@@ -63,11 +103,28 @@ __global__ __launch_bounds__(256) void sort_downsweep(const uint32_t* __restrict
                                                       const uint32_t* __restrict__ vals_in,
                                                       uint32_t* __restrict__ keys_out,
                                                       uint32_t* __restrict__ vals_out, int64_t n, int shift,
-                                                      const uint32_t* __restrict__ hist, int n_tiles) {
+                                                      const uint32_t* __restrict__ hist,
+                                                      const uint32_t* __restrict__ total, int n_tiles) {
     __shared__ uint32_t cnt[4][kRadix];
+    __shared__ uint32_t wsum[4];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     for (int i = tid; i < 4 * kRadix; i += 256) cnt[i / kRadix][i % kRadix] = 0;
+    // digit bases: exclusive scan of the digit totals (two digits per thread)
+    const uint32_t ta = total[2 * tid], tb = total[2 * tid + 1];
+    const uint32_t s = ta + tb;
+    uint32_t inc = s;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t u = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += u;
+    }
+    if (lane == 63) wsum[wave] = inc;
     __syncthreads();
+    uint32_t wpre = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) wpre += w < wave ? wsum[w] : 0u;
+    const uint32_t base_a = wpre + inc - s, base_b = base_a + ta;
+
     const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortChunks * 64);
     uint32_t key[kSortChunks], val[kSortChunks], rank[kSortChunks];
 #pragma unroll
@@ -87,12 +144,14 @@ __global__ __launch_bounds__(256) void sort_downsweep(const uint32_t* __restrict
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    {
-        uint32_t run = hist[(int64_t)tid * n_tiles + blockIdx.x];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int d = 2 * tid + j;
+        uint32_t run = (j ? base_b : base_a) + hist[(int64_t)d * n_tiles + blockIdx.x];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const uint32_t c = cnt[w][tid];
-            cnt[w][tid] = run;
+            const uint32_t c = cnt[w][d];
+            cnt[w][d] = run;
             run += c;
         }
     }
@@ -178,14 +237,16 @@ __global__ __launch_bounds__(kScanThreads) void scan_exclusive(uint32_t* __restr
     if (tid == 0 && total) *total = (int32_t)carry;
 }
 
-// Head count per tile (items thread-contiguous: thread t owns 16 consecutive keys).
+// Head count per tile (items thread-contiguous: thread t owns 4 consecutive keys).
+constexpr int kSegPer = kSortTile / 256;  // keys per thread in the segment kernels
+
 __global__ __launch_bounds__(256) void seg_count(const uint32_t* __restrict__ keys, int64_t n,
                                                  uint32_t* __restrict__ tile_cnt) {
     __shared__ uint32_t red[256];
     const int tid = threadIdx.x;
-    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * 16;
+    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * kSegPer;
     uint32_t c = 0;
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kSegPer; ++i) {
         const int64_t idx = lo + i;
         if (idx < n && (idx == 0 || keys[idx] != keys[idx - 1])) ++c;
     }
@@ -205,9 +266,9 @@ __global__ __launch_bounds__(256) void seg_write(const uint32_t* __restrict__ ke
                                                  int32_t* __restrict__ n_unique, int32_t max_unique) {
     __shared__ uint32_t part[256];
     const int tid = threadIdx.x;
-    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * 16;
+    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * kSegPer;
     uint32_t c = 0;
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kSegPer; ++i) {
         const int64_t idx = lo + i;
         if (idx < n && (idx == 0 || keys[idx] != keys[idx - 1])) ++c;
     }
@@ -221,7 +282,7 @@ __global__ __launch_bounds__(256) void seg_write(const uint32_t* __restrict__ ke
     }
     // slot of the item just before this thread's first head
     int32_t slot = (int32_t)(tile_base[blockIdx.x] + part[tid] - c) - 1;
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kSegPer; ++i) {
         const int64_t idx = lo + i;
         if (idx >= n) break;
         const uint32_t k = keys[idx];
@@ -263,7 +324,7 @@ static int key_bits(int64_t n_experts) {
 
 size_t sort_workspace_bytes(int64_t n) {
     const int64_t tiles = (n + kSortTile - 1) / kSortTile;
-    const size_t words = (size_t)4 * n + (size_t)kRadix * tiles + (size_t)tiles + 64;
+    const size_t words = (size_t)4 * n + (size_t)kRadix * tiles + kRadix + (size_t)tiles + 64;
     return words * sizeof(uint32_t);
 }
 
@@ -275,25 +336,25 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
     uint32_t* kbuf[2] = {w, w + n};
     uint32_t* vbuf[2] = {w + 2 * n, w + 3 * n};
     uint32_t* hist = w + 4 * n;
-    uint32_t* tcnt = hist + (size_t)kRadix * n_tiles;
+    uint32_t* total = hist + (size_t)kRadix * n_tiles;
+    uint32_t* tcnt = total + kRadix;
     const int bits = key_bits(n_experts);
-    const int passes = bits <= 8 ? 1 : (bits + 7) / 8;
+    const int passes = bits <= kRadixBits ? 1 : (bits + kRadixBits - 1) / kRadixBits;
     hipError_t err;
     for (int p = 0; p < passes; ++p) {
         const uint32_t* kin = p == 0 ? reinterpret_cast<const uint32_t*>(ids) : kbuf[(p - 1) & 1];
         const uint32_t* vin = p == 0 ? nullptr : vbuf[(p - 1) & 1];
         uint32_t* kout = kbuf[p & 1];
         uint32_t* vout = p == passes - 1 ? reinterpret_cast<uint32_t*>(perm) : vbuf[p & 1];
-        const int shift = 8 * p;
+        const int shift = kRadixBits * p;
         hipLaunchKernelGGL(sort_upsweep, dim3(n_tiles), dim3(256), 0, stream, kin, n, shift, hist, n_tiles);
-        hipLaunchKernelGGL(scan_exclusive, dim3(1), dim3(kScanThreads), 0, stream, hist, (int64_t)kRadix * n_tiles,
-                           (int32_t*)nullptr);
+        hipLaunchKernelGGL(sort_scan_tiles, dim3(kRadix / 4), dim3(256), 0, stream, hist, n_tiles, total);
         if (p == 0)
             hipLaunchKernelGGL(sort_downsweep<true>, dim3(n_tiles), dim3(256), 0, stream, kin, vin, kout, vout, n,
-                               shift, hist, n_tiles);
+                               shift, (const uint32_t*)hist, (const uint32_t*)total, n_tiles);
         else
             hipLaunchKernelGGL(sort_downsweep<false>, dim3(n_tiles), dim3(256), 0, stream, kin, vin, kout, vout, n,
-                               shift, hist, n_tiles);
+                               shift, (const uint32_t*)hist, (const uint32_t*)total, n_tiles);
         if ((err = hipGetLastError()) != hipSuccess) return (int)err;
     }
     const uint32_t* sorted = kbuf[(passes - 1) & 1];
