@@ -32,10 +32,13 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-source extra flags.  generate.hip: MFMA results go to VGPRs (the VGPR form of
-# v_mfma), leaving the AGPRs to the generator's register-resident hidden activations.
+# Per-source extra flags: MFMA results go to VGPRs (the VGPR form of v_mfma).  In
+# generate.hip that leaves the AGPRs to the register-resident hidden activations; in
+# qproj.hip every accumulator is read by VALU code, which would otherwise copy it out of
+# the AGPRs first.
 EXTRA_FLAGS = {
     "generate.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "qproj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

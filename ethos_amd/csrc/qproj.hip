@@ -144,20 +144,40 @@ __global__ __launch_bounds__(256) void qproj_mfma_kernel(const uint16_t* __restr
     const int t0 = blockIdx.y * kQmRows, c0 = blockIdx.x * kQmCols;
     if (tid == 0) n_local = 0;
 
-    auto stage = [&](int k0) {
-        // x [64 x 64] and w [128 x 64] in 16-byte pieces; rows past the end are zero
-        for (int e = tid; e < (kQmRows + kQmCols) * (kQmKC / 8); e += 256) {
+    // x [64 x 64] and w [128 x 64] chunks in 16-byte pieces (rows past the end are zero):
+    // piece e = tid + 256 j is row e / 8, k offset 8 (e % 8); rows < 64 are x, the rest w
+    constexpr int kPieces = (kQmRows + kQmCols) * (kQmKC / 8) / 256;
+    static_assert((kQmRows + kQmCols) * (kQmKC / 8) % 256 == 0 && kQmRows * (kQmKC / 8) % 256 == 0,
+                  "staging shape");
+    auto fetch = [&](int k0, uint4 (&v)[kPieces]) {
+#pragma unroll
+        for (int j = 0; j < kPieces; ++j) {
+            const int e = tid + 256 * j;
             const int r = e / (kQmKC / 8), kq = (e % (kQmKC / 8)) * 8;
-            uint4 v = make_uint4(0, 0, 0, 0);
+            v[j] = make_uint4(0, 0, 0, 0);
             if (r < kQmRows) {
-                if (t0 + r < n_tok) v = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * d + k0 + kq);
-                *reinterpret_cast<uint4*>(&xs[r * kQmPitch + kq]) = v;
+                if (t0 + r < n_tok) v[j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * d + k0 + kq);
             } else {
                 const int rc = r - kQmRows;
-                if (c0 + rc < ncols) v = *reinterpret_cast<const uint4*>(w + (int64_t)(c0 + rc) * d + k0 + kq);
-                *reinterpret_cast<uint4*>(&ws[rc * kQmPitch + kq]) = v;
+                if (c0 + rc < ncols) v[j] = *reinterpret_cast<const uint4*>(w + (int64_t)(c0 + rc) * d + k0 + kq);
             }
         }
+    };
+    auto put = [&](const uint4 (&v)[kPieces]) {
+#pragma unroll
+        for (int j = 0; j < kPieces; ++j) {
+            const int e = tid + 256 * j;
+            const int r = e / (kQmKC / 8), kq = (e % (kQmKC / 8)) * 8;
+            if (r < kQmRows)
+                *reinterpret_cast<uint4*>(&xs[r * kQmPitch + kq]) = v[j];
+            else
+                *reinterpret_cast<uint4*>(&ws[(r - kQmRows) * kQmPitch + kq]) = v[j];
+        }
+    };
+    auto stage = [&](int k0) {
+        uint4 v[kPieces];
+        fetch(k0, v);
+        put(v);
     };
 
     double acc64[2][16];
@@ -167,10 +187,14 @@ __global__ __launch_bounds__(256) void qproj_mfma_kernel(const uint16_t* __restr
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc64[cb][i] = 0.0;
 
+    // the next chunk is fetched into registers while this one is multiplied
+    uint4 nxt[kPieces];
+    fetch(0, nxt);
     for (int k0 = 0; k0 < d; k0 += kQmKC) {
         __syncthreads();
-        stage(k0);
+        put(nxt);
         __syncthreads();
+        if (k0 + kQmKC < d) fetch(k0 + kQmKC, nxt);
 #pragma unroll
         for (int kk = 0; kk < kQmKC; kk += 16) {
             const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&xs[(wr * 32 + l32) * kQmPitch + kk + 8 * h]);
@@ -233,40 +257,54 @@ __global__ __launch_bounds__(256) void qproj_mfma_kernel(const uint16_t* __restr
     }
     __syncthreads();
     const int nl = n_local < kQmLocal ? n_local : kQmLocal;
-    if (nl == 0) return;
 
-    // exact fp64 chains for the queued elements, re-streaming the same K tiles
-    constexpr int R = kQmLocal / 256;
-    double ex[R];
-    int er[R], ec[R];
+    // Exact fp64 chains for the queued elements, re-streaming the same K tiles: each
+    // thread runs two elements' chains side by side (each in index order, 16-byte LDS
+    // reads of eight terms), 512 elements per pass.
+    for (int g0 = 0; g0 < nl; g0 += 512) {
+        int er[2], ec[2];
+        bool ok[2];
+        double ex[2] = {0.0, 0.0};
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        ex[r] = 0.0;
-        const int j = tid + 256 * r;
-        const uint32_t v = j < nl ? local[j] : 0u;
-        er[r] = (int)(v >> 16);
-        ec[r] = (int)(v & 0xffffu);
-    }
-    for (int k0 = 0; k0 < d; k0 += kQmKC) {
-        __syncthreads();
-        stage(k0);
-        __syncthreads();
+        for (int r = 0; r < 2; ++r) {
+            const int j = g0 + 256 * r + tid;
+            ok[r] = j < nl;
+            const uint32_t v = ok[r] ? local[j] : 0u;
+            er[r] = (int)(v >> 16);
+            ec[r] = (int)(v & 0xffffu);
+        }
+        for (int k0 = 0; k0 < d; k0 += kQmKC) {
+            __syncthreads();
+            stage(k0);
+            __syncthreads();
+#pragma unroll 2
+            for (int kk = 0; kk < kQmKC; kk += 8) {
+                uint4 xa[2], wa[2];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (tid + 256 * r < nl) {
-                const uint16_t* xr = &xs[er[r] * kQmPitch];
-                const uint16_t* wrp = &ws[ec[r] * kQmPitch];
-                for (int kk = 0; kk < kQmKC; ++kk)
-                    ex[r] = fma((double)bf16_bits_to_f32(xr[kk]), (double)bf16_bits_to_f32(wrp[kk]), ex[r]);
+                for (int r = 0; r < 2; ++r) {
+                    xa[r] = *reinterpret_cast<const uint4*>(&xs[er[r] * kQmPitch + kk]);
+                    wa[r] = *reinterpret_cast<const uint4*>(&ws[ec[r] * kQmPitch + kk]);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                        for (int r = 0; r < 2; ++r) {
+                            const uint32_t xv = (&xa[r].x)[q], wv = (&wa[r].x)[q];
+                            const float xf = __uint_as_float(hf ? (xv & 0xffff0000u) : (xv << 16));
+                            const float wf = __uint_as_float(hf ? (wv & 0xffff0000u) : (wv << 16));
+                            ex[r] = fma((double)xf, (double)wf, ex[r]);
+                        }
             }
         }
-    }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (tid + 256 * r < nl) {
-            const int t = t0 + er[r], c = c0 + ec[r];
-            const float ql = Elem<uint16_t>::round64(ex[r] + (double)bf16_bits_to_f32(bias[c]));
-            q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
+        for (int r = 0; r < 2; ++r) {
+            if (ok[r]) {
+                const int t = t0 + er[r], c = c0 + ec[r];
+                const float ql = Elem<uint16_t>::round64(ex[r] + (double)bf16_bits_to_f32(bias[c]));
+                q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
+            }
         }
     }
 }
