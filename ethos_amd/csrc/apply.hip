@@ -92,45 +92,92 @@ constexpr int kTpC = 64;     // hidden columns per tile
 constexpr int kTpK = 64;     // reduction chunk staged in LDS
 constexpr int kTpPitch = kTpK + 8;
 
-// bf16: 32x32x16 MFMA with fp32 accumulation, rounded once.  Computed transposed
-// (xp^T = W_u^T x^T) so that each lane ends with four consecutive hidden columns of
-// one token: 8-byte stores.  W_u is staged transposed (hidden column major) so both
-// operands are read from LDS as 16-byte k-runs.
+// bf16: W_u^T (row n = hidden column, d contiguous values) is first written to the
+// workspace by a tiled transpose of net.2.weight's first d rows, so that both GEMM
+// operands are staged with 16-byte loads.
+__global__ __launch_bounds__(256) void transpose_wu_kernel(const uint16_t* __restrict__ w2, int d, int dh,
+                                                           uint16_t* __restrict__ wut) {
+    // a 64 x 64 tile: rows k0.. of w2 (columns n0..), read and written as 16-byte pieces
+    __shared__ uint16_t tile[64][64 + 2];
+    const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int e = tid + 256 * it, r = e >> 3, c8 = (e & 7) * 8;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (k0 + r < d && n0 + c8 < dh) v = *reinterpret_cast<const uint4*>(w2 + (int64_t)(k0 + r) * dh + n0 + c8);
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            tile[r][c8 + 2 * q] = (uint16_t)(u[q] & 0xffffu);
+            tile[r][c8 + 2 * q + 1] = (uint16_t)(u[q] >> 16);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int e = tid + 256 * it, n = e >> 3, k8 = (e & 7) * 8;  // output row n, columns k8..
+        uint32_t u[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            u[q] = (uint32_t)tile[k8 + 2 * q][n] | ((uint32_t)tile[k8 + 2 * q + 1][n] << 16);
+        if (n0 + n < dh && k0 + k8 < d)
+            *reinterpret_cast<uint4*>(wut + (int64_t)(n0 + n) * d + k0 + k8) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+}
+
+// xp = RN(x W_u) with 32x32x16 MFMAs, fp32 accumulation, rounded once.  Tiles of 64
+// tokens x 64 hidden columns, four waves of 32 x 32 (two accumulators for alternate
+// k-steps, added at the end), K in chunks of 64 staged in LDS with the next chunk
+// fetched into registers meanwhile.  Computed transposed (xp^T = W_u^T x^T) so that each
+// lane ends with four consecutive hidden columns of one token: 8-byte stores.
+constexpr int kTpCols = 64;  // hidden columns per workgroup tile (MFMA path)
 __global__ __launch_bounds__(256) void token_proj_bf16_kernel(const uint16_t* __restrict__ x,
-                                                              const uint16_t* __restrict__ wu, int n_tok, int d,
+                                                              const uint16_t* __restrict__ wut, int n_tok, int d,
                                                               int dh, uint16_t* __restrict__ xp) {
     __shared__ __align__(16) uint16_t xs[kTpT * kTpPitch];
-    __shared__ __align__(16) uint16_t wt[kTpC * kTpPitch];
+    __shared__ __align__(16) uint16_t wt[kTpCols * kTpPitch];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int wr = wave >> 1, wc = wave & 1;
-    const int c0 = blockIdx.x * kTpC;
+    const int c0 = blockIdx.x * kTpCols;
     const int t0 = blockIdx.y * kTpT;
-    f32x16_t acc = f32x16_zero();
+    // (64 + 128) rows x 64 values = 1536 16-byte pieces, six per thread
+    constexpr int kPieces = (kTpT + kTpCols) * (kTpK / 8) / 256;
+    auto fetch = [&](int k0, uint4 (&v)[kPieces]) {
+#pragma unroll
+        for (int j = 0; j < kPieces; ++j) {
+            const int e = tid + 256 * j;
+            const int r = e >> 3, q8 = (e & 7) * 8;
+            v[j] = make_uint4(0, 0, 0, 0);
+            if (r < kTpT) {
+                if (t0 + r < n_tok) v[j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * d + k0 + q8);
+            } else if (c0 + r - kTpT < dh) {
+                v[j] = *reinterpret_cast<const uint4*>(wut + (int64_t)(c0 + r - kTpT) * d + k0 + q8);
+            }
+        }
+    };
+    uint4 nxt[kPieces];
+    fetch(0, nxt);
+    f32x16_t acc[2] = {f32x16_zero(), f32x16_zero()};
     for (int k0 = 0; k0 < d; k0 += kTpK) {
         __syncthreads();
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int e = tid + 256 * it;  // 512 16-byte pieces per operand
+        for (int j = 0; j < kPieces; ++j) {
+            const int e = tid + 256 * j;
             const int r = e >> 3, q8 = (e & 7) * 8;
-            uint4 xv = make_uint4(0, 0, 0, 0);
-            if (t0 + r < n_tok) xv = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * d + k0 + q8);
-            *reinterpret_cast<uint4*>(&xs[r * kTpPitch + q8]) = xv;
-            // W_u row k0 + r, columns c0 + q8 .. + 7 -> wt[column][k]
-            const uint4 wv = *reinterpret_cast<const uint4*>(wu + (int64_t)(k0 + r) * dh + c0 + q8);
-            const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                wt[(q8 + 2 * j) * kTpPitch + r] = (uint16_t)(w4[j] & 0xffffu);
-                wt[(q8 + 2 * j + 1) * kTpPitch + r] = (uint16_t)(w4[j] >> 16);
-            }
+            if (r < kTpT)
+                *reinterpret_cast<uint4*>(&xs[r * kTpPitch + q8]) = nxt[j];
+            else
+                *reinterpret_cast<uint4*>(&wt[(r - kTpT) * kTpPitch + q8]) = nxt[j];
         }
         __syncthreads();
+        if (k0 + kTpK < d) fetch(k0 + kTpK, nxt);
 #pragma unroll
         for (int kk = 0; kk < kTpK; kk += 16) {
-            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&wt[(wc * 32 + l32) * kTpPitch + kk + 8 * h]);
             const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(&xs[(wr * 32 + l32) * kTpPitch + kk + 8 * h]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&wt[(wc * 32 + l32) * kTpPitch + kk + 8 * h]);
+            acc[(kk >> 4) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[(kk >> 4) & 1], 0, 0, 0);
         }
     }
     // acc[i]: hidden column c0 + 32 wc + mfma32_row(i, lane) of token t0 + 32 wr + l32
@@ -139,8 +186,10 @@ __global__ __launch_bounds__(256) void token_proj_bf16_kernel(const uint16_t* __
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int c = c0 + wc * 32 + 8 * g + 4 * h;
-            *reinterpret_cast<uint2*>(xp + (int64_t)t * dh + c) =
-                make_uint2(pack_bf16x2(acc[4 * g], acc[4 * g + 1]), pack_bf16x2(acc[4 * g + 2], acc[4 * g + 3]));
+            if (c < dh)
+                *reinterpret_cast<uint2*>(xp + (int64_t)t * dh + c) =
+                    make_uint2(pack_bf16x2(acc[0][4 * g] + acc[1][4 * g], acc[0][4 * g + 1] + acc[1][4 * g + 1]),
+                               pack_bf16x2(acc[0][4 * g + 2] + acc[1][4 * g + 2], acc[0][4 * g + 3] + acc[1][4 * g + 3]));
         }
     }
 }
@@ -199,13 +248,28 @@ __global__ __launch_bounds__(256) void token_proj_kernel(const T* __restrict__ x
 
 constexpr int kActGroup = 4;  // pairs whose loads are in flight together
 
+// a . b + acc over one lane's raw slice (fp32 accumulation; bf16 pairs by v_dot2c_f32_bf16)
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot_raw(const uint4& a, const uint4& b, float acc) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.x), __builtin_bit_cast(bf16x2_v, b.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.y), __builtin_bit_cast(bf16x2_v, b.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.z), __builtin_bit_cast(bf16x2_v, b.z), acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.w), __builtin_bit_cast(bf16x2_v, b.w), acc,
+                                           false);
+}
+__device__ __forceinline__ float dot_raw(const float4& a, const float4& b, float acc) {
+    acc = __builtin_fmaf(a.x, b.x, acc);
+    acc = __builtin_fmaf(a.y, b.y, acc);
+    acc = __builtin_fmaf(a.z, b.z, acc);
+    return __builtin_fmaf(a.w, b.w, acc);
+}
+
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
                                                         const int32_t* __restrict__ perm,
                                                         const int32_t* __restrict__ sorted_slot,
                                                         const T* __restrict__ gates, int64_t n_pairs, int hk, int dh,
                                                         float* __restrict__ act) {
-    constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
     const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -235,13 +299,7 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
             for (int q = 0; q < kActGroup; ++q) {
                 part[q] = 0.0f;
 #pragma unroll
-                for (int c = 0; c < CH; ++c) {
-                    float uf[N], xf[N];
-                    Vec16<T>::unpack(ur[q][c], uf);
-                    Vec16<T>::unpack(xr[q][c], xf);
-#pragma unroll
-                    for (int v = 0; v < N; ++v) part[q] = __builtin_fmaf(uf[v], xf[v], part[q]);
-                }
+                for (int c = 0; c < CH; ++c) part[q] = dot_raw(ur[q][c], xr[q][c], part[q]);
             }
 #pragma unroll
             for (int q = 0; q < kActGroup; ++q) {
@@ -345,9 +403,15 @@ int apply_chunks(int d, int dtype) {
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// workspace: x_proj [n_tok, dh] T | act [N] fp32 | (bf16) W_u^T [dh, d]
+static size_t wut_offset(int64_t n_tok, int H, int k, int dh, size_t eb) {
+    return align256(align256((size_t)n_tok * dh * eb) + (size_t)n_tok * H * k * sizeof(float));
+}
+
 size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype) {
+    // d is not an argument here: the W_u^T block is sized for d <= 4096, the ABI's limit
     const size_t eb = dtype == kBF16 ? 2 : 4;
-    return align256((size_t)n_tok * dh * eb) + (size_t)n_tok * H * k * sizeof(float);
+    return wut_offset(n_tok, H, k, dh, eb) + (dtype == kBF16 ? (size_t)dh * 4096 * eb : 0);
 }
 
 int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
@@ -358,10 +422,15 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
     // token projection (W_u^T = the first d rows of net.2.weight, row length dh)
     const dim3 tgrid((unsigned)((dh + kTpC - 1) / kTpC), (unsigned)((n_tok + kTpT - 1) / kTpT));
-    if (dtype == kBF16 && d % kTpK == 0 && dh % kTpC == 0)
-        hipLaunchKernelGGL(token_proj_bf16_kernel, tgrid, dim3(256), 0, stream, (const uint16_t*)x,
-                           (const uint16_t*)w2, (int)n_tok, d, dh, (uint16_t*)xp);
-    else if (dtype == kBF16)
+    if (dtype == kBF16 && d % kTpK == 0 && dh % 8 == 0) {
+        uint16_t* wut = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + wut_offset(n_tok, H, k, dh, eb));
+        hipLaunchKernelGGL(transpose_wu_kernel, dim3((unsigned)((dh + 63) / 64), (unsigned)((d + 63) / 64)), dim3(256),
+                           0, stream, (const uint16_t*)w2, d, dh, wut);
+        hipLaunchKernelGGL(token_proj_bf16_kernel,
+                           dim3((unsigned)((dh + kTpCols - 1) / kTpCols), (unsigned)((n_tok + kTpT - 1) / kTpT)),
+                           dim3(256), 0, stream, (const uint16_t*)x, (const uint16_t*)wut, (int)n_tok, d, dh,
+                           (uint16_t*)xp);
+    } else if (dtype == kBF16)
         hipLaunchKernelGGL(token_proj_kernel<uint16_t>, tgrid, dim3(256), 0, stream, (const uint16_t*)x,
                            (const uint16_t*)w2, (int)n_tok, d, dh, (uint16_t*)xp);
     else

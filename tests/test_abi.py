@@ -56,7 +56,7 @@ def test_argument_errors_are_codes():
     # workspace too small
     assert L.ethos_sort_segment(1, 100, 16, 16, 8, 16, 16, 16, 16, 16, 16, None) == -5
     # misaligned apply pointers
-    assert L.ethos_apply_scatter(3, 16, 16, 16, 16, 16, 16, 16, 4, 2, 2, 64, 32, 1, 16, 4096, 16, None) == -4
+    assert L.ethos_apply_scatter(3, 16, 16, 16, 16, 16, 16, 16, 4, 2, 2, 64, 32, 1, 16, 1 << 30, 16, None) == -4
     # apply workspace too small
     assert L.ethos_apply_scatter(16, 16, 16, 16, 16, 16, 16, 16, 4, 2, 2, 64, 32, 1, 16, 8, 16, None) == -5
     # unsupported generator shape
