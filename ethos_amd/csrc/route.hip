@@ -49,10 +49,34 @@ __device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
     return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
+// v of lane (lane ^ mask), mask a compile-time constant after inlining: DPP quad
+// permutes for 1 and 2, ds_swizzle (xor mode, within 32 lanes) up to 31, and
+// v_permlane32_swap for the half-wave exchange; no LDS addressing.
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v, int mask) {
+    if (mask == 1) return dpp_u32<kDppXor1>(v);
+    if (mask == 2) return dpp_u32<kDppXor2>(v);
+    uint32_t r = v;
+    if (mask & 32) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(r, r, false, false);
+        r = (__lane_id() & 32) ? sw[0] : sw[1];
+    }
+    switch (mask & 31) {
+        case 0: break;
+        case 1: r = dpp_u32<kDppXor1>(r); break;
+        case 2: r = dpp_u32<kDppXor2>(r); break;
+        case 4: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (4 << 10) | 0x1f); break;
+        case 8: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (8 << 10) | 0x1f); break;
+        case 16: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (16 << 10) | 0x1f); break;
+        case 31: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (31 << 10) | 0x1f); break;
+        default: r = (uint32_t)__shfl_xor((int)r, mask & 31, kWave); break;
+    }
+    return r;
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
-    const int lo = __shfl_xor((int)(uint32_t)v, mask, kWave);
-    const int hi = __shfl_xor((int)(uint32_t)(v >> 32), mask, kWave);
-    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+    const uint32_t lo = xor_lane_u32((uint32_t)v, mask);
+    const uint32_t hi = xor_lane_u32((uint32_t)(v >> 32), mask);
+    return ((uint64_t)hi << 32) | lo;
 }
 
 // Bitonic sort of one value per lane, descending in lane order.
@@ -62,7 +86,7 @@ template <>
 __device__ __forceinline__ uint64_t shfl_xor_v<uint64_t>(uint64_t v, int mask) { return shfl_xor_u64(v, mask); }
 template <>
 __device__ __forceinline__ uint32_t shfl_xor_v<uint32_t>(uint32_t v, int mask) {
-    return (uint32_t)__shfl_xor((int)v, mask, kWave);
+    return xor_lane_u32(v, mask);
 }
 
 template <typename V>
@@ -263,8 +287,15 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
                 }
             }
             const float emax = __uint_as_float(wave_max_u32(emax_bits));
-            const uint32_t sorted = wave_sort_desc<uint32_t>(lane < K ? ord32(lane_max) : 0u, lane);
-            const uint32_t o = __builtin_amdgcn_readlane(sorted, kc - 1);
+            // o: the largest value with 16 low zero bits such that at least kc lane maxima
+            // are >= o (as ordered keys); it is at most the kc-th largest lane maximum
+            const uint32_t lkey = lane < K ? ord32(lane_max) : 0u;
+            uint32_t o = 0;
+#pragma unroll
+            for (int b = 31; b >= 16; --b) {
+                const uint32_t cand_o = o | (1u << b);
+                if ((int)__popcll(__ballot(lkey >= cand_o)) >= kc) o = cand_o;
+            }
             const float tau_s = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
             const float tau = tau_s - emax * (1.0f + 0x1p-20f) - fabsf(tau_s) * 0x1p-21f;
             const float thr = Elem<T>::round32(tau);
