@@ -52,9 +52,14 @@ __device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
 // v of lane (lane ^ mask), mask a compile-time constant after inlining: DPP quad
 // permutes for 1 and 2, ds_swizzle (xor mode, within 32 lanes) up to 31, and
 // v_permlane32_swap for the half-wave exchange; no LDS addressing.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {  // every lane reads: no "old" operand
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kCtrl, 0xf, 0xf, true);
+}
+
 __device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v, int mask) {
-    if (mask == 1) return dpp_u32<kDppXor1>(v);
-    if (mask == 2) return dpp_u32<kDppXor2>(v);
+    if (mask == 1) return dpp_mov<kDppXor1>(v);
+    if (mask == 2) return dpp_mov<kDppXor2>(v);
     uint32_t r = v;
     if (mask & 32) {
         const auto sw = __builtin_amdgcn_permlane32_swap(r, r, false, false);
@@ -62,8 +67,8 @@ __device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v, int mask) {
     }
     switch (mask & 31) {
         case 0: break;
-        case 1: r = dpp_u32<kDppXor1>(r); break;
-        case 2: r = dpp_u32<kDppXor2>(r); break;
+        case 1: r = dpp_mov<kDppXor1>(r); break;
+        case 2: r = dpp_mov<kDppXor2>(r); break;
         case 4: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (4 << 10) | 0x1f); break;
         case 8: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (8 << 10) | 0x1f); break;
         case 16: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (16 << 10) | 0x1f); break;
@@ -99,7 +104,8 @@ __device__ __forceinline__ V wave_sort_desc(V v, int lane) {
             const bool desc = (lane & k) == 0;
             const bool lower = (lane & j) == 0;
             const bool keep_max = lower == desc;
-            v = keep_max ? (v > p ? v : p) : (v < p ? v : p);
+            // take the partner's value when it is larger (keep_max) or not larger
+            v = (p > v) == keep_max ? p : v;
         }
     }
     return v;
@@ -114,7 +120,7 @@ __device__ __forceinline__ uint64_t wave_merge_desc(uint64_t run, uint64_t chunk
     for (int j = kWave >> 1; j > 0; j >>= 1) {
         const uint64_t p = shfl_xor_u64(v, j);
         const bool lower = (lane & j) == 0;
-        v = lower ? (v > p ? v : p) : (v < p ? v : p);
+        v = (p > v) == lower ? p : v;
     }
     return v;
 }
