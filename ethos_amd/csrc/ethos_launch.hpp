@@ -12,7 +12,7 @@ size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int dtype);
 int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
                  int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream);
 
-size_t route_smem_bytes(int K, int dh2);
+size_t route_smem_bytes(int K, int dh2, int elem_bytes);
 bool route_supported(int K, int dh2, int dtype);
 int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, int64_t rows, int dq, int K,
                  int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream);

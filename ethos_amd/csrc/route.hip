@@ -33,7 +33,7 @@
 
 namespace ethos {
 
-constexpr int kRtWaves = 8;                            // two waves per SIMD
+constexpr int kRtWaves = 8;                            // two workgroups per CU: four waves per SIMD
 constexpr int kRtRows = 32;                            // rows per workgroup (one MFMA row block)
 constexpr int kRtRowsPerWave = kRtRows / kRtWaves;
 constexpr int kRtMaxKc = 32;                           // k_cand <= 32, top_k <= 32
@@ -161,30 +161,57 @@ template <> struct KeyVec<float> {
 };
 
 struct RouteSmem {
-    size_t s_off, kn_off, qd_off, cand_off, lists_off, topk_off, total;
+    size_t s_off, kn_off, qs_off, total;
+    int qs_pitch;  // bytes per staged query-half row
 };
 
-__host__ __device__ inline int route_pitch(int K) { return ((K + 31) / 32) * 32 + 4; }
+// Row pitch of the score tile (floats).  Once a row's K approximate scores are in
+// registers, its storage holds up to 64 8-byte candidate keys (bytes [0, 512)) and the
+// row's list of candidates still to be scored exactly (bytes [512, 768)); 4 floats of
+// padding spread the MFMA result stores over the banks.
+constexpr int kRtPendOff = 2 * kWave;  // float offset of the pending list
+__host__ __device__ inline int route_pitch(int K) {
+    const int p = ((K + 31) / 32) * 32;
+    return (p > 3 * kWave ? p : 3 * kWave) + 4;
+}
 
-__host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2) {
+__host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2, int elem_bytes) {
     RouteSmem L;
     size_t off = 0;
     L.s_off = off;
     off += (size_t)kRtRows * route_pitch(K) * sizeof(float);
     L.kn_off = off;
     off += (size_t)2 * ((K + 31) / 32) * 32 * sizeof(float);
-    off = (off + 15) & ~(size_t)15;
-    L.qd_off = off;
-    off += (size_t)kRtWaves * dh2 * sizeof(double);
-    L.cand_off = 0;   // candidates reuse the row's own score storage
-    L.lists_off = 0;  // the candidate lists stay in registers
-    L.topk_off = 0;
+    L.qs_off = off;
+    // 16 bytes of padding put the query rows of one wave's lanes on different banks
+    L.qs_pitch = dh2 * elem_bytes + 16;
+    off += (size_t)kRtRows * L.qs_pitch;
     L.total = off;
     return L;
 }
 
+// Exact score key of sub-key j: the fp64 FMA chain over the query half qh (staged in
+// LDS) and key row j (global, L2-resident), index order, rounded once to T.
 template <typename T>
-__global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
+__device__ __forceinline__ uint64_t exact_key(const T* qh, const T* __restrict__ keys, int dh2, int j) {
+    const T* kr = keys + (int64_t)j * dh2;
+    double acc = 0.0;
+    for (int i = 0; i < dh2; i += KeyVec<T>::kN) {
+        double qv[KeyVec<T>::kN], kv[KeyVec<T>::kN];
+        KeyVec<T>::load(qh + i, qv);
+        KeyVec<T>::load(kr + i, kv);
+#pragma unroll
+        for (int t = 0; t < KeyVec<T>::kN; ++t) acc = fma(qv[t], kv[t], acc);
+    }
+    return make_key(Elem<T>::round64(acc), (uint32_t)j);
+}
+
+// Certified score of a candidate slot, or this pattern (a NaN, never a certified score)
+// when the slot still needs the exact chain.
+constexpr uint32_t kRtPending = 0xffffffffu;
+
+template <typename T>
+__global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
                                                     const T* __restrict__ keys2, const float* __restrict__ key_norms,
                                                     int64_t rows, int dq, int K, int top_k, int kc,
                                                     T* __restrict__ out_gates, int32_t* __restrict__ out_ids) {
@@ -193,12 +220,11 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
     const int dh2 = dq / 2;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lrow = lane & 31, lk = (lane >> 5) * M::kKL;
-    const RouteSmem L = route_smem_layout(K, dh2);
+    const RouteSmem L = route_smem_layout(K, dh2, (int)sizeof(T));
     const int pitch = route_pitch(K);
     const int kpad = ((K + 31) / 32) * 32;
     float* S = reinterpret_cast<float*>(smem + L.s_off);
     float* kn = reinterpret_cast<float*>(smem + L.kn_off);
-    double* qd = reinterpret_cast<double*>(smem + L.qd_off) + (size_t)wave * dh2;
     // lst[rr][half]: the canonical top-k_cand list of this wave's row rr and query half,
     // entry i held by lane i
     uint64_t lst[kRtRowsPerWave][2];
@@ -260,36 +286,54 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
         }
         __syncthreads();
 
-        // 2-3. per row: certified candidate filter, exact scores, canonical top-k_cand
+        // 2. per row: certified candidate filter.  A candidate whose certified interval
+        //    [s~ - e, s~ + e] rounds to a single T value has that value as its exact score:
+        //    rounding is monotone and the fp64 chain lies inside the interval (its own
+        //    error is below 2^-45 ||q|| ||k||, far inside the 1% slack of e).  The others
+        //    go on the row's pending list, and step 3 scores the pending lists of all the
+        //    wave's rows together.  A row with more than 64 candidates (rare) is scored
+        //    exactly in full in step 4.
+        int n_cand[kRtRowsPerWave], n_pend[kRtRowsPerWave];
+        uint32_t slow_rows = 0;
+        const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
         for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
+            n_cand[rr] = n_pend[rr] = 0;
             const int lr = wave * kRtRowsPerWave + rr;
             const int64_t r = row0 + lr;
             if (r >= rows) break;
+            // stage the query half in LDS (16 bytes per lane) and bound its norm
+            T* qs = reinterpret_cast<T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
             float sq = 0.0f;
-            for (int i = lane; i < dh2; i += kWave) {
-                const float v = Elem<T>::to_f32(q[r * dq + half * dh2 + i]);
-                qd[i] = (double)v;
-                sq = __builtin_fmaf(v, v, sq);
+            for (int i = lane * KeyVec<T>::kN; i < dh2; i += kWave * KeyVec<T>::kN) {
+                const uint4 raw = *reinterpret_cast<const uint4*>(q + r * dq + half * dh2 + i);
+                *reinterpret_cast<uint4*>(qs + i) = raw;
+                double v[KeyVec<T>::kN];
+                KeyVec<T>::load(qs + i, v);
+#pragma unroll
+                for (int t = 0; t < KeyVec<T>::kN; ++t) sq = __builtin_fmaf((float)v[t], (float)v[t], sq);
             }
             const float qn = sqrtf(wave_sum(sq)) * (1.0f + 0x1p-12f);
-            __builtin_amdgcn_wave_barrier();
 
-            float s[kRtSlots], up[kRtSlots];
+            // up: upper bounds of the scores (filter); cs: certified scores or kRtPending
+            float up[kRtSlots];
+            uint32_t cs[kRtSlots];
             float lane_max = -__builtin_huge_valf();
             uint32_t emax_bits = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
                 const int j = lane + m * kWave;
+                up[m] = -__builtin_huge_valf();
+                cs[m] = kRtPending;
                 if (j < K) {
-                    s[m] = S[lr * pitch + j];
-                    const float marg = gamma * qn * kn[half * kpad + j] + fabsf(s[m]) * 0x1p-21f + 0x1p-120f;
-                    up[m] = s[m] + marg;
-                    lane_max = fmaxf(lane_max, s[m]);
+                    const float sj = S[lr * pitch + j];
+                    const float marg = gamma * qn * kn[half * kpad + j] + fabsf(sj) * 0x1p-21f + 0x1p-120f;
+                    up[m] = sj + marg;
+                    const uint32_t lo = __float_as_uint(Elem<T>::round32(sj - marg));
+                    const uint32_t hi = __float_as_uint(Elem<T>::round32(up[m]));
+                    if (lo == hi && (lo & 0x7f800000u) != 0x7f800000u) cs[m] = lo;
+                    lane_max = fmaxf(lane_max, sj);
                     emax_bits = max(emax_bits, __float_as_uint(marg));
-                } else {
-                    s[m] = -__builtin_huge_valf();
-                    up[m] = -__builtin_huge_valf();
                 }
             }
             const float emax = __uint_as_float(wave_max_u32(emax_bits));
@@ -306,42 +350,104 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
             const float tau = tau_s - emax * (1.0f + 0x1p-20f) - fabsf(tau_s) * 0x1p-21f;
             const float thr = Elem<T>::round32(tau);
 
-            // the row's scores are in registers now: its LDS row holds the candidates
-            int32_t* cand = reinterpret_cast<int32_t*>(S + lr * pitch);
-            __builtin_amdgcn_wave_barrier();
-            int n_cand = 0;
+            uint32_t fbits = 0;
+            int n = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
-                const int j = lane + m * kWave;
-                const bool f = j < K && Elem<T>::round32(up[m]) >= thr;
-                const uint64_t bal = __ballot(f);
-                if (f) cand[n_cand + __popcll(bal & ((1ull << lane) - 1ull))] = j;
-                n_cand += (int)__popcll(bal);
+                const bool f = lane + m * kWave < K && Elem<T>::round32(up[m]) >= thr;
+                fbits |= (uint32_t)f << m;
+                n += (int)__popcll(__ballot(f));
+            }
+            n_cand[rr] = n;
+            // the row's scores are in registers now: its LDS row holds the candidates
+            __builtin_amdgcn_wave_barrier();
+            if (n <= kWave) {
+                uint64_t* ck = reinterpret_cast<uint64_t*>(S + lr * pitch);
+                int pos = 0;
+#pragma unroll
+                for (int m = 0; m < kRtSlots; ++m) {
+                    const bool f = (fbits >> m) & 1u;
+                    const uint64_t bal = __ballot(f);
+                    if (f) ck[pos + __popcll(bal & below)] = ((uint64_t)cs[m] << 32) | (uint32_t)(lane + m * kWave);
+                    pos += (int)__popcll(bal);
+                }
+                __builtin_amdgcn_wave_barrier();
+                // certified slots become final keys; the others join the pending list as
+                // (sub-key << 8 | slot)
+                const uint64_t e = lane < n ? ck[lane] : 0ull;
+                const uint32_t sc = (uint32_t)(e >> 32), j = (uint32_t)e;
+                const bool pend = lane < n && sc == kRtPending;
+                const uint64_t bal = __ballot(pend);
+                if (lane < n) {
+                    if (pend) reinterpret_cast<uint32_t*>(S + lr * pitch + kRtPendOff)[__popcll(bal & below)] = (j << 8) | (uint32_t)lane;
+                    else ck[lane] = make_key(__uint_as_float(sc), j);
+                }
+                n_pend[rr] = (int)__popcll(bal);
+            } else {
+                int32_t* cand = reinterpret_cast<int32_t*>(S + lr * pitch);
+                int pos = 0;
+#pragma unroll
+                for (int m = 0; m < kRtSlots; ++m) {
+                    const bool f = (fbits >> m) & 1u;
+                    const uint64_t bal = __ballot(f);
+                    if (f) cand[pos + __popcll(bal & below)] = lane + m * kWave;
+                    pos += (int)__popcll(bal);
+                }
+                slow_rows |= 1u << rr;
             }
             __builtin_amdgcn_wave_barrier();
+        }
 
-            uint64_t run = 0;
-            for (int c0 = 0; c0 < n_cand; c0 += kWave) {
-                const int idx = c0 + lane;
-                uint64_t key = 0;
-                if (idx < n_cand) {
-                    const int j = cand[idx];
-                    const T* kr = keys + (int64_t)j * dh2;
-                    double acc = 0.0;
-                    for (int i = 0; i < dh2; i += KeyVec<T>::kN) {
-                        double kv[KeyVec<T>::kN];
-                        KeyVec<T>::load(kr + i, kv);
+        // 3. exact scores of the pending candidates of all the wave's rows, one per lane,
+        //    written to their slots
+        {
+            int p_end[kRtRowsPerWave];
+            int nq = 0;
 #pragma unroll
-                        for (int t = 0; t < KeyVec<T>::kN; ++t) acc = fma(qd[i + t], kv[t], acc);
+            for (int rr = 0; rr < kRtRowsPerWave; ++rr) p_end[rr] = (nq += n_pend[rr]);
+            for (int c0 = 0; c0 < nq; c0 += kWave) {
+                const int idx = c0 + lane;
+                if (idx < nq) {
+                    int rr = 0, start = 0;
+#pragma unroll
+                    for (int t = 0; t < kRtRowsPerWave - 1; ++t) {
+                        if (idx >= p_end[t]) {
+                            rr = t + 1;
+                            start = p_end[t];
+                        }
                     }
-                    key = make_key(Elem<T>::round64(acc), (uint32_t)j);
+                    const int lr = wave * kRtRowsPerWave + rr;
+                    const uint32_t e = reinterpret_cast<const uint32_t*>(S + lr * pitch + kRtPendOff)[idx - start];
+                    const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
+                    reinterpret_cast<uint64_t*>(S + lr * pitch)[e & 0xffu] = exact_key<T>(qs, keys, dh2, (int)(e >> 8));
                 }
-                key = wave_sort_desc<uint64_t>(key, lane);
-                run = c0 == 0 ? key : wave_merge_desc(run, key, lane);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+
+        // 4. canonical top-k_cand list of each row
+#pragma unroll
+        for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
+            const int lr = wave * kRtRowsPerWave + rr;
+            const int64_t r = row0 + lr;
+            if (r >= rows) break;
+            const int n = n_cand[rr];
+            uint64_t run = 0;
+            if (!((slow_rows >> rr) & 1u)) {
+                const uint64_t* ck = reinterpret_cast<const uint64_t*>(S + lr * pitch);
+                run = wave_sort_desc<uint64_t>(lane < n ? ck[lane] : 0ull, lane);
+            } else {
+                const int32_t* cand = reinterpret_cast<const int32_t*>(S + lr * pitch);
+                const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
+                for (int c0 = 0; c0 < n; c0 += kWave) {
+                    const int idx = c0 + lane;
+                    uint64_t key = idx < n ? exact_key<T>(qs, keys, dh2, cand[idx]) : 0ull;
+                    key = wave_sort_desc<uint64_t>(key, lane);
+                    run = c0 == 0 ? key : wave_merge_desc(run, key, lane);
+                }
             }
             if (half == 0) lst[rr][0] = run;
             else lst[rr][1] = run;
-            __builtin_amdgcn_wave_barrier();
         }
         __syncthreads();
     }
@@ -421,17 +527,17 @@ __global__ __launch_bounds__(kRtWaves * 64) void route_kernel(const T* __restric
     }
 }
 
-size_t route_smem_bytes(int K, int dh2) { return route_smem_layout(K, dh2).total; }
+size_t route_smem_bytes(int K, int dh2, int elem_bytes) { return route_smem_layout(K, dh2, elem_bytes).total; }
 
 bool route_supported(int K, int dh2, int dtype) {
     const int kq = dtype == kBF16 ? 16 : 4;
-    return K <= kRtMaxK && dh2 <= kRtMaxDh2 && dh2 % kq == 0 && route_smem_bytes(K, dh2) <= 160 * 1024;
+    return K <= kRtMaxK && dh2 <= kRtMaxDh2 && dh2 % kq == 0 && route_smem_bytes(K, dh2, dtype == kBF16 ? 2 : 4) <= 160 * 1024;
 }
 
 int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, int64_t rows, int dq, int K,
                  int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream) {
     const int dh2 = dq / 2;
-    const size_t smem = route_smem_bytes(K, dh2);
+    const size_t smem = route_smem_bytes(K, dh2, dtype == kBF16 ? 2 : 4);
     dim3 grid((unsigned)((rows + kRtRows - 1) / kRtRows));
     if (dtype == kBF16)
         hipLaunchKernelGGL(route_kernel<uint16_t>, grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
