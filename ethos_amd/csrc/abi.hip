@@ -56,9 +56,8 @@ int ethos_abi_version(void) { return ETHOS_ABI_VERSION; }
 
 size_t ethos_query_proj_workspace_bytes(int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query,
                                         int32_t dtype) {
-    (void)d_model;
-    if (n_tok <= 0 || n_heads <= 0 || d_query <= 0) return 256;
-    const size_t b = ethos::qproj_workspace_bytes(n_tok, n_heads * d_query, dtype);
+    if (n_tok <= 0 || d_model <= 0 || n_heads <= 0 || d_query <= 0) return 256;
+    const size_t b = ethos::qproj_workspace_bytes(n_tok, n_heads * d_query, d_model, dtype);
     return b < 256 ? 256 : b;
 }
 

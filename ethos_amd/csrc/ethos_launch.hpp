@@ -8,7 +8,7 @@
 
 namespace ethos {
 
-size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int dtype);
+size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int d, int dtype);
 int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
                  int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream);
 

@@ -78,88 +78,197 @@ __global__ __launch_bounds__(256) void qproj_kernel(const T* __restrict__ x, con
 }
 
 // ---------------------------------------------------------------------------------
-// bf16: certified MFMA projection with exact refinement.
+// bf16: exact integer MFMA projection on three int8 digit planes per operand.
 //
-// Every 16-term slice of the dot product is one 32x32x16 MFMA on a zero accumulator;
-// bf16 x bf16 products are exact in fp32, so however the MFMA orders its 15
-// additions, each rounded at worst like a truncating fp32 add, the slice is within
-// 15 * 2^-23 of the sum of its |x_i w_i|.  Slices are added in fp64 (error <= 2^-46 of
-// the same sum over 1024 terms), and A = sum |x_i w_i| itself comes from a second MFMA
-// on sign-cleared operands (fp32, relative error < 2^-12).  Hence
-//     |S~ - S| <= E = (15 * 2^-23 + 2^-46) * 1.001 * A * (1 + 2^-12) + 2^-50 (|S~| + |b|),
-// and when RN_T(S~ + b - E) == RN_T(S~ + b + E) the correctly rounded projection is
-// known; the rest (about 1% on random data) is queued and recomputed exactly.
+// Every row r of x and of Wq gets a fixed-point format of its own:
+//     v_i = 2^(E_r - 21) F_i + res_i,   F_i = trunc(v_i 2^(21 - E_r)),   |v_i| < 2^E_r,
+// so |F_i| < 2^21 and F_i = 2^14 D0_i + 2^7 D1_i + D2_i with D0 in [-128, 127] and D1, D2
+// in [0, 127]: three int8 digit planes.  Elements within 14 binades of 2^E_r are exact
+// (res_i = 0); each of the n_r others has |res_i| < 2^(E_r - 21).  i8 MFMAs add the 9
+// digit-pair products in int32 without rounding (|C_k| < 3 d 2^14 < 2^31 for d <= 16384):
+//     P = sum_i F^x_i F^w_i = sum_k 2^(7 (4 - k)) C_k,   C_k = sum_{a+b=k} sum_i Da^x_i Db^w_i,
+// an exact int64, so V = 2^(E_x + E_w - 42) P is the exact dot product of the truncated
+// operands, and
+//     |x.w - V| <= n_x 2^(E_x - 21) max|w| + n_w 2^(E_w - 21) max|x|.
+// The fp64 FMA chain the contract defines is within d 2^-53 sum_i |x_i w_i| <=
+// d 2^-53 min(max|x| |w|_1, max|w| |x|_1) of x.w.  With those bounds (1% slack), 2^-50 of
+// the magnitudes for the fp64 evaluation and one subnormal ulp (so that a zero sum keeps
+// its sign undecided), RN_T(lo) == RN_T(hi) settles RN_T(fl64(chain + b)).  Rows with a
+// non-finite value and sums within the bound of a rounding boundary are queued and
+// recomputed with the exact chain.
 // ---------------------------------------------------------------------------------
-constexpr int kQmRows = 64;    // tokens per workgroup tile (2 waves x 32)
-constexpr int kQmCols = 128;   // output columns per workgroup tile (2 waves x 64)
-constexpr int kQmKC = 64;      // reduction chunk staged in LDS
-constexpr int kQmPitch = kQmKC + 8;
+constexpr int kQiRows = 64;             // tokens per workgroup tile (2 waves x 32)
+constexpr int kQiCols = 64;             // output columns per workgroup tile (2 waves x 32)
+constexpr int kQiKC = 64;               // reduction chunk (bytes of a digit row) staged in LDS
+constexpr int kQiPitch = kQiKC + 16;    // LDS row pitch (bytes)
+constexpr int kQiMaxD = 16384;          // int32 digit-product sums cannot overflow below this
+
+struct QRowMeta {
+    int32_t e;        // E_r: every |v_i| < 2^E_r
+    int32_t n_inex;   // elements not exact in the digit format; -1: the row holds inf / NaN
+    float l1;         // upper bound of sum |v_i|
+    float amax;       // upper bound of max |v_i|
+};
 
 struct QprojWs {
     int32_t* count;   // [1]   uncertain elements
     int32_t* list;    // [n_tok * ncols]
+    int8_t* xdig;     // [3][n_tok][dpad]
+    int8_t* wdig;     // [3][ncols][dpad]
+    QRowMeta* meta;   // [n_tok + ncols]: x rows, then Wq rows
 };
 
-__host__ __device__ inline size_t qproj_ws_bytes(int64_t n_tok, int ncols) {
-    return 256 + 4 * (size_t)n_tok * ncols + 64;
+__host__ __device__ inline int qproj_dpad(int d) { return (d + kQiKC - 1) / kQiKC * kQiKC; }
+
+__host__ __device__ inline size_t qproj_align(size_t b) { return (b + 255) & ~(size_t)255; }
+
+__host__ __device__ inline size_t qproj_ws_bytes(int64_t n_tok, int ncols, int d) {
+    const size_t rows = (size_t)n_tok + (size_t)ncols;
+    return 256 + qproj_align(4 * (size_t)n_tok * ncols) + qproj_align(3 * rows * (size_t)qproj_dpad(d)) +
+           qproj_align(sizeof(QRowMeta) * rows);
 }
 
-__host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols) {
-    (void)n_tok;
-    (void)ncols;
+__host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols, int d) {
     unsigned char* p = reinterpret_cast<unsigned char*>(ws);
+    const size_t dpad = (size_t)qproj_dpad(d);
     QprojWs w;
     w.count = reinterpret_cast<int32_t*>(p);
-    w.list = reinterpret_cast<int32_t*>(p + 256);
+    p += 256;
+    w.list = reinterpret_cast<int32_t*>(p);
+    p += qproj_align(4 * (size_t)n_tok * ncols);
+    w.xdig = reinterpret_cast<int8_t*>(p);
+    w.wdig = w.xdig + 3 * (size_t)n_tok * dpad;
+    p += qproj_align(3 * ((size_t)n_tok + ncols) * dpad);
+    w.meta = reinterpret_cast<QRowMeta*>(p);
     return w;
 }
 
 __global__ void qproj_clear_kernel(int32_t* __restrict__ count) { *count = 0; }
 
-__device__ __forceinline__ bf16x8_t abs_bf16x8(bf16x8_t v) {
-    uint4 u = __builtin_bit_cast(uint4, v);
-    u.x &= 0x7fff7fffu;
-    u.y &= 0x7fff7fffu;
-    u.z &= 0x7fff7fffu;
-    u.w &= 0x7fff7fffu;
-    return __builtin_bit_cast(bf16x8_t, u);
+__device__ __forceinline__ uint32_t qp_wave_max_u32(uint32_t v) { return (uint32_t)wave_max_u64((uint64_t)v); }
+
+// One wave per row of x (rows < n_tok) or Wq: digit planes and the row's format.
+__global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w, int n_tok, int ncols,
+                                                           int d, int8_t* __restrict__ xdig,
+                                                           int8_t* __restrict__ wdig, QRowMeta* __restrict__ meta) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= (int64_t)n_tok + ncols) return;
+    const bool is_x = row < n_tok;
+    const int64_t r = is_x ? row : row - n_tok;
+    const uint16_t* src = (is_x ? x : w) + r * d;
+    const int dpad = qproj_dpad(d);
+    const int64_t plane = (int64_t)(is_x ? n_tok : ncols) * dpad;
+    int8_t* dst = (is_x ? xdig : wdig) + r * dpad;
+    const int ng = d / 8, npad = dpad / 8;
+
+    // pass 1: largest biased exponent, inf / NaN, |.|_1 and max |.|
+    uint32_t emax = 0, amax_bits = 0;
+    bool bad = false;
+    float l1 = 0.0f;
+    for (int g = lane; g < ng; g += kWave) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * g);
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t bits = (wd[j >> 1] >> (16 * (j & 1))) & 0x7fffu;
+            const uint32_t e = bits >> 7;
+            emax = max(emax, e);
+            bad |= e == 0xffu;
+            amax_bits = max(amax_bits, bits);
+            l1 += __uint_as_float(bits << 16);
+        }
+    }
+    emax = qp_wave_max_u32(emax);
+    bad = __ballot(bad) != 0;
+    // subnormal floor: the bounds stay upper bounds even if fp32 arithmetic flushes them
+    const float amax = __uint_as_float(qp_wave_max_u32(amax_bits) << 16) + 0x1p-126f;
+    l1 = wave_sum(l1) * (1.0f + 0x1p-10f) + (float)d * 0x1p-126f;
+    const int E = (int)max(emax, 1u) - 126;
+
+    // pass 2: F = trunc(v 2^(21 - E)) from the bit fields, split into three digits
+    int n_inex = 0;
+    for (int g = lane; g < npad; g += kWave) {
+        uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
+        if (g < ng && !bad) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * g);
+            const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t bits = (wd[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                const uint32_t be = (bits >> 7) & 0xffu;
+                const uint32_t m = be ? (0x80u | (bits & 0x7fu)) : (bits & 0x7fu);   // v = m 2^(e - 7)
+                const int e = be ? (int)be - 127 : -126;
+                const int sh = e + 14 - E;                                           // F = m 2^sh
+                uint32_t f;
+                if (sh >= 0) {
+                    f = m << sh;
+                } else {
+                    const int rs = -sh;
+                    f = rs < 8 ? (m >> rs) : 0u;
+                    n_inex += (rs < 8 ? (m & ((1u << rs) - 1u)) : m) != 0u;
+                }
+                const int F = (bits & 0x8000u) ? -(int)f : (int)f;
+                const uint32_t d0 = (uint32_t)(F >> 14) & 0xffu, d1 = ((uint32_t)F >> 7) & 0x7fu,
+                               d2 = (uint32_t)F & 0x7fu;
+                const int wi = j >> 2, sb = 8 * (j & 3);
+                p0[wi] |= d0 << sb;
+                p1[wi] |= d1 << sb;
+                p2[wi] |= d2 << sb;
+            }
+        }
+        *reinterpret_cast<uint2*>(dst + 8 * g) = make_uint2(p0[0], p0[1]);
+        *reinterpret_cast<uint2*>(dst + plane + 8 * g) = make_uint2(p1[0], p1[1]);
+        *reinterpret_cast<uint2*>(dst + 2 * plane + 8 * g) = make_uint2(p2[0], p2[1]);
+    }
+    const int total_inex = (int)wave_sum((float)n_inex);
+    if (lane == 0) {
+        QRowMeta mt;
+        mt.e = E;
+        mt.n_inex = bad ? -1 : total_inex;
+        mt.l1 = l1;
+        mt.amax = amax;
+        meta[row] = mt;
+    }
 }
 
-constexpr int kQmLocal = 1024;  // uncertain elements a workgroup resolves itself (4 per thread)
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16_t __attribute__((ext_vector_type(16)));
 
-__global__ __launch_bounds__(256) void qproj_mfma_kernel(const uint16_t* __restrict__ x,
-                                                         const uint16_t* __restrict__ w,
-                                                         const uint16_t* __restrict__ bias,
-                                                         const float* __restrict__ alpha,
-                                                         const float* __restrict__ beta, int n_tok, int d, int ncols,
-                                                         int32_t* __restrict__ count, int32_t* __restrict__ list,
-                                                         uint16_t* __restrict__ q) {
-    __shared__ __align__(16) uint16_t xs[kQmRows * kQmPitch];
-    __shared__ __align__(16) uint16_t ws[kQmCols * kQmPitch];
-    __shared__ uint32_t local[kQmLocal];  // (row << 16) | column within the tile
-    __shared__ int n_local;
+__global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict__ xdig,
+                                                       const int8_t* __restrict__ wdig,
+                                                       const QRowMeta* __restrict__ meta,
+                                                       const uint16_t* __restrict__ bias,
+                                                       const float* __restrict__ alpha,
+                                                       const float* __restrict__ beta, int n_tok, int d, int ncols,
+                                                       int32_t* __restrict__ count, int32_t* __restrict__ list,
+                                                       uint16_t* __restrict__ q) {
+    __shared__ __align__(16) int8_t xs[3][kQiRows * kQiPitch];
+    __shared__ __align__(16) int8_t ws[3][kQiCols * kQiPitch];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int wr = wave >> 1, wc = wave & 1;
-    const int t0 = blockIdx.y * kQmRows, c0 = blockIdx.x * kQmCols;
-    if (tid == 0) n_local = 0;
+    const int t0 = blockIdx.y * kQiRows, c0 = blockIdx.x * kQiCols;
+    const int dpad = qproj_dpad(d);
+    const int64_t xplane = (int64_t)n_tok * dpad, wplane = (int64_t)ncols * dpad;
 
-    // x [64 x 64] and w [128 x 64] chunks in 16-byte pieces (rows past the end are zero):
-    // piece e = tid + 256 j is row e / 8, k offset 8 (e % 8); rows < 64 are x, the rest w
-    constexpr int kPieces = (kQmRows + kQmCols) * (kQmKC / 8) / 256;
-    static_assert((kQmRows + kQmCols) * (kQmKC / 8) % 256 == 0 && kQmRows * (kQmKC / 8) % 256 == 0,
-                  "staging shape");
+    // one K chunk: 3 planes x (64 x rows + 64 w rows) x 4 pieces of 16 bytes = 6 per thread;
+    // piece e = tid + 256 j: plane e / 512, row (e % 512) / 4 (x below 64), bytes 16 (e % 4)
+    constexpr int kPieces = 3 * (kQiRows + kQiCols) * (kQiKC / 16) / 256;
+    static_assert(3 * (kQiRows + kQiCols) * (kQiKC / 16) % 256 == 0, "staging shape");
     auto fetch = [&](int k0, uint4 (&v)[kPieces]) {
 #pragma unroll
         for (int j = 0; j < kPieces; ++j) {
             const int e = tid + 256 * j;
-            const int r = e / (kQmKC / 8), kq = (e % (kQmKC / 8)) * 8;
+            const int p = e / 512, rr = (e % 512) / 4, kq = (e % 4) * 16;
             v[j] = make_uint4(0, 0, 0, 0);
-            if (r < kQmRows) {
-                if (t0 + r < n_tok) v[j] = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * d + k0 + kq);
-            } else {
-                const int rc = r - kQmRows;
-                if (c0 + rc < ncols) v[j] = *reinterpret_cast<const uint4*>(w + (int64_t)(c0 + rc) * d + k0 + kq);
+            if (rr < kQiRows) {
+                if (t0 + rr < n_tok)
+                    v[j] = *reinterpret_cast<const uint4*>(xdig + p * xplane + (int64_t)(t0 + rr) * dpad + k0 + kq);
+            } else if (c0 + rr - kQiRows < ncols) {
+                v[j] = *reinterpret_cast<const uint4*>(wdig + p * wplane + (int64_t)(c0 + rr - kQiRows) * dpad + k0 +
+                                                       kq);
             }
         }
     };
@@ -167,144 +276,85 @@ __global__ __launch_bounds__(256) void qproj_mfma_kernel(const uint16_t* __restr
 #pragma unroll
         for (int j = 0; j < kPieces; ++j) {
             const int e = tid + 256 * j;
-            const int r = e / (kQmKC / 8), kq = (e % (kQmKC / 8)) * 8;
-            if (r < kQmRows)
-                *reinterpret_cast<uint4*>(&xs[r * kQmPitch + kq]) = v[j];
+            const int p = e / 512, rr = (e % 512) / 4, kq = (e % 4) * 16;
+            if (rr < kQiRows)
+                *reinterpret_cast<uint4*>(&xs[p][rr * kQiPitch + kq]) = v[j];
             else
-                *reinterpret_cast<uint4*>(&ws[(r - kQmRows) * kQmPitch + kq]) = v[j];
+                *reinterpret_cast<uint4*>(&ws[p][(rr - kQiRows) * kQiPitch + kq]) = v[j];
         }
     };
-    auto stage = [&](int k0) {
-        uint4 v[kPieces];
-        fetch(k0, v);
-        put(v);
-    };
 
-    double acc64[2][16];
-    f32x16_t accA[2] = {f32x16_zero(), f32x16_zero()};
+    i32x16_t acc[5];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+    for (int k = 0; k < 5; ++k)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc64[cb][i] = 0.0;
+        for (int i = 0; i < 16; ++i) acc[k][i] = 0;
 
-    // the next chunk is fetched into registers while this one is multiplied
     uint4 nxt[kPieces];
     fetch(0, nxt);
-    for (int k0 = 0; k0 < d; k0 += kQmKC) {
+    for (int k0 = 0; k0 < dpad; k0 += kQiKC) {
         __syncthreads();
         put(nxt);
         __syncthreads();
-        if (k0 + kQmKC < d) fetch(k0 + kQmKC, nxt);
+        if (k0 + kQiKC < dpad) fetch(k0 + kQiKC, nxt);
 #pragma unroll
-        for (int kk = 0; kk < kQmKC; kk += 16) {
-            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&xs[(wr * 32 + l32) * kQmPitch + kk + 8 * h]);
-            const bf16x8_t aa = abs_bf16x8(a);
+        for (int s = 0; s < kQiKC; s += 32) {
+            i32x4_t a[3], b[3];
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const bf16x8_t b =
-                    *reinterpret_cast<const bf16x8_t*>(&ws[(wc * 64 + cb * 32 + l32) * kQmPitch + kk + 8 * h]);
-                const f32x16_t c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, f32x16_zero(), 0, 0, 0);
-                accA[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aa, abs_bf16x8(b), accA[cb], 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc64[cb][i] += (double)c[i];
+            for (int p = 0; p < 3; ++p) {
+                a[p] = *reinterpret_cast<const i32x4_t*>(&xs[p][(wr * 32 + l32) * kQiPitch + s + 16 * h]);
+                b[p] = *reinterpret_cast<const i32x4_t*>(&ws[p][(wc * 32 + l32) * kQiPitch + s + 16 * h]);
             }
+#pragma unroll
+            for (int pa = 0; pa < 3; ++pa)
+#pragma unroll
+                for (int pb = 0; pb < 3; ++pb)
+                    acc[pa + pb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[pa], b[pb], acc[pa + pb], 0, 0, 0);
         }
     }
 
-    // certify each element; store it, or queue it: first in LDS, past kQmLocal globally
-    const double kBound = (15.0 * 0x1p-23 + 0x1p-46) * 1.001 * (1.0 + 0x1p-12);
+    // certify each element; store it or queue it for the exact chain
+    const int c = c0 + wc * 32 + l32;
+    const bool col_ok = c < ncols;
+    QRowMeta mw = {0, -1, 0.0f, 0.0f};
+    double b = 0.0;
+    float al = 0.0f, be = 0.0f;
+    if (col_ok) {
+        mw = meta[n_tok + c];
+        b = (double)bf16_bits_to_f32(bias[c]);
+        al = alpha[c];
+        be = beta[c];
+    }
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        const int cl = wc * 64 + cb * 32 + l32;
-        const int c = c0 + cl;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int tl = wr * 32 + mfma32_row(i, lane);
-            const int t = t0 + tl;
-            const bool live = t < n_tok && c < ncols;
-            bool sure = true;
-            if (live) {
-                const double s = acc64[cb][i];
-                const double b = (double)bf16_bits_to_f32(bias[c]);
-                const double e = kBound * (double)accA[cb][i] + 0x1p-50 * (fabs(s) + fabs(b)) + 0x1p-1000;
-                const uint16_t lo = Elem<uint16_t>::from_f64((s - e) + b);
-                const uint16_t hi = Elem<uint16_t>::from_f64((s + e) + b);
+    for (int i = 0; i < 16; ++i) {
+        const int t = t0 + wr * 32 + mfma32_row(i, lane);
+        const bool live = col_ok && t < n_tok;
+        bool sure = false;
+        if (live) {
+            const QRowMeta mx = meta[t];
+            if (mx.n_inex >= 0 && mw.n_inex >= 0) {
+                const int64_t P = ((int64_t)acc[0][i] << 28) + ((int64_t)acc[1][i] << 21) +
+                                  ((int64_t)acc[2][i] << 14) + ((int64_t)acc[3][i] << 7) + (int64_t)acc[4][i];
+                const double V = ldexp((double)P, mx.e + mw.e - 42);
+                const double et = (double)mx.n_inex * ldexp((double)mw.amax, mx.e - 21) +
+                                  (double)mw.n_inex * ldexp((double)mx.amax, mw.e - 21);
+                const double A = fmin((double)mx.amax * mw.l1, (double)mw.amax * mx.l1);
+                const double E = 1.01 * (et + (double)d * 0x1p-52 * A) + 0x1p-50 * (fabs(V) + fabs(b)) + 0x1p-1074;
+                const double sv = V + b;
+                const uint16_t lo = Elem<uint16_t>::from_f64(sv - E);
+                const uint16_t hi = Elem<uint16_t>::from_f64(sv + E);
                 sure = lo == hi;
-                if (sure) {
-                    const float qb = __builtin_fmaf(bf16_bits_to_f32(lo), alpha[c], beta[c]);
-                    q[(int64_t)t * ncols + c] = f32_to_bf16_bits(qb);
-                }
-            }
-            const bool queue = live && !sure;
-            const uint64_t bal = __ballot(queue);
-            if (bal) {
-                const int leader = __builtin_ctzll(bal);
-                const int rank = (int)__popcll(bal & ((1ull << lane) - 1ull));
-                int base = 0;
-                if (lane == leader) base = atomicAdd(&n_local, (int)__popcll(bal));
-                base = __shfl(base, leader, 64);
-                if (queue) {
-                    const int slot = base + rank;
-                    if (slot < kQmLocal) {
-                        local[slot] = ((uint32_t)tl << 16) | (uint32_t)cl;
-                    } else {
-                        const int g = atomicAdd(count, 1);
-                        list[g] = t * ncols + c;
-                    }
-                }
+                if (sure) q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32(lo), al, be));
             }
         }
-    }
-    __syncthreads();
-    const int nl = n_local < kQmLocal ? n_local : kQmLocal;
-
-    // Exact fp64 chains for the queued elements, re-streaming the same K tiles: each
-    // thread runs two elements' chains side by side (each in index order, 16-byte LDS
-    // reads of eight terms), 512 elements per pass.
-    for (int g0 = 0; g0 < nl; g0 += 512) {
-        int er[2], ec[2];
-        bool ok[2];
-        double ex[2] = {0.0, 0.0};
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int j = g0 + 256 * r + tid;
-            ok[r] = j < nl;
-            const uint32_t v = ok[r] ? local[j] : 0u;
-            er[r] = (int)(v >> 16);
-            ec[r] = (int)(v & 0xffffu);
-        }
-        for (int k0 = 0; k0 < d; k0 += kQmKC) {
-            __syncthreads();
-            stage(k0);
-            __syncthreads();
-#pragma unroll 2
-            for (int kk = 0; kk < kQmKC; kk += 8) {
-                uint4 xa[2], wa[2];
-#pragma unroll
-                for (int r = 0; r < 2; ++r) {
-                    xa[r] = *reinterpret_cast<const uint4*>(&xs[er[r] * kQmPitch + kk]);
-                    wa[r] = *reinterpret_cast<const uint4*>(&ws[ec[r] * kQmPitch + kk]);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-#pragma unroll
-                    for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-                        for (int r = 0; r < 2; ++r) {
-                            const uint32_t xv = (&xa[r].x)[q], wv = (&wa[r].x)[q];
-                            const float xf = __uint_as_float(hf ? (xv & 0xffff0000u) : (xv << 16));
-                            const float wf = __uint_as_float(hf ? (wv & 0xffff0000u) : (wv << 16));
-                            ex[r] = fma((double)xf, (double)wf, ex[r]);
-                        }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            if (ok[r]) {
-                const int t = t0 + er[r], c = c0 + ec[r];
-                const float ql = Elem<uint16_t>::round64(ex[r] + (double)bf16_bits_to_f32(bias[c]));
-                q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
-            }
+        const bool queue = live && !sure;
+        const uint64_t bal = __ballot(queue);
+        if (bal) {
+            const int leader = __builtin_ctzll(bal);
+            int base = 0;
+            if (lane == leader) base = atomicAdd(count, (int)__popcll(bal));
+            base = __shfl(base, leader, 64);
+            if (queue) list[base + (int)__popcll(bal & ((1ull << lane) - 1ull))] = t * ncols + c;
         }
     }
 }
@@ -341,18 +391,21 @@ __global__ __launch_bounds__(256) void qproj_fixup_kernel(const uint16_t* __rest
     }
 }
 
-size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int dtype) {
-    return dtype == kBF16 ? qproj_ws_bytes(n_tok, ncols) : 0;
+size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int d, int dtype) {
+    return dtype == kBF16 && d <= kQiMaxD ? qproj_ws_bytes(n_tok, ncols, d) : 0;
 }
 
 int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
                  int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream) {
-    if (dtype == kBF16 && d % kQmKC == 0) {
-        const QprojWs W = qproj_ws(ws, n_tok, ncols);
+    if (dtype == kBF16 && d <= kQiMaxD) {
+        const QprojWs W = qproj_ws(ws, n_tok, ncols, d);
         hipLaunchKernelGGL(qproj_clear_kernel, dim3(1), dim3(1), 0, stream, W.count);
-        dim3 grid((ncols + kQmCols - 1) / kQmCols, (unsigned)((n_tok + kQmRows - 1) / kQmRows));
-        hipLaunchKernelGGL(qproj_mfma_kernel, grid, dim3(256), 0, stream, (const uint16_t*)x, (const uint16_t*)w,
-                           (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q);
+        const int64_t rows = n_tok + ncols;
+        hipLaunchKernelGGL(qproj_digits_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream,
+                           (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, d, W.xdig, W.wdig, W.meta);
+        dim3 grid((ncols + kQiCols - 1) / kQiCols, (unsigned)((n_tok + kQiRows - 1) / kQiRows));
+        hipLaunchKernelGGL(qproj_i8_kernel, grid, dim3(256), 0, stream, W.xdig, W.wdig, W.meta, (const uint16_t*)b,
+                           alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q);
         hipLaunchKernelGGL(qproj_fixup_kernel, dim3((unsigned)num_cus * 4), dim3(256), 0, stream, (const uint16_t*)x,
                            (const uint16_t*)w, (const uint16_t*)b, alpha, beta, d, ncols, W.count, W.list,
                            (uint16_t*)q);

@@ -212,6 +212,11 @@ def _stress_case(kind, rng, rows, K, dh2, dt):
         z = (np.arange(K) + 1.0) ** -1.1
         k1 *= z[:, None]
         k2 *= z[:, None]
+    elif kind == "mixed":          # one wave's rows: all scores tied / cancelling / plain
+        h = dh2 // 2
+        k1[:, h:2 * h] = -k1[:, :h]
+        q[1::3] = 0.0
+        q[2::3, h:2 * h] = q[2::3, :h] * (1 + 1e-3 * rng.standard_normal((len(q[2::3]), h)))
     elif kind == "dynamic_range":  # magnitudes spread over many binades
         q *= np.exp2(rng.integers(-20, 20, q.shape)).astype(np.float32)
         k1 *= np.exp2(rng.integers(-10, 10, k1.shape)).astype(np.float32)
@@ -220,7 +225,7 @@ def _stress_case(kind, rng, rows, K, dh2, dt):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "fp32"])
-@pytest.mark.parametrize("kind", ["all_equal", "near_ties", "cancellation", "zipf", "dynamic_range"])
+@pytest.mark.parametrize("kind", ["all_equal", "near_ties", "cancellation", "zipf", "dynamic_range", "mixed"])
 def test_route_stress_bit_exact(kind, dt):
     rng = np.random.default_rng(hash((kind, dt)) % 2**32)
     rows, K, dh2, top_k = 96, 512, 128, 16
@@ -274,13 +279,33 @@ def test_generate_many_tiles(dh):
     _check_rows(v[rows], v_ref, "bf16")
 
 
-@pytest.mark.parametrize("kind", ["cancellation", "midpoints"])
+@pytest.mark.parametrize("kind", ["cancellation", "midpoints", "binades", "subnormals", "zero_rows", "ragged_d"])
 def test_query_proj_certified_fallback_bit_exact(kind):
-    """Inputs where the MFMA certificate cannot settle most elements, forcing the exact
-    fp64 recomputation path; the result must still equal the oracle bit for bit."""
+    """Inputs aimed at the certificate: cancellation and rounding ties (most elements go
+    to the exact fp64 recomputation), elements spread over many binades (not exact in the
+    per-row digit format), subnormals, all-zero rows against negative-zero bias and
+    BatchNorm shift, and a model width that is not a multiple of the 64-byte K chunk.  The
+    result must equal the oracle bit for bit."""
     rng = np.random.default_rng(11)
     n, d, H, dq = 96, 512, 2, 64
-    if kind == "cancellation":
+    if kind == "ragged_d":
+        d = 200
+    if kind in ("binades", "subnormals", "zero_rows", "ragged_d"):
+        x = rng.standard_normal((n, d)).astype(np.float32)
+        w = rng.uniform(-1, 1, (H, dq, d)).astype(np.float32) / np.sqrt(d)
+        b = rng.uniform(-0.1, 0.1, (H, dq)).astype(np.float32)
+        if kind == "binades":
+            x *= np.exp2(rng.integers(-24, 8, x.shape)).astype(np.float32)
+            w *= np.exp2(rng.integers(-24, 8, w.shape)).astype(np.float32)
+        elif kind == "subnormals":
+            tiny = rng.random(x.shape) < 0.2
+            x[tiny] = (rng.integers(-127, 128, int(tiny.sum())) * 2.0 ** -133).astype(np.float32)
+            x[::7] *= 2.0 ** -120
+            w[0, :4] = (rng.integers(-127, 128, (4, d)) * 2.0 ** -133).astype(np.float32)
+        elif kind == "zero_rows":
+            x[::3] = 0.0
+            b[:, ::2] = -0.0
+    elif kind == "cancellation":
         half = rng.standard_normal((n, d // 2)).astype(np.float32)
         x = np.concatenate([half, half], axis=1)
         a = rng.uniform(-1, 1, (H, dq, d // 2)).astype(np.float32) / np.sqrt(d)
@@ -294,6 +319,9 @@ def test_query_proj_certified_fallback_bit_exact(kind):
     x, w, b = (O.f32_to_bf16_bits(v) for v in (x, w, b))
     alpha = rng.uniform(0.5, 1.5, (H, dq)).astype(np.float32)
     beta = rng.uniform(-0.1, 0.1, (H, dq)).astype(np.float32)
+    if kind == "zero_rows":
+        beta[:, ::4] = -0.0
+        beta[:, 1::4] = 0.0
     q_ref = O.query_proj(x, w, b, alpha, beta, "bf16")
     q = hip.query_proj(to_dev(x), to_dev(w), to_dev(b), to_dev(alpha), to_dev(beta))
     torch.cuda.synchronize()
