@@ -246,6 +246,7 @@ __global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict_
                                                        uint16_t* __restrict__ q) {
     __shared__ __align__(16) int8_t xs[3][kQiRows * kQiPitch];
     __shared__ __align__(16) int8_t ws[3][kQiCols * kQiPitch];
+    __shared__ QRowMeta xmeta[kQiRows];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int wr = wave >> 1, wc = wave & 1;
@@ -253,34 +254,44 @@ __global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict_
     const int dpad = qproj_dpad(d);
     const int64_t xplane = (int64_t)n_tok * dpad, wplane = (int64_t)ncols * dpad;
 
-    // one K chunk: 3 planes x (64 x rows + 64 w rows) x 4 pieces of 16 bytes = 6 per thread;
-    // piece e = tid + 256 j: plane e / 512, row (e % 512) / 4 (x below 64), bytes 16 (e % 4)
-    constexpr int kPieces = 3 * (kQiRows + kQiCols) * (kQiKC / 16) / 256;
-    static_assert(3 * (kQiRows + kQiCols) * (kQiKC / 16) % 256 == 0, "staging shape");
+    // One K chunk: per plane, each thread moves one 16-byte piece of an x row and one of a
+    // w row (row tid / kRowPieces, bytes 16 (tid % kRowPieces) of the chunk).  Buffer loads
+    // bounded by the tile's live rows return zeros past the last token / column.
+    constexpr int kRowPieces = kQiKC / 16;
+    static_assert(kQiRows * kRowPieces == 256 && kQiCols * kRowPieces == 256, "staging shape");
+    constexpr int kPieces = 6;
+    const int prow = tid / kRowPieces, kq = (tid % kRowPieces) * 16;
+    const int xrows = max(0, min(kQiRows, n_tok - t0)), wrows = max(0, min(kQiCols, ncols - c0));
+    // descriptors are wave-uniform: built from readfirstlane values so that they live in SGPRs
+    auto uniform_ptr = [](const int8_t* ptr) {
+        const uint64_t v = (uint64_t)(size_t)ptr;
+        const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+        const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+        return reinterpret_cast<int8_t*>((size_t)(lo | (hi << 32)));
+    };
+    const int xbytes = __builtin_amdgcn_readfirstlane(xrows * dpad);
+    const int wbytes = __builtin_amdgcn_readfirstlane(wrows * dpad);
+    __amdgpu_buffer_rsrc_t xrs[3], wrs[3];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        xrs[p] = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(xdig + p * xplane + (int64_t)t0 * dpad), (short)0,
+                                                   xbytes, 0x00020000);
+        wrs[p] = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(wdig + p * wplane + (int64_t)c0 * dpad), (short)0,
+                                                   wbytes, 0x00020000);
+    }
+    const int voff = prow * dpad + kq;
     auto fetch = [&](int k0, uint4 (&v)[kPieces]) {
 #pragma unroll
-        for (int j = 0; j < kPieces; ++j) {
-            const int e = tid + 256 * j;
-            const int p = e / 512, rr = (e % 512) / 4, kq = (e % 4) * 16;
-            v[j] = make_uint4(0, 0, 0, 0);
-            if (rr < kQiRows) {
-                if (t0 + rr < n_tok)
-                    v[j] = *reinterpret_cast<const uint4*>(xdig + p * xplane + (int64_t)(t0 + rr) * dpad + k0 + kq);
-            } else if (c0 + rr - kQiRows < ncols) {
-                v[j] = *reinterpret_cast<const uint4*>(wdig + p * wplane + (int64_t)(c0 + rr - kQiRows) * dpad + k0 +
-                                                       kq);
-            }
+        for (int p = 0; p < 3; ++p) {
+            v[2 * p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs[p], voff, k0, 0));
+            v[2 * p + 1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[p], voff, k0, 0));
         }
     };
     auto put = [&](const uint4 (&v)[kPieces]) {
 #pragma unroll
-        for (int j = 0; j < kPieces; ++j) {
-            const int e = tid + 256 * j;
-            const int p = e / 512, rr = (e % 512) / 4, kq = (e % 4) * 16;
-            if (rr < kQiRows)
-                *reinterpret_cast<uint4*>(&xs[p][rr * kQiPitch + kq]) = v[j];
-            else
-                *reinterpret_cast<uint4*>(&ws[p][(rr - kQiRows) * kQiPitch + kq]) = v[j];
+        for (int p = 0; p < 3; ++p) {
+            *reinterpret_cast<uint4*>(&xs[p][prow * kQiPitch + kq]) = v[2 * p];
+            *reinterpret_cast<uint4*>(&ws[p][prow * kQiPitch + kq]) = v[2 * p + 1];
         }
     };
 
@@ -290,6 +301,7 @@ __global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict_
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[k][i] = 0;
 
+    if (tid < kQiRows && t0 + tid < n_tok) xmeta[tid] = meta[t0 + tid];
     uint4 nxt[kPieces];
     fetch(0, nxt);
     for (int k0 = 0; k0 < dpad; k0 += kQiKC) {
@@ -331,21 +343,25 @@ __global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict_
         const bool live = col_ok && t < n_tok;
         bool sure = false;
         if (live) {
-            const QRowMeta mx = meta[t];
-            if (mx.n_inex >= 0 && mw.n_inex >= 0) {
-                const int64_t P = ((int64_t)acc[0][i] << 28) + ((int64_t)acc[1][i] << 21) +
-                                  ((int64_t)acc[2][i] << 14) + ((int64_t)acc[3][i] << 7) + (int64_t)acc[4][i];
-                const double V = ldexp((double)P, mx.e + mw.e - 42);
-                const double et = (double)mx.n_inex * ldexp((double)mw.amax, mx.e - 21) +
-                                  (double)mw.n_inex * ldexp((double)mx.amax, mw.e - 21);
-                const double A = fmin((double)mx.amax * mw.l1, (double)mw.amax * mx.l1);
-                const double E = 1.01 * (et + (double)d * 0x1p-52 * A) + 0x1p-50 * (fabs(V) + fabs(b)) + 0x1p-1074;
-                const double sv = V + b;
-                const uint16_t lo = Elem<uint16_t>::from_f64(sv - E);
-                const uint16_t hi = Elem<uint16_t>::from_f64(sv + E);
-                sure = lo == hi;
-                if (sure) q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32(lo), al, be));
-            }
+            const QRowMeta mx = xmeta[t - t0];
+            const int64_t P = ((int64_t)acc[0][i] << 28) + ((int64_t)acc[1][i] << 21) + ((int64_t)acc[2][i] << 14) +
+                              ((int64_t)acc[3][i] << 7) + (int64_t)acc[4][i];
+            const double V = ldexp((double)P, mx.e + mw.e - 42);
+            const double A = fmin((double)mx.amax * mw.l1, (double)mw.amax * mx.l1);
+            // Both rows exact in the digit format and sum |F_i G_i| < 2^53: every partial sum
+            // of the chain is an integer multiple of 2^(E_x + E_w - 42) below 2^53 of them, so
+            // the chain never rounds and equals V (+0 for a zero sum, as the chain from +0
+            // gives); otherwise the certified interval.
+            const bool exact = mx.n_inex == 0 && mw.n_inex == 0 && A < ldexp(1.0, mx.e + mw.e + 11);
+            const double et = (double)mx.n_inex * ldexp((double)mw.amax, mx.e - 21) +
+                              (double)mw.n_inex * ldexp((double)mx.amax, mw.e - 21);
+            const double E =
+                exact ? 0.0 : 1.01 * (et + (double)d * 0x1p-52 * A) + 0x1p-50 * (fabs(V) + fabs(b)) + 0x1p-1074;
+            const double sv = V + b;
+            const uint16_t lo = Elem<uint16_t>::from_f64(sv - E);
+            const uint16_t hi = exact ? lo : Elem<uint16_t>::from_f64(sv + E);
+            sure = mx.n_inex >= 0 && mw.n_inex >= 0 && lo == hi;
+            if (sure) q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32(lo), al, be));
         }
         const bool queue = live && !sure;
         const uint64_t bal = __ballot(queue);
@@ -359,7 +375,13 @@ __global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict_
     }
 }
 
-// Exact fp64 chain for the queued elements (index order, as the contract defines).
+// Exact fp64 chain for the queued elements (index order, as the contract defines).  A
+// bf16 x bf16 product is exact in fp64 (16 significant bits, exponents within
+// [-266, 256]), so fma(x_i, w_i, acc) == acc + x_i w_i bit for bit: one wave per element
+// loads both rows with coalesced 16-byte loads, its 64 lanes write the products to LDS
+// (1024 per pass), and the first lane runs the dependent additions in index order.
+constexpr int kFixChunk = 1024;
+
 __global__ __launch_bounds__(256) void qproj_fixup_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
                                                           const uint16_t* __restrict__ bias,
@@ -367,27 +389,41 @@ __global__ __launch_bounds__(256) void qproj_fixup_kernel(const uint16_t* __rest
                                                           const float* __restrict__ beta, int d, int ncols,
                                                           const int32_t* __restrict__ count,
                                                           const int32_t* __restrict__ list, uint16_t* __restrict__ q) {
+    __shared__ __align__(16) double prod[4][kFixChunk];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    double* pw = prod[wave];
     const int n = *count;
-    for (int idx = blockIdx.x * 256 + threadIdx.x; idx < n; idx += gridDim.x * 256) {
+    for (int idx = blockIdx.x * 4 + wave; idx < n; idx += gridDim.x * 4) {
         const int e = list[idx];
         const int t = e / ncols, c = e - t * ncols;
         const uint16_t* xr = x + (int64_t)t * d;
         const uint16_t* wr = w + (int64_t)c * d;
         double acc = 0.0;
-        for (int i = 0; i < d; i += 8) {
-            const uint4 xa = *reinterpret_cast<const uint4*>(xr + i);
-            const uint4 wa = *reinterpret_cast<const uint4*>(wr + i);
-            const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
-            const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
+        for (int k0 = 0; k0 < d; k0 += kFixChunk) {
+            const int len = min(kFixChunk, d - k0);  // a multiple of 8
+            for (int g = lane; g < len / 8; g += kWave) {
+                const uint4 xa = *reinterpret_cast<const uint4*>(xr + k0 + 8 * g);
+                const uint4 wa = *reinterpret_cast<const uint4*>(wr + k0 + 8 * g);
+                const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
+                const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc = fma((double)__uint_as_float(xv[j] << 16), (double)__uint_as_float(wv[j] << 16), acc);
-                acc = fma((double)__uint_as_float(xv[j] & 0xffff0000u), (double)__uint_as_float(wv[j] & 0xffff0000u),
-                          acc);
+                for (int j = 0; j < 4; ++j) {
+                    pw[8 * g + 2 * j] = (double)__uint_as_float(xv[j] << 16) * (double)__uint_as_float(wv[j] << 16);
+                    pw[8 * g + 2 * j + 1] =
+                        (double)__uint_as_float(xv[j] & 0xffff0000u) * (double)__uint_as_float(wv[j] & 0xffff0000u);
+                }
             }
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) {
+#pragma unroll 16
+                for (int i = 0; i < len; ++i) acc = acc + pw[i];
+            }
+            __builtin_amdgcn_wave_barrier();
         }
-        const float ql = Elem<uint16_t>::round64(acc + (double)bf16_bits_to_f32(bias[c]));
-        q[e] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
+        if (lane == 0) {
+            const float ql = Elem<uint16_t>::round64(acc + (double)bf16_bits_to_f32(bias[c]));
+            q[e] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
+        }
     }
 }
 
