@@ -160,29 +160,6 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
-typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
-
-// Raw buffer resource (byte-addressed, stride 0, 32-bit num_records) for a global array.
-__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)base;
-    return i32x4_t{(int32_t)(uint32_t)a, (int32_t)(uint32_t)((a >> 32) & 0xffffu), (int32_t)bytes, 0x00020000};
-}
-
-// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (lds is the
-// wave-uniform LDS byte address).  Issued as inline asm so that the compiler does not
-// make later LDS reads of other buffers wait for the copy; the caller waits (vmcnt)
-// and synchronises before the copied data is read.
-__device__ __forceinline__ void lds_dma16(i32x4_t rsrc, int voff, int soff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
-                 "s"(soff)
-                 : "memory");
-}
-
-template <typename P>
-__device__ __forceinline__ uint32_t lds_addr(P* p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(__attribute__((address_space(3))) P*)p);
-}
-
 // Hidden rows, bf16: h = RN(gelu(RN(z W1^T))) for the unique experts, a workgroup of
 // 16 waves per CU with W1 resident in LDS (loaded once) and 32 experts per wave and
 // pass.  GEMM1 is computed transposed, hid^T = W1 . Z^T (A = W1 rows, B = gathered

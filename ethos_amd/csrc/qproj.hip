@@ -97,10 +97,7 @@ __global__ __launch_bounds__(256) void qproj_kernel(const T* __restrict__ x, con
 // non-finite value and sums within the bound of a rounding boundary are queued and
 // recomputed with the exact chain.
 // ---------------------------------------------------------------------------------
-constexpr int kQiRows = 64;             // tokens per workgroup tile (2 waves x 32)
-constexpr int kQiCols = 64;             // output columns per workgroup tile (2 waves x 32)
 constexpr int kQiKC = 64;               // reduction chunk (bytes of a digit row) staged in LDS
-constexpr int kQiPitch = kQiKC + 16;    // LDS row pitch (bytes)
 constexpr int kQiMaxD = 16384;          // int32 digit-product sums cannot overflow below this
 
 struct QRowMeta {
@@ -233,134 +230,216 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
     }
 }
 
-typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16_t __attribute__((ext_vector_type(16)));
 
-__global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict__ xdig,
-                                                       const int8_t* __restrict__ wdig,
-                                                       const QRowMeta* __restrict__ meta,
-                                                       const uint16_t* __restrict__ bias,
-                                                       const float* __restrict__ alpha,
-                                                       const float* __restrict__ beta, int n_tok, int d, int ncols,
-                                                       int32_t* __restrict__ count, int32_t* __restrict__ list,
-                                                       uint16_t* __restrict__ q) {
-    __shared__ __align__(16) int8_t xs[3][kQiRows * kQiPitch];
-    __shared__ __align__(16) int8_t ws[3][kQiCols * kQiPitch];
-    __shared__ QRowMeta xmeta[kQiRows];
+// Tile configuration: kWaves waves in kWaves / 2 rows x 2 columns, each wave 32 rows x
+// 32 kCB columns; kStages chunk buffers in LDS (kStages - 1 chunks in flight).
+template <int Waves, int CB, int Stages>
+struct QiCfg {
+    static constexpr int kWaves = Waves, kCB = CB, kStages = Stages;
+    static constexpr int kRows = 16 * kWaves;  // = 32 (kWaves / 2)
+    static constexpr int kCols = 64 * kCB;
+    static constexpr int kXB = kRows / (16 * kWaves);  // 16-row blocks each wave copies per x plane
+    static constexpr int kWB = kCols / (16 * kWaves);  // ... per w plane
+    static constexpr int kCopies = 3 * (kXB + kWB);    // 1 KB copies per wave per chunk
+    static constexpr int kStage = 3 * (kRows + kCols) * kQiKC;  // bytes of one chunk buffer
+    static constexpr size_t kTiles = (size_t)kStages * kStage;
+    static constexpr size_t kSmem = kTiles + kRows * (sizeof(float4) + sizeof(int2));
+    static_assert(kXB == 1 && kWB >= 1 && kCols == 16 * kWaves * kWB, "copy blocks");
+};
+using QiLaunch = QiCfg<4, 1, 2>;
+
+// s_waitcnt with vmcnt(n) and no expcnt / lgkmcnt wait (gfx9 encoding: vmcnt bits [3:0]
+// and [15:14], expcnt [6:4], lgkmcnt [11:8])
+constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
+
+// LDS chunk buffer layout: x digit planes 0-2 (kRows rows of 64 bytes each), then w digit
+// planes 0-2 (kCols rows each); each row's four 16-byte slots XOR-swizzled with bits 2-3 of
+// the row so that the MFMA fragment reads (16 lanes on 16 consecutive rows, one slot) hit 64
+// distinct banks.  The chunk buffers form a ring: the copies of the next kStages - 1 chunks
+// are in flight while one chunk is multiplied.
+__device__ __forceinline__ int qi_slot(int row, int piece) { return piece ^ ((row >> 2) & 3); }
+
+template <int kWaves, int kCB, int kStages>
+__global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __restrict__ xdig,
+                                                                 const int8_t* __restrict__ wdig,
+                                                                 const QRowMeta* __restrict__ meta,
+                                                                 const uint16_t* __restrict__ bias,
+                                                                 const float* __restrict__ alpha,
+                                                                 const float* __restrict__ beta, int n_tok, int d,
+                                                                 int ncols, int32_t* __restrict__ count,
+                                                                 int32_t* __restrict__ list,
+                                                                 uint16_t* __restrict__ q) {
+    using C = QiCfg<kWaves, kCB, kStages>;
+    constexpr int kQiRows = C::kRows, kQiCols = C::kCols;
+    extern __shared__ __align__(16) unsigned char qsm[];
+    int8_t* tiles = reinterpret_cast<int8_t*>(qsm);  // [stage][x planes, w planes][row][64 B]
+    // x row formats, scaled by 2^-E_x: {max|x| 2^-E, |x|_1 2^-E, n_inex 2^-21} and {E, n_inex}
+    float4* xpf = reinterpret_cast<float4*>(qsm + C::kTiles);
+    int2* xpi = reinterpret_cast<int2*>(qsm + C::kTiles + kQiRows * sizeof(float4));
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
-    const int wr = wave >> 1, wc = wave & 1;
+    const int wr = wave >> 1, wc = wave & 1;  // rows 32 wr .., columns 32 kCB wc ..
     const int t0 = blockIdx.y * kQiRows, c0 = blockIdx.x * kQiCols;
     const int dpad = qproj_dpad(d);
     const int64_t xplane = (int64_t)n_tok * dpad, wplane = (int64_t)ncols * dpad;
 
-    // One K chunk: per plane, each thread moves one 16-byte piece of an x row and one of a
-    // w row (row tid / kRowPieces, bytes 16 (tid % kRowPieces) of the chunk).  Buffer loads
-    // bounded by the tile's live rows return zeros past the last token / column.
-    constexpr int kRowPieces = kQiKC / 16;
-    static_assert(kQiRows * kRowPieces == 256 && kQiCols * kRowPieces == 256, "staging shape");
-    constexpr int kPieces = 6;
-    const int prow = tid / kRowPieces, kq = (tid % kRowPieces) * 16;
+    // Copies: wave w moves 16-row block w of every x plane and blocks w, w + kWaves, ... of
+    // every w plane, 1 KB each; lane l writes block bytes 16 l .. 16 l + 15 = block row
+    // l / 4, slot l % 4, so it loads the piece that the swizzle puts in that slot.  Buffer
+    // descriptors bounded by the tile's live rows return zeros past the last token / column.
     const int xrows = max(0, min(kQiRows, n_tok - t0)), wrows = max(0, min(kQiCols, ncols - c0));
-    // descriptors are wave-uniform: built from readfirstlane values so that they live in SGPRs
-    auto uniform_ptr = [](const int8_t* ptr) {
-        const uint64_t v = (uint64_t)(size_t)ptr;
-        const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-        const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
-        return reinterpret_cast<int8_t*>((size_t)(lo | (hi << 32)));
-    };
-    const int xbytes = __builtin_amdgcn_readfirstlane(xrows * dpad);
-    const int wbytes = __builtin_amdgcn_readfirstlane(wrows * dpad);
-    __amdgpu_buffer_rsrc_t xrs[3], wrs[3];
+    i32x4_t rs[6];
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
-        xrs[p] = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(xdig + p * xplane + (int64_t)t0 * dpad), (short)0,
-                                                   xbytes, 0x00020000);
-        wrs[p] = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(wdig + p * wplane + (int64_t)c0 * dpad), (short)0,
-                                                   wbytes, 0x00020000);
+        rs[p] = buffer_rsrc(xdig + p * xplane + (int64_t)t0 * dpad, (uint32_t)(xrows * dpad));
+        rs[3 + p] = buffer_rsrc(wdig + p * wplane + (int64_t)c0 * dpad, (uint32_t)(wrows * dpad));
     }
-    const int voff = prow * dpad + kq;
-    auto fetch = [&](int k0, uint4 (&v)[kPieces]) {
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
-            v[2 * p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs[p], voff, k0, 0));
-            v[2 * p + 1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[p], voff, k0, 0));
+    for (int r = 0; r < 6; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rs[r][j] = __builtin_amdgcn_readfirstlane(rs[r][j]);
+    auto xplane_lds = [&](int stage, int p) { return tiles + (size_t)stage * C::kStage + p * kQiRows * kQiKC; };
+    auto wplane_lds = [&](int stage, int p) {
+        return tiles + (size_t)stage * C::kStage + (3 * kQiRows + p * kQiCols) * kQiKC;
+    };
+    const int xrow = 16 * wave + lane / 4;
+    const int xvoff = xrow * dpad + 16 * qi_slot(xrow, lane % 4);
+    auto issue = [&](int k0, int stage) {
+#pragma unroll
+        for (int p = 0; p < 3; ++p) lds_dma16(rs[p], xvoff, k0, lds_addr(xplane_lds(stage, p) + wave * 1024));
+#pragma unroll
+        for (int j = 0; j < C::kWB; ++j) {
+            const int blk = wave + kWaves * j;
+            const int wrow = 16 * blk + lane / 4;
+            const int wvoff = wrow * dpad + 16 * qi_slot(wrow, lane % 4);
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+                lds_dma16(rs[3 + p], wvoff, k0, lds_addr(wplane_lds(stage, p) + blk * 1024));
         }
     };
-    auto put = [&](const uint4 (&v)[kPieces]) {
-#pragma unroll
-        for (int p = 0; p < 3; ++p) {
-            *reinterpret_cast<uint4*>(&xs[p][prow * kQiPitch + kq]) = v[2 * p];
-            *reinterpret_cast<uint4*>(&ws[p][prow * kQiPitch + kq]) = v[2 * p + 1];
-        }
-    };
+    static_assert(kStages >= 2 && kStages <= 4, "waits cover at most two chunks in flight past the current one");
 
-    i32x16_t acc[5];
-#pragma unroll
-    for (int k = 0; k < 5; ++k)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[k][i] = 0;
+    if (tid < kQiRows && t0 + tid < n_tok) {
+        const QRowMeta m = meta[t0 + tid];
+        xpf[tid] = make_float4(ldexpf(m.amax, -m.e), ldexpf(m.l1, -m.e), (float)m.n_inex * 0x1p-21f, 0.0f);
+        xpi[tid] = make_int2(m.e, m.n_inex);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the meta load is not counted among the copies below
 
-    if (tid < kQiRows && t0 + tid < n_tok) xmeta[tid] = meta[t0 + tid];
-    uint4 nxt[kPieces];
-    fetch(0, nxt);
-    for (int k0 = 0; k0 < dpad; k0 += kQiKC) {
-        __syncthreads();
-        put(nxt);
-        __syncthreads();
-        if (k0 + kQiKC < dpad) fetch(k0 + kQiKC, nxt);
+    i32x16_t acc[kCB][5];
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+        for (int k = 0; k < 5; ++k)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[cb][k][i] = 0;
+
+    const int arow = wr * 32 + l32;
+    const int nch = dpad / kQiKC;
+    issue(0, 0);
+#pragma unroll
+    for (int j = 1; j < kStages - 1; ++j)
+        if (j < nch) issue(j * kQiKC, j);
+    for (int kc = 0; kc < nch; ++kc) {
+        const int stage = kc % kStages;
+        // this wave's copies of chunk kc have landed once at most those of the chunks after
+        // it that are already issued (up to kStages - 2 of them, kCopies each) are pending
+        const int ahead = min(kStages - 2, nch - 1 - kc);
+        if (kStages == 2 || ahead == 0)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        else if (ahead == 1)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::kCopies));
+        else
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * C::kCopies));
+        __syncthreads();  // every wave's copies of chunk kc landed; chunk kc - 1 fully read
+        const int kn = kc + kStages - 1;
+        if (kn < nch) issue(kn * kQiKC, kn % kStages);  // into chunk kc - 1's buffer
 #pragma unroll
         for (int s = 0; s < kQiKC; s += 32) {
-            i32x4_t a[3], b[3];
+            const int piece = s / 16 + h;
+            i32x4_t a[3], b[kCB][3];
+            const int aoff = arow * kQiKC + 16 * qi_slot(arow, piece);
 #pragma unroll
-            for (int p = 0; p < 3; ++p) {
-                a[p] = *reinterpret_cast<const i32x4_t*>(&xs[p][(wr * 32 + l32) * kQiPitch + s + 16 * h]);
-                b[p] = *reinterpret_cast<const i32x4_t*>(&ws[p][(wc * 32 + l32) * kQiPitch + s + 16 * h]);
+            for (int p = 0; p < 3; ++p) a[p] = *reinterpret_cast<const i32x4_t*>(xplane_lds(stage, p) + aoff);
+#pragma unroll
+            for (int cb = 0; cb < kCB; ++cb) {
+                const int brow = wc * 32 * kCB + cb * 32 + l32;
+                const int boff = brow * kQiKC + 16 * qi_slot(brow, piece);
+#pragma unroll
+                for (int p = 0; p < 3; ++p) b[cb][p] = *reinterpret_cast<const i32x4_t*>(wplane_lds(stage, p) + boff);
             }
 #pragma unroll
-            for (int pa = 0; pa < 3; ++pa)
+            for (int cb = 0; cb < kCB; ++cb)
 #pragma unroll
-                for (int pb = 0; pb < 3; ++pb)
-                    acc[pa + pb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[pa], b[pb], acc[pa + pb], 0, 0, 0);
+                for (int pa = 0; pa < 3; ++pa)
+#pragma unroll
+                    for (int pb = 0; pb < 3; ++pb)
+                        acc[cb][pa + pb] =
+                            __builtin_amdgcn_mfma_i32_32x32x32_i8(a[pa], b[cb][pb], acc[cb][pa + pb], 0, 0, 0);
         }
     }
 
-    // certify each element; store it or queue it for the exact chain
-    const int c = c0 + wc * 32 + l32;
+    // Certify each element; store it or queue it for the exact chain.  The error bounds are
+    // evaluated in fp32 scaled by 2^-(E_x + E_w), where every term is O(1) (max|v| 2^-E lies
+    // in [1/2, 1), |v|_1 2^-E in [1/2, d]); the 1% slack covers their fp32 rounding.
+#pragma unroll
+  for (int cb = 0; cb < kCB; ++cb) {
+    const int c = c0 + wc * 32 * kCB + cb * 32 + l32;
     const bool col_ok = c < ncols;
-    QRowMeta mw = {0, -1, 0.0f, 0.0f};
+    int ew = 0, nw = -1;
+    float aw = 0.0f, lw = 0.0f, mw = 0.0f;
     double b = 0.0;
     float al = 0.0f, be = 0.0f;
     if (col_ok) {
-        mw = meta[n_tok + c];
+        const QRowMeta m = meta[n_tok + c];
+        ew = m.e;
+        nw = m.n_inex;
+        aw = ldexpf(m.amax, -m.e);
+        lw = ldexpf(m.l1, -m.e);
+        mw = (float)m.n_inex * 0x1p-21f;
         b = (double)bf16_bits_to_f32(bias[c]);
         al = alpha[c];
         be = beta[c];
     }
+    const float dscale = (float)d * 0x1p-52f;  // chain rounding: d 2^-52 A'
+    const float dterm = (float)d * 0x1p-12f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int t = t0 + wr * 32 + mfma32_row(i, lane);
+        const int tl = wr * 32 + mfma32_row(i, lane);
+        const int t = t0 + tl;
         const bool live = col_ok && t < n_tok;
         bool sure = false;
         if (live) {
-            const QRowMeta mx = xmeta[t - t0];
-            const int64_t P = ((int64_t)acc[0][i] << 28) + ((int64_t)acc[1][i] << 21) + ((int64_t)acc[2][i] << 14) +
-                              ((int64_t)acc[3][i] << 7) + (int64_t)acc[4][i];
-            const double V = ldexp((double)P, mx.e + mw.e - 42);
-            const double A = fmin((double)mx.amax * mw.l1, (double)mw.amax * mx.l1);
-            // Both rows exact in the digit format and sum |F_i G_i| < 2^53: every partial sum
-            // of the chain is an integer multiple of 2^(E_x + E_w - 42) below 2^53 of them, so
-            // the chain never rounds and equals V (+0 for a zero sum, as the chain from +0
-            // gives); otherwise the certified interval.
-            const bool exact = mx.n_inex == 0 && mw.n_inex == 0 && A < ldexp(1.0, mx.e + mw.e + 11);
-            const double et = (double)mx.n_inex * ldexp((double)mw.amax, mx.e - 21) +
-                              (double)mw.n_inex * ldexp((double)mx.amax, mw.e - 21);
+            const float4 xf = xpf[tl];
+            const int2 xi = xpi[tl];
+            // P = sum_k 2^(7 (4 - k)) C_k by an fp64 Horner chain on the int32 sums.  Its
+            // partial sums (scaled to units of P) are integers of magnitude at most
+            // B = sum_i (|F_i| + 2^15)(|G_i| + 2^15) <= 2^42 H', where in units of
+            // 2^(E_x + E_w) H' = A' + 2^-6 (|x|_1 + |w|_1) + d 2^-12 and A' bounds
+            // sum |x_i w_i|.  Below 2^53 (H' < 2^11) the chain is exact; otherwise its four
+            // roundings add at most 2^-51 H' to the error.
+            double Pd = (double)acc[cb][0][i];
+            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][1][i]);
+            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][2][i]);
+            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][3][i]);
+            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][4][i]);
+            const double V = ldexp(Pd, xi.x + ew - 42);
+            const float As = fminf(xf.x * lw, aw * xf.y);
+            const float Hs = As + 0x1p-6f * (xf.y + lw) + dterm;
+            // Both rows exact in the digit format and H' < 2^11 (with margin for the rounding
+            // of H'): V is exact, and so is every partial sum of the chain (an integer multiple
+            // of 2^(E_x + E_w - 42) below 2^53 of them), so the chain never rounds and equals V
+            // (+0 for a zero sum, as the chain from +0 gives); otherwise the certified interval.
+            const bool exact = (xi.y | nw) == 0 && Hs < 2047.0f;
+            const float Es =
+                1.01f * (__builtin_fmaf(dscale, As, __builtin_fmaf(xf.z, aw, mw * xf.x)) + 0x1p-51f * Hs);
             const double E =
-                exact ? 0.0 : 1.01 * (et + (double)d * 0x1p-52 * A) + 0x1p-50 * (fabs(V) + fabs(b)) + 0x1p-1074;
+                exact ? 0.0 : ldexp((double)Es, xi.x + ew) + 0x1p-50 * (fabs(V) + fabs(b)) + 0x1p-1074;
             const double sv = V + b;
             const uint16_t lo = Elem<uint16_t>::from_f64(sv - E);
             const uint16_t hi = exact ? lo : Elem<uint16_t>::from_f64(sv + E);
-            sure = mx.n_inex >= 0 && mw.n_inex >= 0 && lo == hi;
+            sure = xi.y >= 0 && nw >= 0 && lo == hi;
             if (sure) q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32(lo), al, be));
         }
         const bool queue = live && !sure;
@@ -373,6 +452,7 @@ __global__ __launch_bounds__(256) void qproj_i8_kernel(const int8_t* __restrict_
             if (queue) list[base + (int)__popcll(bal & ((1ull << lane) - 1ull))] = t * ncols + c;
         }
     }
+  }
 }
 
 // Exact fp64 chain for the queued elements (index order, as the contract defines).  A
@@ -439,9 +519,11 @@ int launch_qproj(const void* x, const void* w, const void* b, const float* alpha
         const int64_t rows = n_tok + ncols;
         hipLaunchKernelGGL(qproj_digits_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream,
                            (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, d, W.xdig, W.wdig, W.meta);
-        dim3 grid((ncols + kQiCols - 1) / kQiCols, (unsigned)((n_tok + kQiRows - 1) / kQiRows));
-        hipLaunchKernelGGL(qproj_i8_kernel, grid, dim3(256), 0, stream, W.xdig, W.wdig, W.meta, (const uint16_t*)b,
-                           alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q);
+        using C = QiLaunch;
+        dim3 grid((ncols + C::kCols - 1) / C::kCols, (unsigned)((n_tok + C::kRows - 1) / C::kRows));
+        hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages>), grid, dim3(C::kWaves * 64), C::kSmem,
+                           stream, W.xdig, W.wdig, W.meta, (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols,
+                           W.count, W.list, (uint16_t*)q);
         hipLaunchKernelGGL(qproj_fixup_kernel, dim3((unsigned)num_cus * 4), dim3(256), 0, stream, (const uint16_t*)x,
                            (const uint16_t*)w, (const uint16_t*)b, alpha, beta, d, ncols, W.count, W.list,
                            (uint16_t*)q);
