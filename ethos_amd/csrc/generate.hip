@@ -291,7 +291,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
     parts = parts < 1 ? 1 : (parts > n_chunks ? n_chunks : parts);
     const int cpp = (n_chunks + parts - 1) / parts;  // chunks per part
     const int n_units = n_full + rem * parts;
-    constexpr int kOOB = 0x7fff0000;  // a byte offset past any tile's rows
+    constexpr int kOOB = 0x40000000;  // a byte offset past any tile's rows (and kOOB + 56 d2 * 2 < 2^31)
 
     for (int w = blockIdx.x; w < n_units; w += G) {
         int tile = w, c_begin = 0, c_end = n_chunks;
@@ -448,6 +448,201 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
     }
 }
 
+// ---------------------------------------------------------------------------------
+// v rows, bf16, W_v-stationary: v = RN(h W_v^T) where each workgroup owns 256 output
+// columns (64 per wave) for the whole launch, their W_v rows held in AGPRs (loaded
+// once), and the hidden rows stream through LDS in tiles of 64 experts.  A tile's rows
+// (64 x DH bf16, contiguous in h) are copied global -> LDS by buffer_load ... lds one
+// tile ahead, double buffered; each B-fragment read from LDS feeds two MFMAs (one per
+// 32-column block).  The d / 256 workgroups that share a tile (one per column group)
+// form a group placed on one XCD, so one of them brings the tile in from HBM and the
+// others find it in that XCD's L2.  Operands and k-steps are those of
+// expand_bf16_kernel (A = W_v rows, B = hidden rows, k-steps in order), so v is
+// bit-identical to it; the difference is that no tile waits for its hidden rows.
+// ---------------------------------------------------------------------------------
+constexpr int kWsCols = 256;  // output columns per workgroup, 64 per wave
+constexpr int kWsRows = 64;   // experts per tile
+
+template <int DH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void expand_ws_bf16_kernel(
+    const int32_t* __restrict__ n_unique, int64_t max_unique, const uint16_t* __restrict__ hin,
+    const uint16_t* __restrict__ w2, int d2, int n_cg, uint16_t* __restrict__ uv) {
+    constexpr int KS2 = DH / 16;                         // k-steps
+    constexpr int GPR = DH / 8;                          // 16-byte groups per hidden row
+    constexpr int kCopiesW = kWsRows * GPR / 64 / 4;     // copy instructions per wave and tile
+    constexpr int LA = 4;                                // fragment reads run LA k-steps ahead
+    constexpr int kCS = kCopiesW / 4;                    // k-steps that issue copies (4 each)
+    constexpr int kNSt = 8;                              // v-row stores per wave and tile
+    static_assert(GPR >= 16 && (GPR & (GPR - 1)) == 0 && kCopiesW % 4 == 0 && kCS + kNSt <= KS2,
+                  "tile staging shape");
+    // Hidden tiles: row r's 16-byte group g sits at slot g ^ (r % 16) of the row, so a
+    // fragment read (one group, 16 consecutive rows per 256 bytes of banks) is
+    // conflict-free.
+    __shared__ uint4 hs[2][kWsRows * GPR];
+    // Output staging, per wave: 64 experts x 64 columns of bf16; expert r's 128-byte
+    // row holds its 16-byte group q at slot q ^ (r % 8).
+    __shared__ u32x4_t stg[4][kWsRows * 8];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    // the h and v outputs hold max_unique rows
+    const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
+    const int n_tiles = (U + kWsRows - 1) / kWsRows;
+    // Workgroup b runs on XCD b % 8.  Slots b / 8 of one XCD are taken n_cg at a time:
+    // the members of one group, column groups 0 .. n_cg - 1.  (The launch makes the
+    // grid a multiple of 8 n_cg.)
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int per_xcd = ((int)gridDim.x >> 3) / n_cg;
+    const int cg = slot % n_cg, grp = xcd * per_xcd + slot / n_cg;
+    const int n_groups = 8 * per_xcd;
+    const int col0 = cg * kWsCols + wave * 64;  // the wave's first output column
+
+    // the wave's W_v rows: A fragment (cb, s) = W_v[col0 + 32 cb + l32][16 s + 8 h ..]
+    bf16x8_t wf[2][KS2];
+    {
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(w2), (short)0, d2 * DH * (int)sizeof(uint16_t), 0x00020000);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int s = 0; s < KS2; ++s)
+                wf[cb][s] = __builtin_bit_cast(
+                    bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                  wr, ((col0 + 32 * cb + l32) * DH + 16 * s + 8 * h) * (int)sizeof(uint16_t), 0, 0));
+    }
+    // Copy instruction j = 4 it + wave of a tile moves LDS slots 64 j .. 64 j + 63 (lane
+    // i: slot f = 64 j + i, row f / GPR, slot f % GPR of that row, which holds global
+    // group (f % GPR) ^ (row % 16)).  Rows at or past U read as zero (the descriptor
+    // covers rows below U only).
+    auto copy = [&](int64_t tile, int buf, int it) {
+        const int64_t row0 = tile * kWsRows;
+        const int64_t live = U - row0;
+        const int rows = live < kWsRows ? (int)live : kWsRows;
+        const i32x4_t rs = buffer_rsrc(hin + row0 * DH, (uint32_t)rows * DH * (uint32_t)sizeof(uint16_t));
+        const int j = 4 * it + wave;
+        const int f = 64 * j + lane;
+        const int r = f / GPR, gs = f % GPR;
+        lds_dma16(rs, (r * DH + 8 * (gs ^ (r & 15))) * (int)sizeof(uint16_t), 0, lds_addr(&hs[buf][64 * j]));
+    };
+    // B fragment (mb, s) of the current tile: row 32 mb + l32, group 2 s + h, at slot
+    // (2 s + h) ^ (l32 % 16) = ((2 (s % 8) + h) ^ (l32 % 16)) + 16 (s / 8)
+    int bq_off[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) bq_off[q] = l32 * GPR + ((2 * q + h) ^ (l32 & 15));
+    // lane's store k covers staged row 8 k + lane / 8, 16-byte group lane % 8
+    const int st_voff = ((lane >> 3) * d2 + col0 + 8 * (lane & 7)) * (int)sizeof(uint16_t);
+    constexpr int kOOB = 0x40000000;  // a byte offset past any tile's rows (and kOOB + 56 d2 * 2 < 2^31)
+    u32x4_t* my = stg[wave];
+    u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
+    // s_waitcnt vmcnt(8) (gfx9 immediate: vmcnt [3:0] and [15:14], expcnt [6:4],
+    // lgkmcnt [11:8]; expcnt 7 and lgkmcnt 15 do not wait)
+    constexpr int kWaitVm8 = 0x0f78;
+    constexpr int kWaitVm0 = 0x0f70;
+
+    if (grp < n_tiles) {
+#pragma unroll
+        for (int it = 0; it < kCopiesW; ++it) copy(grp, 0, it);
+    }
+    // the W_v rows and the first tile
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+
+    // stores of the previous tile's staged rows go through that tile's descriptor
+    // (rows below max_unique)
+    __amdgpu_buffer_rsrc_t uvr_prev = __builtin_amdgcn_make_buffer_rsrc(uv, (short)0, 0, 0x00020000);
+    bool have_prev = false;
+    int i = 0;
+    for (int64_t t = grp; t < n_tiles; t += n_groups, ++i) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this tile's copies have landed
+        __syncthreads();
+        const int64_t t_next = t + n_groups;
+        u32x4_t outv[kNSt];
+#pragma unroll
+        for (int k = 0; k < kNSt; ++k) {
+            const int r = 8 * k + (lane >> 3);
+            outv[k] = my[r * 8 + ((lane & 7) ^ (r & 7))];
+        }
+        const int st_base = have_prev ? st_voff : kOOB;
+        const uint4* cur = hs[i & 1];
+        auto bfrag = [&](int s, int mb) {
+            return __builtin_bit_cast(bf16x8_t, cur[bq_off[s & 7] + 16 * (s >> 3) + mb * 32 * GPR]);
+        };
+        bf16x8_t bfr[LA + 1][2];
+        f32x16_t acc[2][2];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) acc[mb][cb] = f32x16_zero();
+#pragma unroll
+        for (int s = 0; s < LA; ++s)
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) bfr[s][mb] = bfrag(s, mb);
+#pragma unroll
+        for (int s = 0; s < KS2; ++s) {
+            if (s + LA < KS2) {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) bfr[(s + LA) % (LA + 1)][mb] = bfrag(s + LA, mb);
+            }
+            // the W_v fragments stay in AGPRs: the MFMAs take them from there directly
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) asm volatile("" : "+a"(wf[cb][s]));
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                    acc[mb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb][s], bfr[s % (LA + 1)][mb],
+                                                                         acc[mb][cb], 0, 0, 0);
+            // copies of the next tile, four per k-step
+            if (s < kCS && t_next < n_tiles) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) copy(t_next, (i + 1) & 1, 4 * s + j);
+            }
+            // the previous tile's rows, one store per k-step
+            if (s >= kCS && s < kCS + kNSt)
+                __builtin_amdgcn_raw_buffer_store_b128(outv[s - kCS], uvr_prev, st_base + (s - kCS) * 8 * d2 * 2, 0,
+                                                       2);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, kNSt + 2 * LA, 0);
+#pragma unroll
+        for (int s = 0; s < KS2; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            if (s >= kCS && s < kCS + kNSt) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
+        }
+        // acc[mb][cb][i]: column col0 + 32 cb + 8 (i/4) + 4h + i%4 of expert 32 mb + l32
+        // of the tile, i.e. 8-byte half h of 16-byte group 4 cb + i/4 of staged row
+        // 32 mb + l32
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int r = mb * 32 + l32;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    const int q = 4 * cb + a4;
+                    my2[r * 16 + (q ^ (r & 7)) * 2 + h] =
+                        u32x2_t{pack_bf16x2(acc[mb][cb][4 * a4], acc[mb][cb][4 * a4 + 1]),
+                                pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3])};
+                }
+        }
+        const int64_t row0 = t * kWsRows;
+        const int64_t rows_left = max_unique - row0;
+        const int tile_rows = rows_left < kWsRows ? (int)rows_left : kWsRows;
+        uvr_prev = __builtin_amdgcn_make_buffer_rsrc(uv + row0 * d2, (short)0,
+                                                     tile_rows * d2 * (int)sizeof(uint16_t), 0x00020000);
+        have_prev = true;
+    }
+    // the last tile's rows (the staging writes above are this wave's own LDS operations,
+    // which complete in order)
+    if (have_prev) {
+#pragma unroll
+        for (int k = 0; k < kNSt; ++k) {
+            const int r = 8 * k + (lane >> 3);
+            __builtin_amdgcn_raw_buffer_store_b128(my[r * 8 + ((lane & 7) ^ (r & 7))], uvr_prev,
+                                                   st_voff + k * 8 * d2 * 2, 0, 2);
+        }
+    }
+}
+
 template <int DL, int DH>
 static bool launch_generate_bf16(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                                  int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* hout,
@@ -457,6 +652,15 @@ static bool launch_generate_bf16(const void* latents, int64_t n_experts, const i
     const unsigned g1 = (unsigned)(blocks < num_cus ? (blocks > 0 ? blocks : 1) : num_cus);
     hipLaunchKernelGGL((hidden_bf16_kernel<DL, DH>), dim3(g1), dim3(kHWaves * 64), 0, stream,
                        (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (uint16_t*)hout);
+    // W_v-stationary when d2 splits into 256-column groups that fill the XCDs evenly
+    const int n_cg = d2 / kWsCols;
+    const int per_xcd = d2 % kWsCols == 0 && n_cg > 0 ? (num_cus / 8) / n_cg : 0;
+    if (per_xcd > 0 && (int64_t)d2 * DH * 2 < (1ll << 31)) {
+        const unsigned g2 = (unsigned)(8 * per_xcd * n_cg);
+        hipLaunchKernelGGL((expand_ws_bf16_kernel<DH>), dim3(g2), dim3(256), 0, stream, n_unique, max_unique,
+                           (const uint16_t*)hout, (const uint16_t*)w2, d2, n_cg, (uint16_t*)uv);
+        return true;
+    }
     const int64_t tiles = (max_unique + kG2Rows - 1) / kG2Rows;
     const int64_t cap = num_cus;  // one workgroup per CU
     const unsigned grid = (unsigned)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);

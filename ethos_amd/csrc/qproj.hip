@@ -140,15 +140,17 @@ __host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols, 
     return w;
 }
 
-__global__ void qproj_clear_kernel(int32_t* __restrict__ count) { *count = 0; }
-
 __device__ __forceinline__ uint32_t qp_wave_max_u32(uint32_t v) { return (uint32_t)wave_max_u64((uint64_t)v); }
 
-// One wave per row of x (rows < n_tok) or Wq: digit planes and the row's format.
+// One wave per row of x (rows < n_tok) or Wq: digit planes and the row's format.  The
+// first thread also resets the uncertain-element count (read by the kernels after this one
+// on the same stream).
 __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ w, int n_tok, int ncols,
                                                            int d, int8_t* __restrict__ xdig,
-                                                           int8_t* __restrict__ wdig, QRowMeta* __restrict__ meta) {
+                                                           int8_t* __restrict__ wdig, QRowMeta* __restrict__ meta,
+                                                           int32_t* __restrict__ count) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *count = 0;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= (int64_t)n_tok + ncols) return;
@@ -515,10 +517,10 @@ int launch_qproj(const void* x, const void* w, const void* b, const float* alpha
                  int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream) {
     if (dtype == kBF16 && d <= kQiMaxD) {
         const QprojWs W = qproj_ws(ws, n_tok, ncols, d);
-        hipLaunchKernelGGL(qproj_clear_kernel, dim3(1), dim3(1), 0, stream, W.count);
         const int64_t rows = n_tok + ncols;
         hipLaunchKernelGGL(qproj_digits_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream,
-                           (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, d, W.xdig, W.wdig, W.meta);
+                           (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, d, W.xdig, W.wdig, W.meta,
+                           W.count);
         using C = QiLaunch;
         dim3 grid((ncols + C::kCols - 1) / C::kCols, (unsigned)((n_tok + C::kRows - 1) / C::kRows));
         hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages>), grid, dim3(C::kWaves * 64), C::kSmem,

@@ -244,10 +244,11 @@ def test_route_stress_bit_exact(kind, dt):
 
 
 @pytest.mark.parametrize("dl,dh,d,U", [(128, 256, 1024, 1000), (128, 512, 512, 300), (128, 512, 1024, 129),
-                                        (128, 512, 1024, 1)])
+                                        (128, 512, 1024, 1), (128, 512, 768, 3001), (128, 256, 320, 1000)])
 def test_generate_shapes(dl, dh, d, U):
-    """Generator over shapes the configs do not hit (hidden 256, a 512-wide model, tile
-    remainders and a single expert)."""
+    """Generator over shapes the configs do not hit (hidden 256, 512- and 768-wide models
+    (two and three 256-column groups), a 320-wide model (not a multiple of 256 columns),
+    tile remainders and a single expert)."""
     rng = np.random.default_rng(dl + dh + d + U)
     E = 5000
     lat = O.f32_to_bf16_bits(rng.standard_normal((E, dl)).astype(np.float32))

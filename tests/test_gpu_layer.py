@@ -135,6 +135,50 @@ def test_layer_cfg2_full_size():
     check_out(O.to_f32(to_host(y), "bf16")[sub[:64]], r["out"], "bf16", nerr_max=2e-3)
 
 
+def test_layer_cfg4_zipf_full_size():
+    """Config 4 at full size: 32,768 tokens with Zipf(1.1)-skewed sub-key rows, so a few
+    thousand unique experts carry 4.2 M pairs and the largest segments hold tens of
+    thousands of pairs.  Every routing row (ids and gates) bit-exact against the oracle,
+    segment offsets against a histogram of the ids, and the output of a token subset
+    against the oracle."""
+    sh = SHAPES["cfg4"]
+    x, sd = make_inputs(sh)
+    m = _layer(sh, sd)
+    xd = x.cuda()
+    with torch.no_grad():
+        q = m.router.queries(xd)
+        gates, ids = m.router.route(xd)
+        seg = hip.sort_segment(ids.view(-1), sh.num_experts)
+        y = m(xd.view(sh.batch, -1, sh.d_model)).view(sh.n_tok, -1)
+    torch.cuda.synchronize()
+    P = O.unpack_state(sd, sh.num_heads)
+    xs = O.from_torch(x)
+    qh = to_host(q)
+    sub = np.arange(0, sh.n_tok, 128)
+    q_ref = O.query_proj(xs[sub], P["Wq"], P["bq"], P["alpha"], P["beta"], "bf16")
+    assert np.array_equal(qh[sub], q_ref)
+    g_ref, ids_ref = O.route(qh, P["K1"], P["K2"], sh.top_k, "bf16")
+    assert np.array_equal(to_host(ids), ids_ref)
+    # gates: a bf16 rounding of an fp32 softmax whose expf may differ by an fp32 ulp from the
+    # oracle's, which flips the bf16 rounding of about 2^-15 of 4.2 M positive values
+    gd = np.abs(to_host(gates).view(np.uint16).astype(np.int32) - g_ref.view(np.uint16).astype(np.int32))
+    assert gd.max() <= 1 and np.count_nonzero(gd) <= 1e-4 * gd.size, (gd.max(), np.count_nonzero(gd))
+    # segments: unique ids ascending, offsets = running histogram of the ids
+    flat = ids.view(-1).long()
+    U = int(seg["n_unique"].item())
+    uq, counts = torch.unique(flat, return_counts=True)
+    assert U == uq.numel() and torch.equal(seg["uniq"][:U].long(), uq)
+    off = seg["seg_off"][: U + 1].long()
+    assert int(off[0]) == 0 and torch.equal(off[1:] - off[:-1], counts)
+    assert int(counts.max()) > 10_000, "the skew should give segments of tens of thousands of pairs"
+    perm = seg["perm"].long()
+    assert torch.equal(torch.sort(perm).values, torch.arange(flat.numel(), device="cuda"))
+    assert bool((flat[perm][1:] >= flat[perm][:-1]).all())
+    # output for a token subset
+    r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub[:64], q=qh)
+    check_out(O.to_f32(to_host(y), "bf16")[sub[:64]], r["out"], "bf16", nerr_max=2e-3)
+
+
 def test_router_rejects_cpu_and_bad_shapes():
     sh = SHAPES["tiny"]
     x, sd = make_inputs(sh)
