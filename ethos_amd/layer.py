@@ -16,8 +16,15 @@ d_intermediate_hypernet and d_query.
 Forward runs five HIP stages on the current stream (include/ethos_hip.h): query
 projection + BatchNorm, product-key routing, reordering by expert id, expert
 generation over the unique experts, and apply + scatter-back.  Inputs must be HIP
-tensors; there is no CPU path.  Like the reference Triton layer (kernels.py:145-221),
-the forward is not differentiable: the output carries no autograd graph.
+tensors; there is no CPU path.
+
+With autograd enabled (the input or a parameter requires grad, outside torch.no_grad)
+the output carries a graph whose gradients are those of the reference's pure-PyTorch
+layer (model.py:288-343, differentiated by autograd there): through the routing gates
+to the query projections, BatchNorm affine parameters and sub-keys (the topk values
+and softmax, model.py:215-234), and through the generated experts to x, the expert
+latents and both generator weights.  The forward values are the HIP kernels' in both
+cases; the reference's Triton layer (kernels.py:145-221) has no backward at all.
 """
 from __future__ import annotations
 
@@ -46,6 +53,93 @@ def _bn_eval_coefficients(m: nn.BatchNorm1d, n: int):
     alpha = (w / np.sqrt(var + float(m.eps))).astype(np.float32)
     beta = (b - mu * alpha.astype(np.float64)).astype(np.float32)
     return alpha, beta
+
+
+def _gelu_grad(x: torch.Tensor) -> torch.Tensor:
+    """Derivative of the erf GELU x·Φ(x): Φ(x) + x·φ(x)."""
+    cdf = 0.5 * (1.0 + torch.erf(x * (1.0 / math.sqrt(2.0))))
+    pdf = torch.exp(-0.5 * x * x) * (1.0 / math.sqrt(2.0 * math.pi))
+    return cdf + x * pdf
+
+
+class _ExpertStages(torch.autograd.Function):
+    """Expert generation, apply and scatter-back as one autograd node.
+
+    Forward: the HIP generator and apply kernels, given the routing (gates, the sorted
+    pair segments).  Backward: the derivative of the reference's per-pair expression
+    (model.py:312-341), evaluated in float32 from the saved routing and generated rows.
+    With A = W2[:d], B = W2[d:] (net.2.weight halves), C = W1 (net.0.weight), pair p of
+    token t(p) using unique expert s(p):
+
+        pre_s = z_s C^T,  h_s = gelu(pre_s),  v_s = h_s B^T,  xp_t = x_t A,
+        c_p = h_s · xp_t,  a_p = gelu(c_p) g_p,  y_t = (1/H) Σ_p a_p v_s
+
+    so with dY_t = dy_t / H:  da_p = dY_t · v_s;  dv_s = Σ_p a_p dY_t;  dg_p = gelu(c_p) da_p;
+    dc_p = g_p gelu'(c_p) da_p;  dxp_t = Σ_p dc_p h_s;  dh_s = Σ_p dc_p xp_t + dv_s B;
+    dA = x^T dxp,  dB = dv^T h,  dx = dxp A^T;  dpre = gelu'(pre) dh,  dC = dpre^T z,
+    dz = dpre C (added into the latent rows of the unique experts).  The per-pair sums run
+    over chunks of pairs with index_add, so temporaries stay bounded.
+
+    The gates enter as `gates_exact` (the values the forward uses) and `gate_path` (a
+    float32 tensor of the same values carrying the router's graph), whose gradient is dg.
+    """
+
+    @staticmethod
+    def forward(ctx, x, gate_path, latents_w, w1_w, w2_w, layer, gates_exact, seg):
+        latents, w1, w2 = layer._generator_params(x.dtype, x.device)
+        h, v = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2)
+        out = hip.apply_scatter(x, w2, h, v, seg, gates_exact, layer.num_heads, layer.top_k)
+        ctx.save_for_backward(x, gates_exact, h, v, seg["uniq"], seg["pair_slot"], seg["n_unique"], latents, w1, w2)
+        ctx.heads, ctx.top_k = layer.num_heads, layer.top_k
+        ctx.param_dtypes = (latents_w.dtype, w1_w.dtype, w2_w.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, gates, h, v, uniq, pair_slot, n_unique, latents, w1, w2 = ctx.saved_tensors
+        H, k = ctx.heads, ctx.top_k
+        n, d = x.shape
+        f = torch.float32
+        U = int(n_unique.item())
+        A, B, C = w2[:d].to(f), w2[d:].to(f), w1.to(f)
+        xf = x.to(f)
+        xp = xf @ A
+        hf, vf = h[:U].to(f), v[:U].to(f)
+        g = gates.reshape(-1).to(f)
+        slot = pair_slot.long()
+        dY = dy.to(f) * (1.0 / H)
+        n_pairs = n * H * k
+        dv = torch.zeros_like(vf)
+        dh = torch.zeros_like(hf)
+        dxp = torch.zeros_like(xp)
+        dg = torch.empty(n_pairs, dtype=f, device=x.device)
+        chunk = max(1024, (1 << 25) // max(d, 1))
+        for p0 in range(0, n_pairs, chunk):
+            p = torch.arange(p0, min(n_pairs, p0 + chunk), device=x.device)
+            t, s = p // (H * k), slot[p]
+            hp, xpp, dYp = hf[s], xp[t], dY[t]
+            c = (hp * xpp).sum(-1)
+            act = F.gelu(c)
+            da = (dYp * vf[s]).sum(-1)
+            gp = g[p]
+            dv.index_add_(0, s, (act * gp)[:, None] * dYp)
+            dg[p] = act * da
+            dc = gp * _gelu_grad(c) * da
+            dxp.index_add_(0, t, dc[:, None] * hp)
+            dh.index_add_(0, s, dc[:, None] * xpp)
+        dh += dv @ B
+        dB = dv.T @ hf
+        dA = xf.T @ dxp
+        dx = dxp @ A.T
+        ids = uniq[:U].long()
+        z = latents[ids].to(f)
+        dpre = _gelu_grad(z @ C.T) * dh
+        dC = dpre.T @ z
+        dlat = torch.zeros(latents.shape, dtype=f, device=x.device)
+        dlat.index_add_(0, ids, dpre @ C)
+        lat_dt, w1_dt, w2_dt = ctx.param_dtypes
+        return (dx.to(x.dtype), dg.view(gates.shape), dlat.to(lat_dt), dC.to(w1_dt),
+                torch.cat([dA, dB], 0).to(w2_dt), None, None, None)
 
 
 class ExpertGenerationNetwork(nn.Module):
@@ -144,10 +238,42 @@ class ProductKeyRouter(nn.Module):
             mark("route")
         return out
 
+    def gate_path(self, x_flat: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+        """float32 gates [n, H, k] recomputed with torch operations from the chosen expert ids,
+        carrying autograd to x, the query projections, the BatchNorm affine parameters and
+        both sub-key tables as the reference's topk values and softmax do (model.py:215-234):
+        g = softmax(q1 · K1[i1] + q2 · K2[i2]) with i1 = id // K, i2 = id % K.  BatchNorm uses
+        the module's mode (batch statistics when training) without touching the running
+        statistics, which the routing pass has already updated."""
+        f = torch.float32
+        H, dq, K = self.num_heads, self.d_query, self.num_sub_keys
+        w = torch.stack([m.weight for m in self.query_projs]).to(f).reshape(H * dq, -1)
+        b = torch.stack([m.bias for m in self.query_projs]).to(f).reshape(-1)
+        q = (x_flat.to(f) @ w.T + b).view(-1, H, dq)
+        qs = []
+        for h, m in enumerate(self.query_norms):
+            batch = m.training or not m.track_running_stats
+            qs.append(F.batch_norm(q[:, h], None if batch else m.running_mean.to(f),
+                                   None if batch else m.running_var.to(f),
+                                   m.weight.to(f) if m.affine else None, m.bias.to(f) if m.affine else None,
+                                   batch, 0.0, m.eps))
+        q = torch.stack(qs, dim=1)
+        half = dq // 2
+        i1, i2 = ids // K, ids % K
+        s1 = (q[:, :, None, :half] * self.sub_keys_1.weight.to(f)[i1]).sum(-1)
+        s2 = (q[:, :, None, half:] * self.sub_keys_2.weight.to(f)[i2]).sum(-1)
+        return torch.softmax(s1 + s2, dim=-1)
+
     def forward(self, x_flat: torch.Tensor):
+        """(scores [n, H, k], expert ids [n, H, k] int64) as model.py:208-254.  With autograd
+        enabled the scores carry the gradient of the reference's topk + softmax."""
         with torch.no_grad():
             gates, ids = self.route(_as_input(x_flat, 2))
-        return gates, ids.long()
+        ids = ids.long()
+        if _wants_grad(x_flat, self):
+            g = self.gate_path(x_flat, ids)
+            gates = gates + (g - g.detach()).to(gates.dtype)
+        return gates, ids
 
 
 class EthosExpertLayer(nn.Module):
@@ -192,6 +318,13 @@ class EthosExpertLayer(nn.Module):
     def forward_flat(self, x_flat: torch.Tensor, mark=None) -> torch.Tensor:
         """The layer on [n_tok, d_model] rows (model.py:288-343).  `mark(stage)`, if given, is
         called after each of the five stages is enqueued on the current stream."""
+        if _wants_grad(x_flat, self):
+            with torch.no_grad():
+                gates, ids = self.router.route(x_flat)
+                seg = hip.sort_segment(ids.view(-1), self.num_experts)
+            g = self.router.gate_path(x_flat, ids.long())
+            return _ExpertStages.apply(x_flat, g, self.expert_latents.weight, self.generation_network.net[0].weight,
+                                       self.generation_network.net[2].weight, self, gates, seg)
         with torch.no_grad():
             gates, ids = self.router.route(x_flat, mark)
             seg = hip.sort_segment(ids.view(-1), self.num_experts)
@@ -205,6 +338,10 @@ class EthosExpertLayer(nn.Module):
             if mark is not None:
                 mark("apply_scatter")
         return out
+
+
+def _wants_grad(x: torch.Tensor, module: nn.Module) -> bool:
+    return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in module.parameters()))
 
 
 def _as_input(x: torch.Tensor, dim: int) -> torch.Tensor:
