@@ -161,9 +161,11 @@ int ethos_generate(const void* latents, int64_t n_experts, const int32_t* uniq_i
     if (ethos::generate_smem_bytes(d_latent, d_hidden, dtype) > 160 * 1024)
         return fail(ETHOS_EUNSUPPORTED, "ethos_generate: d_latent + d_hidden too large for LDS");
     if (max_unique == 0) return 0;
-    if (!latents || !uniq_ids || !n_unique || !w1 || !w2 || !h_out || !v_out)
+    // v_out == NULL: hidden rows only (w2 is then not read)
+    if (!latents || !uniq_ids || !n_unique || !w1 || !h_out || (v_out && !w2))
         return fail(ETHOS_ENULL, "ethos_generate: null pointer");
-    if (dtype == ETHOS_BF16 && (!aligned16(w1) || !aligned16(w2) || !aligned16(h_out) || !aligned16(v_out)))
+    if (dtype == ETHOS_BF16 &&
+        (!aligned16(w1) || (v_out && !aligned16(w2)) || !aligned16(h_out) || (v_out && !aligned16(v_out))))
         return fail(ETHOS_EALIGN, "ethos_generate: weights and outputs must be 16-byte aligned");
     return hip_status(ethos::launch_generate(latents, n_experts, uniq_ids, n_unique, max_unique, w1, w2, d_latent,
                                              d_hidden, d_model, dtype, h_out, v_out, num_cus(), (hipStream_t)stream),
@@ -204,6 +206,42 @@ int ethos_apply_scatter(const void* x, const void* w2, const void* h, const void
     return hip_status(ethos::launch_apply(x, w2, h, v, perm, sorted_slot, pair_slot, scores, n_tok, n_heads, top_k,
                                           d_model, d_hidden, dtype, workspace, out, num_cus(), (hipStream_t)stream),
                       "ethos_apply_scatter");
+}
+
+size_t ethos_apply_hidden_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_model,
+                                          int32_t d_hidden, int32_t dtype) {
+    if (n_tok <= 0 || n_heads <= 0 || top_k <= 0 || d_model <= 0 || d_hidden <= 0) return 256;
+    return ethos::apply_hidden_workspace_bytes(n_tok, n_heads, top_k, d_model, d_hidden, dtype);
+}
+
+int ethos_apply_hidden(const void* x, const void* w2, const void* h, const int32_t* perm, const int32_t* sorted_slot,
+                       const int32_t* pair_slot, const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k,
+                       int32_t d_model, int32_t d_hidden, int32_t dtype, void* workspace, size_t workspace_bytes,
+                       void* out, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_apply_hidden: unknown dtype %d", dtype);
+    if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || d_model <= 0 || d_hidden <= 0)
+        return fail(ETHOS_ESIZE, "ethos_apply_hidden: bad sizes");
+    const int vec = dtype == ETHOS_BF16 ? 8 : 4;
+    if (d_model % vec || d_hidden % vec || d_model > 4096 || ethos::apply_chunks(d_hidden, dtype) > 8)
+        return fail(ETHOS_EUNSUPPORTED,
+                    "ethos_apply_hidden: d_model=%d and d_hidden=%d must be multiples of %d, d_model <= 4096, "
+                    "d_hidden <= %d", d_model, d_hidden, vec, 8 * 64 * vec);
+    if (n_tok * n_heads * top_k > INT32_MAX || n_tok > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_apply_hidden: too many pairs");
+    if (n_tok == 0) return 0;
+    if (!x || !w2 || !h || !perm || !sorted_slot || !pair_slot || !scores || !workspace || !out)
+        return fail(ETHOS_ENULL, "ethos_apply_hidden: null pointer");
+    const size_t need = ethos::apply_hidden_workspace_bytes(n_tok, n_heads, top_k, d_model, d_hidden, dtype);
+    if (workspace_bytes < need)
+        return fail(ETHOS_EWORKSPACE, "ethos_apply_hidden: workspace of %zu bytes, %zu needed", workspace_bytes,
+                    need);
+    if (!aligned16(x) || !aligned16(w2) || !aligned16(h) || !aligned16(workspace) || !aligned16(out))
+        return fail(ETHOS_EALIGN, "ethos_apply_hidden: x, w2, h, workspace and out must be 16-byte aligned");
+    const int rc = ethos::launch_apply_hidden(x, w2, h, perm, sorted_slot, pair_slot, scores, n_tok, n_heads, top_k,
+                                              d_model, d_hidden, dtype, workspace, out, num_cus(), (hipStream_t)stream);
+    if (rc < 0) return fail(ETHOS_EUNSUPPORTED, "ethos_apply_hidden: d_hidden=%d not supported", d_hidden);
+    return hip_status(rc, "ethos_apply_hidden");
 }
 
 }  // extern "C"

@@ -376,6 +376,78 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
     }
 }
 
+// Hidden-space reordering (paper/ETHOS.pdf p.10, Algorithm 1): per token,
+// hs_t = RN_T((1/H) sum_p RN32(a_p h_s)) over its pairs in order (heads, then k), the sum in
+// float32.  One wave per token; the pairs' hidden rows are gathered kScatterUnroll at a
+// time, each lane owning CH chunks of N consecutive columns.
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void apply_hacc_kernel(const T* __restrict__ hid,
+                                                         const int32_t* __restrict__ pair_slot,
+                                                         const float* __restrict__ act, int64_t n_tok, int H,
+                                                         int k, int dh, T* __restrict__ hs) {
+    constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t n_waves = (int64_t)gridDim.x * 4;
+    const int np = H * k;
+    for (int64_t t = wave_id; t < n_tok; t += n_waves) {
+        float acc[CH * N];
+#pragma unroll
+        for (int e = 0; e < CH * N; ++e) acc[e] = 0.0f;
+        const int64_t pbase = t * np;
+        for (int j0 = 0; j0 < np; j0 += kScatterUnroll) {
+            Raw hr[kScatterUnroll][CH];
+            float a[kScatterUnroll];
+#pragma unroll
+            for (int q = 0; q < kScatterUnroll; ++q) {
+                if (j0 + q < np) {
+                    const int s = pair_slot[pbase + j0 + q];
+                    a[q] = act[pbase + j0 + q];
+                    load_raw<T, CH>(hid + (int64_t)s * dh, dh, lane, hr[q]);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kScatterUnroll; ++q) {
+                if (j0 + q < np) {
+#pragma unroll
+                    for (int c = 0; c < CH; ++c) {
+                        float hf[N];
+                        Vec16<T>::unpack(hr[q][c], hf);
+#pragma unroll
+                        for (int v = 0; v < N; ++v) acc[c * N + v] += a[q] * hf[v];  // float32 products
+                    }
+                }
+            }
+        }
+        const float hdiv = (float)H;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int e = c * 64 * N + lane * N;
+            if (e < dh) {
+                float r[N];
+#pragma unroll
+                for (int v = 0; v < N; ++v) r[v] = acc[c * N + v] / hdiv;
+                *reinterpret_cast<Raw*>(hs + t * dh + e) = Vec16<T>::pack(r);
+            }
+        }
+    }
+}
+
+// out[j][i] = in[i][j] for in [rows, cols] (32 x 32 tiles through LDS)
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ in, int rows, int cols,
+                                                        T* __restrict__ out) {
+    __shared__ T tile[32][33];
+    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int r = ty; r < 32; r += 8)
+        if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = in[(int64_t)(r0 + r) * cols + c0 + tx];
+    __syncthreads();
+    for (int c = ty; c < 32; c += 8)
+        if (c0 + c < cols && r0 + tx < rows) out[(int64_t)(c0 + c) * rows + r0 + tx] = tile[tx][c];
+}
+
 template <typename T, int CH1, int CH2>
 static int launch_apply_t(const void* xp, const void* hid, const void* v, const int32_t* perm,
                           const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,
@@ -414,13 +486,12 @@ size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype) {
     return wut_offset(n_tok, H, k, dh, eb) + (dtype == kBF16 ? (size_t)dh * 4096 * eb : 0);
 }
 
-int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
-                 const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k,
-                 int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream) {
+// xp = RN_T(x W_u) into the workspace (W_u^T = the first d rows of net.2.weight, row
+// length dh)
+static void launch_token_proj(const void* x, const void* w2, int64_t n_tok, int H, int k, int d, int dh, int dtype,
+                              void* ws, hipStream_t stream) {
     const size_t eb = dtype == kBF16 ? 2 : 4;
     void* xp = ws;
-    float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
-    // token projection (W_u^T = the first d rows of net.2.weight, row length dh)
     const dim3 tgrid((unsigned)((dh + kTpC - 1) / kTpC), (unsigned)((n_tok + kTpT - 1) / kTpT));
     if (dtype == kBF16 && d % kTpK == 0 && dh % 8 == 0) {
         uint16_t* wut = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + wut_offset(n_tok, H, k, dh, eb));
@@ -436,6 +507,15 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
     else
         hipLaunchKernelGGL(token_proj_kernel<float>, tgrid, dim3(256), 0, stream, (const float*)x, (const float*)w2,
                            (int)n_tok, d, dh, (float*)xp);
+}
+
+int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
+                 const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k,
+                 int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    void* xp = ws;
+    float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
+    launch_token_proj(x, w2, n_tok, H, k, d, dh, dtype, ws, stream);
     const int c1 = apply_chunks(dh, dtype), c2 = apply_chunks(d, dtype);
 #define ETHOS_APPLY_CASE(TT, C1, C2)                                                                             \
     if (c1 <= C1 && c2 <= C2)                                                                                    \
@@ -460,6 +540,96 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
     }
 #undef ETHOS_APPLY_CASE
     return -1;
+}
+
+// workspace for the hidden-space form: the apply workspace, then hs [n_tok, dh] T, then
+// (fp32, or shapes the MFMA projection does not take) W_v^T [dh, d] T
+static bool hidden_proj_mfma(int d, int dh, int dtype) { return dtype == kBF16 && dh % kTpK == 0 && d % 8 == 0; }
+
+static size_t hs_offset(int64_t n_tok, int H, int k, int dh, int dtype) {
+    return align256(apply_workspace_bytes(n_tok, H, k, dh, dtype));
+}
+
+size_t apply_hidden_workspace_bytes(int64_t n_tok, int H, int k, int d, int dh, int dtype) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    size_t b = hs_offset(n_tok, H, k, dh, dtype) + align256((size_t)n_tok * dh * eb);
+    if (!hidden_proj_mfma(d, dh, dtype)) b += (size_t)d * dh * eb;
+    return b;
+}
+
+template <typename T, int CH1>
+static void launch_hidden_t(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
+                            const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k, int dh,
+                            float* act, void* hs, int num_cus, hipStream_t stream) {
+    const int64_t n_pairs = n_tok * H * k;
+    const int64_t cap = (int64_t)num_cus * 16;
+    int64_t g1 = ((n_pairs + 63) / 64 + 3) / 4;
+    g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
+    hipLaunchKernelGGL((apply_act_kernel<T, CH1>), dim3((unsigned)g1), dim3(256), 0, stream, (const T*)xp,
+                       (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, H * k, dh, act);
+    int64_t g2 = (n_tok + 3) / 4;
+    g2 = g2 > cap ? cap : (g2 < 1 ? 1 : g2);
+    hipLaunchKernelGGL((apply_hacc_kernel<T, CH1>), dim3((unsigned)g2), dim3(256), 0, stream, (const T*)hid,
+                       pair_slot, (const float*)act, n_tok, H, k, dh, (T*)hs);
+}
+
+int launch_apply_hidden(const void* x, const void* w2, const void* hid, const int32_t* perm,
+                        const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,
+                        int k, int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    void* xp = ws;
+    float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
+    unsigned char* hs = static_cast<unsigned char*>(ws) + hs_offset(n_tok, H, k, dh, dtype);
+    launch_token_proj(x, w2, n_tok, H, k, d, dh, dtype, ws, stream);
+    const int c1 = apply_chunks(dh, dtype);
+#define ETHOS_HIDDEN_CASE(TT, C1)                                                                                   \
+    else if (c1 <= C1) launch_hidden_t<TT, C1>(xp, hid, perm, sorted_slot, pair_slot, gates, n_tok, H, k, dh, act, hs, \
+                                               num_cus, stream);
+    if (dtype == kBF16) {
+        if (false) {
+        }
+        ETHOS_HIDDEN_CASE(uint16_t, 1)
+        ETHOS_HIDDEN_CASE(uint16_t, 2)
+        ETHOS_HIDDEN_CASE(uint16_t, 4)
+        ETHOS_HIDDEN_CASE(uint16_t, 8)
+        else return -1;
+    } else {
+        if (false) {
+        }
+        ETHOS_HIDDEN_CASE(float, 1)
+        ETHOS_HIDDEN_CASE(float, 2)
+        ETHOS_HIDDEN_CASE(float, 4)
+        ETHOS_HIDDEN_CASE(float, 8)
+        else return -1;
+    }
+#undef ETHOS_HIDDEN_CASE
+    // projection back: out = RN_T(hs W_v^T), W_v^T = rows d .. 2d-1 of net.2.weight, which
+    // as a [d, dh] row-major block is the output-major operand layout of the token
+    // projection kernels (K = dh, N = d)
+    const unsigned char* wv = static_cast<const unsigned char*>(w2) + (size_t)d * dh * eb;
+    if (hidden_proj_mfma(d, dh, dtype)) {
+        hipLaunchKernelGGL(token_proj_bf16_kernel,
+                           dim3((unsigned)((d + kTpCols - 1) / kTpCols), (unsigned)((n_tok + kTpT - 1) / kTpT)),
+                           dim3(256), 0, stream, (const uint16_t*)hs, (const uint16_t*)wv, (int)n_tok, dh, d,
+                           (uint16_t*)out);
+        return (int)hipGetLastError();
+    }
+    // generic: W_v as [dh, d] row-major (the token_proj_kernel operand layout), then the
+    // float64-accumulating projection
+    unsigned char* wvt = hs + align256((size_t)n_tok * dh * eb);
+    const dim3 tg((unsigned)((dh + 31) / 32), (unsigned)((d + 31) / 32));
+    const dim3 pg((unsigned)((d + kTpC - 1) / kTpC), (unsigned)((n_tok + kTpT - 1) / kTpT));
+    if (dtype == kBF16) {
+        hipLaunchKernelGGL(transpose_kernel<uint16_t>, tg, dim3(256), 0, stream, (const uint16_t*)wv, d, dh,
+                           (uint16_t*)wvt);
+        hipLaunchKernelGGL(token_proj_kernel<uint16_t>, pg, dim3(256), 0, stream, (const uint16_t*)hs,
+                           (const uint16_t*)wvt, (int)n_tok, dh, d, (uint16_t*)out);
+    } else {
+        hipLaunchKernelGGL(transpose_kernel<float>, tg, dim3(256), 0, stream, (const float*)wv, d, dh, (float*)wvt);
+        hipLaunchKernelGGL(token_proj_kernel<float>, pg, dim3(256), 0, stream, (const float*)hs, (const float*)wvt,
+                           (int)n_tok, dh, d, (float*)out);
+    }
+    return (int)hipGetLastError();
 }
 
 }  // namespace ethos

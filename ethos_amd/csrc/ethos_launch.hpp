@@ -29,6 +29,10 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
                     void* vout, int num_cus, hipStream_t stream);
 
 int apply_chunks(int d, int dtype);
+size_t apply_hidden_workspace_bytes(int64_t n_tok, int H, int k, int d, int dh, int dtype);
+int launch_apply_hidden(const void* x, const void* w2, const void* hid, const int32_t* perm,
+                        const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,
+                        int k, int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream);
 size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype);
 int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
                  const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k,

@@ -652,6 +652,7 @@ static bool launch_generate_bf16(const void* latents, int64_t n_experts, const i
     const unsigned g1 = (unsigned)(blocks < num_cus ? (blocks > 0 ? blocks : 1) : num_cus);
     hipLaunchKernelGGL((hidden_bf16_kernel<DL, DH>), dim3(g1), dim3(kHWaves * 64), 0, stream,
                        (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (uint16_t*)hout);
+    if (uv == nullptr) return true;  // hidden rows only
     // W_v-stationary when d2 splits into 256-column groups that fill the XCDs evenly
     const int n_cg = d2 / kWsCols;
     const int per_xcd = d2 % kWsCols == 0 && n_cg > 0 ? (num_cus / 8) / n_cg : 0;
@@ -681,9 +682,10 @@ size_t generate_smem_bytes(int dl, int dh, int dtype) {
 int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                     int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d, int dtype, void* hout,
                     void* vout, int num_cus, hipStream_t stream) {
-    // W_v^T: rows d .. 2d-1 of net.2.weight
+    // W_v^T: rows d .. 2d-1 of net.2.weight; vout == nullptr asks for the hidden rows only
     const size_t eb = dtype == kBF16 ? 2 : 4;
-    const void* wv = static_cast<const unsigned char*>(w2) + (size_t)d * dh * eb;
+    const void* wv = vout ? static_cast<const unsigned char*>(w2) + (size_t)d * dh * eb : nullptr;
+    const int d2 = vout ? d : 0;
     if (dtype == kBF16) {
         if (launch_generate_bf16<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout,
                                               vout, num_cus, stream) ||
@@ -698,11 +700,11 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
     const size_t smem = generate_smem_bytes(dl, dh, dtype);
     if (dtype == kBF16)
         hipLaunchKernelGGL(generate_kernel<uint16_t>, dim3(grid), dim3(256), smem, stream, (const uint16_t*)latents,
-                           n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)wv, dl, dh, d,
+                           n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)wv, dl, dh, d2,
                            (uint16_t*)hout, (uint16_t*)vout);
     else
         hipLaunchKernelGGL(generate_kernel<float>, dim3(grid), dim3(256), smem, stream, (const float*)latents,
-                           n_experts, uniq, n_unique, (const float*)w1, (const float*)wv, dl, dh, d, (float*)hout,
+                           n_experts, uniq, n_unique, (const float*)w1, (const float*)wv, dl, dh, d2, (float*)hout,
                            (float*)vout);
     return (int)hipGetLastError();
 }

@@ -120,9 +120,10 @@ def sort_segment(ids: torch.Tensor, n_experts: int) -> dict:
 
 
 def generate(latents: torch.Tensor, uniq: torch.Tensor, n_unique: torch.Tensor, max_unique: int, w1: torch.Tensor,
-             w2: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+             w2: torch.Tensor, with_v: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Hidden rows h [max_unique, d_hidden] and v rows [max_unique, d] of the unique experts
-    (rows >= U unspecified)."""
+    (rows >= U unspecified).  with_v=False produces h only (v is None), as the
+    hidden-space apply needs."""
     _need(latents, "latents", dim=2)
     _need(uniq, "uniq", torch.int32)
     _need(n_unique, "n_unique", torch.int32)
@@ -134,10 +135,10 @@ def generate(latents: torch.Tensor, uniq: torch.Tensor, n_unique: torch.Tensor, 
         raise RuntimeError("generate: inconsistent weight shapes")
     d = w2.shape[0] // 2
     h = torch.empty((max_unique, dh), dtype=latents.dtype, device=latents.device)
-    v = torch.empty((max_unique, d), dtype=latents.dtype, device=latents.device)
+    v = torch.empty((max_unique, d), dtype=latents.dtype, device=latents.device) if with_v else None
     rc = load().ethos_generate(latents.data_ptr(), E, uniq.data_ptr(), n_unique.data_ptr(), max_unique, w1.data_ptr(),
-                               w2.data_ptr(), dl, dh, d, dtype_code(latents.dtype), h.data_ptr(), v.data_ptr(),
-                               _stream())
+                               w2.data_ptr(), dl, dh, d, dtype_code(latents.dtype), h.data_ptr(),
+                               v.data_ptr() if with_v else None, _stream())
     check(rc, "ethos_generate")
     return h, v
 
@@ -161,4 +162,26 @@ def apply_scatter(x: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, v: torch.T
                                     seg["sorted_slot"].data_ptr(), seg["pair_slot"].data_ptr(), gates.data_ptr(), n,
                                     n_heads, top_k, d, dh, code, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
     check(rc, "ethos_apply_scatter")
+    return out
+
+
+def apply_hidden(x: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, seg: dict, gates: torch.Tensor, n_heads: int,
+                 top_k: int) -> torch.Tensor:
+    """out [n, d] by hidden-space reordering: per token (1/H) sum_p a_p h_s, projected by W_v
+    once (no v rows)."""
+    _need(x, "x", dim=2)
+    _need(w2, "w2", x.dtype, 2)
+    _need(h, "h", x.dtype, 2)
+    _need(gates, "gates", x.dtype)
+    n, d = x.shape
+    dh = h.shape[1]
+    if w2.shape != (2 * d, dh) or gates.numel() != n * n_heads * top_k:
+        raise RuntimeError("apply_hidden: inconsistent shapes")
+    code = dtype_code(x.dtype)
+    ws, ws_bytes = workspace(load().ethos_apply_hidden_workspace_bytes(n, n_heads, top_k, d, dh, code), x.device)
+    out = torch.empty_like(x)
+    rc = load().ethos_apply_hidden(x.data_ptr(), w2.data_ptr(), h.data_ptr(), seg["perm"].data_ptr(),
+                                   seg["sorted_slot"].data_ptr(), seg["pair_slot"].data_ptr(), gates.data_ptr(), n,
+                                   n_heads, top_k, d, dh, code, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
+    check(rc, "ethos_apply_hidden")
     return out

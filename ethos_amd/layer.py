@@ -74,11 +74,13 @@ class _ExpertStages(torch.autograd.Function):
         pre_s = z_s C^T,  h_s = gelu(pre_s),  v_s = h_s B^T,  xp_t = x_t A,
         c_p = h_s · xp_t,  a_p = gelu(c_p) g_p,  y_t = (1/H) Σ_p a_p v_s
 
-    so with dY_t = dy_t / H:  da_p = dY_t · v_s;  dv_s = Σ_p a_p dY_t;  dg_p = gelu(c_p) da_p;
-    dc_p = g_p gelu'(c_p) da_p;  dxp_t = Σ_p dc_p h_s;  dh_s = Σ_p dc_p xp_t + dv_s B;
-    dA = x^T dxp,  dB = dv^T h,  dx = dxp A^T;  dpre = gelu'(pre) dh,  dC = dpre^T z,
-    dz = dpre C (added into the latent rows of the unique experts).  The per-pair sums run
-    over chunks of pairs with index_add, so temporaries stay bounded.
+    so with dY_t = dy_t / H:  da_p = dY_t · v_s = (dY_t B) · h_s;  dg_p = gelu(c_p) da_p;
+    dc_p = g_p gelu'(c_p) da_p;  dxp_t = Σ_p dc_p h_s;  dh_s = Σ_p (dc_p xp_t + a_p dY_t B);
+    dA = x^T dxp,  dB = dY^T hacc with hacc_t = Σ_p a_p h_s,  dx = dxp A^T;
+    dpre = gelu'(pre) dh,  dC = dpre^T z,  dz = dpre C (added into the latent rows of the
+    unique experts).  v rows are not needed.  The per-pair sums run over chunks of pairs with
+    index_add, so temporaries stay bounded.  Both execution orders (scatter of v rows,
+    hidden-space reordering) compute this same function, so they share the backward.
 
     The gates enter as `gates_exact` (the values the forward uses) and `gate_path` (a
     float32 tensor of the same values carrying the router's graph), whose gradient is dg.
@@ -86,17 +88,18 @@ class _ExpertStages(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, gate_path, latents_w, w1_w, w2_w, layer, gates_exact, seg):
+        out, h = layer._expert_stages(x, gates_exact, seg)
         latents, w1, w2 = layer._generator_params(x.dtype, x.device)
-        h, v = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2)
-        out = hip.apply_scatter(x, w2, h, v, seg, gates_exact, layer.num_heads, layer.top_k)
-        ctx.save_for_backward(x, gates_exact, h, v, seg["uniq"], seg["pair_slot"], seg["n_unique"], latents, w1, w2)
+        ctx.save_for_backward(x, gates_exact, h, seg["uniq"], seg["pair_slot"], seg["n_unique"], latents, w1, w2)
         ctx.heads, ctx.top_k = layer.num_heads, layer.top_k
         ctx.param_dtypes = (latents_w.dtype, w1_w.dtype, w2_w.dtype)
         return out
 
     @staticmethod
     def backward(ctx, dy):
-        x, gates, h, v, uniq, pair_slot, n_unique, latents, w1, w2 = ctx.saved_tensors
+        # v_s = h_s B^T never needs forming: dY_t . v_s = (dY_t B) . h_s, the dv_s B term of
+        # dh_s is sum_p a_p (dY_t B), and dB = dv^T h = dY^T hacc with hacc_t = sum_p a_p h_s.
+        x, gates, h, uniq, pair_slot, n_unique, latents, w1, w2 = ctx.saved_tensors
         H, k = ctx.heads, ctx.top_k
         n, d = x.shape
         f = torch.float32
@@ -104,31 +107,32 @@ class _ExpertStages(torch.autograd.Function):
         A, B, C = w2[:d].to(f), w2[d:].to(f), w1.to(f)
         xf = x.to(f)
         xp = xf @ A
-        hf, vf = h[:U].to(f), v[:U].to(f)
+        hf = h[:U].to(f)
         g = gates.reshape(-1).to(f)
         slot = pair_slot.long()
         dY = dy.to(f) * (1.0 / H)
+        dYB = dY @ B
         n_pairs = n * H * k
-        dv = torch.zeros_like(vf)
+        hacc = torch.zeros_like(xp)
         dh = torch.zeros_like(hf)
         dxp = torch.zeros_like(xp)
         dg = torch.empty(n_pairs, dtype=f, device=x.device)
-        chunk = max(1024, (1 << 25) // max(d, 1))
+        chunk = max(1024, (1 << 25) // max(hf.shape[1], 1))
         for p0 in range(0, n_pairs, chunk):
             p = torch.arange(p0, min(n_pairs, p0 + chunk), device=x.device)
             t, s = p // (H * k), slot[p]
-            hp, xpp, dYp = hf[s], xp[t], dY[t]
+            hp, xpp, dwp = hf[s], xp[t], dYB[t]
             c = (hp * xpp).sum(-1)
             act = F.gelu(c)
-            da = (dYp * vf[s]).sum(-1)
             gp = g[p]
-            dv.index_add_(0, s, (act * gp)[:, None] * dYp)
+            a = act * gp
+            da = (dwp * hp).sum(-1)
             dg[p] = act * da
             dc = gp * _gelu_grad(c) * da
+            hacc.index_add_(0, t, a[:, None] * hp)
             dxp.index_add_(0, t, dc[:, None] * hp)
-            dh.index_add_(0, s, dc[:, None] * xpp)
-        dh += dv @ B
-        dB = dv.T @ hf
+            dh.index_add_(0, s, a[:, None] * dwp + dc[:, None] * xpp)
+        dB = dY.T @ hacc
         dA = xf.T @ dxp
         dx = dxp @ A.T
         ids = uniq[:U].long()
@@ -280,7 +284,7 @@ class EthosExpertLayer(nn.Module):
     """The ETHOS expert layer: product-key routing over num_experts generated experts,
     reordered execution by expert id, head-averaged weighted scatter-back."""
 
-    def __init__(self, config):
+    def __init__(self, config, hidden_space: bool | None = None):
         super().__init__()
         self.d_model = config.d_model
         self.num_experts = config.num_experts
@@ -288,6 +292,12 @@ class EthosExpertLayer(nn.Module):
         self.num_heads = config.num_routing_heads
         self.d_latent = config.d_latent
         self.d_hidden = config.d_intermediate_hypernet
+        # Execution order of the expert stages: False (default) generates v_e = h_e W_v per
+        # unique expert and scatters a_p v_e into the tokens (model.py:320-341, the layer's
+        # rounding points); True is the paper's hidden-space reordering (Algorithm 1,
+        # paper/ETHOS.pdf p.10): h_acc = sum_p a_p h_e per token, projected by W_v once.
+        # Same function, different rounding points; no v rows.
+        self.hidden_space = bool(getattr(config, "hidden_space", False) if hidden_space is None else hidden_space)
         self.expert_latents = nn.Embedding(config.num_experts, config.d_latent)
         self.generation_network = ExpertGenerationNetwork(config.d_latent, config.d_model,
                                                           config.d_intermediate_hypernet)
@@ -305,6 +315,22 @@ class EthosExpertLayer(nn.Module):
                 self._gen = tuple(p.detach().to(device=device, dtype=dtype).contiguous() for p in ps)
             self._gen_key = key
         return self._gen
+
+    def _expert_stages(self, x_flat: torch.Tensor, gates: torch.Tensor, seg: dict, mark=None):
+        """(out, h): generation over the unique experts, then apply + scatter-back in the
+        layer's execution order."""
+        latents, w1, w2 = self._generator_params(x_flat.dtype, x_flat.device)
+        h, v = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2,
+                            with_v=not self.hidden_space)
+        if mark is not None:
+            mark("generate")
+        if self.hidden_space:
+            out = hip.apply_hidden(x_flat, w2, h, seg, gates, self.num_heads, self.top_k)
+        else:
+            out = hip.apply_scatter(x_flat, w2, h, v, seg, gates, self.num_heads, self.top_k)
+        if mark is not None:
+            mark("apply_scatter")
+        return out, h
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.dim() != 3 or x.shape[-1] != self.d_model:
@@ -330,13 +356,7 @@ class EthosExpertLayer(nn.Module):
             seg = hip.sort_segment(ids.view(-1), self.num_experts)
             if mark is not None:
                 mark("sort_segment")
-            latents, w1, w2 = self._generator_params(x_flat.dtype, x_flat.device)
-            h, v = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2)
-            if mark is not None:
-                mark("generate")
-            out = hip.apply_scatter(x_flat, w2, h, v, seg, gates, self.num_heads, self.top_k)
-            if mark is not None:
-                mark("apply_scatter")
+            out, _ = self._expert_stages(x_flat, gates, seg, mark)
         return out
 
 

@@ -12,6 +12,7 @@
  *   ethos_sort_segment   reordering of (token, head, k) pairs by expert id
  *   ethos_generate       hypernetwork expert generation over the unique experts
  *   ethos_apply_scatter  per-pair activation and weighted scatter-back into tokens
+ *   ethos_apply_hidden   the same, by hidden-space reordering (no v rows)
  *
  * Conventions (every entry point):
  *   - All pointers are device pointers owned by the caller; nothing is allocated.
@@ -129,6 +130,8 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
  *   w2       [2 * d_model, d_hidden]        dtype T  (generation_network.net.2.weight)
  *   h_out    [max_unique, d_hidden]         dtype T  rows u < U written
  *   v_out    [max_unique, d_model]          dtype T  rows u < U written
+ * v_out may be NULL: then only the hidden rows are produced (w2 is not read), as
+ * ethos_apply_hidden needs.
  * Limits: d_latent % 16 (bf16) or % 2 (fp32) == 0, d_hidden % 32 == 0, d_model % 32 == 0;
  * bf16 weights and outputs 16-byte aligned.
  */
@@ -161,6 +164,29 @@ int ethos_apply_scatter(const void* x, const void* w2, const void* h, const void
                         const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores, int64_t n_tok,
                         int32_t n_heads, int32_t top_k, int32_t d_model, int32_t d_hidden, int32_t dtype,
                         void* workspace, size_t workspace_bytes, void* out, void* stream);
+
+/* Workspace size for ethos_apply_hidden. */
+size_t ethos_apply_hidden_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_model,
+                                          int32_t d_hidden, int32_t dtype);
+
+/*
+ * Expert apply by hidden-space reordering: the paper's Algorithm 1 (paper/ETHOS.pdf p.10,
+ * "Reordered MoE Execution Kernel": x_proj = x W_u once, h_accum += a_j h_j over the
+ * selected experts, y = h_accum W_v once), the execution order kernels.py:123-145 names,
+ * with the head average of model.py:341.  The same function as ethos_apply_scatter with
+ * different rounding points; v rows are never formed (generate with v_out = NULL).
+ *   x, w2, h, perm, sorted_slot, pair_slot, scores, out   as for ethos_apply_scatter
+ *   workspace     >= ethos_apply_hidden_workspace_bytes(...) bytes (scratch)
+ * a_p as in ethos_apply_scatter;
+ * hs_t = RN_T((1/n_heads) sum_p RN32(a_p h_e)) over the token's pairs (heads, then k, float32);
+ * out[t] = RN_T(hs_t W_v) (W_v^T = rows d_model .. 2 d_model - 1 of w2).
+ * Limits: d_model and d_hidden multiples of 8 (bf16) or 4 (fp32), d_model <= 4096,
+ * d_hidden <= 4096 (bf16) / 2048 (fp32); x, w2, h, workspace and out 16-byte aligned.
+ */
+int ethos_apply_hidden(const void* x, const void* w2, const void* h, const int32_t* perm, const int32_t* sorted_slot,
+                       const int32_t* pair_slot, const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k,
+                       int32_t d_model, int32_t d_hidden, int32_t dtype, void* workspace, size_t workspace_bytes,
+                       void* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -295,6 +295,46 @@ def apply(xp, h, v, pair_slot, gates, n_heads: int, top_k: int, dt: str, tokens=
     return out
 
 
+def apply_hidden(xp, h, W2, pair_slot, gates, n_heads: int, top_k: int, dt: str, tokens=None,
+                 hacc_round: str = "T"):
+    """Hidden-space reordering (paper/ETHOS.pdf p.10, Algorithm 1): per token
+    h_acc = sum over the token's pairs of a_p h_s, then y = h_acc W_v, projected back once.
+
+    Per pair p = (t, head, j) with expert slot s, a_p is the activation of ``apply``
+    (RN(RN(gelu(RN(h_s . xp_t))) * g_p)).  h_acc sums RN32(a_p h_s) over heads, then j, in
+    float32, scaled by 1/H (the layer's head average, model.py:341).  ``hacc_round``
+    rounds h_acc / H before the projection: "T" to the layer dtype, "none" keeps float32.
+    y = RN_T((h_acc / H) W_v) with an exact product (W_v = W2[d:]^T).  v rows never exist.
+    Returns float32 [len(tokens), d] holding T values."""
+    xpf = np.asarray(xp, np.float32)
+    n_tok = xpf.shape[0]
+    W2f = to_f32(W2, dt) if np.asarray(W2).dtype == np.uint16 else np.asarray(W2, np.float32)
+    d = W2f.shape[0] // 2
+    Wv = W2f[d:].astype(np.float64)                                      # [d, d_hidden]
+    g = to_f32(gates, dt).reshape(n_tok, n_heads, top_k)
+    slot = np.asarray(pair_slot).reshape(n_tok, n_heads, top_k)
+    toks = np.arange(n_tok) if tokens is None else np.asarray(tokens)
+    hh = np.asarray(h).astype(np.float64)
+    hf32 = np.asarray(h, np.float32)
+    out = np.empty((len(toks), d), np.float32)
+    for i0 in range(0, len(toks), 32):
+        tk = toks[i0:i0 + 32]
+        xs = xpf[tk].astype(np.float64)
+        s = slot[tk]
+        dots = np.einsum("bj,bhkj->bhk", xs, hh[s])
+        act = round_T(gelu64(round_T(dots, dt).astype(np.float64)), dt)
+        a = round_T((act * g[tk]).astype(np.float32), dt).astype(np.float32)
+        acc = np.zeros((len(tk), hh.shape[1]), np.float32)
+        for hd in range(n_heads):
+            for j in range(top_k):
+                acc = (acc + (a[:, hd, j, None] * hf32[s[:, hd, j]]).astype(np.float32)).astype(np.float32)
+        acc = (acc / np.float32(n_heads)).astype(np.float32)
+        if hacc_round == "T":
+            acc = round_T(acc, dt).astype(np.float32)
+        out[i0:i0 + len(tk)] = round_T(acc.astype(np.float64) @ Wv.T, dt)
+    return out
+
+
 # ------------------------------------------------------------------ whole layer
 def unpack_state(sd: dict, H: int):
     """Reference state_dict (torch CPU tensors) -> numpy arrays in storage convention."""

@@ -19,10 +19,10 @@ def _nerr(a: torch.Tensor, b: torch.Tensor) -> float:
     return float((a - b).norm() / max(float(b.norm()), 1e-30))
 
 
-def _grads(name, train, signal=True):
+def _grads(name, train, signal=True, hidden=False):
     sh = SHAPES[name]
     x, sd = make_inputs(sh, signal=signal)
-    m = ethos_amd.EthosExpertLayer(sh.config()).to(sh.torch_dtype)
+    m = ethos_amd.EthosExpertLayer(sh.config(), hidden_space=hidden).to(sh.torch_dtype)
     m.load_state_dict(sd)
     m = m.cuda().train(train)
     xd = x.cuda().view(sh.batch, -1, sh.d_model).clone().requires_grad_(True)
@@ -43,9 +43,11 @@ def _grads(name, train, signal=True):
     return sh, m, y, yr, ours, ref
 
 
-@pytest.mark.parametrize("name,train", [("tiny_fp32", False), ("tiny_fp32", True), ("cfg1", False), ("cfg1", True)])
-def test_grads_match_reference_fp32(name, train):
-    sh, m, y, yr, ours, ref = _grads(name, train)
+@pytest.mark.parametrize("name,train,hidden", [("tiny_fp32", False, False), ("tiny_fp32", True, False),
+                                               ("cfg1", False, False), ("cfg1", True, False),
+                                               ("tiny_fp32", True, True), ("cfg1", False, True)])
+def test_grads_match_reference_fp32(name, train, hidden):
+    sh, m, y, yr, ours, ref = _grads(name, train, hidden=hidden)
     assert _nerr(y.view(-1, sh.d_model), yr) < 1e-5
     for k in ref:
         assert ours[k] is not None, k

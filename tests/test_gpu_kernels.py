@@ -327,3 +327,58 @@ def test_query_proj_certified_fallback_bit_exact(kind):
     q = hip.query_proj(to_dev(x), to_dev(w), to_dev(b), to_dev(alpha), to_dev(beta))
     torch.cuda.synchronize()
     assert np.array_equal(to_host(q), q_ref), f"{np.sum(to_host(q) != q_ref)} elements differ"
+
+
+@pytest.mark.parametrize("name,signal", [("tiny", False), ("tiny", True), ("tiny_fp32", True), ("cfg1", False),
+                                         ("cfg3", True), ("cfg3", False)])
+def test_apply_hidden_matches_oracle(name, signal):
+    """Hidden-space reordering through the C-ABI: hidden-only generation gives the same h
+    rows as the full generator, and the apply matches the oracle's Algorithm-1 form (fp32: to
+    1e-4; bf16: the stated tolerance, mostly identical elements) and the scatter form within
+    the bf16 tolerance of the layer."""
+    sh, x, P = _setup(name, signal=signal)
+    q = O.query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype)
+    g, ids = O.route(q, P["K1"], P["K2"], sh.top_k, sh.dtype)
+    seg = hip.sort_segment(to_dev(ids.reshape(-1)), sh.num_experts)
+    U = int(seg["n_unique"].item())
+    w2 = to_dev(P["W2"])
+    args = (to_dev(P["latents"]), seg["uniq"], seg["n_unique"], seg["max_unique"], to_dev(P["W1"]), w2)
+    h_only, none = hip.generate(*args, with_v=False)
+    h_dev, v_dev = hip.generate(*args)
+    out = hip.apply_hidden(to_dev(x), w2, h_only, seg, to_dev(g), sh.num_heads, sh.top_k)
+    torch.cuda.synchronize()
+    assert none is None and torch.equal(h_only[:U], h_dev[:U])
+    h = O.to_f32(to_host(h_dev), sh.dtype)[:U]
+    v = O.to_f32(to_host(v_dev), sh.dtype)[:U]
+    xp = O.token_proj(x, P["W2"], sh.dtype)
+    slot = to_host(seg["pair_slot"])
+    ref = O.apply_hidden(xp, h, P["W2"], slot, g, sh.num_heads, sh.top_k, sh.dtype)
+    got = O.to_f32(to_host(out), sh.dtype)
+    check_out(got, ref, sh.dtype, signal=signal, nerr_max=2e-3)
+    if sh.dtype == "bf16":
+        assert np.mean(got == ref) > 0.9
+    scatter = O.apply(xp, h, v, slot, g, sh.num_heads, sh.top_k, sh.dtype)
+    check_out(got, scatter, sh.dtype, signal=signal, nerr_max=1e-2)
+
+
+@pytest.mark.parametrize("n_tok,d,dh,dt", [(100, 1024, 512, "bf16"), (37, 256, 128, "bf16"), (70, 96, 64, "bf16"),
+                                           (33, 128, 96, "fp32"), (5, 4096, 256, "bf16")])
+def test_apply_hidden_shapes(n_tok, d, dh, dt):
+    """Hidden-space apply over shapes the configs do not hit: the MFMA projection (d_hidden a
+    multiple of 64), the generic transposed projection (d_hidden = 96) and d_model 4096."""
+    rng = np.random.default_rng(n_tok + d + dh + 1)
+    H, k, E = 2, 4, 300
+    enc = (lambda a: O.f32_to_bf16_bits(a)) if dt == "bf16" else (lambda a: a.astype(np.float32))
+    x = enc(rng.standard_normal((n_tok, d)).astype(np.float32))
+    w2 = enc((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(d)).astype(np.float32))
+    ids = rng.integers(0, E, (n_tok, H, k)).astype(np.int32)
+    g = enc(rng.uniform(0, 1, (n_tok, H, k)).astype(np.float32))
+    seg = hip.sort_segment(to_dev(ids.reshape(-1)), E)
+    U = int(seg["n_unique"].item())
+    h = enc(rng.standard_normal((seg["max_unique"], dh)).astype(np.float32) * 0.3)
+    out = hip.apply_hidden(to_dev(x), to_dev(w2), to_dev(h), seg, to_dev(g), H, k)
+    torch.cuda.synchronize()
+    xp = O.token_proj(x, w2, dt)
+    ref = O.apply_hidden(xp, O.to_f32(h, dt)[:U], w2, to_host(seg["pair_slot"]), g, H, k, dt)
+    got = O.to_f32(to_host(out), dt)
+    check_out(got, ref, dt, signal=True, nerr_max=2e-3)

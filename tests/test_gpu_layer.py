@@ -198,3 +198,47 @@ def test_empty_input():
     m = _layer(sh, sd)
     y = m(torch.empty((0, 5, sh.d_model), dtype=sh.torch_dtype, device="cuda"))
     assert y.shape == (0, 5, sh.d_model)
+
+
+@pytest.mark.parametrize("name,signal", [("tiny", True), ("tiny_fp32", True), ("cfg1", False), ("cfg3", False),
+                                         ("cfg3", True)])
+def test_layer_hidden_space(name, signal):
+    """The layer with hidden_space=True: the same routing as the default layer, the output
+    against the oracle's whole layer (reference algorithm) at the layer tolerance, and the
+    autograd-free output of the default layer within it."""
+    sh = SHAPES[name]
+    x, sd = make_inputs(sh, signal=signal)
+    m = _layer(sh, sd)
+    mh = ethos_amd.EthosExpertLayer(sh.config(), hidden_space=True).to(sh.torch_dtype)
+    mh.load_state_dict(sd)
+    mh = mh.cuda().eval()
+    xd = x.cuda().view(sh.batch, -1, sh.d_model)
+    with torch.no_grad():
+        y = m(xd).view(sh.n_tok, -1)
+        yh = mh(xd).view(sh.n_tok, -1)
+    torch.cuda.synchronize()
+    P = O.unpack_state(sd, sh.num_heads)
+    r = O.layer_forward(O.from_torch(x), P, sh.num_heads, sh.top_k, sh.dtype)
+    got = O.to_f32(to_host(yh), sh.dtype)
+    check_out(got, r["out"], sh.dtype, signal=signal, nerr_max=1e-2)
+    check_out(got, O.to_f32(to_host(y), sh.dtype), sh.dtype, signal=signal, nerr_max=1e-2)
+
+
+def test_layer_hidden_space_cfg2_subset():
+    """Config 2 in hidden-space order: a token subset against the oracle's reference-algorithm
+    layer and its Algorithm-1 form."""
+    sh = SHAPES["cfg2"]
+    x, sd = make_inputs(sh)
+    mh = ethos_amd.EthosExpertLayer(sh.config(), hidden_space=True).to(sh.torch_dtype)
+    mh.load_state_dict(sd)
+    mh = mh.cuda().eval()
+    xd = x.cuda()
+    with torch.no_grad():
+        q = mh.router.queries(xd)
+        y = mh(xd.view(sh.batch, -1, sh.d_model)).view(sh.n_tok, -1)
+    torch.cuda.synchronize()
+    P = O.unpack_state(sd, sh.num_heads)
+    xs = O.from_torch(x)
+    sub = np.arange(0, sh.n_tok, 64)
+    r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub, q=to_host(q))
+    check_out(O.to_f32(to_host(y), "bf16")[sub], r["out"], "bf16", nerr_max=1e-2)

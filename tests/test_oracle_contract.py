@@ -193,3 +193,24 @@ def test_sort_segment_is_stable_counting_sort(n, E):
 def test_sort_segment_rejects_out_of_range():
     with pytest.raises(ValueError):
         O.sort_segment(np.array([0, 5], np.int32), 5)
+
+
+@pytest.mark.parametrize("H,k,d,dh", [(2, 4, 64, 32), (4, 8, 96, 64)])
+def test_apply_hidden_is_apply_by_linearity(H, k, d, dh):
+    """sum_p a_p (h_s W_v^T) = (sum_p a_p h_s) W_v^T: in fp32 with h_acc kept in float32 the
+    hidden-space form equals the scatter form to float32 rounding; a missing head average,
+    the W_u half in place of W_v or a transposed W_v does not."""
+    rng = np.random.default_rng(H * k + d)
+    n, U = 24, 40
+    xp = rng.standard_normal((n, dh)).astype(np.float32)
+    h = rng.standard_normal((U, dh)).astype(np.float32)
+    W2 = (rng.standard_normal((2 * d, dh)) / np.sqrt(dh)).astype(np.float32)
+    v = (h.astype(np.float64) @ W2[d:].astype(np.float64).T).astype(np.float32)
+    slot = rng.integers(0, U, n * H * k).astype(np.int32)
+    gates = rng.uniform(0, 1, (n, H, k)).astype(np.float32)
+    ref = O.apply(xp, h, v, slot, gates, H, k, "fp32").astype(np.float64)
+    got = O.apply_hidden(xp, h, W2, slot, gates, H, k, "fp32", hacc_round="none").astype(np.float64)
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() <= 1e-5 * scale
+    wrong = O.apply_hidden(xp, h, np.concatenate([W2[d:], W2[:d]]), slot, gates, H, k, "fp32", hacc_round="none")
+    assert np.abs(wrong - ref).max() > 1e-2 * scale

@@ -152,3 +152,18 @@ def test_full_layer_fp32_matches_reference(name):
     P = O.unpack_state(sd, sh.num_heads)
     r = O.layer_forward(O.from_torch(x), P, sh.num_heads, sh.top_k, sh.dtype)
     _check_output(r["out"], f["ref_out"].astype(np.float64), "fp32")
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_hidden_reorder_with_reference_routing(name):
+    """The hidden-space reordering (paper p.10, Algorithm 1) computes the same function with
+    other rounding points: fed the reference's routing it meets the reference's outputs at
+    the same tolerance as the scatter form."""
+    f, meta, sh, x, sd = _setup(name)
+    dt = sh.dtype
+    P = O.unpack_state(sd, sh.num_heads)
+    perm, uniq, seg, inv = O.sort_segment(f["ref_indices"].reshape(-1), sh.num_experts)
+    h, _ = O.generate(P["latents"], uniq, P["W1"], P["W2"], dt)
+    xp = O.token_proj(O.from_torch(x), P["W2"], dt)
+    out = O.apply_hidden(xp, h, P["W2"], inv, f["ref_scores"], sh.num_heads, sh.top_k, dt)
+    _check_output(out, O.to_f32(f["ref_out"], dt).astype(np.float64), dt, meta["signal"])
