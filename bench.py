@@ -1,6 +1,7 @@
 """Benchmark: ETHOS expert-layer forward tokens/s on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config cfg2]
+    python bench.py --config cfg5     # whole language-model forward (12 expert blocks)
 
 A step is one full forward of the drop-in layer (query projection + BatchNorm,
 product-key routing, reordering, expert generation, apply + scatter-back) over one
@@ -142,6 +143,85 @@ def cpu_baseline(sh, x_cpu, sd_cpu, n_tokens: int) -> dict:
     }
 
 
+def bench_model(args) -> None:
+    """Whole ETHOS LM forward (the reference's CompressedMoEModel with the drop-in expert
+    layer in every block): 12 blocks, d_model 1024, MLA 16 heads with a 256-wide KV latent,
+    vocabulary 100,277, batch 4 x 2048 uniform token ids, bf16, random init."""
+    from ethos_amd.model import CompressedMoEModel, init_random_, lm_config
+    cfg = lm_config()
+    batch, seq = 4, 2048
+    log("[bench] building the language model (random init on the host)")
+    m = init_random_(CompressedMoEModel(cfg), seed=0).to(torch.bfloat16).cuda().eval()
+    ids = torch.randint(0, cfg.vocab_size, (batch, seq), generator=torch.Generator().manual_seed(0)).cuda()
+    with torch.no_grad():
+        log("[bench] warmup")
+        for _ in range(args.warmup):
+            m(ids)
+        torch.cuda.synchronize()
+        log(f"[bench] timing {args.steps} model forwards")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            m(ids)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps * 1e3
+        ms = e0.elapsed_time(e1) / args.steps
+        # one block's expert layer alone, on the block's actual input
+        inputs = {}
+        hk = m.layers[0].mlp.register_forward_pre_hook(lambda mod, a: inputs.__setitem__("x", a[0]))
+        m(ids)
+        hk.remove()
+        x = inputs["x"]
+        for _ in range(2):
+            m.layers[0].mlp(x)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            m.layers[0].mlp(x)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_layer = e0.elapsed_time(e1) / args.steps
+        # the same weights with the expert layers in hidden-space order
+        for layer in m.layers:
+            layer.mlp.hidden_space = True
+        for _ in range(args.warmup):
+            m(ids)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            m(ids)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_h = e0.elapsed_time(e1) / args.steps
+    n_tok = batch * seq
+    line = {
+        "metric": "ETHOS LM forward tokens/sec @1 MI355X",
+        "value": round(n_tok / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "wall_ms_per_step": round(wall, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: uniform token ids, random-init weights",
+        "config": {"workload": f"ETHOS LM forward, {cfg.num_layers} blocks (all expert layers), d_model "
+                               f"{cfg.d_model}, MLA {cfg.num_heads} heads kv {cfg.kv_lora_rank}, vocab "
+                               f"{cfg.vocab_size}, tokens {batch}x{seq}, bf16",
+                   "num_layers": cfg.num_layers, "batch": batch, "seq_len": seq, "parallelism": "single GPU"},
+        "expert_layer_ms": round(ms_layer, 4),
+        "expert_layers_share": round(cfg.num_layers * ms_layer / ms, 4),
+        "alternatives": {"hidden_space": dict(ms_per_step=round(ms_h, 4), value=round(n_tok / (ms_h * 1e-3), 1),
+                                              unit="tokens/s")},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -157,6 +237,10 @@ def main():
         print("bench.py measures one GPU: the expert layer is benchmarked at N=1 only "
               "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
         sys.exit(2)
+
+    if args.config == "cfg5":
+        bench_model(args)
+        return
 
     import ethos_amd
     from ethos_amd.workloads import SHAPES, make_inputs

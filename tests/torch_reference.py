@@ -63,3 +63,68 @@ def layer_forward(P: dict, x: torch.Tensor, n_heads: int, top_k: int, bn_batch_s
     v = hid @ W2[d:].t()                        # h_i W_v, W_v = W2[d:]^T
     y = (a.unsqueeze(-1) * v).sum(dim=2).sum(dim=1) / n_heads
     return y, e
+
+
+# ----------------------------------------------------------------- whole language model
+def _rms(x, w, eps):
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * xf.to(x.dtype)
+
+
+def _rot_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def _attention(P, pre, x, cfg):
+    """DeepseekV3Attention.forward (model.py:103-165) on its matmul + additive-mask path."""
+    b, n, _ = x.shape
+    H, nope, rope, vd = cfg.num_heads, cfg.qk_nope_head_dim, cfg.qk_rope_head_dim, cfg.v_head_dim
+    qd = nope + rope
+    eps = cfg.rms_norm_eps
+    q = F.linear(_rms(F.linear(x, P[pre + "q_a_proj.weight"]), P[pre + "q_a_layernorm.weight"], eps),
+                 P[pre + "q_b_proj.weight"]).view(b, n, H, qd)
+    q_nope, q_pe = q[..., :nope], q[..., nope:]
+    ckv = F.linear(x, P[pre + "kv_a_proj_with_mqa.weight"])
+    c, k_pe = ckv[..., : cfg.kv_lora_rank], ckv[..., cfg.kv_lora_rank:]
+    kv = F.linear(_rms(c, P[pre + "kv_a_layernorm.weight"], eps), P[pre + "kv_b_proj.weight"]).view(b, n, H, nope + vd)
+    k_nope, v = kv[..., :nope], kv[..., nope:]
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, rope, 2).float() / rope))
+    f = torch.outer(torch.arange(n).float(), inv)
+    emb = torch.cat((f, f), dim=-1)
+    cos, sin = emb.cos().to(x.dtype), emb.sin().to(x.dtype)
+    qp = q_pe.transpose(1, 2)
+    kp = k_pe.view(b, n, 1, rope).transpose(1, 2)
+    qp = qp * cos + _rot_half(qp) * sin
+    kp = kp * cos + _rot_half(kp) * sin
+    Q = torch.cat([q_nope.transpose(1, 2), qp], dim=-1)
+    K = torch.cat([k_nope.transpose(1, 2), kp.expand(b, H, n, rope)], dim=-1)
+    mask = torch.triu(torch.full((n, n), float("-inf")), diagonal=1)
+    w = torch.matmul(Q, K.transpose(-2, -1)) * qd ** (-0.5) + mask
+    w = F.softmax(w, dim=-1, dtype=torch.float32).to(Q.dtype)
+    o = torch.matmul(w, v.transpose(1, 2)).transpose(1, 2).reshape(b, n, H * vd)
+    return F.linear(o, P[pre + "o_proj.weight"])
+
+
+def lm_forward(P: dict, ids: torch.Tensor, cfg, routing: dict):
+    """CompressedMoEModel.forward (model.py:384-396) in float32; the expert layer of block i
+    uses the imposed expert ids routing[i] ([n_tok, H, k])."""
+    eps = cfg.rms_norm_eps
+    h = P["tok_embeddings.weight"][ids]
+    b, n, d = h.shape
+    for i in range(cfg.num_layers):
+        pre = f"layers.{i}."
+        hh = h + _attention(P, pre + "self_attn.", _rms(h, P[pre + "input_layernorm.weight"], eps), cfg)
+        z = _rms(hh, P[pre + "post_attention_layernorm.weight"], eps)
+        if i < cfg.num_dense_layers:
+            mp = pre + "mlp."
+            m = F.linear(F.silu(F.linear(z, P[mp + "w1.weight"])) * F.linear(z, P[mp + "w3.weight"]),
+                         P[mp + "w2.weight"])
+        else:
+            sub = {k[len(pre + "mlp."):]: v for k, v in P.items() if k.startswith(pre + "mlp.")}
+            y, _ = layer_forward(sub, z.reshape(-1, d), cfg.num_routing_heads, cfg.top_k, bn_batch_stats=False,
+                                 ids=routing[i])
+            m = y.view(b, n, d)
+        h = hh + m
+    return F.linear(_rms(h, P["norm.weight"], eps), P["output.weight"])
