@@ -229,6 +229,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="token sample for the CPU baseline (0 = skip)")
+    ap.add_argument("--no-alternatives", action="store_true",
+                    help="skip the hidden-space timing (profiling runs: keeps per-kernel averages to one order)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain copy of this many MiB (counter calibration for profiling)")
     args = ap.parse_args()
@@ -285,21 +287,23 @@ def main():
     # The paper's hidden-space reordering (Algorithm 1) of the same layer: no v rows, one
     # projection back per token.  Reported beside the headline, which measures the layer's
     # default execution order.
-    mh = ethos_amd.EthosExpertLayer(sh.config(), hidden_space=True).to(sh.torch_dtype)
-    mh.load_state_dict(sd_cpu)
-    mh = mh.cuda().eval()
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            mh(x)
-        torch.cuda.synchronize()
-        log(f"[bench] timing {args.steps} steps, hidden-space order")
-        ms_h, st_h = timed_steps(mh, x_flat, args.steps)
-    del mh
-    alternatives = {"hidden_space": dict(
-        ms_per_step=round(ms_h, 4), value=round(sh.n_tok / (ms_h * 1e-3), 1), unit="tokens/s",
-        stage_us={k: round(v * 1e3, 2) for k, v in st_h.items()},
-        note="paper Algorithm 1: h_acc = sum a h per token, one W_v projection; same function, "
-             "other rounding points (hidden_space=True)")}
+    alternatives = None
+    if not args.no_alternatives:
+        mh = ethos_amd.EthosExpertLayer(sh.config(), hidden_space=True).to(sh.torch_dtype)
+        mh.load_state_dict(sd_cpu)
+        mh = mh.cuda().eval()
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                mh(x)
+            torch.cuda.synchronize()
+            log(f"[bench] timing {args.steps} steps, hidden-space order")
+            ms_h, st_h = timed_steps(mh, x_flat, args.steps)
+        del mh
+        alternatives = {"hidden_space": dict(
+            ms_per_step=round(ms_h, 4), value=round(sh.n_tok / (ms_h * 1e-3), 1), unit="tokens/s",
+            stage_us={k: round(v * 1e3, 2) for k, v in st_h.items()},
+            note="paper Algorithm 1: h_acc = sum a h per token, one W_v projection; same function, "
+                 "other rounding points (hidden_space=True)")}
 
     cpu = None
     if args.cpu_tokens > 0:
