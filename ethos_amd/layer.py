@@ -117,21 +117,26 @@ class _ExpertStages(torch.autograd.Function):
         dh = torch.zeros_like(hf)
         dxp = torch.zeros_like(xp)
         dg = torch.empty(n_pairs, dtype=f, device=x.device)
-        chunk = max(1024, (1 << 25) // max(hf.shape[1], 1))
-        for p0 in range(0, n_pairs, chunk):
-            p = torch.arange(p0, min(n_pairs, p0 + chunk), device=x.device)
-            t, s = p // (H * k), slot[p]
-            hp, xpp, dwp = hf[s], xp[t], dYB[t]
-            c = (hp * xpp).sum(-1)
+        # chunks of whole tokens: the token sums are reshape-and-sum, only the expert sums
+        # scatter (index_add over the pairs' slots)
+        hk = H * k
+        tok_chunk = max(1, ((1 << 25) // max(hf.shape[1], 1)) // hk)
+        for t0 in range(0, n, tok_chunk):
+            t1 = min(n, t0 + tok_chunk)
+            nt = t1 - t0
+            s = slot[t0 * hk:t1 * hk]
+            hp = hf[s].view(nt, hk, -1)
+            xpp, dwp = xp[t0:t1, None, :], dYB[t0:t1, None, :]
+            c = (hp * xpp).sum(-1)                                       # [nt, hk]
             act = F.gelu(c)
-            gp = g[p]
+            gp = g[t0 * hk:t1 * hk].view(nt, hk)
             a = act * gp
             da = (dwp * hp).sum(-1)
-            dg[p] = act * da
+            dg[t0 * hk:t1 * hk] = (act * da).reshape(-1)
             dc = gp * _gelu_grad(c) * da
-            hacc.index_add_(0, t, a[:, None] * hp)
-            dxp.index_add_(0, t, dc[:, None] * hp)
-            dh.index_add_(0, s, a[:, None] * dwp + dc[:, None] * xpp)
+            hacc[t0:t1] = (a[..., None] * hp).sum(1)
+            dxp[t0:t1] = (dc[..., None] * hp).sum(1)
+            dh.index_add_(0, s, (a[..., None] * dwp + dc[..., None] * xpp).view(nt * hk, -1))
         dB = dY.T @ hacc
         dA = xf.T @ dxp
         dx = dxp @ A.T
@@ -251,22 +256,35 @@ class ProductKeyRouter(nn.Module):
         statistics, which the routing pass has already updated."""
         f = torch.float32
         H, dq, K = self.num_heads, self.d_query, self.num_sub_keys
+        n = x_flat.shape[0]
         w = torch.stack([m.weight for m in self.query_projs]).to(f).reshape(H * dq, -1)
         b = torch.stack([m.bias for m in self.query_projs]).to(f).reshape(-1)
-        q = (x_flat.to(f) @ w.T + b).view(-1, H, dq)
-        qs = []
-        for h, m in enumerate(self.query_norms):
-            batch = m.training or not m.track_running_stats
-            qs.append(F.batch_norm(q[:, h], None if batch else m.running_mean.to(f),
-                                   None if batch else m.running_var.to(f),
-                                   m.weight.to(f) if m.affine else None, m.bias.to(f) if m.affine else None,
-                                   batch, 0.0, m.eps))
-        q = torch.stack(qs, dim=1)
+        q = x_flat.to(f) @ w.T + b                                       # [n, H dq]
+        # the H per-head BatchNorms as one over H dq channels (same per-channel statistics)
+        norms = list(self.query_norms)
+        batch = [m.training or not m.track_running_stats for m in norms]
+        if all(batch) or not any(batch):
+            cat = lambda ts: torch.cat([t.to(f) for t in ts])  # noqa: E731
+            affine = all(m.affine for m in norms)
+            q = F.batch_norm(q, None if batch[0] else cat(m.running_mean for m in norms),
+                             None if batch[0] else cat(m.running_var for m in norms),
+                             cat(m.weight for m in norms) if affine else None,
+                             cat(m.bias for m in norms) if affine else None,
+                             batch[0], 0.0, norms[0].eps) if len({m.eps for m in norms}) == 1 else None
+        else:
+            q = None
+        if q is None:  # heads in different modes or with different eps: one call per head
+            q = (x_flat.to(f) @ w.T + b).view(n, H, dq)
+            q = torch.stack([F.batch_norm(q[:, h], None if bt else m.running_mean.to(f),
+                                          None if bt else m.running_var.to(f),
+                                          m.weight.to(f) if m.affine else None, m.bias.to(f) if m.affine else None,
+                                          bt, 0.0, m.eps) for h, (m, bt) in enumerate(zip(norms, batch))], dim=1)
+        q = q.view(n * H, dq)
         half = dq // 2
-        i1, i2 = ids // K, ids % K
-        s1 = (q[:, :, None, :half] * self.sub_keys_1.weight.to(f)[i1]).sum(-1)
-        s2 = (q[:, :, None, half:] * self.sub_keys_2.weight.to(f)[i2]).sum(-1)
-        return torch.softmax(s1 + s2, dim=-1)
+        # dense sub-scores, then the chosen columns: the backward is a GEMM for the keys
+        s1 = (q[:, :half] @ self.sub_keys_1.weight.to(f).T).gather(1, (ids // K).view(n * H, -1))
+        s2 = (q[:, half:] @ self.sub_keys_2.weight.to(f).T).gather(1, (ids % K).view(n * H, -1))
+        return torch.softmax(s1 + s2, dim=-1).view(ids.shape)
 
     def forward(self, x_flat: torch.Tensor):
         """(scores [n, H, k], expert ids [n, H, k] int64) as model.py:208-254.  With autograd
