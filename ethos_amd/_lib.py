@@ -35,6 +35,8 @@ SIGNATURES = {
     "ethos_apply_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "ethos_apply_scatter": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
                                            _vp, _sz, _vp, _vp]),
+    "ethos_expert_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                             _vp]),
     "ethos_apply_hidden_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ethos_apply_hidden": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
                                           _vp, _sz, _vp, _vp]),

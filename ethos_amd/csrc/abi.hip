@@ -244,4 +244,27 @@ int ethos_apply_hidden(const void* x, const void* w2, const void* h, const int32
     return hip_status(rc, "ethos_apply_hidden");
 }
 
+int ethos_expert_backward(const void* h, const float* xp, const float* dyb, const int32_t* pair_slot,
+                          const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden,
+                          int32_t dtype, float* dscores, float* hacc, float* dxp, float* dh, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_expert_backward: unknown dtype %d", dtype);
+    if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || d_hidden <= 0)
+        return fail(ETHOS_ESIZE, "ethos_expert_backward: bad sizes");
+    const int vec = dtype == ETHOS_BF16 ? 8 : 4;
+    if (d_hidden % vec || ethos::apply_chunks(d_hidden, dtype) > 8)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_expert_backward: d_hidden=%d must be a multiple of %d and <= %d",
+                    d_hidden, vec, 8 * 64 * vec);
+    if (n_tok * n_heads * top_k > INT32_MAX || n_tok > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_expert_backward: too many pairs");
+    if (n_tok == 0) return 0;
+    if (!h || !xp || !dyb || !pair_slot || !scores || !dscores || !hacc || !dxp || !dh)
+        return fail(ETHOS_ENULL, "ethos_expert_backward: null pointer");
+    if (!aligned16(h)) return fail(ETHOS_EALIGN, "ethos_expert_backward: h must be 16-byte aligned");
+    const int rc = ethos::launch_expert_backward(h, xp, dyb, pair_slot, scores, n_tok, n_heads, top_k, d_hidden, dtype,
+                                                 dscores, hacc, dxp, dh, num_cus(), (hipStream_t)stream);
+    if (rc < 0) return fail(ETHOS_EUNSUPPORTED, "ethos_expert_backward: d_hidden=%d not supported", d_hidden);
+    return hip_status(rc, "ethos_expert_backward");
+}
+
 }  // extern "C"

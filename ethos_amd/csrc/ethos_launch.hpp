@@ -29,6 +29,9 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
                     void* vout, int num_cus, hipStream_t stream);
 
 int apply_chunks(int d, int dtype);
+int launch_expert_backward(const void* hid, const float* xp, const float* dyb, const int32_t* pair_slot,
+                           const void* gates, int64_t n_tok, int H, int k, int dh, int dtype, float* dg, float* hacc,
+                           float* dxp, float* dhs, int num_cus, hipStream_t stream);
 size_t apply_hidden_workspace_bytes(int64_t n_tok, int H, int k, int d, int dh, int dtype);
 int launch_apply_hidden(const void* x, const void* w2, const void* hid, const int32_t* perm,
                         const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,

@@ -185,3 +185,27 @@ def apply_hidden(x: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, seg: dict, 
                                    n_heads, top_k, d, dh, code, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
     check(rc, "ethos_apply_hidden")
     return out
+
+
+def expert_backward(h: torch.Tensor, xp: torch.Tensor, dyb: torch.Tensor, pair_slot: torch.Tensor, gates: torch.Tensor,
+                    n_heads: int, top_k: int, U: int):
+    """Per-pair part of the expert stages' backward: (dgates [n, H, k], hacc [n, dh], dxp [n, dh],
+    dh [U, dh]), all float32, from xp = x W_u and dyb = (dy / H) W_v^T (float32 [n, dh])."""
+    _need(h, "h", dim=2)
+    _need(xp, "xp", torch.float32, 2)
+    _need(dyb, "dyb", torch.float32, 2)
+    _need(pair_slot, "pair_slot", torch.int32)
+    _need(gates, "gates", h.dtype)
+    n, dh = xp.shape
+    if dyb.shape != (n, dh) or h.shape[1] != dh or gates.numel() != n * n_heads * top_k:
+        raise RuntimeError("expert_backward: inconsistent shapes")
+    dev = h.device
+    dg = torch.empty(gates.shape, dtype=torch.float32, device=dev)
+    hacc = torch.empty((n, dh), dtype=torch.float32, device=dev)
+    dxp = torch.empty((n, dh), dtype=torch.float32, device=dev)
+    dhs = torch.zeros((max(U, 1), dh), dtype=torch.float32, device=dev)
+    rc = load().ethos_expert_backward(h.data_ptr(), xp.data_ptr(), dyb.data_ptr(), pair_slot.data_ptr(),
+                                      gates.data_ptr(), n, n_heads, top_k, dh, dtype_code(h.dtype), dg.data_ptr(),
+                                      hacc.data_ptr(), dxp.data_ptr(), dhs.data_ptr(), _stream())
+    check(rc, "ethos_expert_backward")
+    return dg, hacc, dxp, dhs[:U]

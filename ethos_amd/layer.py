@@ -78,9 +78,10 @@ class _ExpertStages(torch.autograd.Function):
     dc_p = g_p gelu'(c_p) da_p;  dxp_t = Σ_p dc_p h_s;  dh_s = Σ_p (dc_p xp_t + a_p dY_t B);
     dA = x^T dxp,  dB = dY^T hacc with hacc_t = Σ_p a_p h_s,  dx = dxp A^T;
     dpre = gelu'(pre) dh,  dC = dpre^T z,  dz = dpre C (added into the latent rows of the
-    unique experts).  v rows are not needed.  The per-pair sums run over chunks of pairs with
-    index_add, so temporaries stay bounded.  Both execution orders (scatter of v rows,
-    hidden-space reordering) compute this same function, so they share the backward.
+    unique experts).  v rows are not needed.  The per-pair terms, the token sums (hacc, dxp)
+    and the expert sums (dh, float atomics) come from one HIP kernel (ethos_expert_backward);
+    the rest are GEMMs.  Both execution orders (scatter of v rows, hidden-space reordering)
+    compute this same function, so they share the backward.
 
     The gates enter as `gates_exact` (the values the forward uses) and `gate_path` (a
     float32 tensor of the same values carrying the router's graph), whose gradient is dg.
@@ -107,36 +108,10 @@ class _ExpertStages(torch.autograd.Function):
         A, B, C = w2[:d].to(f), w2[d:].to(f), w1.to(f)
         xf = x.to(f)
         xp = xf @ A
-        hf = h[:U].to(f)
-        g = gates.reshape(-1).to(f)
-        slot = pair_slot.long()
         dY = dy.to(f) * (1.0 / H)
         dYB = dY @ B
-        n_pairs = n * H * k
-        hacc = torch.zeros_like(xp)
-        dh = torch.zeros_like(hf)
-        dxp = torch.zeros_like(xp)
-        dg = torch.empty(n_pairs, dtype=f, device=x.device)
-        # chunks of whole tokens: the token sums are reshape-and-sum, only the expert sums
-        # scatter (index_add over the pairs' slots)
-        hk = H * k
-        tok_chunk = max(1, ((1 << 25) // max(hf.shape[1], 1)) // hk)
-        for t0 in range(0, n, tok_chunk):
-            t1 = min(n, t0 + tok_chunk)
-            nt = t1 - t0
-            s = slot[t0 * hk:t1 * hk]
-            hp = hf[s].view(nt, hk, -1)
-            xpp, dwp = xp[t0:t1, None, :], dYB[t0:t1, None, :]
-            c = (hp * xpp).sum(-1)                                       # [nt, hk]
-            act = F.gelu(c)
-            gp = g[t0 * hk:t1 * hk].view(nt, hk)
-            a = act * gp
-            da = (dwp * hp).sum(-1)
-            dg[t0 * hk:t1 * hk] = (act * da).reshape(-1)
-            dc = gp * _gelu_grad(c) * da
-            hacc[t0:t1] = (a[..., None] * hp).sum(1)
-            dxp[t0:t1] = (dc[..., None] * hp).sum(1)
-            dh.index_add_(0, s, (a[..., None] * dwp + dc[..., None] * xpp).view(nt * hk, -1))
+        # per-pair terms, token sums and expert sums in one HIP kernel (ethos_expert_backward)
+        dg, hacc, dxp, dh = hip.expert_backward(h, xp, dYB, pair_slot, gates, H, k, U)
         dB = dY.T @ hacc
         dA = xf.T @ dxp
         dx = dxp @ A.T

@@ -13,6 +13,7 @@
  *   ethos_generate       hypernetwork expert generation over the unique experts
  *   ethos_apply_scatter  per-pair activation and weighted scatter-back into tokens
  *   ethos_apply_hidden   the same, by hidden-space reordering (no v rows)
+ *   ethos_expert_backward  per-pair part of the expert stages' backward
  *
  * Conventions (every entry point):
  *   - All pointers are device pointers owned by the caller; nothing is allocated.
@@ -187,6 +188,25 @@ int ethos_apply_hidden(const void* x, const void* w2, const void* h, const int32
                        const int32_t* pair_slot, const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k,
                        int32_t d_model, int32_t d_hidden, int32_t dtype, void* workspace, size_t workspace_bytes,
                        void* out, void* stream);
+
+/*
+ * Per-pair part of the expert stages' backward: the derivative of model.py:312-341, which
+ * the reference obtains from autograd on its pure-PyTorch layer (its Triton layer,
+ * kernels.py:145-221, has no backward).  With xp = x W_u and dyb = (dy / n_heads) W_v^T
+ * (both float32 [n_tok, d_hidden], formed by the caller's GEMMs), for pair p of token t
+ * with expert slot s: c = h_s . xp_t, a = gelu(c) g_p, da = dyb_t . h_s;
+ *   dscores[p] = gelu(c) da                               float32 [n_tok, n_heads, top_k]
+ *   hacc[t]    = sum_p a h_s                              float32 [n_tok, d_hidden]
+ *   dxp[t]     = sum_p g gelu'(c) da h_s                  float32 [n_tok, d_hidden]
+ *   dh[s]     += a dyb_t + g gelu'(c) da xp_t             float32 [>= U, d_hidden], added
+ *                                                          to (zero it first); float atomics,
+ *                                                          so the sums' order varies per run
+ *   h, pair_slot, scores  as for ethos_apply_scatter (h 16-byte aligned).
+ * Limits: d_hidden a multiple of 8 (bf16) or 4 (fp32), <= 4096 (bf16) / 2048 (fp32).
+ */
+int ethos_expert_backward(const void* h, const float* xp, const float* dyb, const int32_t* pair_slot,
+                          const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden,
+                          int32_t dtype, float* dscores, float* hacc, float* dxp, float* dh, void* stream);
 
 #ifdef __cplusplus
 }
