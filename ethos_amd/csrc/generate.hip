@@ -236,6 +236,180 @@ __global__ __launch_bounds__(kHWaves * 64) void hidden_bf16_kernel(const uint16_
 }
 
 // ---------------------------------------------------------------------------------
+// Hidden rows, bf16, W1-stationary (the form of expand_ws_bf16_kernel applied to GEMM1):
+// h = RN(gelu(RN(z W1^T))).  Each wave owns 64 hidden units for the whole launch, its W1
+// rows in AGPRs (64 registers, loaded once); the latent rows of 64 unique experts at a
+// time are gathered global -> LDS by buffer_load ... lds one tile ahead (double buffered;
+// row r's 16-byte piece p at slot p ^ (r % 16), so fragment reads are conflict-free) and
+// each fragment read feeds two MFMAs.  The unique ids of all of a workgroup's tiles are
+// copied to LDS once at the start, so the loop issues no id loads.  GELU comes from the
+// table in LDS; the rows leave through a per-wave staging area as whole 128-byte lines.
+// The products (A = W1 rows, B = latent rows, k-steps in order) are those of
+// hidden_bf16_kernel with the operands exchanged, so the pre-activations and h are equal
+// to within the order of the MFMA's internal sums.
+// ---------------------------------------------------------------------------------
+constexpr int kHsRows = 64;       // experts per tile
+constexpr int kHsMaxTiles = 32;   // tiles per workgroup whose ids fit the LDS id table
+
+template <int DL, int DH>
+__global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __restrict__ latents, int64_t n_experts,
+                                                            const int32_t* __restrict__ uniq,
+                                                            const int32_t* __restrict__ n_unique, int64_t max_unique,
+                                                            const uint16_t* __restrict__ w1,
+                                                            uint16_t* __restrict__ hout) {
+    constexpr int kWaves = DH / 64;
+    constexpr int KS1 = DL / 16;                 // k-steps
+    constexpr int PPR = DL / 8;                  // 16-byte pieces per latent row
+    constexpr int kCopies = kHsRows * PPR / 64;  // copy instructions per tile
+    constexpr int kCW = kCopies / kWaves;        // per wave
+    constexpr int kNSt = 8;                      // h-row stores per wave and tile
+    constexpr int LA = 2;                        // fragment reads run LA k-steps ahead
+    static_assert(PPR == 16 && kCopies % kWaves == 0 && KS1 >= kNSt && KS1 > LA, "latent tile shape");
+    __shared__ __align__(16) uint16_t lut[kGeluLutSize];
+    __shared__ uint4 zs[2][kHsRows * PPR];
+    __shared__ u32x4_t stg[kWaves][kHsRows * 8];
+    __shared__ int32_t ids_s[kHsMaxTiles][kHsRows];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
+    const int n_tiles = (U + kHsRows - 1) / kHsRows;
+    const int G = gridDim.x;
+    const int hid0 = wave * 64;
+
+    // the GELU table and this workgroup's tile ids (-1 past U or for ids outside the table)
+    for (int e = tid; e < kGeluLutSize / 8; e += DH) reinterpret_cast<uint4*>(lut)[e] = reinterpret_cast<const uint4*>(kGeluLut)[e];
+    for (int e = tid; e < kHsMaxTiles * kHsRows; e += DH) {
+        const int i = e / kHsRows, r = e % kHsRows;
+        const int64_t u = ((int64_t)blockIdx.x + (int64_t)i * G) * kHsRows + r;
+        int id = -1;
+        if (u < U) {
+            const int v = uniq[u];
+            id = v >= 0 && v < n_experts ? v : -1;
+        }
+        ids_s[i][r] = id;
+    }
+    const uint32_t lut_bytes = lds_addr(lut);
+    // the wave's W1 rows: A fragment (cb, s) = W1[hid0 + 32 cb + l32][16 s + 8 h ..]
+    bf16x8_t wf[2][KS1];
+    {
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(w1), (short)0, DH * DL * (int)sizeof(uint16_t), 0x00020000);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int s = 0; s < KS1; ++s)
+                wf[cb][s] = __builtin_bit_cast(
+                    bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                  wr, ((hid0 + 32 * cb + l32) * DL + 16 * s + 8 * h) * (int)sizeof(uint16_t), 0, 0));
+    }
+    // latent rows: the whole table as one descriptor (the launch checks its size); absent
+    // rows take an offset past it and read as zero
+    const i32x4_t zr = buffer_rsrc(latents, (uint32_t)(n_experts * DL * (int64_t)sizeof(uint16_t)));
+    constexpr int kZOOB = 0x7ffffff0;
+    // copy instruction j = it * kWaves + wave of a tile moves rows 4 j .. 4 j + 3: lane i
+    // takes row 4 j + i / 16, LDS slot i % 16, global piece (i % 16) ^ (row % 16)
+    auto copy = [&](int i_tile, int buf) {
+#pragma unroll
+        for (int it = 0; it < kCW; ++it) {
+            const int j = it * kWaves + wave;
+            const int r = 4 * j + (lane >> 4), sl = lane & 15;
+            const int id = ids_s[i_tile][r];
+            const int voff = id >= 0 ? (id * DL + 8 * (sl ^ (r & 15))) * (int)sizeof(uint16_t) : kZOOB;
+            lds_dma16(zr, voff, 0, lds_addr(&zs[buf][64 * j]));
+        }
+    };
+    // B fragment (mb, s): row 32 mb + l32, piece 2 s + h, at slot (2 s + h) ^ (l32 % 16)
+    const int zb_off = l32 * PPR;
+    const int st_voff = ((lane >> 3) * DH + hid0 + 8 * (lane & 7)) * (int)sizeof(uint16_t);
+    constexpr int kOOB = 0x40000000;
+    u32x4_t* my = stg[wave];
+    u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
+    constexpr int kWaitVm8 = 0x0f78;  // s_waitcnt vmcnt(8)
+    constexpr int kWaitVm0 = 0x0f70;  // s_waitcnt vmcnt(0)
+
+    __syncthreads();  // table and ids in place
+    if ((int)blockIdx.x < n_tiles) copy(0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // W1 rows and the first tile
+
+    __amdgpu_buffer_rsrc_t hr_prev = __builtin_amdgcn_make_buffer_rsrc(hout, (short)0, 0, 0x00020000);
+    bool have_prev = false;
+    int i = 0;
+    for (int64_t t = blockIdx.x; t < n_tiles; t += G, ++i) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this tile's rows have landed
+        __syncthreads();
+        u32x4_t outv[kNSt];
+#pragma unroll
+        for (int k = 0; k < kNSt; ++k) {
+            const int r = 8 * k + (lane >> 3);
+            outv[k] = my[r * 8 + ((lane & 7) ^ (r & 7))];
+        }
+        const int st_base = have_prev ? st_voff : kOOB;
+        if (t + G < n_tiles) copy(i + 1, (i + 1) & 1);
+        const uint4* cur = zs[i & 1];
+        auto bfrag = [&](int s, int mb) {
+            return __builtin_bit_cast(bf16x8_t, cur[zb_off + mb * 32 * PPR + ((2 * s + h) ^ (l32 & 15))]);
+        };
+        bf16x8_t bfr[LA + 1][2];
+        f32x16_t acc[2][2];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) acc[mb][cb] = f32x16_zero();
+#pragma unroll
+        for (int s = 0; s < LA; ++s)
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) bfr[s][mb] = bfrag(s, mb);
+#pragma unroll
+        for (int s = 0; s < KS1; ++s) {
+            if (s + LA < KS1) {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) bfr[(s + LA) % (LA + 1)][mb] = bfrag(s + LA, mb);
+            }
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) asm volatile("" : "+a"(wf[cb][s]));
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                    acc[mb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb][s], bfr[s % (LA + 1)][mb],
+                                                                         acc[mb][cb], 0, 0, 0);
+            // the previous tile's rows, one store per k-step (after this tile's copies)
+            if (s < kNSt)
+                __builtin_amdgcn_raw_buffer_store_b128(outv[s], hr_prev, st_base + s * 8 * DH * 2, 0, 0);
+        }
+        // acc[mb][cb][i]: hidden unit hid0 + 32 cb + 8 (i/4) + 4h + i%4 of expert 32 mb + l32,
+        // i.e. 8-byte half h of 16-byte piece 4 cb + i/4 of staged row 32 mb + l32
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const int r = mb * 32 + l32;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4) {
+                    const int q = 4 * cb + a4;
+                    my2[r * 16 + (q ^ (r & 7)) * 2 + h] = u32x2_t{
+                        gelu_bf16x2_lut(pack_bf16x2(acc[mb][cb][4 * a4], acc[mb][cb][4 * a4 + 1]), lut_bytes),
+                        gelu_bf16x2_lut(pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3]), lut_bytes)};
+                }
+        }
+        const int64_t row0 = t * kHsRows;
+        const int live = U - (int)row0 < kHsRows ? U - (int)row0 : kHsRows;
+        hr_prev = __builtin_amdgcn_make_buffer_rsrc(hout + row0 * DH, (short)0, live * DH * (int)sizeof(uint16_t),
+                                                    0x00020000);
+        have_prev = true;
+    }
+    if (have_prev) {
+#pragma unroll
+        for (int k = 0; k < kNSt; ++k) {
+            const int r = 8 * k + (lane >> 3);
+            __builtin_amdgcn_raw_buffer_store_b128(my[r * 8 + ((lane & 7) ^ (r & 7))], hr_prev,
+                                                   st_voff + k * 8 * DH * 2, 0, 0);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // v rows, bf16: v = RN(h W_v^T) over tiles of 256 experts, one workgroup of 4 waves per
 // CU, 64 experts (two blocks of 32) per wave.  The wave's hidden rows (64 x DH bf16,
 // 256 registers per lane) are loaded into AGPRs, which the MFMAs read directly; every
@@ -648,10 +822,20 @@ static bool launch_generate_bf16(const void* latents, int64_t n_experts, const i
                                  int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* hout,
                                  void* uv, int num_cus, hipStream_t stream) {
     if (dl != DL || dh != DH || d2 % kG2Cols) return false;
-    const int64_t blocks = (max_unique + 32 * kHWaves - 1) / (32 * kHWaves);
-    const unsigned g1 = (unsigned)(blocks < num_cus ? (blocks > 0 ? blocks : 1) : num_cus);
-    hipLaunchKernelGGL((hidden_bf16_kernel<DL, DH>), dim3(g1), dim3(kHWaves * 64), 0, stream,
-                       (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (uint16_t*)hout);
+    // W1-stationary hidden rows when every workgroup's tile ids fit its LDS table and the
+    // latent table fits one buffer descriptor
+    const int64_t htiles = (max_unique + kHsRows - 1) / kHsRows;
+    const int64_t hgrid = htiles < num_cus ? (htiles > 0 ? htiles : 1) : num_cus;
+    if ((htiles + hgrid - 1) / hgrid <= kHsMaxTiles && n_experts * DL * 2 < 0x7ff00000ll) {
+        hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
+                           (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
+                           (uint16_t*)hout);
+    } else {
+        const int64_t blocks = (max_unique + 32 * kHWaves - 1) / (32 * kHWaves);
+        const unsigned g1 = (unsigned)(blocks < num_cus ? (blocks > 0 ? blocks : 1) : num_cus);
+        hipLaunchKernelGGL((hidden_bf16_kernel<DL, DH>), dim3(g1), dim3(kHWaves * 64), 0, stream,
+                           (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (uint16_t*)hout);
+    }
     if (uv == nullptr) return true;  // hidden rows only
     // W_v-stationary when d2 splits into 256-column groups that fill the XCDs evenly
     const int n_cg = d2 / kWsCols;
