@@ -148,6 +148,57 @@ __device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t 
     return (m & a) | (~m & b);
 }
 
+__device__ __forceinline__ uint32_t pk_max_i16(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_pk_max_i16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_min_i16_vv(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_pk_min_i16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ uint32_t pk_lshl_b16(uint32_t a, uint32_t sh) {  // sh: wave-uniform (SGPR)
+    uint32_t r;
+    asm("v_pk_lshlrev_b16 %0, %1, %2" : "=v"(r) : "s"(sh), "v"(a));
+    return r;
+}
+
+// The same function as gelu_bf16x2_lut from a table of float32 pairs (M, C) with
+// RN(GELU(x)) = RN_bf16(fma(x, M, C)) for every input, so that no per-case selection is
+// needed: entries 0 .. kGeluMcSize / 2 - 1 serve x >= +0, the rest x <= -0, each half
+// ordered as (|x| < 2^-10: M = 0.5, C = +-0), (the table inputs: M = 0, C = the table
+// value), (x >= 4: M = 1, C = 0 / x <= -16: M = 0, C = -0).  The index is
+// clamp(|x|bits - 0x3a7f, 0, hi) + base with hi = 1537 / 1793 and base = 0 / 1538.
+constexpr int kGeluMcPos = 1538;               // entries for x >= +0
+constexpr int kGeluMcSize = kGeluMcPos + 1794;  // and for x <= -0
+__device__ __forceinline__ f32x2_t gelu_mc_entry(int i, const uint16_t* lut16) {
+    if (i < kGeluMcPos) {
+        if (i == 0) return f32x2_t{0.5f, 0.0f};
+        if (i == kGeluMcPos - 1) return f32x2_t{1.0f, 0.0f};
+        return f32x2_t{0.0f, __uint_as_float((uint32_t)lut16[i - 1] << 16)};
+    }
+    const int j = i - kGeluMcPos;
+    if (j == 0) return f32x2_t{0.5f, -0.0f};
+    if (j == 1793) return f32x2_t{0.0f, -0.0f};
+    return f32x2_t{0.0f, __uint_as_float((uint32_t)lut16[1536 + j - 1] << 16)};
+}
+__device__ __forceinline__ uint32_t gelu_bf16x2_mc(uint32_t pk, uint32_t mc_bytes) {
+    const uint32_t a = pk & 0x7fff7fffu;
+    const uint32_t negm = pk_sign_mask(pk);
+    // |x|bits - 0x3a7f as a signed 16-bit value: <= 0 below the table, 1 + d inside it
+    const uint32_t d = pk_max_i16(pk_sub_u16(a, 0x3a7f3a7fu), 0u);
+    const uint32_t hi = 0x06010601u + (negm & 0x01000100u);  // 1537 or 1793
+    const uint32_t idx = pk_min_i16_vv(d, hi) + (negm & 0x06020602u);  // + 1538 for x <= -0
+    const uint32_t off = pk_lshl_b16(idx, 0x00030003u);  // 8-byte entries (max offset 26.6 KB)
+    typedef const __attribute__((address_space(3))) f32x2_t* lds_f2_ptr;
+    const f32x2_t e0 = *(lds_f2_ptr)(size_t)(mc_bytes + (off & 0xffffu));
+    const f32x2_t e1 = *(lds_f2_ptr)(size_t)(mc_bytes + (off >> 16));
+    const float r0 = __builtin_fmaf(__uint_as_float(pk << 16), e0[0], e0[1]);
+    const float r1 = __builtin_fmaf(__uint_as_float(pk & 0xffff0000u), e1[0], e1[1]);
+    return pack_bf16x2(r0, r1);
+}
+
 __device__ __forceinline__ uint32_t gelu_bf16x2_lut(uint32_t pk, uint32_t lut_bytes) {
     const uint32_t a = pk & 0x7fff7fffu;
     const uint32_t negm = pk_sign_mask(pk);

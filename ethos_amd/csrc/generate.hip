@@ -265,7 +265,7 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
     constexpr int kNSt = 8;                      // h-row stores per wave and tile
     constexpr int LA = 2;                        // fragment reads run LA k-steps ahead
     static_assert(PPR == 16 && kCopies % kWaves == 0 && KS1 >= kNSt && KS1 > LA, "latent tile shape");
-    __shared__ __align__(16) uint16_t lut[kGeluLutSize];
+    __shared__ __align__(16) f32x2_t gmc[kGeluMcSize];
     __shared__ uint4 zs[2][kHsRows * PPR];
     __shared__ u32x4_t stg[kWaves][kHsRows * 8];
     __shared__ int32_t ids_s[kHsMaxTiles][kHsRows];
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
     const int hid0 = wave * 64;
 
     // the GELU table and this workgroup's tile ids (-1 past U or for ids outside the table)
-    for (int e = tid; e < kGeluLutSize / 8; e += DH) reinterpret_cast<uint4*>(lut)[e] = reinterpret_cast<const uint4*>(kGeluLut)[e];
+    for (int e = tid; e < kGeluMcSize; e += DH) gmc[e] = gelu_mc_entry(e, kGeluLut);
     for (int e = tid; e < kHsMaxTiles * kHsRows; e += DH) {
         const int i = e / kHsRows, r = e % kHsRows;
         const int64_t u = ((int64_t)blockIdx.x + (int64_t)i * G) * kHsRows + r;
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
         }
         ids_s[i][r] = id;
     }
-    const uint32_t lut_bytes = lds_addr(lut);
+    const uint32_t mc_bytes = lds_addr(gmc);
     // the wave's W1 rows: A fragment (cb, s) = W1[hid0 + 32 cb + l32][16 s + 8 h ..]
     bf16x8_t wf[2][KS1];
     {
@@ -389,8 +389,8 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
                 for (int a4 = 0; a4 < 4; ++a4) {
                     const int q = 4 * cb + a4;
                     my2[r * 16 + (q ^ (r & 7)) * 2 + h] = u32x2_t{
-                        gelu_bf16x2_lut(pack_bf16x2(acc[mb][cb][4 * a4], acc[mb][cb][4 * a4 + 1]), lut_bytes),
-                        gelu_bf16x2_lut(pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3]), lut_bytes)};
+                        gelu_bf16x2_mc(pack_bf16x2(acc[mb][cb][4 * a4], acc[mb][cb][4 * a4 + 1]), mc_bytes),
+                        gelu_bf16x2_mc(pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3]), mc_bytes)};
                 }
         }
         const int64_t row0 = t * kHsRows;
