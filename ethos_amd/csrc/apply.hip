@@ -297,13 +297,25 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
                             float vf[N];
                             Vec16<T>::unpack(vr[q][c], vf);
 #pragma unroll
-                            for (int v = 0; v < N; ++v) hacc[c * N + v] += Elem<T>::round32(a[q] * vf[v]);
+                            for (int v = 0; v < N; v += 2) {
+                                float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
+                                Elem<T>::round32x2(p0, p1);  // RN_T(a v)
+                                hacc[c * N + v] += p0;
+                                hacc[c * N + v + 1] += p1;
+                            }
                         }
                     }
                 }
             }
 #pragma unroll
-            for (int e = 0; e < CH * N; ++e) o[e] = Elem<T>::round32(o[e] + Elem<T>::round32(hacc[e]));
+            for (int e = 0; e < CH * N; e += 2) {
+                float h0 = hacc[e], h1 = hacc[e + 1];
+                Elem<T>::round32x2(h0, h1);  // the head's sum cast to T
+                float o0 = o[e] + h0, o1 = o[e + 1] + h1;
+                Elem<T>::round32x2(o0, o1);  // the running head sum in T
+                o[e] = o0;
+                o[e + 1] = o1;
+            }
         }
 #pragma unroll
         for (int c = 0; c < CH; ++c) {

@@ -54,6 +54,7 @@ template <> struct Elem<float> {
     __device__ __forceinline__ static float from_f64(double v) { return (float)v; }
     // round a float to T and return the T value as float
     __device__ __forceinline__ static float round32(float v) { return v; }
+    __device__ __forceinline__ static void round32x2(float& a, float& b) {}
     __device__ __forceinline__ static float round64(double v) { return (float)v; }
 };
 template <> struct Elem<uint16_t> {
@@ -63,8 +64,16 @@ template <> struct Elem<uint16_t> {
     __device__ __forceinline__ static uint16_t from_f32(float v) { return f32_to_bf16_bits(v); }
     __device__ __forceinline__ static uint16_t from_f64(double v) { return f32_to_bf16_bits(f64_to_f32_odd(v)); }
     __device__ __forceinline__ static float round32(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+    // two values at once through the hardware conversion (round to nearest even)
+    __device__ __forceinline__ static void round32x2(float& a, float& b);
     __device__ __forceinline__ static float round64(double v) { return bf16_bits_to_f32(from_f64(v)); }
 };
+
+__device__ __forceinline__ void Elem<uint16_t>::round32x2(float& a, float& b) {
+    const uint32_t pk = pack_bf16x2(a, b);
+    a = __uint_as_float(pk << 16);
+    b = __uint_as_float(pk & 0xffff0000u);
+}
 
 // Exact GELU (erf form), fp32.
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }

@@ -316,7 +316,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             const float qn = sqrtf(wave_sum(sq)) * (1.0f + 0x1p-12f);
 
             // up: upper bounds of the scores (filter); cs: certified scores or kRtPending
-            float up[kRtSlots];
+            float up[kRtSlots];   // RN_T of the upper bounds
             uint32_t cs[kRtSlots];
             float lane_max = -__builtin_huge_valf();
             uint32_t emax_bits = 0;
@@ -328,9 +328,11 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
                 if (j < K) {
                     const float sj = S[lr * pitch + j];
                     const float marg = gamma * qn * kn[half * kpad + j] + fabsf(sj) * 0x1p-21f + 0x1p-120f;
-                    up[m] = sj + marg;
-                    const uint32_t lo = __float_as_uint(Elem<T>::round32(sj - marg));
-                    const uint32_t hi = __float_as_uint(Elem<T>::round32(up[m]));
+                    float lo_f = sj - marg, hi_f = sj + marg;
+                    Elem<T>::round32x2(lo_f, hi_f);  // RN_T of both ends (rounding is monotone)
+                    up[m] = hi_f;
+                    const uint32_t lo = __float_as_uint(lo_f);
+                    const uint32_t hi = __float_as_uint(hi_f);
                     if (lo == hi && (lo & 0x7f800000u) != 0x7f800000u) cs[m] = lo;
                     lane_max = fmaxf(lane_max, sj);
                     emax_bits = max(emax_bits, __float_as_uint(marg));
@@ -354,7 +356,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             int n = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
-                const bool f = lane + m * kWave < K && Elem<T>::round32(up[m]) >= thr;
+                const bool f = lane + m * kWave < K && up[m] >= thr;
                 fbits |= (uint32_t)f << m;
                 n += (int)__popcll(__ballot(f));
             }
