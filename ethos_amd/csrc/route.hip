@@ -504,8 +504,10 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         const float theta = key_score(readlane_u64(run, top_k - 1));
         // A tie with theta needs c[a][0] >= theta and c[0][b] >= theta: a < na, b < nb.
         const float v1_0 = key_score(readlane_u64(L1, 0)), v2_0 = key_score(readlane_u64(L2, 0));
-        const bool in_a = lane < kc && Elem<T>::round32(key_score(L1) + v2_0) >= theta;
-        const bool in_b = lane < kc && Elem<T>::round32(v1_0 + key_score(L2)) >= theta;
+        float ca = key_score(L1) + v2_0, cb = v1_0 + key_score(L2);
+        Elem<T>::round32x2(ca, cb);
+        const bool in_a = lane < kc && ca >= theta;
+        const bool in_b = lane < kc && cb >= theta;
         const int na = (int)__popcll(__ballot(in_a)), nb = (int)__popcll(__ballot(in_b));
         for (int p0 = 0; p0 < na * nb; p0 += kWave) {
             const int p = p0 + lane;
