@@ -647,7 +647,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int LA = 4;                                // fragment reads run LA k-steps ahead
     constexpr int kCS = kCopiesW / 4;                    // k-steps that issue copies (4 each)
     constexpr int kNSt = 8;                              // v-row stores per wave and tile
-    static_assert(GPR >= 16 && (GPR & (GPR - 1)) == 0 && kCopiesW % 4 == 0 && kCS + kNSt <= KS2,
+    // the previous tile's stores go out every kStride k-steps after the copies, spread over
+    // the tile's MFMAs
+    constexpr int kStride = (KS2 - 1 - kCS) / (kNSt - 1) > 0 ? (KS2 - 1 - kCS) / (kNSt - 1) : 1;
+    static_assert(GPR >= 16 && (GPR & (GPR - 1)) == 0 && kCopiesW % 4 == 0 && kCS + kStride * (kNSt - 1) < KS2,
                   "tile staging shape");
     // Hidden tiles: row r's 16-byte group g sits at slot g ^ (r % 16) of the row, so a
     // fragment read (one group, 16 consecutive rows per 256 bytes of banks) is
@@ -770,17 +773,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                 for (int j = 0; j < 4; ++j) copy(t_next, (i + 1) & 1, 4 * s + j);
             }
-            // the previous tile's rows, one store per k-step
-            if (s >= kCS && s < kCS + kNSt)
-                __builtin_amdgcn_raw_buffer_store_b128(outv[s - kCS], uvr_prev, st_base + (s - kCS) * 8 * d2 * 2, 0,
-                                                       2);
+            // the previous tile's rows, one store every kStride k-steps
+            if (s >= kCS && (s - kCS) % kStride == 0 && (s - kCS) / kStride < kNSt)
+                __builtin_amdgcn_raw_buffer_store_b128(outv[(s - kCS) / kStride], uvr_prev,
+                                                       st_base + ((s - kCS) / kStride) * 8 * d2 * 2, 0, 2);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, kNSt + 2 * LA, 0);
 #pragma unroll
         for (int s = 0; s < KS2; ++s) {
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
             if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            if (s >= kCS && s < kCS + kNSt) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
+            if (s >= kCS && (s - kCS) % kStride == 0 && (s - kCS) / kStride < kNSt)
+                __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
         }
         // acc[mb][cb][i]: column col0 + 32 cb + 8 (i/4) + 4h + i%4 of expert 32 mb + l32
         // of the tile, i.e. 8-byte half h of 16-byte group 4 cb + i/4 of staged row
