@@ -83,6 +83,8 @@ def timed_steps(m, x_flat, steps: int) -> tuple[float, dict]:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     per = {k: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, k in enumerate(STAGES)}
+    steps_ms = sorted(e[0].elapsed_time(e[-1]) for e in evs)
+    per["_p50"] = steps_ms[len(steps_ms) // 2]
     return elapsed / steps * 1e3, per
 
 
@@ -265,6 +267,7 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] timing {args.steps} steps")
         ms, st = timed_steps(m, x_flat, args.steps)
+        p50 = st.pop("_p50")
         U = unique_experts(m, x_flat)
     work = stage_work(sh, U)
     kernels = {}
@@ -298,6 +301,7 @@ def main():
             torch.cuda.synchronize()
             log(f"[bench] timing {args.steps} steps, hidden-space order")
             ms_h, st_h = timed_steps(mh, x_flat, args.steps)
+            st_h.pop("_p50")
         del mh
         alternatives = {"hidden_space": dict(
             ms_per_step=round(ms_h, 4), value=round(sh.n_tok / (ms_h * 1e-3), 1), unit="tokens/s",
@@ -318,6 +322,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "p50_step_ms": round(p50, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -402,10 +402,107 @@ __global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ in
         if (c0 + c < cols && r0 + tx < rows) out[(int64_t)(c0 + c) * rows + r0 + tx] = tile[tx][c];
 }
 
+// Small batches: the scatter-back split by head, so that n_tok * H waves (not n_tok) share
+// the gathers.  apply_scatter_head_kernel writes each (token, head)'s RN_T(sum_k RN_T(a v))
+// to headbuf [n_tok, H, d]; apply_head_sum_kernel adds the heads in order in T and divides
+// by H.  The same operations in the same order as apply_scatter_kernel, so the output is
+// bit-identical.
+constexpr int64_t kSplitHeadMaxTok = 1024;
+
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void apply_scatter_head_kernel(const T* __restrict__ vr_,
+                                                                 const int32_t* __restrict__ pair_slot,
+                                                                 const float* __restrict__ act, int64_t n_items,
+                                                                 int k, int d, T* __restrict__ headbuf) {
+    constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t n_waves = (int64_t)gridDim.x * 4;
+    for (int64_t it = wave_id; it < n_items; it += n_waves) {  // item = t * H + head
+        float hacc[CH * N];
+#pragma unroll
+        for (int e = 0; e < CH * N; ++e) hacc[e] = 0.0f;
+        const int64_t pbase = it * k;
+        for (int j0 = 0; j0 < k; j0 += kScatterUnroll) {
+            Raw vr[kScatterUnroll][CH];
+            float a[kScatterUnroll];
+#pragma unroll
+            for (int q = 0; q < kScatterUnroll; ++q) {
+                if (j0 + q < k) {
+                    const int s = pair_slot[pbase + j0 + q];
+                    a[q] = act[pbase + j0 + q];
+                    load_raw<T, CH>(vr_ + (int64_t)s * d, d, lane, vr[q]);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kScatterUnroll; ++q) {
+                if (j0 + q < k) {
+#pragma unroll
+                    for (int c = 0; c < CH; ++c) {
+                        float vf[N];
+                        Vec16<T>::unpack(vr[q][c], vf);
+#pragma unroll
+                        for (int v = 0; v < N; v += 2) {
+                            float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
+                            Elem<T>::round32x2(p0, p1);  // RN_T(a v)
+                            hacc[c * N + v] += p0;
+                            hacc[c * N + v + 1] += p1;
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int e = c * 64 * N + lane * N;
+            if (e < d) *reinterpret_cast<Raw*>(headbuf + it * d + e) = Vec16<T>::pack(hacc + c * N);  // RN_T
+        }
+    }
+}
+
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void apply_head_sum_kernel(const T* __restrict__ headbuf, int64_t n_tok, int H,
+                                                             int d, T* __restrict__ out) {
+    constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t n_waves = (int64_t)gridDim.x * 4;
+    const float hdiv = (float)H;
+    for (int64_t t = wave_id; t < n_tok; t += n_waves) {
+        float o[CH * N];
+#pragma unroll
+        for (int e = 0; e < CH * N; ++e) o[e] = 0.0f;
+        for (int h = 0; h < H; ++h) {
+            float hv[CH * N];
+            load_row<T, CH>(headbuf + (t * H + h) * d, d, lane, hv);
+#pragma unroll
+            for (int e = 0; e < CH * N; e += 2) {
+                float o0 = o[e] + hv[e], o1 = o[e + 1] + hv[e + 1];
+                Elem<T>::round32x2(o0, o1);  // the running head sum in T
+                o[e] = o0;
+                o[e + 1] = o1;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int e = c * 64 * N + lane * N;
+            if (e < d) {
+                float r[N];
+#pragma unroll
+                for (int v = 0; v < N; ++v) r[v] = o[c * N + v] / hdiv;
+                *reinterpret_cast<Raw*>(out + t * d + e) = Vec16<T>::pack(r);
+            }
+        }
+    }
+}
+
 template <typename T, int CH1, int CH2>
 static int launch_apply_t(const void* xp, const void* hid, const void* v, const int32_t* perm,
                           const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,
-                          int k, int d, int dh, float* act, void* out, int num_cus, hipStream_t stream) {
+                          int k, int d, int dh, float* act, void* headbuf, void* out, int num_cus,
+                          hipStream_t stream) {
     const int64_t n_pairs = n_tok * H * k;
     const int64_t chunks = (n_pairs + 63) / 64;
     int64_t g1 = (chunks + 3) / 4;
@@ -414,6 +511,18 @@ static int launch_apply_t(const void* xp, const void* hid, const void* v, const 
     if (g1 < 1) g1 = 1;
     hipLaunchKernelGGL((apply_act_kernel<T, CH1>), dim3((unsigned)g1), dim3(256), 0, stream, (const T*)xp,
                        (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, H * k, dh, act);
+    if (headbuf != nullptr) {
+        const int64_t items = n_tok * H;
+        int64_t g3 = (items + 3) / 4;
+        g3 = g3 > cap ? cap : (g3 < 1 ? 1 : g3);
+        hipLaunchKernelGGL((apply_scatter_head_kernel<T, CH2>), dim3((unsigned)g3), dim3(256), 0, stream,
+                           (const T*)v, pair_slot, (const float*)act, items, k, d, (T*)headbuf);
+        int64_t g4 = (n_tok + 3) / 4;
+        g4 = g4 > cap ? cap : (g4 < 1 ? 1 : g4);
+        hipLaunchKernelGGL((apply_head_sum_kernel<T, CH2>), dim3((unsigned)g4), dim3(256), 0, stream,
+                           (const T*)headbuf, n_tok, H, d, (T*)out);
+        return (int)hipGetLastError();
+    }
     int64_t g2 = (n_tok + 3) / 4;
     if (g2 > cap) g2 = cap;
     if (g2 < 1) g2 = 1;
@@ -434,10 +543,16 @@ static size_t wut_offset(int64_t n_tok, int H, int k, int dh, size_t eb) {
     return align256(align256((size_t)n_tok * dh * eb) + (size_t)n_tok * H * k * sizeof(float));
 }
 
+// d is not an argument here: the W_u^T block and the per-head rows of small batches are
+// sized for d <= 4096, the ABI's limit
+static size_t headbuf_offset(int64_t n_tok, int H, int k, int dh, size_t eb, int dtype) {
+    return align256(wut_offset(n_tok, H, k, dh, eb) + (dtype == kBF16 ? (size_t)dh * 4096 * eb : 0));
+}
+
 size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype) {
-    // d is not an argument here: the W_u^T block is sized for d <= 4096, the ABI's limit
     const size_t eb = dtype == kBF16 ? 2 : 4;
-    return wut_offset(n_tok, H, k, dh, eb) + (dtype == kBF16 ? (size_t)dh * 4096 * eb : 0);
+    return headbuf_offset(n_tok, H, k, dh, eb, dtype) +
+           (n_tok <= kSplitHeadMaxTok ? (size_t)n_tok * H * 4096 * eb : 0);
 }
 
 // xp = RN_T(x W_u) into the workspace (W_u^T = the first d rows of net.2.weight, row
@@ -471,10 +586,13 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
     launch_token_proj(x, w2, n_tok, H, k, d, dh, dtype, ws, stream);
     const int c1 = apply_chunks(dh, dtype), c2 = apply_chunks(d, dtype);
+    void* headbuf = n_tok <= kSplitHeadMaxTok
+                        ? static_cast<unsigned char*>(ws) + headbuf_offset(n_tok, H, k, dh, eb, dtype)
+                        : nullptr;
 #define ETHOS_APPLY_CASE(TT, C1, C2)                                                                             \
     if (c1 <= C1 && c2 <= C2)                                                                                    \
         return launch_apply_t<TT, C1, C2>(xp, hid, v, perm, sorted_slot, pair_slot, gates, n_tok, H, k, d, dh, act, \
-                                          out, num_cus, stream);
+                                          headbuf, out, num_cus, stream);
     if (dtype == kBF16) {
         ETHOS_APPLY_CASE(uint16_t, 1, 1)
         ETHOS_APPLY_CASE(uint16_t, 1, 2)
