@@ -134,14 +134,34 @@ def cpu_baseline(sh, x_cpu, sd_cpu, n_tokens: int) -> dict:
     with torch.no_grad():
         loop_faithful.layer(xs, sd_cpu, sh.num_heads, sh.top_k)
     dt = time.perf_counter() - t0
+    # the vectorised oracle (numpy, float64 arithmetic with the reference's rounding points) on
+    # the same sample, reported beside the loop-faithful port
+    from oracle import oracle as O
+    P = O.unpack_state(sd_cpu, sh.num_heads)
+    n_vec = min(n_tokens, 64)  # its generator covers every unique expert of the sample: keep it short
+    t1 = time.perf_counter()
+    O.layer_forward(O.from_torch(xs[:n_vec]), P, sh.num_heads, sh.top_k, sh.dtype)
+    dt_vec = time.perf_counter() - t1
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {
         "value": round(n_tokens / dt, 3),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model,
         "sample": f"first {n_tokens} of the {sh.n_tok} tokens of the same workload, full reference loop "
                   f"({n_tokens * sh.num_heads * sh.top_k} (token, head, k) iterations), {dt:.1f} s on "
                   f"{threads} threads",
+        "vectorised_oracle": {"value": round(n_vec / dt_vec, 3), "unit": "tokens/s",
+                              "sample": f"first {n_vec} tokens, {dt_vec:.1f} s"},
     }
 
 
