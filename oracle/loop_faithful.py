@@ -1,4 +1,4 @@
-"""Loop-faithful CPU restatement of the reference expert layer -- TEST / BASELINE ONLY.
+"""Loop-faithful CPU restatement of the reference expert layer -- for tests and the CPU baseline only.
 
 Times what the reference's own CPU path costs (bench.py's ``cpu_baseline`` leg) and
 never runs in the product.  It performs the reference's operations in the
