@@ -123,3 +123,38 @@ def test_cfg3_backward_runs_and_matches_reference_on_experts():
     unused = np.setdiff1d(np.arange(sh.num_experts), used)[:1000]
     assert float(lat[unused].abs().max()) == 0.0
     assert _nerr(xd.grad.view(-1, sh.d_model).float(), xr.grad) < 3e-2
+
+
+@pytest.mark.parametrize("dt,n,H,k,dh,U", [("bf16", 50, 2, 4, 64, 37), ("bf16", 33, 8, 16, 512, 900),
+                                           ("fp32", 20, 4, 8, 96, 11), ("bf16", 7, 3, 5, 40, 3)])
+def test_expert_backward_entry_point(dt, n, H, k, dh, U):
+    """ethos_expert_backward through the C-ABI against a float64 torch evaluation of its four
+    outputs (dscores, hacc, dxp, dh), with repeated experts so the expert sums collide."""
+    from ethos_amd import hip
+    g = torch.Generator().manual_seed(n + dh)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    h = (torch.randn(U, dh, generator=g) * 0.5).to(tdt)
+    xp = torch.randn(n, dh, generator=g)
+    dyb = torch.randn(n, dh, generator=g)
+    slot = torch.randint(0, U, (n * H * k,), generator=g, dtype=torch.int32)
+    gates = torch.rand(n, H, k, generator=g).to(tdt)
+    dg, hacc, dxp, dhs = hip.expert_backward(h.cuda(), xp.cuda(), dyb.cuda(), slot.cuda(), gates.cuda(), H, k, U)
+    torch.cuda.synchronize()
+    hd, x64, y64 = h.double(), xp.double(), dyb.double()
+    t = torch.arange(n * H * k) // (H * k)
+    hs = hd[slot.long()]
+    c = (hs * x64[t]).sum(-1)
+    act = torch.nn.functional.gelu(c)
+    gp = gates.double().reshape(-1)
+    da = (hs * y64[t]).sum(-1)
+    cdf = 0.5 * torch.erfc(-c / 2 ** 0.5)
+    dgelu = cdf + c * torch.exp(-0.5 * c * c) / (2 * torch.pi) ** 0.5
+    dc = gp * dgelu * da
+    a = act * gp
+    ref_dg = (act * da).view(n, H, k)
+    ref_hacc = torch.zeros(n, dh, dtype=torch.float64).index_add_(0, t, a[:, None] * hs)
+    ref_dxp = torch.zeros(n, dh, dtype=torch.float64).index_add_(0, t, dc[:, None] * hs)
+    ref_dh = torch.zeros(U, dh, dtype=torch.float64).index_add_(0, slot.long(), a[:, None] * y64[t] + dc[:, None] * x64[t])
+    for got, ref, name in ((dg, ref_dg, "dscores"), (hacc, ref_hacc, "hacc"), (dxp, ref_dxp, "dxp"), (dhs, ref_dh, "dh")):
+        assert got.shape == ref.shape, name
+        assert _nerr(got, ref) < 1e-5, (name, _nerr(got, ref))
