@@ -10,7 +10,9 @@
 //            index for the per-half lists and the expert id e = i1*K + i2 for the
 //            combined list -- "ties broken to the lowest index".
 //   c[a,b] = RN_T(fp32(v1[a] + v2[b]))
-//   gate_i = RN_T(expf(c_i - c_0) / sum_i expf(c_i - c_0)), sum in list order.
+//   gate_i = RN_T(ex_i / sum_i ex_i), ex_i = RN_f32(exp(c_i - c_0)) with exp evaluated in
+//            fp64 (the correctly rounded fp32 exponential whenever the fp64 result is not
+//            within its own error of an fp32 rounding boundary), fp32 sum in list order.
 //
 // Certified filter, exact refinement.  Computing all K sub-key scores exactly is
 // the expensive way; instead:
@@ -521,7 +523,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         }
         // gates: exponentials in parallel, their sum in list order
         const float m = key_score(readlane_u64(run, 0));
-        const float ex = lane < top_k ? expf(key_score(run) - m) : 0.0f;
+        const float ex = lane < top_k ? (float)exp((double)(key_score(run) - m)) : 0.0f;
         float sum = 0.0f;
         for (int i = 0; i < top_k; ++i) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ex), i));
         if (lane < top_k) {

@@ -23,7 +23,10 @@
  *     enqueued), or a positive hipError_t from the launch.  ethos_last_error() gives a
  *     message for the calling thread's last failure.
  *   - dtype: ETHOS_F32 or ETHOS_BF16; tensors of "dtype T" hold that type, row-major.
- *   - Deterministic: the same inputs give bit-identical outputs on every run.
+ *   - The forward entry points are deterministic: the same inputs give bit-identical
+ *     outputs on every run (no atomics).  The one exception is ethos_expert_backward,
+ *     whose per-expert sums use float atomics and so vary in their last bits from run
+ *     to run.
  */
 #ifndef ETHOS_HIP_H
 #define ETHOS_HIP_H

@@ -31,7 +31,8 @@
  *                  index for the per-half lists, expert id for the combined list);
  *                  -0.0 compares equal to +0.0.
  *   c[a][b]      = RN_T((float)v1[a] + (float)v2[b])  (the add is an fp32 add)
- *   g            = RN_T(expf(f_i - f_0) / sum_i expf(f_i - f_0)), fp32, sum in list order
+ *   g            = RN_T(ex_i / sum_i ex_i), ex_i = (float)exp((double)(f_i - f_0)): the fp64
+ *                  exponential rounded once to fp32, fp32 sum and divide, sum in list order
  *   e            = i1[a] * K + i2[b]
  */
 #include <math.h>
@@ -232,7 +233,7 @@ static void orc_select_row(const float* s1, const float* s2, int64_t r, int K, i
     }
     float m = s->fv[0], sum = 0.0f;
     for (int i = 0; i < top_k; ++i) {
-        s->ex[i] = expf(s->fv[i] - m);
+        s->ex[i] = (float)exp((double)(s->fv[i] - m));
         sum += s->ex[i];
     }
     for (int i = 0; i < top_k; ++i) orc_store(out_scores, r * top_k + i, orc_round32(s->ex[i] / sum, dt), dt);

@@ -14,7 +14,8 @@ shape the fixture holds:
   ref_scores    router gates  [n_tok, H, k]      (model.py:234,251)
   ref_indices   router experts [n_tok, H, k]     (model.py:245,252), int32
   ref_out       layer output  [n_tok, d_model]   (model.py:288-343)
-  ref_q         per-head query after BatchNorm [n_tok, H, dq] (model.py:215-216), small shapes
+  ref_q         per-head query after BatchNorm [n_tok, H, dq] (model.py:215-216), small
+                shapes and the 64-token layer
   ref_s1/ref_s2 per-head sub-key scores [n_tok, H, K] (model.py:220-221), small shapes
   in_*          the inputs themselves, for the tiny shapes
 
@@ -42,17 +43,18 @@ REF = "/root/reference"
 sys.path.insert(0, REPO)
 from ethos_amd.workloads import SHAPES, make_inputs  # noqa: E402
 
-# (fixture name, shape name, signal, store ref_q/ref_s, store inputs)
+# (fixture name, shape name, signal, internals to store: "qs" = ref_q and ref_s1/ref_s2,
+# "q" = ref_q only, "" = none, store inputs)
 PLAN = [
-    ("tiny", "tiny", False, True, True),
-    ("tiny_signal", "tiny", True, True, True),
-    ("tiny_fp32", "tiny_fp32", False, True, True),
-    ("tiny_fp32_signal", "tiny_fp32", True, True, True),
-    ("cfg1", "cfg1", False, True, False),
-    ("cfg1_signal", "cfg1", True, False, False),
-    ("cfg1_dq128", "cfg1_dq128", False, True, False),
-    ("cfg3", "cfg3", False, False, False),
-    ("cfg3_signal", "cfg3", True, False, False),
+    ("tiny", "tiny", False, "qs", True),
+    ("tiny_signal", "tiny", True, "qs", True),
+    ("tiny_fp32", "tiny_fp32", False, "qs", True),
+    ("tiny_fp32_signal", "tiny_fp32", True, "qs", True),
+    ("cfg1", "cfg1", False, "qs", False),
+    ("cfg1_signal", "cfg1", True, "", False),
+    ("cfg1_dq128", "cfg1_dq128", False, "qs", False),
+    ("cfg3", "cfg3", False, "q", False),
+    ("cfg3_signal", "cfg3", True, "q", False),
 ]
 
 
@@ -114,6 +116,7 @@ def main(only=None):
             rec["sha_" + k] = np.array(sha(v))
         if store_internals:
             rec["ref_q"] = to_np(torch.stack(qs, dim=1))
+        if store_internals == "qs":
             rec["ref_s1"] = to_np(torch.stack(s1s, dim=1))
             rec["ref_s2"] = to_np(torch.stack(s2s, dim=1))
         if store_inputs:

@@ -63,9 +63,25 @@ def test_layer_against_reference_outputs(name):
     else:
         # same multiset of gate values in every row (the gates are a function of the
         # combined scores), i.e. any difference is a choice inside a tied group
-        ours = np.sort(O.to_f32(to_host(gates), "bf16"), -1)
         theirs = np.sort(O.to_f32(f["ref_scores"], "bf16"), -1)
-        assert np.mean(np.any(ours != theirs, -1)) <= 0.01
+        # 1. routing of the reference's own queries: every (token, head) row selects the
+        #    same multiset of gates as the reference (ids can differ only inside tied
+        #    groups, which torch.topk breaks arbitrarily)
+        rq = to_dev(f["ref_q"])
+        g_rq, _ = hip.route_topk(rq, m.router.sub_keys_1.weight.detach(), m.router.sub_keys_2.weight.detach(),
+                                 sh.top_k)
+        rows_rq = int(np.any(np.sort(O.to_f32(to_host(g_rq), "bf16"), -1) != theirs, -1).sum())
+        print(f"{name}: routing the reference's queries, {rows_rq} of {theirs.shape[0] * theirs.shape[1]} rows "
+              "with differing gate multisets")
+        assert rows_rq == 0, rows_rq
+        # 2. routing from x: the layer's queries are the correctly rounded projection, the
+        #    reference's are torch's bf16 GEMM; a row may differ only where those differ
+        ours = np.sort(O.to_f32(to_host(gates), "bf16"), -1)
+        rows = np.any(ours != theirs, -1)
+        q_rows = np.any(to_host(m.router.queries(xd)) != f["ref_q"], -1)
+        print(f"{name}: routing from x, {int(rows.sum())} rows with differing gate multisets, all among the "
+              f"{int(q_rows.sum())} rows whose reference query differs from the correctly rounded one")
+        assert not np.any(rows & ~q_rows)
         # expert stage with the reference's routing
         seg = hip.sort_segment(to_dev(ref_ids.reshape(-1).astype(np.int32)), sh.num_experts)
         w2 = m.generation_network.net[2].weight.detach()
@@ -100,9 +116,9 @@ def test_layer_linear_in_v():
 
 
 def test_layer_cfg2_full_size():
-    """Config 2 at full size: every routing row bit-exact against the oracle (fed the
-    layer's own queries, which are themselves checked bit-exact on a token subset),
-    sort invariants on all pairs, and the output of a token subset against the oracle."""
+    """Config 2 at full size: the queries of all 4,096 tokens and every routing row (ids
+    and gates) bit-exact against the oracle, sort invariants on all pairs, and the
+    output of 512 tokens (every 8th) against the oracle."""
     sh = SHAPES["cfg2"]
     x, sd = make_inputs(sh)
     m = _layer(sh, sd)
@@ -115,12 +131,16 @@ def test_layer_cfg2_full_size():
     torch.cuda.synchronize()
     P = O.unpack_state(sd, sh.num_heads)
     xs = O.from_torch(x)
-    sub = np.arange(0, sh.n_tok, 16)
-    q_ref = O.query_proj(xs[sub], P["Wq"], P["bq"], P["alpha"], P["beta"], "bf16")
+    q_ref = O.query_proj(xs, P["Wq"], P["bq"], P["alpha"], P["beta"], "bf16")
     qh = to_host(q)
-    assert np.array_equal(qh[sub], q_ref)
+    print(f"cfg2: {int(np.count_nonzero(qh != q_ref))} of {qh.size} query elements differ from the oracle")
+    assert np.array_equal(qh, q_ref)
     g_ref, ids_ref = O.route(qh, P["K1"], P["K2"], sh.top_k, "bf16")
-    assert np.array_equal(to_host(ids), ids_ref)
+    ih, gh = to_host(ids), to_host(gates)
+    print(f"cfg2: {int(np.any(ih != ids_ref, -1).sum())} routing rows with differing ids, "
+          f"{int(np.count_nonzero(gh != g_ref))} differing gates")
+    assert np.array_equal(ih, ids_ref)
+    assert np.array_equal(gh, g_ref)
     # sort invariants on the full pair set
     flat = ids.view(-1).long()
     perm = seg["perm"].long()
@@ -130,9 +150,10 @@ def test_layer_cfg2_full_size():
     assert bool((ks[1:] >= ks[:-1]).all())
     uq = torch.unique(flat)
     assert U == uq.numel() and torch.equal(seg["uniq"][:U].long(), uq)
-    # output for a token subset
-    r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub[:64], q=qh)
-    check_out(O.to_f32(to_host(y), "bf16")[sub[:64]], r["out"], "bf16", nerr_max=2e-3)
+    # output for 512 tokens
+    sub = np.arange(0, sh.n_tok, 8)
+    r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub, q=qh)
+    check_out(O.to_f32(to_host(y), "bf16")[sub], r["out"], "bf16", nerr_max=2e-3)
 
 
 def test_layer_cfg4_zipf_full_size():
@@ -154,15 +175,14 @@ def test_layer_cfg4_zipf_full_size():
     P = O.unpack_state(sd, sh.num_heads)
     xs = O.from_torch(x)
     qh = to_host(q)
-    sub = np.arange(0, sh.n_tok, 128)
+    sub = np.arange(0, sh.n_tok, 16)
     q_ref = O.query_proj(xs[sub], P["Wq"], P["bq"], P["alpha"], P["beta"], "bf16")
     assert np.array_equal(qh[sub], q_ref)
     g_ref, ids_ref = O.route(qh, P["K1"], P["K2"], sh.top_k, "bf16")
     assert np.array_equal(to_host(ids), ids_ref)
-    # gates: a bf16 rounding of an fp32 softmax whose expf may differ by an fp32 ulp from the
-    # oracle's, which flips the bf16 rounding of about 2^-15 of 4.2 M positive values
-    gd = np.abs(to_host(gates).view(np.uint16).astype(np.int32) - g_ref.view(np.uint16).astype(np.int32))
-    assert gd.max() <= 1 and np.count_nonzero(gd) <= 1e-4 * gd.size, (gd.max(), np.count_nonzero(gd))
+    gh = to_host(gates)
+    print(f"cfg4: {int(np.count_nonzero(gh != g_ref))} of {gh.size} gates differ from the oracle")
+    assert np.array_equal(gh, g_ref)
     # segments: unique ids ascending, offsets = running histogram of the ids
     flat = ids.view(-1).long()
     U = int(seg["n_unique"].item())
@@ -175,8 +195,8 @@ def test_layer_cfg4_zipf_full_size():
     assert torch.equal(torch.sort(perm).values, torch.arange(flat.numel(), device="cuda"))
     assert bool((flat[perm][1:] >= flat[perm][:-1]).all())
     # output for a token subset
-    r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub[:64], q=qh)
-    check_out(O.to_f32(to_host(y), "bf16")[sub[:64]], r["out"], "bf16", nerr_max=2e-3)
+    r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub[::8], q=qh)
+    check_out(O.to_f32(to_host(y), "bf16")[sub[::8]], r["out"], "bf16", nerr_max=2e-3)
 
 
 def test_router_rejects_cpu_and_bad_shapes():

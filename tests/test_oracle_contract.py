@@ -121,8 +121,15 @@ def test_select_equals_exhaustive_topk_without_ties(K, top_k):
     for r in range(rows):
         want_e, want_c = _brute_topk(s1[r], s2[r], K, top_k, "fp32")
         assert np.array_equal(ids[r], want_e)
-        ex = np.exp((want_c - want_c[0]).astype(np.float32))
-        np.testing.assert_allclose(gates[r], ex / ex.sum(), rtol=2e-6)
+        # the softmax closed form, and the contract's exact fp32 form: the fp64 exponential
+        # rounded once, an fp32 sum in list order, an fp32 divide
+        d = (want_c - want_c[0]).astype(np.float64)
+        np.testing.assert_allclose(gates[r], np.exp(d) / np.exp(d).sum(), rtol=2e-6)
+        ex = np.exp(d).astype(np.float32)
+        tot = np.float32(0)
+        for e in ex:
+            tot = np.float32(tot + e)
+        assert np.array_equal(gates[r], (ex / tot).astype(np.float32))
 
 
 def test_select_decode_uses_first_half_as_high_digit():
