@@ -31,6 +31,7 @@ SIGNATURES = {
     "ethos_route_topk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "ethos_sort_workspace_bytes": (_sz, [_i64, _i64]),
     "ethos_sort_segment": (ctypes.c_int, [_vp, _i64, _i64, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ethos_sort_segment_noalloc": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ethos_generate": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "ethos_apply_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "ethos_apply_scatter": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
@@ -41,6 +42,9 @@ SIGNATURES = {
     "ethos_apply_hidden": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
                                           _vp, _sz, _vp, _vp]),
 }
+
+# ethos_sort_segment_noalloc's limit (ETHOS_NOALLOC_MAX_PAIRS in the header)
+NOALLOC_MAX_PAIRS = 1 << 20
 
 _lib = None
 

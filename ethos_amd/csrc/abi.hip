@@ -46,6 +46,40 @@ int num_cus() {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool dtype_ok(int dtype) { return dtype == ETHOS_F32 || dtype == ETHOS_BF16; }
 
+// Sort workspace of ethos_sort_segment_noalloc: one array per GPU, in the code object's
+// device data, sized for ETHOS_NOALLOC_MAX_PAIRS pairs.  Its name is only a host-side
+// stand-in; kernels receive the device address that hipGetSymbolAddress returns for the
+// current device (g_scratch_ptr), looked up once per device on the first call there.
+constexpr size_t kScratchWords = (size_t)4 * ETHOS_NOALLOC_MAX_PAIRS + (size_t)512 * (ETHOS_NOALLOC_MAX_PAIRS / 1024) +
+                                 512 + ETHOS_NOALLOC_MAX_PAIRS / 1024 + 64;
+static __device__ __align__(256) uint32_t scratch[kScratchWords];
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device (nullptr and the error in g_err on failure).
+void* scratch_ptr(int* rc) {
+    int dev = 0;
+    *rc = (int)hipGetDevice(&dev);
+    if (*rc != 0) {
+        fail(*rc, "ethos_sort_segment_noalloc: hipGetDevice: %s", hipGetErrorString((hipError_t)*rc));
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        *rc = ETHOS_EUNSUPPORTED;
+        fail(*rc, "ethos_sort_segment_noalloc: device %d beyond the %d this library tracks", dev, kMaxDevices);
+        return nullptr;
+    }
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    *rc = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*rc != 0 || !p) {
+        if (*rc == 0) *rc = (int)hipErrorInvalidSymbol;
+        fail(*rc, "ethos_sort_segment_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString((hipError_t)*rc));
+        return nullptr;
+    }
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+    return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -144,6 +178,33 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
     return hip_status(ethos::launch_sort_segment(ids, n_pairs, n_experts, workspace, perm, uniq_ids, seg_off,
                                                  pair_slot, sorted_slot, n_unique, (hipStream_t)stream),
                       "ethos_sort_segment");
+}
+
+int ethos_sort_segment_noalloc(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* perm,
+                               int32_t* uniq_ids, int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot,
+                               int32_t* n_unique, void* stream) {
+    g_err[0] = 0;
+    if (n_pairs < 0 || n_experts <= 0 || n_experts > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_sort_segment_noalloc: bad sizes n_pairs=%lld n_experts=%lld",
+                    (long long)n_pairs, (long long)n_experts);
+    if (n_pairs > ETHOS_NOALLOC_MAX_PAIRS)
+        return fail(ETHOS_ESIZE,
+                    "ethos_sort_segment_noalloc: %lld pairs exceed the %d its static workspace holds; use "
+                    "ethos_sort_segment with a caller workspace", (long long)n_pairs, ETHOS_NOALLOC_MAX_PAIRS);
+    if (!seg_off || !n_unique) return fail(ETHOS_ENULL, "ethos_sort_segment_noalloc: null pointer");
+    if (n_pairs == 0)
+        return hip_status(ethos::launch_sort_empty(seg_off, n_unique, (hipStream_t)stream),
+                          "ethos_sort_segment_noalloc");
+    if (!ids || !perm || !uniq_ids || !pair_slot || !sorted_slot)
+        return fail(ETHOS_ENULL, "ethos_sort_segment_noalloc: null pointer");
+    if (ethos::sort_workspace_bytes(n_pairs) > sizeof(scratch))
+        return fail(ETHOS_EWORKSPACE, "ethos_sort_segment_noalloc: static workspace sizing");
+    int rc = 0;
+    void* ws = scratch_ptr(&rc);
+    if (!ws) return rc;
+    return hip_status(ethos::launch_sort_segment(ids, n_pairs, n_experts, ws, perm, uniq_ids, seg_off, pair_slot,
+                                                 sorted_slot, n_unique, (hipStream_t)stream),
+                      "ethos_sort_segment_noalloc");
 }
 
 int ethos_generate(const void* latents, int64_t n_experts, const int32_t* uniq_ids, const int32_t* n_unique,

@@ -122,6 +122,24 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
                        int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique, void* stream);
 
 /*
+ * ethos_sort_segment without a caller workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, fixed-memory serving loops).  It has no
+ * counterpart in the reference.  The sort workspace is a static array in the library's
+ * device data, one per GPU, sized for ETHOS_NOALLOC_MAX_PAIRS pairs (about 19 MiB, held
+ * from the first call on a GPU until the process ends); larger n_pairs returns
+ * ETHOS_ESIZE.  Every other argument and every output is as for ethos_sort_segment, and
+ * the outputs are bit-identical to it.  All calls on one GPU share that array: calls that
+ * overlap on one GPU (on different streams, or from different threads) race and must be
+ * serialised by the caller.  No allocation happens inside (no hipMalloc or hipFree); the
+ * first call on a GPU looks the array's device address up once.
+ */
+#define ETHOS_NOALLOC_MAX_PAIRS (1 << 20)
+
+int ethos_sort_segment_noalloc(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* perm,
+                               int32_t* uniq_ids, int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot,
+                               int32_t* n_unique, void* stream);
+
+/*
  * Expert generation for the unique experts, u = 0 .. U-1, z = latents[uniq_ids[u]]:
  *   h[u] = RN_T(gelu(RN_T(W1 z)))        the hidden row h_i (model.py:323), erf-form GELU
  *   v[u] = RN_T(W_v h[u])                h_i @ W_v (model.py:332), W_v^T = w2 rows d_model .. 2 d_model - 1

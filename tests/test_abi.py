@@ -91,3 +91,16 @@ def test_route_rejects_top_k_above_32():
     assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 1024, 4, 8, 1, 16, 16, None) == -6
     assert L.ethos_route_topk(18, 16, 16, None, 4, 32, 64, 4, 8, 1, 16, 16, None) == -4
     assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 4096, 40, 32, 1, 16, 16, None) == -6
+
+
+def test_sort_noalloc_rejects_pairs_beyond_its_static_workspace():
+    """The no-allocation sort takes at most NOALLOC_MAX_PAIRS pairs (checked before any
+    HIP call, so no GPU is needed), and validates like ethos_sort_segment."""
+    L = _lib.load()
+    n = _lib.NOALLOC_MAX_PAIRS + 1
+    assert L.ethos_sort_segment_noalloc(16, n, 262144, 16, 16, 16, 16, 16, 16, None) == -2
+    assert b"static workspace" in L.ethos_last_error()
+    assert L.ethos_sort_segment_noalloc(16, 100, 0, 16, 16, 16, 16, 16, 16, None) == -2
+    assert L.ethos_sort_segment_noalloc(None, 100, 262144, 16, 16, 16, 16, 16, 16, None) == -3
+    # the static array covers the library's own workspace formula at the limit
+    assert L.ethos_sort_workspace_bytes(_lib.NOALLOC_MAX_PAIRS, 262144) <= 20 * 2 ** 20
