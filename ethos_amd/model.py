@@ -1,16 +1,23 @@
 """The ETHOS language model around the drop-in expert layer (the whole-model forward).
 
-Module tree, constructor attributes and state_dict keys follow the reference's
-CompressedMoEModel (model.py:367-396): token embedding tied to the output head, blocks of
-pre-norm MLA attention (model.py:79-165) and an expert layer (or, for the first
-num_dense_layers blocks, the SwiGLU FFN of model.py:257-265), a final RMSNorm.  A
-reference checkpoint therefore loads with load_state_dict(strict=True).
+What is shared with the reference's CompressedMoEModel (model.py:367-396) is the interface
+only: the module names and parameter shapes of the state_dict (so a reference checkpoint
+loads with strict=True), the tied embedding/head, and the function each block computes:
+pre-norm multi-head latent attention (model.py:79-165) plus, per block, the expert layer
+or, for the first num_dense_layers blocks, a SwiGLU FFN (model.py:257-265).
 
-The expert layer is EthosExpertLayer (HIP kernels); attention runs on
-torch.nn.functional.scaled_dot_product_attention with a causal mask, which computes the
-reference's masked softmax(QK^T * scale) V (model.py:156-163; its flash-attention branch,
-model.py:133-155, pads V to the QK head width the same way this module does).  Inputs live
-on a HIP device.
+How it is computed here:
+  - the two projections that read the block input (q_a_proj and kv_a_proj_with_mqa) run
+    as one GEMM over their stacked weights;
+  - the rotary embedding is a rotation of the two halves of each rotary slice by
+    per-position angles, applied once to the single rotary key that all heads share
+    (model.py:118-125 broadcast it to the heads after rotating);
+  - queries, keys and values are written into token-major [batch, seq, heads, width]
+    buffers, which SDPA reads through transposed views; the values sit in a buffer as
+    wide as the query/key heads (zero columns beyond v_head_dim), the layout the fused
+    SDPA kernels take;
+  - the dense FFN's gate and up projections run as one GEMM.
+The expert layer is EthosExpertLayer (HIP kernels).  Inputs live on a HIP device.
 """
 from __future__ import annotations
 
@@ -23,8 +30,8 @@ import torch.nn.functional as F
 
 from .layer import EthosExpertLayer
 
-# configs/default.yaml of the reference, with the expert-layer shape of the benchmarked
-# layer (d_query 256) and the 12-block, all-expert-layer depth of the whole-model workload
+# the reference's configs/default.yaml, with the benchmarked expert-layer shape (d_query
+# 256) and the 12-block, all-expert-layer depth of the whole-model workload
 LM_DEFAULTS = dict(vocab_size=100277, d_model=1024, num_layers=12, num_heads=16, num_dense_layers=0,
                    q_lora_rank=768, kv_lora_rank=256, v_head_dim=64, qk_nope_head_dim=64, qk_rope_head_dim=64,
                    num_experts=262144, d_latent=128, d_intermediate_hypernet=512, top_k=16, num_routing_heads=8,
@@ -37,118 +44,116 @@ def lm_config(**overrides) -> SimpleNamespace:
     return SimpleNamespace(**cfg)
 
 
-class RMSNorm(nn.Module):
-    """weight * RN_T(x / sqrt(mean(x^2) + eps)) with the statistics in float32
-    (DeepseekV3RMSNorm, model.py:19-30)."""
+def _stacked(owner: nn.Module, mods) -> torch.Tensor:
+    """The weights of several nn.Linear modules stacked along the output dimension.
+    Cached on `owner` while no gradient is wanted (until a weight changes); under
+    autograd it is rebuilt each call, so gradients reach every weight."""
+    ws = [m.weight for m in mods]
+    if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
+        return torch.cat(ws, 0)
+    key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+    if getattr(owner, "_stack_key", None) != key:
+        owner._stack = torch.cat([w.detach() for w in ws], 0)
+        owner._stack_key = key
+    return owner._stack
 
-    def __init__(self, hidden_size: int, eps: float = 1e-6):
+
+class RMSNorm(nn.Module):
+    """Root-mean-square normalisation with a learned gain: statistics in float32, the
+    normalised value rounded to the input dtype, then scaled (model.py:19-30)."""
+
+    def __init__(self, size: int, eps: float = 1e-6):
         super().__init__()
-        self.weight = nn.Parameter(torch.ones(hidden_size))
-        self.variance_epsilon = eps
+        self.weight = nn.Parameter(torch.ones(size))
+        self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        dt = x.dtype
-        xf = x.to(torch.float32)
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
-        return self.weight * xf.to(dt)
+        y = F.rms_norm(x.float(), (x.shape[-1],), eps=self.eps)
+        return self.weight * y.to(x.dtype)
 
 
-class RotaryEmbedding(nn.Module):
-    """cos / sin tables of the rotary position embedding (model.py:33-59): frequencies
-    base^(-2i/dim), each repeated for both halves of the rotated dimension."""
+class Rotary(nn.Module):
+    """Rotary position embedding by half-rotation: a slice r = [a, b] of even width 2m at
+    position p becomes [a cos t - b sin t, b cos t + a sin t] with t_i = p base^(-2i/2m),
+    i < m (model.py:33-76 writes the same rotation with duplicated tables).  Angles,
+    cosines and sines are float32, rounded to the activation dtype when used; they are
+    formed for the given positions (no table, so no position can fall outside one)."""
 
-    def __init__(self, dim: int, max_position_embeddings: int = 2048, base: float = 10000.0):
+    def __init__(self, width: int, base: float):
         super().__init__()
-        self.dim = dim
-        self.base = base
-        inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2).float() / dim))
-        self.register_buffer("inv_freq", inv_freq, persistent=False)
-        self._cache = None
-        self._cache_len = max_position_embeddings
+        self.half = width // 2
+        self.base = float(base)
+        self._rate = None
 
-    def forward(self, x: torch.Tensor, seq_len: int):
-        n = max(seq_len, self._cache_len)
-        c = self._cache
-        if c is None or c[0].shape[0] < seq_len or c[0].device != x.device:
-            t = torch.arange(n, device=x.device, dtype=torch.float32)
-            freqs = torch.outer(t, self.inv_freq.to(x.device))
-            emb = torch.cat((freqs, freqs), dim=-1)
-            # the reference builds its tables in the default dtype (float32) and casts per call
-            c = self._cache = (emb.cos(), emb.sin())
-        return c[0][:seq_len].to(x.dtype), c[1][:seq_len].to(x.dtype)
-
-
-def rotate_half(x: torch.Tensor) -> torch.Tensor:
-    h = x.shape[-1] // 2
-    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
-
-
-def apply_rotary(q, k, cos, sin, position_ids):
-    """(q cos + rot(q) sin, k cos + rot(k) sin) at the given positions (model.py:68-76)."""
-    if position_ids.dim() == 1:
-        position_ids = position_ids.unsqueeze(0)
-    cos = cos[position_ids].unsqueeze(1)
-    sin = sin[position_ids].unsqueeze(1)
-    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+    def rotate(self, r: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """r [batch, seq, ..., 2m], positions [seq] -> the rotated slice, same shape and dtype."""
+        if self._rate is None or self._rate.device != r.device:
+            # rates base^(-2i/2m) as the reciprocal of the power, the reference's float32
+            # rounding of the frequencies (model.py:40)
+            self._rate = 1.0 / self.base ** (torch.arange(0, 2 * self.half, 2, device=r.device,
+                                                          dtype=torch.float32) / (2 * self.half))
+        ang = positions.to(device=r.device, dtype=torch.float32)[:, None] * self._rate[None, :]
+        shape = (1, positions.numel()) + (1,) * (r.dim() - 3) + (self.half,)
+        c = ang.cos().to(r.dtype).view(shape)
+        s = ang.sin().to(r.dtype).view(shape)
+        a, b = r[..., : self.half], r[..., self.half:]
+        return torch.cat((a * c - b * s, b * c + a * s), dim=-1)
 
 
 class MLAttention(nn.Module):
-    """Multi-head latent attention (DeepseekV3Attention, model.py:79-165): queries through a
-    low-rank projection with RMSNorm, keys and values from a compressed KV latent plus one
-    shared rotary key, causal softmax attention with scale q_head_dim^-1/2."""
+    """Multi-head latent attention.  Queries come from a low-rank bottleneck with an
+    RMSNorm; keys and values from a normalised compressed latent, plus one rotary key
+    shared by all heads.  Causal softmax attention with scale 1/sqrt(query head width)."""
 
     def __init__(self, config):
         super().__init__()
-        self.hidden_size = config.d_model
-        self.num_heads = config.num_heads
-        self.q_lora_rank = config.q_lora_rank
-        self.qk_rope_head_dim = config.qk_rope_head_dim
-        self.kv_lora_rank = config.kv_lora_rank
-        self.v_head_dim = config.v_head_dim
-        self.qk_nope_head_dim = config.qk_nope_head_dim
-        self.q_head_dim = config.qk_nope_head_dim + config.qk_rope_head_dim
-        self.q_a_proj = nn.Linear(self.hidden_size, config.q_lora_rank, bias=False)
-        self.q_a_layernorm = RMSNorm(config.q_lora_rank, eps=config.rms_norm_eps)
-        self.q_b_proj = nn.Linear(config.q_lora_rank, self.num_heads * self.q_head_dim, bias=False)
-        self.kv_a_proj_with_mqa = nn.Linear(self.hidden_size, config.kv_lora_rank + config.qk_rope_head_dim,
-                                            bias=False)
-        self.kv_a_layernorm = RMSNorm(config.kv_lora_rank, eps=config.rms_norm_eps)
-        self.kv_b_proj = nn.Linear(config.kv_lora_rank,
-                                   self.num_heads * (self.qk_nope_head_dim + self.v_head_dim), bias=False)
-        self.o_proj = nn.Linear(self.num_heads * self.v_head_dim, self.hidden_size, bias=False)
-        self.rotary_emb = RotaryEmbedding(self.qk_rope_head_dim, config.max_seq_len, config.rope_theta)
-        self.softmax_scale = self.q_head_dim ** (-0.5)
+        d, H = config.d_model, config.num_heads
+        self.n_heads = H
+        self.nope, self.rope, self.vdim = config.qk_nope_head_dim, config.qk_rope_head_dim, config.v_head_dim
+        self.qk_width = self.nope + self.rope
+        self.q_rank, self.kv_rank = config.q_lora_rank, config.kv_lora_rank
+        # parameter names and shapes are the checkpoint format (model.py:93-100)
+        self.q_a_proj = nn.Linear(d, self.q_rank, bias=False)
+        self.q_a_layernorm = RMSNorm(self.q_rank, eps=config.rms_norm_eps)
+        self.q_b_proj = nn.Linear(self.q_rank, H * self.qk_width, bias=False)
+        self.kv_a_proj_with_mqa = nn.Linear(d, self.kv_rank + self.rope, bias=False)
+        self.kv_a_layernorm = RMSNorm(self.kv_rank, eps=config.rms_norm_eps)
+        self.kv_b_proj = nn.Linear(self.kv_rank, H * (self.nope + self.vdim), bias=False)
+        self.o_proj = nn.Linear(H * self.vdim, d, bias=False)
+        self.rotary = Rotary(self.rope, config.rope_theta)
+        self.scale = 1.0 / math.sqrt(self.qk_width)
 
-    def forward(self, hidden_states: torch.Tensor, attention_mask, position_ids: torch.Tensor) -> torch.Tensor:
-        """`attention_mask`: None for causal attention, else an additive [seq, seq] mask (the
-        reference passes triu(-inf, 1), model.py:389-390, which is the causal case)."""
-        b, n, _ = hidden_states.shape
-        H = self.num_heads
-        q = self.q_b_proj(self.q_a_layernorm(self.q_a_proj(hidden_states))).view(b, n, H, self.q_head_dim)
-        q_nope, q_pe = torch.split(q, [self.qk_nope_head_dim, self.qk_rope_head_dim], dim=-1)
-        ckv = self.kv_a_proj_with_mqa(hidden_states)
-        ckv, k_pe = torch.split(ckv, [self.kv_lora_rank, self.qk_rope_head_dim], dim=-1)
-        k_pe = k_pe.view(b, n, 1, self.qk_rope_head_dim)
-        kv = self.kv_b_proj(self.kv_a_layernorm(ckv)).view(b, n, H, self.qk_nope_head_dim + self.v_head_dim)
-        k_nope, v = torch.split(kv, [self.qk_nope_head_dim, self.v_head_dim], dim=-1)
-        cos, sin = self.rotary_emb(v, n)
-        q_pe, k_pe = apply_rotary(q_pe.transpose(1, 2), k_pe.transpose(1, 2), cos, sin, position_ids)
-        q = torch.cat([q_nope.transpose(1, 2), q_pe], dim=-1).contiguous()
-        k = torch.cat([k_nope.transpose(1, 2), k_pe.expand(b, H, n, self.qk_rope_head_dim)], dim=-1).contiguous()
-        v = v.transpose(1, 2)
-        if self.v_head_dim != self.q_head_dim:
-            v = F.pad(v, [0, self.q_head_dim - self.v_head_dim])
+    def forward(self, x: torch.Tensor, attention_mask, position_ids: torch.Tensor) -> torch.Tensor:
+        """x [b, n, d].  `attention_mask`: None for causal attention, else an additive
+        [n, n] mask (the reference passes triu(-inf, 1), model.py:388-389: the causal
+        case).  `position_ids` [n] or [1, n]."""
+        b, n, _ = x.shape
+        H, nope, rope, w = self.n_heads, self.nope, self.rope, self.qk_width
+        pos = position_ids.reshape(-1)
+        # one GEMM for both projections of the block input: [q latent | kv latent | rotary key]
+        a = F.linear(x, _stacked(self, (self.q_a_proj, self.kv_a_proj_with_mqa)))
+        q_lat, kv_lat, k_rot = a.split((self.q_rank, self.kv_rank, rope), dim=-1)
+        q = self.q_b_proj(self.q_a_layernorm(q_lat)).view(b, n, H, w)
+        kv = self.kv_b_proj(self.kv_a_layernorm(kv_lat)).view(b, n, H, nope + self.vdim)
+        # token-major buffers: q (rotary slice rotated), k (per-head nope part | the shared
+        # rotated key), v (zero columns past v_head_dim)
+        qb = torch.cat((q[..., :nope], self.rotary.rotate(q[..., nope:], pos)), dim=-1)
+        kb = torch.empty((b, n, H, w), dtype=x.dtype, device=x.device)
+        kb[..., :nope] = kv[..., :nope]
+        kb[..., nope:] = self.rotary.rotate(k_rot, pos).unsqueeze(2)
+        vb = kv.new_zeros((b, n, H, w))
+        vb[..., : self.vdim] = kv[..., nope:]
+        qh, kh, vh = (t.transpose(1, 2) for t in (qb, kb, vb))  # [b, H, n, w] views
         if attention_mask is None:
-            o = F.scaled_dot_product_attention(q, k, v.contiguous(), is_causal=True, scale=self.softmax_scale)
+            o = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=self.scale)
         else:
-            o = F.scaled_dot_product_attention(q, k, v.contiguous(), attn_mask=attention_mask.to(q.dtype),
-                                               scale=self.softmax_scale)
-        o = o[..., : self.v_head_dim].transpose(1, 2).reshape(b, n, H * self.v_head_dim)
-        return self.o_proj(o)
+            o = F.scaled_dot_product_attention(qh, kh, vh, attn_mask=attention_mask.to(x.dtype), scale=self.scale)
+        return self.o_proj(o.transpose(1, 2)[..., : self.vdim].reshape(b, n, H * self.vdim))
 
 
 class FFN(nn.Module):
-    """SwiGLU feed-forward of the dense blocks: w2(silu(w1 x) * w3 x) (model.py:257-265)."""
+    """SwiGLU feed-forward of the dense blocks, w2(silu(w1 x) * (w3 x)) (model.py:257-265),
+    with the gate and up projections as one GEMM over their stacked weights."""
 
     def __init__(self, config):
         super().__init__()
@@ -156,12 +161,14 @@ class FFN(nn.Module):
         self.w2 = nn.Linear(config.d_ffn_intermediate, config.d_model, bias=False)
         self.w3 = nn.Linear(config.d_model, config.d_ffn_intermediate, bias=False)
 
-    def forward(self, x):
-        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate, up = F.linear(x, _stacked(self, (self.w1, self.w3))).chunk(2, dim=-1)
+        return self.w2(F.silu(gate) * up)
 
 
 class TransformerBlock(nn.Module):
-    """h = x + attn(norm(x)); out = h + mlp(norm(h)) (model.py:345-365)."""
+    """Pre-norm residual block: h = x + attn(norm1(x)); out = h + mlp(norm2(h))
+    (model.py:345-365)."""
 
     def __init__(self, config, is_moe_layer: bool):
         super().__init__()
@@ -186,14 +193,14 @@ class CompressedMoEModel(nn.Module):
                                      for i in range(config.num_layers)])
         self.norm = RMSNorm(config.d_model, eps=config.rms_norm_eps)
         self.output = nn.Linear(config.d_model, config.vocab_size, bias=False)
-        self.tok_embeddings.weight = self.output.weight
+        self.output.weight = self.tok_embeddings.weight  # one matrix for embedding and head
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
-        _, seq_len = input_ids.shape
+        seq = input_ids.shape[1]
+        pos = torch.arange(seq, device=input_ids.device)
         h = self.tok_embeddings(input_ids)
-        position_ids = torch.arange(seq_len, dtype=torch.long, device=input_ids.device)
-        for layer in self.layers:
-            h = layer(h, None, position_ids)  # None: causal, as the reference's triu(-inf, 1) mask
+        for block in self.layers:
+            h = block(h, None, pos)  # None: causal attention
         return self.output(self.norm(h))
 
 

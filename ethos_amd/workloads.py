@@ -138,3 +138,31 @@ def make_inputs(shape: LayerShape, seed: int = 0, signal: bool = False):
     x = x.to(dt)
     sd = {k: (v.to(dt) if v.is_floating_point() else v) for k, v in sd.items()}
     return x, sd
+
+
+# A small whole language model (3 blocks: one dense SwiGLU block, two expert blocks) for
+# parity checks of the model around the expert layer.  v_head_dim 16 differs from the
+# 32-wide query/key heads, as in the reference's default configuration (64 vs 128).
+LM_TINY = dict(vocab_size=500, d_model=64, num_layers=3, num_heads=4, num_dense_layers=1, q_lora_rank=48,
+               kv_lora_rank=32, v_head_dim=16, qk_nope_head_dim=16, qk_rope_head_dim=16, num_experts=256,
+               d_latent=16, d_intermediate_hypernet=32, top_k=4, num_routing_heads=2, d_query=32,
+               d_ffn_intermediate=128, max_seq_len=64)
+
+
+def make_lm_inputs(seed: int = 0, batch: int = 2, seq: int = 24, expert_scale: float = 50.0):
+    """``(config, state_dict, token ids)`` of the small language model, on the CPU in
+    float32.  Parameters come from ``ethos_amd.model.init_random_(seed)``; the expert
+    latents are then scaled by ``expert_scale`` so that the expert layers' outputs are of
+    the order of the residual stream (at the benchmark scale they are ~1e-5 and would not
+    show in the logits).  Token ids are uniform over the vocabulary."""
+    from .layer import EthosExpertLayer
+    from .model import CompressedMoEModel, init_random_, lm_config
+
+    cfg = lm_config(**LM_TINY)
+    m = init_random_(CompressedMoEModel(cfg), seed=seed)
+    with torch.no_grad():
+        for block in m.layers:
+            if isinstance(block.mlp, EthosExpertLayer):
+                block.mlp.expert_latents.weight.mul_(expert_scale)
+    ids = torch.randint(0, cfg.vocab_size, (batch, seq), generator=torch.Generator().manual_seed(seed))
+    return cfg, {k: v.detach().clone() for k, v in m.state_dict().items()}, ids

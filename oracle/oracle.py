@@ -359,15 +359,17 @@ def unpack_state(sd: dict, H: int):
     )
 
 
-def layer_forward(x, P: dict, n_heads: int, top_k: int, dt: str, tokens=None, q=None):
+def layer_forward(x, P: dict, n_heads: int, top_k: int, dt: str, tokens=None, q=None, routed=None):
     """Full expert-layer forward; returns a dict of every intermediate.
 
     ``tokens`` restricts the generator and apply stages to those tokens (routing
-    still covers every token).  ``q`` skips the projection with a given query.
+    still covers every token).  ``q`` skips the projection with a given query;
+    ``routed`` = (gates, ids), this function's own routing of that query computed
+    earlier, skips the routing as well.
     """
     if q is None:
         q = query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], dt)
-    gates, ids = route(q, P["K1"], P["K2"], top_k, dt)
+    gates, ids = route(q, P["K1"], P["K2"], top_k, dt) if routed is None else routed
     n_tok = x.shape[0]
     E = P["latents"].shape[0]
     sel_ids = ids if tokens is None else ids[np.asarray(tokens)]

@@ -2,7 +2,8 @@
 
 Run in the build container only (the reference tree is not present on GPU machines):
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py        # the expert-layer fixtures
+    python tests/golden/make_golden.py lm     # the whole-model fixture (lm_tiny.npz)
 
 The reference (wrmedford/ETHOS, model.py) is imported read-only from
 /root/reference, its modules are built from this repository's seeded synthetic
@@ -131,5 +132,63 @@ def main(only=None):
         print(f"{name}: {os.path.getsize(path) / 1024:.0f} KiB, reference forward {dt_s:.2f}s", flush=True)
 
 
+def lm_main():
+    """The reference's whole model (CompressedMoEModel, model.py:367-396) on the small
+    language model of ethos_amd.workloads (LM_TINY: one dense block, two expert blocks),
+    in eval mode on its matmul + additive-mask attention path (model.py:156-163), in
+    float32 and bfloat16.  lm_tiny.npz holds:
+
+      meta                JSON: seed, batch, seq, torch version, thread count
+      sha_*               sha256 of the regenerated float32 parameters
+      in_ids              token ids [batch, seq]
+      ref_logits_fp32     logits [batch, seq, vocab] float32
+      ref_logits_bf16     logits [batch, seq, vocab] bfloat16 (model cast with .to(bf16))
+      ref_ids_fp32_<i>    expert ids [batch * seq, H, k] chosen by block i's router (fp32 run)
+      ref_scores_fp32_<i> its gates
+    """
+    from types import SimpleNamespace
+
+    sys.dont_write_bytecode = True
+    sys.path.insert(0, REF)
+    import model as ref_model  # noqa: E402  (reference, read-only)
+
+    from ethos_amd.workloads import make_lm_inputs  # noqa: E402
+
+    seed, batch, seq = 0, 2, 24
+    cfg, sd, ids = make_lm_inputs(seed=seed, batch=batch, seq=seq)
+    rcfg = SimpleNamespace(**vars(cfg), use_triton=False)
+    rec = {"in_ids": ids.numpy().astype(np.int32)}
+    for k, v in sd.items():
+        rec["sha_" + k] = np.array(sha(v))
+    for dt, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        m = ref_model.CompressedMoEModel(rcfg)
+        m.load_state_dict(sd, strict=True)
+        m = m.to(dt).eval()
+        routed = {}
+        hooks = [blk.mlp.router.register_forward_hook(
+            lambda mod, inp, out, i=i: routed.__setitem__(i, out))
+            for i, blk in enumerate(m.layers) if i >= cfg.num_dense_layers]
+        t0 = time.time()
+        with torch.no_grad():
+            logits = m(ids)
+        for h in hooks:
+            h.remove()
+        rec[f"ref_logits_{tag}"] = to_np(logits)
+        if tag == "fp32":
+            for i, (scores, indices) in routed.items():
+                rec[f"ref_ids_fp32_{i}"] = to_np(indices)
+                rec[f"ref_scores_fp32_{i}"] = to_np(scores)
+        print(f"lm_tiny {tag}: reference forward {time.time() - t0:.2f}s", flush=True)
+    meta = dict(seed=seed, batch=batch, seq=seq, torch=torch.__version__, threads=torch.get_num_threads())
+    rec["meta"] = np.array(json.dumps(meta))
+    path = os.path.join(HERE, "lm_tiny.npz")
+    np.savez_compressed(path, **rec)
+    print(f"lm_tiny: {os.path.getsize(path) / 1024:.0f} KiB", flush=True)
+
+
 if __name__ == "__main__":
-    main(sys.argv[1:] or None)
+    args = sys.argv[1:]
+    if args == ["lm"]:
+        lm_main()
+    else:
+        main(args or None)

@@ -5,11 +5,10 @@ import torch
 from ethos_amd import checkpoint as ck
 from ethos_amd.layer import EthosExpertLayer
 from ethos_amd.model import CompressedMoEModel, FFN, init_random_, lm_config
+from ethos_amd.workloads import LM_TINY, make_lm_inputs
+from torch_reference import _attention, _rms
 
-TINY = dict(vocab_size=500, d_model=64, num_layers=3, num_heads=4, num_dense_layers=1, q_lora_rank=48,
-            kv_lora_rank=32, v_head_dim=16, qk_nope_head_dim=16, qk_rope_head_dim=16, num_experts=256, d_latent=16,
-            d_intermediate_hypernet=32, top_k=4, num_routing_heads=2, d_query=32, d_ffn_intermediate=128,
-            max_seq_len=64)
+TINY = LM_TINY
 
 # per-block keys of the reference (model.py:79-100 attention, 257-265 FFN, 345-360 block)
 ATTN = ["q_a_proj.weight", "q_a_layernorm.weight", "q_b_proj.weight", "kv_a_proj_with_mqa.weight",
@@ -48,3 +47,51 @@ def test_checkpoint_round_trip_and_expert_prefixes():
         assert torch.equal(v, b.state_dict()[k]), k
     assert ck.expert_layer_prefixes(a.state_dict()) == ["layers.1.mlp.", "layers.2.mlp."]
     assert ck.replace_expert_layers(a) == []
+
+
+def _nerr(a, b):
+    return float((a.double() - b.double()).norm() / b.double().norm())
+
+
+def test_dense_block_matches_restatement():
+    """The first block (attention + dense FFN, no expert layer, so it runs on the CPU)
+    against the float32 restatement of the reference's block (itself pinned to the
+    reference's logits), at positions 0..n-1 and at shifted positions."""
+    cfg, sd, ids = make_lm_inputs(seed=0)
+    m = CompressedMoEModel(cfg)
+    m.load_state_dict(sd)
+    m.eval()
+    blk = m.layers[0]
+    P = {k: v.float() for k, v in sd.items()}
+    x = P["tok_embeddings.weight"][ids]
+    eps = cfg.rms_norm_eps
+    with torch.no_grad():
+        hh = x + _attention(P, "layers.0.self_attn.", _rms(x, P["layers.0.input_layernorm.weight"], eps), cfg)
+        z = _rms(hh, P["layers.0.post_attention_layernorm.weight"], eps)
+        mlp = torch.nn.functional.linear(
+            torch.nn.functional.silu(torch.nn.functional.linear(z, P["layers.0.mlp.w1.weight"]))
+            * torch.nn.functional.linear(z, P["layers.0.mlp.w3.weight"]), P["layers.0.mlp.w2.weight"])
+        want = hh + mlp
+        got = blk(x, None, torch.arange(ids.shape[1]))
+        assert _nerr(got, want) < 1e-6
+        # an explicit additive causal mask gives the same result as the causal flag
+        mask = torch.triu(torch.full((ids.shape[1],) * 2, float("-inf")), diagonal=1)
+        assert _nerr(blk(x, mask, torch.arange(ids.shape[1])), want) < 1e-6
+
+
+def test_rotary_matches_duplicated_table_form():
+    """The half-rotation equals x cos(t) + rot(x) sin(t) with the angle table duplicated over
+    both halves and rot(x) = [-x2, x1], in float32 and bit-for-bit in bfloat16."""
+    from ethos_amd.model import Rotary
+
+    r = Rotary(16, 10000.0)
+    g = torch.Generator().manual_seed(0)
+    for dt in (torch.float32, torch.bfloat16):
+        x = torch.randn((2, 40, 3, 16), generator=g).to(dt)
+        pos = torch.arange(5, 45)
+        inv = 1.0 / (10000.0 ** (torch.arange(0, 16, 2).float() / 16))
+        ang = torch.outer(pos.float(), inv)
+        emb = torch.cat((ang, ang), -1)
+        cos, sin = emb.cos().to(dt)[None, :, None, :], emb.sin().to(dt)[None, :, None, :]
+        rot = torch.cat((-x[..., 8:], x[..., :8]), -1)
+        assert torch.equal(r.rotate(x, pos), x * cos + rot * sin)
