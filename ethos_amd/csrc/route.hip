@@ -295,12 +295,15 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         //    go on the row's pending list, and step 3 scores the pending lists of all the
         //    wave's rows together.  A row with more than 64 candidates (rare) is scored
         //    exactly in full in step 4.
+        // zero for every row slot, including the slots past the last row of a partial
+        // tile (the loop below stops at that row, and step 3 sums all of n_pend)
         int n_cand[kRtRowsPerWave], n_pend[kRtRowsPerWave];
+#pragma unroll
+        for (int rr = 0; rr < kRtRowsPerWave; ++rr) n_cand[rr] = n_pend[rr] = 0;
         uint32_t slow_rows = 0;
         const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
         for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
-            n_cand[rr] = n_pend[rr] = 0;
             const int lr = wave * kRtRowsPerWave + rr;
             const int64_t r = row0 + lr;
             if (r >= rows) break;

@@ -208,6 +208,10 @@ class ProductKeyRouter(nn.Module):
                                      m.eps))
             if m.training and m.track_running_stats:
                 m.num_batches_tracked.add_(1)
+        # batch_norm updated the running statistics in place without bumping their version
+        # counters, so the eval-mode coefficients cached by _packed are stale
+        if any(m.training and m.track_running_stats for m in self.query_norms):
+            self._cache_key = None
         return torch.stack(outs, dim=1).contiguous()
 
     def route(self, x_flat: torch.Tensor, mark=None):

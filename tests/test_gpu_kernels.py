@@ -48,6 +48,22 @@ def test_route_bit_exact(name):
     assert np.array_equal(O.to_f32(to_host(g), sh.dtype), O.to_f32(g_ref, sh.dtype))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "fp32"])
+@pytest.mark.parametrize("rows", [1, 17, 80, 95, 200])
+def test_route_partial_tiles_bit_exact(rows, dt):
+    """Row counts that leave the last 32-row workgroup partly empty (one wave with live and
+    dead rows, whole waves of dead rows): a regression test for per-row counters that were
+    left unset past the last row."""
+    rng = np.random.default_rng(rows)
+    K, dh2, top_k = 16 if rows < 100 else 512, 16 if rows < 100 else 128, 4 if rows < 100 else 16
+    q, k1, k2 = _stress_case("zipf", rng, rows, K, dh2, dt)
+    g_ref, ids_ref = O.route(q, k1, k2, top_k, dt)
+    g, ids = hip.route_topk(to_dev(q), to_dev(k1), to_dev(k2), top_k)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(ids), ids_ref)
+    assert np.array_equal(O.to_f32(to_host(g), dt), O.to_f32(g_ref, dt))
+
+
 def test_route_ties_break_to_lowest_index():
     """Duplicate sub-key rows force exact score ties in both halves."""
     sh, x, P = _setup("tiny")
