@@ -14,7 +14,8 @@ Besides throughput, the line carries
   kernels       the same figures for every stage;
   cpu_baseline  the reference's CPU path (a loop-faithful restatement of
                 model.py:288-343, bit-identical to it on the golden fixtures) timed on a
-                bounded token sample on this host.
+                bounded token sample on this host, with every CPU the process may use;
+  decode_64_tokens  the decode-like 64-token layer: p50 latency and its CPU baseline.
 """
 from __future__ import annotations
 
@@ -53,9 +54,10 @@ def stage_work(sh, U: int) -> dict:
         "sort_segment": dict(bound="hbm", work=16 * N + 4 * (U + 1), unit="GB/s"),
         # 2 U (dl dh + dh d) flops: hidden rows and v rows of the unique experts
         "generate": dict(bound="mfma", work=2 * U * (sh.d_latent * sh.d_hidden + sh.d_hidden * d), unit="TFLOP/s"),
-        # h and v once per unique expert, x in, W_u in, y out, id + score + pair per pair
-        "apply_scatter": dict(bound="hbm", work=U * (sh.d_hidden + d) * eb + 2 * sh.n_tok * d * eb
-                              + d * sh.d_hidden * eb + N * (4 + eb + 4), unit="GB/s"),
+        # the per-unit bytes of the expert apply + scatter-back: u and v rows once per unique
+        # expert (U 2d), x in and y out, expert id + gate + pair index per pair
+        "apply_scatter": dict(bound="hbm", work=U * 2 * d * eb + 2 * sh.n_tok * d * eb + N * (4 + eb + 4),
+                              unit="GB/s"),
     }
 
 
@@ -125,15 +127,46 @@ def copy_probe(mib: int) -> None:
     del src, dst
 
 
+def host_cpu() -> dict:
+    """The host's CPU model (/proc/cpuinfo, else lscpu), its logical CPU count and the CPUs
+    this process may run on."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() == "Model name" and val.strip() and (model is None or len(val.strip()) > len(model)):
+                model = val.strip()
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    return {"cpu_model": model or "unknown", "logical_cpus": os.cpu_count(),
+            "cpus_available": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline(sh, x_cpu, sd_cpu, n_tokens: int) -> dict:
     from oracle import loop_faithful
 
-    threads = torch.get_num_threads()
+    host = host_cpu()
+    # every CPU this process may run on (the host's cores unless a CPU set restricts it)
+    threads = host["cpus_available"]
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
     xs = x_cpu[:n_tokens].contiguous()
     t0 = time.perf_counter()
     with torch.no_grad():
         loop_faithful.layer(xs, sd_cpu, sh.num_heads, sh.top_k)
     dt = time.perf_counter() - t0
+    torch.set_num_threads(prev)
     # the vectorised oracle (numpy, float64 arithmetic with the reference's rounding points) on
     # the same sample, reported beside the loop-faithful port
     from oracle import oracle as O
@@ -142,21 +175,13 @@ def cpu_baseline(sh, x_cpu, sd_cpu, n_tokens: int) -> dict:
     t1 = time.perf_counter()
     O.layer_forward(O.from_torch(xs[:n_vec]), P, sh.num_heads, sh.top_k, sh.dtype)
     dt_vec = time.perf_counter() - t1
-    cpu_model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {
         "value": round(n_tokens / dt, 3),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "cpu_model": cpu_model,
+        "cpu_model": host["cpu_model"],
+        "logical_cpus": host["logical_cpus"],
         "sample": f"first {n_tokens} of the {sh.n_tok} tokens of the same workload, full reference loop "
                   f"({n_tokens * sh.num_heads * sh.top_k} (token, head, k) iterations), {dt:.1f} s on "
                   f"{threads} threads",
@@ -253,6 +278,7 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="token sample for the CPU baseline (0 = skip)")
     ap.add_argument("--no-alternatives", action="store_true",
                     help="skip the hidden-space timing (profiling runs: keeps per-kernel averages to one order)")
+    ap.add_argument("--no-decode", action="store_true", help="skip the 64-token layer's latency measurement")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain copy of this many MiB (counter calibration for profiling)")
     args = ap.parse_args()
@@ -334,6 +360,10 @@ def main():
         log(f"[bench] CPU baseline on {args.cpu_tokens} tokens")
         cpu = cpu_baseline(sh, x_cpu, sd_cpu, args.cpu_tokens)
 
+    decode = None
+    if args.config == "cfg2" and not args.no_decode:
+        decode = decode_latency(args, with_cpu=args.cpu_tokens > 0)
+
     line = {
         "metric": METRIC,
         "value": round(sh.n_tok / (ms * 1e-3), 1),
@@ -361,8 +391,41 @@ def main():
         "kernels": kernels,
         "alternatives": alternatives,
         "cpu_baseline": cpu,
+        "decode_64_tokens": decode,
     }
     print(json.dumps(line), flush=True)
+
+
+def decode_latency(args, with_cpu: bool) -> dict:
+    """The decode-like layer (64 tokens, the same 262,144-expert layer, bf16): p50 latency
+    of 50 forwards after warmup, and the CPU port on all 64 tokens."""
+    import ethos_amd
+    from ethos_amd.workloads import SHAPES, make_inputs
+
+    sh = SHAPES["cfg3"]
+    x_cpu, sd_cpu = make_inputs(sh, seed=0)
+    m = ethos_amd.EthosExpertLayer(sh.config()).to(sh.torch_dtype)
+    m.load_state_dict(sd_cpu)
+    m = m.cuda().eval()
+    x_flat = x_cpu.cuda()
+    steps = 50
+    with torch.no_grad():
+        for _ in range(max(args.warmup, 5)):
+            m.forward_flat(x_flat)
+        torch.cuda.synchronize()
+        log(f"[bench] timing {steps} forwards of the 64-token layer")
+        ms, st = timed_steps(m, x_flat, steps)
+    p50 = st.pop("_p50")
+    out = {"workload": "ETHOS expert-layer forward, 64 tokens x d_model 1024, 262144 experts, 8 routing heads, "
+                       "top-16, d_query 256, bf16",
+           "p50_ms": round(p50, 4), "mean_ms": round(ms, 4), "steps": steps,
+           "value": round(sh.n_tok / (p50 * 1e-3), 1), "unit": "tokens/s (at the p50 latency)",
+           "stage_us": {k: round(v * 1e3, 2) for k, v in st.items()}}
+    if with_cpu:
+        log("[bench] CPU baseline on the 64-token layer")
+        out["cpu_baseline"] = cpu_baseline(sh, x_cpu, sd_cpu, sh.n_tok)
+    del m
+    return out
 
 
 if __name__ == "__main__":

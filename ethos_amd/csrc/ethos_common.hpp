@@ -78,35 +78,6 @@ __device__ __forceinline__ void Elem<uint16_t>::round32x2(float& a, float& b) {
 // Exact GELU (erf form), fp32.
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
 
-// Branch-free erf-form GELU for results that are rounded to bf16.
-//   GELU(x) = x Phi(x) = max(x, 0) - |x| hc(|x|),  hc(a) = erfc(a / sqrt 2) / 2,
-// since for x < 0, x Phi(x) = -|x| hc(|x|), and for x >= 0, x Phi(x) = x - x hc(x).
-//   hc(a) = t 2^(Q(t) - a^2 log2(e) / 2),  t = 1 / (1 + 0.32 a),
-// Q a degree-7 polynomial fitted (minimax, in the log domain) to
-// log2(hc(a) / t) + a^2 log2(e) / 2 on a in [0, 9]: relative error of hc below 1.1e-7
-// in exact arithmetic; evaluated in fp32 with v_rcp_f32 / v_exp_f32 the result stays
-// within 4.5e-6 relative over [-9, 9] (worst in the far negative tail, where it is
-// ~1e-17 in magnitude), far inside half a bf16 ulp (2^-9).  |x| is clamped in the
-// product so that GELU(+inf) = +inf.  max(x, 0) and the clamp are integer operations
-// on the bit patterns (same results for all non-NaN inputs; a NaN input still yields
-// NaN through hc), which spares the IEEE-mode canonicalisation of float min / max.
-__device__ __forceinline__ float gelu_bf16_fit(float x) {
-    const float ax = fabsf(x);
-    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.32f, ax, 1.0f));
-    float q = -0.29732826f;
-    q = __builtin_fmaf(q, t, 1.39243793f);
-    q = __builtin_fmaf(q, t, -2.37004828f);
-    q = __builtin_fmaf(q, t, 1.58912885f);
-    q = __builtin_fmaf(q, t, -0.51493132f);
-    q = __builtin_fmaf(q, t, 0.75075698f);
-    q = __builtin_fmaf(q, t, 1.41815186f);
-    q = __builtin_fmaf(q, t, -2.96816778f);
-    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x * -0.72134752f, x, q));  // -log2(e)/2
-    const float pos = __int_as_float(max(__float_as_int(x), 0));                         // max(x, 0)
-    const float axc = __int_as_float(min(__float_as_int(ax), 0x7f61b1e6));              // min(|x|, 3e38)
-    return __builtin_fmaf(-axc, t * e, pos);
-}
-
 // erf-form GELU of two packed bf16 values (low and high half), correctly rounded to
 // bf16, from a table of the 3328 inputs that are not a closed form (gelu_bf16_lut.inc,
 // written by gelu_lut.py): table entry d for x = +bf16(0x3a80 + d), d < 1536

@@ -31,9 +31,9 @@ constexpr int kGenPad = 8;  // LDS row padding (elements)
 template <typename T>
 __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ latents, int64_t n_experts,
                                                        const int32_t* __restrict__ uniq,
-                                                       const int32_t* __restrict__ n_unique, const T* __restrict__ w1,
-                                                       const T* __restrict__ w2, int dl, int dh, int d2,
-                                                       T* __restrict__ hout, T* __restrict__ uv) {
+                                                       const int32_t* __restrict__ n_unique, int64_t max_unique,
+                                                       const T* __restrict__ w1, const T* __restrict__ w2, int dl,
+                                                       int dh, int d2, T* __restrict__ hout, T* __restrict__ uv) {
     using M = Mfma<T>;
     constexpr int R = GenTile<T>::kRows;
     constexpr int RB = R / 32;
@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
     T* hs = zs + R * zp;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lrow = lane & 31, lk = (lane >> 5) * M::kKL;
-    const int U = *n_unique;
+    // uniq, h and v hold max_unique rows
+    const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
     const int n_tiles = (U + R - 1) / R;
     const int nb1 = dh / 32, nb2 = d2 / 32;
 
@@ -142,9 +143,10 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
 
 // ---------------------------------------------------------------------------------
 // bf16 generator for the common shapes (d_latent 128, d_hidden 256 or 512), two kernels:
-// hidden_bf16_kernel writes h (GEMM1 + GELU, VALU heavy, high occupancy) and
-// expand_bf16_kernel reads it back into registers for v = h W_v^T (MFMA bound, one
-// wave per SIMD holding 64 experts' hidden rows).
+// hidden_ws_bf16_kernel writes h (GEMM1 + GELU, VALU heavy) and an expand kernel reads it
+// back for v = h W_v^T (MFMA bound): expand_ws_bf16_kernel (W_v-stationary) when d_model
+// splits into 256-column groups, else expand_bf16_kernel (one wave per SIMD holding 64
+// experts' hidden rows).
 // ---------------------------------------------------------------------------------
 constexpr int kG2Waves = 4;
 constexpr int kG2MB = 2;                          // expert blocks of 32 per wave
@@ -160,80 +162,11 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* v) {
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
-// Hidden rows, bf16: h = RN(gelu(RN(z W1^T))) for the unique experts, a workgroup of
-// 16 waves per CU with W1 resident in LDS (loaded once) and 32 experts per wave and
-// pass.  GEMM1 is computed transposed, hid^T = W1 . Z^T (A = W1 rows, B = gathered
-// latent rows).  Lane l reads W1 row pi(l % 32) of each 32-row block, pi swapping bits
-// 2 and 3 of the row index, so that accumulator elements 8p..8p+7 of lane half h hold
-// the eight consecutive hidden values 16p + 8h .. 16p + 8h + 7 of expert l % 32: one
-// 16-byte store each.  GELU comes from a 6.5 KB table in LDS (the pre-activation is a
-// bf16 value); four waves per SIMD overlap one wave's GELU with the others' MFMAs,
-// latent gathers and stores.
-constexpr int kHWaves = 16;
-
+// The GELU table (gelu_bf16_lut.inc): the correctly rounded erf-form GELU of the bf16
+// inputs that are not a closed form.
 __device__ const uint16_t kGeluLut[kGeluLutSize] = {
 #include "gelu_bf16_lut.inc"
 };
-
-template <int DL, int DH>
-__global__ __launch_bounds__(kHWaves * 64) void hidden_bf16_kernel(const uint16_t* __restrict__ latents,
-                                                                   int64_t n_experts, const int32_t* __restrict__ uniq,
-                                                                   const int32_t* __restrict__ n_unique,
-                                                                   const uint16_t* __restrict__ w1,
-                                                                   uint16_t* __restrict__ hout) {
-    constexpr int KS1 = DL / 16;  // GEMM1 k-steps
-    constexpr int NB1 = DH / 32;  // hidden blocks of 32
-    constexpr int kPitch = DL + 8;  // W1 row pitch in LDS (elements): rows 16 apart share banks
-    // the GELU table first (LDS byte 0 upward), then W1
-    __shared__ __align__(16) uint16_t smem[kGeluLutSize + DH * kPitch];
-    uint16_t* lut = smem;
-    uint16_t* w1s = smem + kGeluLutSize;
-    static_assert(kGeluLutSize % 8 == 0, "W1 rows stay 16-byte aligned");
-    const uint32_t lut_bytes = (uint32_t)(size_t)(__attribute__((address_space(3))) uint16_t*)smem;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int h = lane >> 5, l32 = lane & 31;
-    const int prow = (l32 & ~0xc) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);  // bits 2 <-> 3
-    const int U = *n_unique;
-    for (int e = tid; e < DH * DL / 8; e += kHWaves * 64) {
-        const int r = e / (DL / 8), g = e % (DL / 8);
-        *reinterpret_cast<uint4*>(&w1s[r * kPitch + 8 * g]) = *reinterpret_cast<const uint4*>(w1 + r * DL + 8 * g);
-    }
-    for (int e = tid; e < kGeluLutSize; e += kHWaves * 64) lut[e] = kGeluLut[e];
-    __syncthreads();
-    // blocks go round-robin over the workgroups first, so every CU gets the same count
-    // to within one
-    const int n_blocks = (U + 31) / 32;
-    for (int b = blockIdx.x + gridDim.x * wave; b < n_blocks; b += gridDim.x * kHWaves) {
-        const int u = b * 32 + l32;
-        const int64_t id = u < U ? (int64_t)uniq[u] : -1;
-        const bool ok = id >= 0 && id < n_experts;
-        const uint16_t* zr = latents + (ok ? id : 0) * DL + 8 * h;
-        bf16x8_t zf[KS1];
-#pragma unroll
-        for (int ks = 0; ks < KS1; ++ks)
-            zf[ks] = ok ? __builtin_bit_cast(bf16x8_t, __builtin_nontemporal_load(
-                                                           reinterpret_cast<const u32x4_t*>(zr + ks * 16)))
-                        : bf16x8_t{};
-        uint16_t* hr = hout + (int64_t)u * DH + 8 * h;
-#pragma unroll 2
-        for (int t = 0; t < NB1; ++t) {
-            f32x16_t acc = f32x16_zero();
-#pragma unroll
-            for (int ks = 0; ks < KS1; ++ks) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&w1s[(t * 32 + prow) * kPitch + ks * 16 + 8 * h]);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, zf[ks], acc, 0, 0, 0);
-            }
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                uint32_t g[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)  // bf16-round two pre-activations, then the table
-                    g[j] = gelu_bf16x2_lut(pack_bf16x2(acc[8 * p + 2 * j], acc[8 * p + 2 * j + 1]), lut_bytes);
-                if (u < U) *reinterpret_cast<uint4*>(hr + 32 * t + 16 * p) = make_uint4(g[0], g[1], g[2], g[3]);
-            }
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------------
 // Hidden rows, bf16, W1-stationary (the form of expand_ws_bf16_kernel applied to GEMM1):
@@ -244,9 +177,7 @@ __global__ __launch_bounds__(kHWaves * 64) void hidden_bf16_kernel(const uint16_
 // each fragment read feeds two MFMAs.  The unique ids of all of a workgroup's tiles are
 // copied to LDS once at the start, so the loop issues no id loads.  GELU comes from the
 // table in LDS; the rows leave through a per-wave staging area as whole 128-byte lines.
-// The products (A = W1 rows, B = latent rows, k-steps in order) are those of
-// hidden_bf16_kernel with the operands exchanged, so the pre-activations and h are equal
-// to within the order of the MFMA's internal sums.
+// The products are A = W1 rows, B = latent rows, k-steps in order, fp32 accumulation.
 // ---------------------------------------------------------------------------------
 constexpr int kHsRows = 64;       // experts per tile
 constexpr int kHsMaxTiles = 32;   // tiles per workgroup whose ids fit the LDS id table
@@ -436,7 +367,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
-    const int U = *n_unique;
+    const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
     const int n_tiles = (U + kG2Rows - 1) / kG2Rows;
     const int n_chunks = d2 / kG2Cols;
     // W2 as a buffer resource (raw, byte-addressed; loads beyond its size return 0)
@@ -827,19 +758,13 @@ static bool launch_generate_bf16(const void* latents, int64_t n_experts, const i
                                  void* uv, int num_cus, hipStream_t stream) {
     if (dl != DL || dh != DH || d2 % kG2Cols) return false;
     // W1-stationary hidden rows when every workgroup's tile ids fit its LDS table and the
-    // latent table fits one buffer descriptor
+    // latent table fits one buffer descriptor; other sizes take the generic kernel
     const int64_t htiles = (max_unique + kHsRows - 1) / kHsRows;
     const int64_t hgrid = htiles < num_cus ? (htiles > 0 ? htiles : 1) : num_cus;
-    if ((htiles + hgrid - 1) / hgrid <= kHsMaxTiles && n_experts * DL * 2 < 0x7ff00000ll) {
-        hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
-                           (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
-                           (uint16_t*)hout);
-    } else {
-        const int64_t blocks = (max_unique + 32 * kHWaves - 1) / (32 * kHWaves);
-        const unsigned g1 = (unsigned)(blocks < num_cus ? (blocks > 0 ? blocks : 1) : num_cus);
-        hipLaunchKernelGGL((hidden_bf16_kernel<DL, DH>), dim3(g1), dim3(kHWaves * 64), 0, stream,
-                           (const uint16_t*)latents, n_experts, uniq, n_unique, (const uint16_t*)w1, (uint16_t*)hout);
-    }
+    if ((htiles + hgrid - 1) / hgrid > kHsMaxTiles || n_experts * DL * 2 >= 0x7ff00000ll) return false;
+    hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
+                       (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
+                       (uint16_t*)hout);
     if (uv == nullptr) return true;  // hidden rows only
     // W_v-stationary when d2 splits into 256-column groups that fill the XCDs evenly
     const int n_cg = d2 / kWsCols;
@@ -888,11 +813,12 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
     const size_t smem = generate_smem_bytes(dl, dh, dtype);
     if (dtype == kBF16)
         hipLaunchKernelGGL(generate_kernel<uint16_t>, dim3(grid), dim3(256), smem, stream, (const uint16_t*)latents,
-                           n_experts, uniq, n_unique, (const uint16_t*)w1, (const uint16_t*)wv, dl, dh, d2,
+                           n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1, (const uint16_t*)wv, dl, dh, d2,
                            (uint16_t*)hout, (uint16_t*)vout);
     else
         hipLaunchKernelGGL(generate_kernel<float>, dim3(grid), dim3(256), smem, stream, (const float*)latents,
-                           n_experts, uniq, n_unique, (const float*)w1, (const float*)wv, dl, dh, d2, (float*)hout,
+                           n_experts, uniq, n_unique, max_unique, (const float*)w1, (const float*)wv, dl, dh, d2,
+                           (float*)hout,
                            (float*)vout);
     return (int)hipGetLastError();
 }

@@ -273,6 +273,28 @@ def test_generate_shapes(dl, dh, d, U):
     _check_rows(v[:U], v_ref, "bf16")
 
 
+@pytest.mark.parametrize("dl,dh,d,dt", [(16, 32, 64, "fp32"), (16, 32, 64, "bf16"), (128, 512, 1024, "bf16"),
+                                         (128, 512, 320, "bf16")])
+def test_generate_clamps_unique_count(dl, dh, d, dt):
+    """A device unique-expert count above max_unique (the rows uniq, h and v hold) is
+    clamped: rows below max_unique are generated, nothing past the buffers is touched.
+    Covers the generic kernel (fp32, d_latent 16), the W-stationary kernels (d 1024) and
+    the H-stationary expand (d 320)."""
+    rng = np.random.default_rng(dl + dh + d)
+    E, max_u = 2000, 100
+    enc = (lambda a: O.f32_to_bf16_bits(a)) if dt == "bf16" else (lambda a: a.astype(np.float32))
+    lat = enc(rng.standard_normal((E, dl)).astype(np.float32))
+    w1 = enc((rng.uniform(-1, 1, (dh, dl)) * 4 / np.sqrt(dl)).astype(np.float32))
+    w2 = enc((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(dh)).astype(np.float32))
+    uniq = np.sort(rng.choice(E, max_u, replace=False)).astype(np.int32)
+    n_unique = torch.tensor([3 * max_u], dtype=torch.int32, device="cuda")
+    h, v = hip.generate(to_dev(lat), to_dev(uniq), n_unique, max_u, to_dev(w1), to_dev(w2))
+    torch.cuda.synchronize()
+    h_ref, v_ref = O.generate(lat, uniq, w1, w2, dt)
+    _check_rows(O.to_f32(to_host(h), dt), h_ref, dt)
+    _check_rows(O.to_f32(to_host(v), dt), v_ref, dt)
+
+
 @pytest.mark.parametrize("dh", [512, 256])
 def test_generate_many_tiles(dh):
     """Enough experts that each workgroup runs several whole tiles back to back plus the
