@@ -61,31 +61,54 @@ def stage_work(sh, U: int) -> dict:
     }
 
 
-STAGES = ["query_proj", "route", "sort_segment", "generate", "apply_scatter"]
+# Stage boundaries: three marked by the layer between its library calls, five recorded by
+# the library inside the expert-stage call (ethos_stage_events).
+OUTER = ["query_proj", "route", "sort_segment"]
+INNER = ["token_proj", "hidden_rows", "activations", "v_rows", "scatter_back"]
+# the graded stages as groups of those
+STAGES = {"query_proj": ["query_proj"], "route": ["route"], "sort_segment": ["sort_segment"],
+          "generate": ["hidden_rows", "v_rows"], "apply_scatter": ["token_proj", "activations", "scatter_back"]}
 
 
 def timed_steps(m, x_flat, steps: int) -> tuple[float, dict]:
     """Run `steps` layer forwards; return wall ms/step and the mean per-stage ms.
 
     Stage boundaries are HIP events recorded on the stream every kernel is launched on
-    (torch's current stream, which the library is handed), inside the same timed region.
+    (torch's current stream, which the library is handed), inside the same timed region:
+    by the layer between its calls, and by the library between the kernels of its
+    expert-stage call.
     """
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)] for _ in range(steps)]
+    from ethos_amd import hip
+
+    mk = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    outer = [[mk() for _ in range(len(OUTER) + 1)] for _ in range(steps)]
+    inner = [[mk() for _ in INNER] for _ in range(steps)]
+    for e in (ev for step in inner for ev in step):
+        e.record()  # the library records into existing events
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        e = evs[i]
+        e = outer[i]
         e[0].record()
-        pos = iter(range(1, len(STAGES) + 1))
+        pos = iter(range(1, len(OUTER) + 1))
 
         def mark(stage, e=e, pos=pos):
             e[next(pos)].record()
 
+        hip.stage_events(inner[i])
         m.forward_flat(x_flat, mark)
+    hip.stage_events([])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    per = {k: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, k in enumerate(STAGES)}
-    steps_ms = sorted(e[0].elapsed_time(e[-1]) for e in evs)
+    per_k = {}
+    for j, k in enumerate(OUTER):
+        per_k[k] = sum(e[j].elapsed_time(e[j + 1]) for e in outer) / steps
+    for j, k in enumerate(INNER):
+        prev = (lambda i: outer[i][-1]) if j == 0 else (lambda i, j=j: inner[i][j - 1])
+        per_k[k] = sum(prev(i).elapsed_time(inner[i][j]) for i in range(steps)) / steps
+    per = {g: sum(per_k[k] for k in ks) for g, ks in STAGES.items()}
+    per["_kernels"] = per_k
+    steps_ms = sorted(outer[i][0].elapsed_time(inner[i][-1]) for i in range(steps))
     per["_p50"] = steps_ms[len(steps_ms) // 2]
     return elapsed / steps * 1e3, per
 
@@ -314,6 +337,7 @@ def main():
         log(f"[bench] timing {args.steps} steps")
         ms, st = timed_steps(m, x_flat, args.steps)
         p50 = st.pop("_p50")
+        sub_us = {k: round(v * 1e3, 2) for k, v in st.pop("_kernels").items()}
         U = unique_experts(m, x_flat)
     work = stage_work(sh, U)
     kernels = {}
@@ -326,7 +350,7 @@ def main():
             ach = w["work"] / (ms_k * 1e-3) / 1e9
             peak = HBM_PEAK_GBS
         kernels[k] = dict(us=round(ms_k * 1e3, 2), bound=w["bound"], achieved=round(ach, 2), peak=peak,
-                          unit=w["unit"], frac=round(ach / peak, 4), work=w["work"])
+                          unit=w["unit"], frac=round(ach / peak, 4), work=w["work"], parts=STAGES[k])
     graded = {k: kernels[k] for k in ("generate", "apply_scatter")}
     dom = max(graded, key=lambda k: graded[k]["us"])
     kd = kernels[dom]
@@ -348,6 +372,7 @@ def main():
             log(f"[bench] timing {args.steps} steps, hidden-space order")
             ms_h, st_h = timed_steps(mh, x_flat, args.steps)
             st_h.pop("_p50")
+            st_h.pop("_kernels")
         del mh
         alternatives = {"hidden_space": dict(
             ms_per_step=round(ms_h, 4), value=round(sh.n_tok / (ms_h * 1e-3), 1), unit="tokens/s",
@@ -389,6 +414,7 @@ def main():
         "unique_experts": U,
         "roofline": roofline,
         "kernels": kernels,
+        "stage_us": sub_us,
         "alternatives": alternatives,
         "cpu_baseline": cpu,
         "decode_64_tokens": decode,
@@ -416,6 +442,7 @@ def decode_latency(args, with_cpu: bool) -> dict:
         log(f"[bench] timing {steps} forwards of the 64-token layer")
         ms, st = timed_steps(m, x_flat, steps)
     p50 = st.pop("_p50")
+    st.pop("_kernels")
     out = {"workload": "ETHOS expert-layer forward, 64 tokens x d_model 1024, 262144 experts, 8 routing heads, "
                        "top-16, d_query 256, bf16",
            "p50_ms": round(p50, 4), "mean_ms": round(ms, 4), "steps": steps,

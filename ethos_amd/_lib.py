@@ -26,6 +26,7 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "ethos_last_error": (ctypes.c_char_p, []),
     "ethos_abi_version": (ctypes.c_int, []),
+    "ethos_stage_events": (ctypes.c_int, [_vp, _i32]),
     "ethos_query_proj_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "ethos_query_proj": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _vp]),
     "ethos_route_topk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
@@ -38,6 +39,9 @@ SIGNATURES = {
                                            _vp, _sz, _vp, _vp]),
     "ethos_expert_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                              _vp]),
+    "ethos_expert_forward_workspace_bytes": (_sz, [_i64, _i32, _i32, _i64, _i32, _i32, _i32, _i32]),
+    "ethos_expert_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64,
+                                            _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _vp, _vp]),
     "ethos_apply_hidden_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ethos_apply_hidden": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
                                           _vp, _sz, _vp, _vp]),

@@ -80,9 +80,33 @@ void* scratch_ptr(int* rc) {
     return p;
 }
 
+// Stage events of the calling thread (ethos_stage_events): recorded in order, one per
+// stage boundary, until the list is used up.
+thread_local hipEvent_t g_events[16];
+thread_local int g_n_events = 0, g_next_event = 0;
+
 }  // namespace
 
+namespace ethos {
+void stage_mark(hipStream_t stream) {
+    if (g_next_event < g_n_events) (void)hipEventRecord(g_events[g_next_event++], stream);
+}
+}  // namespace ethos
+
 extern "C" {
+
+int ethos_stage_events(void* const* events, int32_t n_events) {
+    g_err[0] = 0;
+    if (n_events < 0 || n_events > 16 || (n_events > 0 && !events))
+        return fail(ETHOS_ESIZE, "ethos_stage_events: 0 to 16 events, got %d", n_events);
+    for (int i = 0; i < n_events; ++i) {
+        if (!events[i]) return fail(ETHOS_ENULL, "ethos_stage_events: event %d is NULL", i);
+        g_events[i] = (hipEvent_t)events[i];
+    }
+    g_n_events = n_events;
+    g_next_event = 0;
+    return 0;
+}
 
 const char* ethos_last_error(void) { return g_err; }
 
@@ -303,6 +327,59 @@ int ethos_apply_hidden(const void* x, const void* w2, const void* h, const int32
                                               d_model, d_hidden, dtype, workspace, out, num_cus(), (hipStream_t)stream);
     if (rc < 0) return fail(ETHOS_EUNSUPPORTED, "ethos_apply_hidden: d_hidden=%d not supported", d_hidden);
     return hip_status(rc, "ethos_apply_hidden");
+}
+
+size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int64_t max_unique,
+                                            int32_t d_model, int32_t d_hidden, int32_t dtype, int32_t order) {
+    if (n_tok <= 0 || n_heads <= 0 || top_k <= 0 || max_unique < 0 || d_model <= 0 || d_hidden <= 0 ||
+        (order != 0 && order != 1))
+        return 256;
+    return ethos::expert_forward_workspace_bytes(n_tok, n_heads, top_k, max_unique, d_model, d_hidden, dtype, order);
+}
+
+int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
+                         const void* wut, const int32_t* uniq_ids, const int32_t* n_unique, int64_t max_unique,
+                         const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores,
+                         int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_latent, int32_t d_hidden,
+                         int32_t d_model, int32_t dtype, int32_t order, void* workspace, size_t workspace_bytes,
+                         void* h_out, void* out, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_expert_forward: unknown dtype %d", dtype);
+    if (order != 0 && order != 1) return fail(ETHOS_ESIZE, "ethos_expert_forward: order must be 0 or 1, got %d", order);
+    if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || n_experts <= 0 || max_unique < 0 || d_latent <= 0 ||
+        d_hidden <= 0 || d_model <= 0)
+        return fail(ETHOS_ESIZE, "ethos_expert_forward: bad sizes");
+    if (n_tok * n_heads * top_k > INT32_MAX || n_tok > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_expert_forward: too many pairs");
+    const int kq = dtype == ETHOS_BF16 ? 16 : 2;
+    const int vec = dtype == ETHOS_BF16 ? 8 : 4;
+    if (d_latent % kq || d_hidden % 32 || d_model % 32 || d_model > 4096 ||
+        ethos::apply_chunks(d_model, dtype) > 8 || ethos::apply_chunks(d_hidden, dtype) > 8 ||
+        ethos::generate_smem_bytes(d_latent, d_hidden, dtype) > 160 * 1024 || d_model % vec || d_hidden % vec)
+        return fail(ETHOS_EUNSUPPORTED,
+                    "ethos_expert_forward: needs d_latent %% %d == 0, d_hidden and d_model multiples of 32 with "
+                    "d_model <= 4096 and d_hidden <= %d (got %d, %d, %d)", kq, 8 * 64 * vec, d_latent, d_hidden,
+                    d_model);
+    if (n_tok == 0) return 0;
+    if (max_unique < 1) return fail(ETHOS_ESIZE, "ethos_expert_forward: max_unique must be >= 1 for a nonempty batch");
+    if (!x || !latents || !w1 || !w2 || !uniq_ids || !n_unique || !perm || !sorted_slot || !pair_slot || !scores ||
+        !workspace || !h_out || !out)
+        return fail(ETHOS_ENULL, "ethos_expert_forward: null pointer");
+    const size_t need = ethos::expert_forward_workspace_bytes(n_tok, n_heads, top_k, max_unique, d_model, d_hidden,
+                                                              dtype, order);
+    if (workspace_bytes < need)
+        return fail(ETHOS_EWORKSPACE, "ethos_expert_forward: workspace of %zu bytes, %zu needed", workspace_bytes,
+                    need);
+    if (!aligned16(x) || !aligned16(w1) || !aligned16(w2) || (wut && !aligned16(wut)) || !aligned16(workspace) ||
+        !aligned16(h_out) || !aligned16(out))
+        return fail(ETHOS_EALIGN, "ethos_expert_forward: x, w1, w2, wut, workspace, h_out and out must be 16-byte "
+                                  "aligned");
+    const int rc = ethos::launch_expert_forward(x, latents, n_experts, w1, w2, dtype == ETHOS_BF16 ? wut : nullptr,
+                                                uniq_ids, n_unique, max_unique, perm, sorted_slot, pair_slot, scores,
+                                                n_tok, n_heads, top_k, d_latent, d_hidden, d_model, dtype, order,
+                                                workspace, h_out, out, num_cus(), (hipStream_t)stream);
+    if (rc < 0) return fail(ETHOS_EUNSUPPORTED, "ethos_expert_forward: shape not supported");
+    return hip_status(rc, "ethos_expert_forward");
 }
 
 int ethos_expert_backward(const void* h, const float* xp, const float* dyb, const int32_t* pair_slot,

@@ -256,6 +256,67 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
     }
 }
 
+// Per-pair activations with 8 lanes per pair.  A wave takes 64 consecutive sorted pairs
+// and works through them 8 at a time: lane l serves pair l / 8 of the group and holds the
+// 16-byte pieces (l % 8) + 8 i, i < P, of its h row and its xp row, so each load
+// instruction reads 8 whole 128-byte lines.  Per lane: P pieces of dot products in fp32,
+// then a 3-step reduction over the pair's 8 lanes; the 64 dot products wait in LDS and
+// the epilogue (rounding, GELU, gate) runs once per 64 pairs, one pair per lane.
+// P = pieces per lane: dh <= 64 P elements (bf16) or 32 P (fp32).
+constexpr int kAct8Waves = 4;
+
+template <typename T, int P>
+__global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
+                                                                     const int32_t* __restrict__ perm,
+                                                                     const int32_t* __restrict__ sorted_slot,
+                                                                     const T* __restrict__ gates, int64_t n_pairs,
+                                                                     int hk, int dh, float* __restrict__ act) {
+    constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
+    __shared__ float dots[kAct8Waves][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int part = lane & 7, slot = lane >> 3;
+    const int64_t wave_id = (int64_t)blockIdx.x * kAct8Waves + wave;
+    const int64_t n_waves = (int64_t)gridDim.x * kAct8Waves;
+    const int64_t n_chunks = (n_pairs + 63) / 64;
+    for (int64_t chunk = wave_id; chunk < n_chunks; chunk += n_waves) {
+        const int64_t i0 = chunk * 64;
+        const int cnt = (int)min((int64_t)64, n_pairs - i0);
+        const int my_p = lane < cnt ? perm[i0 + lane] : 0;
+        const int my_s = lane < cnt ? sorted_slot[i0 + lane] : 0;
+        for (int g = 0; g < cnt; g += 8) {
+            // this lane's pair of the group (a tail group repeats the last pair)
+            const int src = g + slot < cnt ? g + slot : cnt - 1;
+            const int p = __shfl(my_p, src, 64);
+            const int sl = __shfl(my_s, src, 64);
+            const T* hr = hid + (int64_t)sl * dh;
+            const T* xr = xp + (int64_t)(p / hk) * dh;
+            Raw hv[P], xv[P];
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                const int e = (part + 8 * i) * N;
+                hv[i] = e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
+                xv[i] = e < dh ? *reinterpret_cast<const Raw*>(xr + e) : Raw{};
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < P; ++i) acc = dot_raw(hv[i], xv[i], acc);
+            // sum over the pair's 8 lanes (lanes 8 slot .. 8 slot + 7)
+            acc += dpp_f32<kDppXor1>(acc);
+            acc += dpp_f32<kDppXor2>(acc);
+            acc += dpp_f32<kDppRowHalfMirror>(acc);
+            if (part == 0) dots[wave][g + slot] = acc;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < cnt) {
+            const float g = Elem<T>::to_f32(gates[my_p]);
+            const float a = Elem<T>::round32(gelu_erf(Elem<T>::round32(dots[wave][lane])));
+            act[my_p] = Elem<T>::round32(a * g);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 constexpr int kScatterUnroll = 8;  // v rows in flight per wave
 
 template <typename T, int CH>
@@ -498,37 +559,105 @@ __global__ __launch_bounds__(256) void apply_head_sum_kernel(const T* __restrict
     }
 }
 
-template <typename T, int CH1, int CH2>
-static int launch_apply_t(const void* xp, const void* hid, const void* v, const int32_t* perm,
-                          const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,
-                          int k, int d, int dh, float* act, void* headbuf, void* out, int num_cus,
-                          hipStream_t stream) {
-    const int64_t n_pairs = n_tok * H * k;
-    const int64_t chunks = (n_pairs + 63) / 64;
-    int64_t g1 = (chunks + 3) / 4;
+template <typename T, int CH1>
+static void launch_act_t(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
+                         const void* gates, int64_t n_pairs, int hk, int dh, float* act, int num_cus,
+                         hipStream_t stream) {
     const int64_t cap = (int64_t)num_cus * 16;
-    if (g1 > cap) g1 = cap;
-    if (g1 < 1) g1 = 1;
+    int64_t g1 = ((n_pairs + 63) / 64 + 3) / 4;
+    g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
     hipLaunchKernelGGL((apply_act_kernel<T, CH1>), dim3((unsigned)g1), dim3(256), 0, stream, (const T*)xp,
-                       (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, H * k, dh, act);
+                       (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, hk, dh, act);
+}
+
+template <typename T, int CH2>
+static void launch_scatter_t(const void* v, const int32_t* pair_slot, const float* act, int64_t n_tok, int H, int k,
+                             int d, void* headbuf, void* out, int num_cus, hipStream_t stream) {
+    const int64_t cap = (int64_t)num_cus * 16;
     if (headbuf != nullptr) {
         const int64_t items = n_tok * H;
         int64_t g3 = (items + 3) / 4;
         g3 = g3 > cap ? cap : (g3 < 1 ? 1 : g3);
         hipLaunchKernelGGL((apply_scatter_head_kernel<T, CH2>), dim3((unsigned)g3), dim3(256), 0, stream,
-                           (const T*)v, pair_slot, (const float*)act, items, k, d, (T*)headbuf);
+                           (const T*)v, pair_slot, act, items, k, d, (T*)headbuf);
         int64_t g4 = (n_tok + 3) / 4;
         g4 = g4 > cap ? cap : (g4 < 1 ? 1 : g4);
         hipLaunchKernelGGL((apply_head_sum_kernel<T, CH2>), dim3((unsigned)g4), dim3(256), 0, stream,
                            (const T*)headbuf, n_tok, H, d, (T*)out);
-        return (int)hipGetLastError();
+        return;
     }
     int64_t g2 = (n_tok + 3) / 4;
-    if (g2 > cap) g2 = cap;
-    if (g2 < 1) g2 = 1;
+    g2 = g2 > cap ? cap : (g2 < 1 ? 1 : g2);
     hipLaunchKernelGGL((apply_scatter_kernel<T, CH2>), dim3((unsigned)g2), dim3(256), 0, stream, (const T*)v,
-                       pair_slot, (const float*)act, n_tok, H, k, d, (T*)out);
-    return (int)hipGetLastError();
+                       pair_slot, act, n_tok, H, k, d, (T*)out);
+}
+
+template <typename T, int P>
+static void launch_act8_t(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
+                          const void* gates, int64_t n_pairs, int hk, int dh, float* act, int num_cus,
+                          hipStream_t stream) {
+    const int64_t cap = (int64_t)num_cus * 16;
+    int64_t g1 = ((n_pairs + 63) / 64 + kAct8Waves - 1) / kAct8Waves;
+    g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
+    hipLaunchKernelGGL((apply_act8_kernel<T, P>), dim3((unsigned)g1), dim3(kAct8Waves * 64), 0, stream, (const T*)xp,
+                       (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, hk, dh, act);
+}
+
+// Per-pair activations a_p (phase 1): 8 lanes per pair for rows of up to 64 pieces of 16
+// bytes (d_hidden <= 512 bf16 / 256 fp32), one wave per pair beyond; -1 past the limits.
+static int launch_act(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
+                      const void* gates, int64_t n_pairs, int hk, int dh, int dtype, float* act, int num_cus,
+                      hipStream_t stream) {
+    const int pieces = (dh + (dtype == kBF16 ? 8 : 4) - 1) / (dtype == kBF16 ? 8 : 4);
+    const int pp = (pieces + 7) / 8;
+    const int P = pp <= 1 ? 1 : pp <= 2 ? 2 : pp <= 4 ? 4 : pp <= 8 ? 8 : 0;
+#define ETHOS_ACT8_CASE(TT, PP)                                                                                \
+    if (P == PP) {                                                                                             \
+        launch_act8_t<TT, PP>(xp, hid, perm, sorted_slot, gates, n_pairs, hk, dh, act, num_cus, stream);        \
+        return 0;                                                                                              \
+    }
+    if (dtype == kBF16) {
+        ETHOS_ACT8_CASE(uint16_t, 1) ETHOS_ACT8_CASE(uint16_t, 2) ETHOS_ACT8_CASE(uint16_t, 4)
+        ETHOS_ACT8_CASE(uint16_t, 8)
+    } else {
+        ETHOS_ACT8_CASE(float, 1) ETHOS_ACT8_CASE(float, 2) ETHOS_ACT8_CASE(float, 4) ETHOS_ACT8_CASE(float, 8)
+    }
+#undef ETHOS_ACT8_CASE
+    const int c = apply_chunks(dh, dtype);
+    const int ch = c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : c <= 8 ? 8 : 0;
+#define ETHOS_ACT_CASE(TT, CC)                                                                                 \
+    if (ch == CC) {                                                                                            \
+        launch_act_t<TT, CC>(xp, hid, perm, sorted_slot, gates, n_pairs, hk, dh, act, num_cus, stream);         \
+        return 0;                                                                                              \
+    }
+    if (dtype == kBF16) {
+        ETHOS_ACT_CASE(uint16_t, 1) ETHOS_ACT_CASE(uint16_t, 2) ETHOS_ACT_CASE(uint16_t, 4) ETHOS_ACT_CASE(uint16_t, 8)
+    } else {
+        ETHOS_ACT_CASE(float, 1) ETHOS_ACT_CASE(float, 2) ETHOS_ACT_CASE(float, 4) ETHOS_ACT_CASE(float, 8)
+    }
+#undef ETHOS_ACT_CASE
+    return -1;
+}
+
+// Weighted scatter-back (phase 2) for lane chunk counts 1, 2, 4 or 8; -1 beyond.
+static int launch_scatter(const void* v, const int32_t* pair_slot, const float* act, int64_t n_tok, int H, int k,
+                          int d, int dtype, void* headbuf, void* out, int num_cus, hipStream_t stream) {
+    const int c = apply_chunks(d, dtype);
+    const int ch = c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : c <= 8 ? 8 : 0;
+#define ETHOS_SCATTER_CASE(TT, CC)                                                                             \
+    if (ch == CC) {                                                                                            \
+        launch_scatter_t<TT, CC>(v, pair_slot, act, n_tok, H, k, d, headbuf, out, num_cus, stream);            \
+        return 0;                                                                                              \
+    }
+    if (dtype == kBF16) {
+        ETHOS_SCATTER_CASE(uint16_t, 1) ETHOS_SCATTER_CASE(uint16_t, 2) ETHOS_SCATTER_CASE(uint16_t, 4)
+        ETHOS_SCATTER_CASE(uint16_t, 8)
+    } else {
+        ETHOS_SCATTER_CASE(float, 1) ETHOS_SCATTER_CASE(float, 2) ETHOS_SCATTER_CASE(float, 4)
+        ETHOS_SCATTER_CASE(float, 8)
+    }
+#undef ETHOS_SCATTER_CASE
+    return -1;
 }
 
 int apply_chunks(int d, int dtype) {
@@ -557,15 +686,21 @@ size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype) {
 
 // xp = RN_T(x W_u) into the workspace (W_u^T = the first d rows of net.2.weight, row
 // length dh)
-static void launch_token_proj(const void* x, const void* w2, int64_t n_tok, int H, int k, int d, int dh, int dtype,
-                              void* ws, hipStream_t stream) {
+// `wut_in` (bf16, may be null): W_u^T [dh, d] prepared by the caller; otherwise it is
+// transposed into the workspace here.
+static void launch_token_proj(const void* x, const void* w2, const void* wut_in, int64_t n_tok, int H, int k, int d,
+                              int dh, int dtype, void* ws, hipStream_t stream) {
     const size_t eb = dtype == kBF16 ? 2 : 4;
     void* xp = ws;
     const dim3 tgrid((unsigned)((dh + kTpC - 1) / kTpC), (unsigned)((n_tok + kTpT - 1) / kTpT));
     if (dtype == kBF16 && d % kTpK == 0 && dh % 8 == 0) {
-        uint16_t* wut = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + wut_offset(n_tok, H, k, dh, eb));
-        hipLaunchKernelGGL(transpose_wu_kernel, dim3((unsigned)((dh + 63) / 64), (unsigned)((d + 63) / 64)), dim3(256),
-                           0, stream, (const uint16_t*)w2, d, dh, wut);
+        const uint16_t* wut = static_cast<const uint16_t*>(wut_in);
+        if (wut == nullptr) {
+            uint16_t* w = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + wut_offset(n_tok, H, k, dh, eb));
+            hipLaunchKernelGGL(transpose_wu_kernel, dim3((unsigned)((dh + 63) / 64), (unsigned)((d + 63) / 64)),
+                               dim3(256), 0, stream, (const uint16_t*)w2, d, dh, w);
+            wut = w;
+        }
         hipLaunchKernelGGL(token_proj_bf16_kernel,
                            dim3((unsigned)((dh + kTpCols - 1) / kTpCols), (unsigned)((n_tok + kTpT - 1) / kTpT)),
                            dim3(256), 0, stream, (const uint16_t*)x, (const uint16_t*)wut, (int)n_tok, d, dh,
@@ -584,34 +719,14 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
     const size_t eb = dtype == kBF16 ? 2 : 4;
     void* xp = ws;
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
-    launch_token_proj(x, w2, n_tok, H, k, d, dh, dtype, ws, stream);
-    const int c1 = apply_chunks(dh, dtype), c2 = apply_chunks(d, dtype);
     void* headbuf = n_tok <= kSplitHeadMaxTok
                         ? static_cast<unsigned char*>(ws) + headbuf_offset(n_tok, H, k, dh, eb, dtype)
                         : nullptr;
-#define ETHOS_APPLY_CASE(TT, C1, C2)                                                                             \
-    if (c1 <= C1 && c2 <= C2)                                                                                    \
-        return launch_apply_t<TT, C1, C2>(xp, hid, v, perm, sorted_slot, pair_slot, gates, n_tok, H, k, d, dh, act, \
-                                          headbuf, out, num_cus, stream);
-    if (dtype == kBF16) {
-        ETHOS_APPLY_CASE(uint16_t, 1, 1)
-        ETHOS_APPLY_CASE(uint16_t, 1, 2)
-        ETHOS_APPLY_CASE(uint16_t, 2, 2)
-        ETHOS_APPLY_CASE(uint16_t, 2, 4)
-        ETHOS_APPLY_CASE(uint16_t, 4, 4)
-        ETHOS_APPLY_CASE(uint16_t, 4, 8)
-        ETHOS_APPLY_CASE(uint16_t, 8, 8)
-    } else {
-        ETHOS_APPLY_CASE(float, 1, 1)
-        ETHOS_APPLY_CASE(float, 1, 2)
-        ETHOS_APPLY_CASE(float, 2, 2)
-        ETHOS_APPLY_CASE(float, 2, 4)
-        ETHOS_APPLY_CASE(float, 4, 4)
-        ETHOS_APPLY_CASE(float, 4, 8)
-        ETHOS_APPLY_CASE(float, 8, 8)
-    }
-#undef ETHOS_APPLY_CASE
-    return -1;
+    if (apply_chunks(dh, dtype) > 8 || apply_chunks(d, dtype) > 8) return -1;
+    launch_token_proj(x, w2, nullptr, n_tok, H, k, d, dh, dtype, ws, stream);
+    launch_act(xp, hid, perm, sorted_slot, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus, stream);
+    launch_scatter(v, pair_slot, act, n_tok, H, k, d, dtype, headbuf, out, num_cus, stream);
+    return (int)hipGetLastError();
 }
 
 // workspace for the hidden-space form: the apply workspace, then hs [n_tok, dh] T, then
@@ -630,20 +745,20 @@ size_t apply_hidden_workspace_bytes(int64_t n_tok, int H, int k, int d, int dh, 
 }
 
 template <typename T, int CH1>
-static void launch_hidden_t(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
-                            const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k, int dh,
-                            float* act, void* hs, int num_cus, hipStream_t stream) {
-    const int64_t n_pairs = n_tok * H * k;
+static void launch_hacc_t(const void* hid, const int32_t* pair_slot, const float* act, int64_t n_tok, int H, int k,
+                          int dh, void* hs, int num_cus, hipStream_t stream) {
     const int64_t cap = (int64_t)num_cus * 16;
-    int64_t g1 = ((n_pairs + 63) / 64 + 3) / 4;
-    g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
-    hipLaunchKernelGGL((apply_act_kernel<T, CH1>), dim3((unsigned)g1), dim3(256), 0, stream, (const T*)xp,
-                       (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, H * k, dh, act);
     int64_t g2 = (n_tok + 3) / 4;
     g2 = g2 > cap ? cap : (g2 < 1 ? 1 : g2);
     hipLaunchKernelGGL((apply_hacc_kernel<T, CH1>), dim3((unsigned)g2), dim3(256), 0, stream, (const T*)hid,
-                       pair_slot, (const float*)act, n_tok, H, k, dh, (T*)hs);
+                       pair_slot, act, n_tok, H, k, dh, (T*)hs);
 }
+
+// The hidden-space form after the activations: hs = RN_T((1/H) sum_p a_p h_s), then
+// out = RN_T(hs W_v^T).
+static int launch_hidden_tail(const void* w2, const void* hid, const int32_t* pair_slot, const float* act,
+                              int64_t n_tok, int H, int k, int d, int dh, int dtype, void* ws, void* out, int num_cus,
+                              hipStream_t stream);
 
 int launch_apply_hidden(const void* x, const void* w2, const void* hid, const int32_t* perm,
                         const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H,
@@ -651,30 +766,30 @@ int launch_apply_hidden(const void* x, const void* w2, const void* hid, const in
     const size_t eb = dtype == kBF16 ? 2 : 4;
     void* xp = ws;
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
+    if (apply_chunks(dh, dtype) > 8) return -1;
+    launch_token_proj(x, w2, nullptr, n_tok, H, k, d, dh, dtype, ws, stream);
+    launch_act(xp, hid, perm, sorted_slot, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus, stream);
+    return launch_hidden_tail(w2, hid, pair_slot, act, n_tok, H, k, d, dh, dtype, ws, out, num_cus, stream);
+}
+
+static int launch_hidden_tail(const void* w2, const void* hid, const int32_t* pair_slot, const float* act,
+                              int64_t n_tok, int H, int k, int d, int dh, int dtype, void* ws, void* out, int num_cus,
+                              hipStream_t stream) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
     unsigned char* hs = static_cast<unsigned char*>(ws) + hs_offset(n_tok, H, k, dh, dtype);
-    launch_token_proj(x, w2, n_tok, H, k, d, dh, dtype, ws, stream);
     const int c1 = apply_chunks(dh, dtype);
-#define ETHOS_HIDDEN_CASE(TT, C1)                                                                                   \
-    else if (c1 <= C1) launch_hidden_t<TT, C1>(xp, hid, perm, sorted_slot, pair_slot, gates, n_tok, H, k, dh, act, hs, \
-                                               num_cus, stream);
+    const int ch = c1 <= 1 ? 1 : c1 <= 2 ? 2 : c1 <= 4 ? 4 : 8;
     if (dtype == kBF16) {
-        if (false) {
-        }
-        ETHOS_HIDDEN_CASE(uint16_t, 1)
-        ETHOS_HIDDEN_CASE(uint16_t, 2)
-        ETHOS_HIDDEN_CASE(uint16_t, 4)
-        ETHOS_HIDDEN_CASE(uint16_t, 8)
-        else return -1;
+        if (ch == 1) launch_hacc_t<uint16_t, 1>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
+        else if (ch == 2) launch_hacc_t<uint16_t, 2>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
+        else if (ch == 4) launch_hacc_t<uint16_t, 4>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
+        else launch_hacc_t<uint16_t, 8>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
     } else {
-        if (false) {
-        }
-        ETHOS_HIDDEN_CASE(float, 1)
-        ETHOS_HIDDEN_CASE(float, 2)
-        ETHOS_HIDDEN_CASE(float, 4)
-        ETHOS_HIDDEN_CASE(float, 8)
-        else return -1;
+        if (ch == 1) launch_hacc_t<float, 1>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
+        else if (ch == 2) launch_hacc_t<float, 2>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
+        else if (ch == 4) launch_hacc_t<float, 4>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
+        else launch_hacc_t<float, 8>(hid, pair_slot, act, n_tok, H, k, dh, hs, num_cus, stream);
     }
-#undef ETHOS_HIDDEN_CASE
     // projection back: out = RN_T(hs W_v^T), W_v^T = rows d .. 2d-1 of net.2.weight, which
     // as a [d, dh] row-major block is the output-major operand layout of the token
     // projection kernels (K = dh, N = d)
@@ -701,6 +816,85 @@ int launch_apply_hidden(const void* x, const void* w2, const void* hid, const in
         hipLaunchKernelGGL(token_proj_kernel<float>, pg, dim3(256), 0, stream, (const float*)hs, (const float*)wvt,
                            (int)n_tok, dh, d, (float*)out);
     }
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
+// The expert stages as one call (generation, apply, scatter-back) on the sorted pairs.
+// Order 0 (the layer's rounding points): xp, h rows, activations, v rows, scatter-back;
+// order 1 (hidden-space reordering): xp, h rows, activations, per-token hidden sums,
+// projection back.  With the two-kernel bf16 generator the activations run between its
+// kernels, while the freshly written h rows are still in the memory-side cache; other
+// shapes generate first (one kernel) and apply after.
+// Workspace: the apply workspace of the order, then (order 0) v [max_unique, d].
+// ---------------------------------------------------------------------------------
+static size_t order_ws_bytes(int64_t n_tok, int H, int k, int d, int dh, int dtype, int order) {
+    return order == 0 ? apply_workspace_bytes(n_tok, H, k, dh, dtype)
+                      : apply_hidden_workspace_bytes(n_tok, H, k, d, dh, dtype);
+}
+
+size_t expert_forward_workspace_bytes(int64_t n_tok, int H, int k, int64_t max_unique, int d, int dh, int dtype,
+                                      int order) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    size_t b = align256(order_ws_bytes(n_tok, H, k, d, dh, dtype, order));
+    if (order == 0) b += (size_t)max_unique * d * eb;
+    return b;
+}
+
+int launch_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
+                          const void* wut, const int32_t* uniq, const int32_t* n_unique, int64_t max_unique,
+                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot,
+                          const void* gates, int64_t n_tok, int H, int k, int dl, int dh, int d, int dtype, int order,
+                          void* ws, void* hout, void* out, int num_cus, hipStream_t stream) {
+    const size_t eb = dtype == kBF16 ? 2 : 4;
+    unsigned char* v = order == 0 ? static_cast<unsigned char*>(ws) +
+                                        align256(order_ws_bytes(n_tok, H, k, d, dh, dtype, order))
+                                  : nullptr;
+    if (apply_chunks(dh, dtype) > 8 || (order == 0 && apply_chunks(d, dtype) > 8)) return -1;
+    // Stage marks (stage_mark), five per call: after the token projection, the hidden rows,
+    // the activations, the v rows (order 0; nothing for order 1) and the scatter-back (or
+    // the hidden-space tail).  Shapes without the two-kernel generator mark the one
+    // generator launch as the hidden rows and the whole apply as the scatter-back.
+    if (!generate_split_supported(n_experts, max_unique, dl, dh, d, dtype, num_cus)) {
+        stage_mark(stream);
+        int rc = launch_generate(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d, dtype, hout, v,
+                                 num_cus, stream);
+        if (rc != 0) return rc;
+        stage_mark(stream);
+        stage_mark(stream);
+        stage_mark(stream);
+        rc = order == 0 ? launch_apply(x, w2, hout, v, perm, sorted_slot, pair_slot, gates, n_tok, H, k, d, dh, dtype,
+                                       ws, out, num_cus, stream)
+                        : launch_apply_hidden(x, w2, hout, perm, sorted_slot, pair_slot, gates, n_tok, H, k, d, dh,
+                                              dtype, ws, out, num_cus, stream);
+        stage_mark(stream);
+        return rc;
+    }
+    void* xp = ws;
+    float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
+    launch_token_proj(x, w2, wut, n_tok, H, k, d, dh, dtype, ws, stream);
+    stage_mark(stream);
+    int rc = launch_generate_part(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d, hout, v, 1,
+                                  num_cus, stream);
+    if (rc != 0) return rc;
+    stage_mark(stream);
+    launch_act(xp, hout, perm, sorted_slot, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus, stream);
+    stage_mark(stream);
+    if (order == 1) {
+        stage_mark(stream);
+        rc = launch_hidden_tail(w2, hout, pair_slot, act, n_tok, H, k, d, dh, dtype, ws, out, num_cus, stream);
+        stage_mark(stream);
+        return rc;
+    }
+    rc = launch_generate_part(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d, hout, v, 2, num_cus,
+                              stream);
+    if (rc != 0) return rc;
+    stage_mark(stream);
+    void* headbuf = n_tok <= kSplitHeadMaxTok
+                        ? static_cast<unsigned char*>(ws) + headbuf_offset(n_tok, H, k, dh, eb, dtype)
+                        : nullptr;
+    launch_scatter(v, pair_slot, act, n_tok, H, k, d, dtype, headbuf, out, num_cus, stream);
+    stage_mark(stream);
     return (int)hipGetLastError();
 }
 

@@ -8,6 +8,9 @@
 
 namespace ethos {
 
+// Records the calling thread's next stage event (ethos_stage_events) on `stream`, if any.
+void stage_mark(hipStream_t stream);
+
 size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int d, int dtype);
 int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
                  int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream);
@@ -28,6 +31,13 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
                     int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d, int dtype, void* hout,
                     void* vout, int num_cus, hipStream_t stream);
 
+// The bf16 generator's two kernels one at a time (part 1: hidden rows, part 2: v rows from
+// them), for shapes where generate_split_supported; -1 when not supported.
+bool generate_split_supported(int64_t n_experts, int64_t max_unique, int dl, int dh, int d, int dtype, int num_cus);
+int launch_generate_part(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
+                         int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d, void* hout,
+                         void* vout, int part, int num_cus, hipStream_t stream);
+
 int apply_chunks(int d, int dtype);
 int launch_expert_backward(const void* hid, const float* xp, const float* dyb, const int32_t* pair_slot,
                            const void* gates, int64_t n_tok, int H, int k, int dh, int dtype, float* dg, float* hacc,
@@ -40,5 +50,12 @@ size_t apply_workspace_bytes(int64_t n_tok, int H, int k, int dh, int dtype);
 int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
                  const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k,
                  int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream);
+size_t expert_forward_workspace_bytes(int64_t n_tok, int H, int k, int64_t max_unique, int d, int dh, int dtype,
+                                      int order);
+int launch_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
+                          const void* wut, const int32_t* uniq, const int32_t* n_unique, int64_t max_unique,
+                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot,
+                          const void* gates, int64_t n_tok, int H, int k, int dl, int dh, int d, int dtype, int order,
+                          void* ws, void* hout, void* out, int num_cus, hipStream_t stream);
 
 }  // namespace ethos

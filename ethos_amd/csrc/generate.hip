@@ -752,20 +752,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
+// The two-kernel bf16 generator takes d_latent DL, d_hidden DH, d_model % 64 == 0, at most
+// 32 hidden-row tiles per workgroup and a latent table within one buffer descriptor.
+template <int DL, int DH>
+static bool generate_bf16_ok(int64_t n_experts, int64_t max_unique, int dl, int dh, int d2, int num_cus) {
+    if (dl != DL || dh != DH || d2 % kG2Cols) return false;
+    const int64_t htiles = (max_unique + kHsRows - 1) / kHsRows;
+    const int64_t hgrid = htiles < num_cus ? (htiles > 0 ? htiles : 1) : num_cus;
+    return (htiles + hgrid - 1) / hgrid <= kHsMaxTiles && n_experts * DL * 2 < 0x7ff00000ll;
+}
+
+// parts: 1 = the hidden rows (W1-stationary kernel), 2 = the v rows from them (an expand
+// kernel), 3 = both.  False (nothing launched) when the shape is not one these kernels take.
 template <int DL, int DH>
 static bool launch_generate_bf16(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                                  int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d2, void* hout,
-                                 void* uv, int num_cus, hipStream_t stream) {
-    if (dl != DL || dh != DH || d2 % kG2Cols) return false;
-    // W1-stationary hidden rows when every workgroup's tile ids fit its LDS table and the
-    // latent table fits one buffer descriptor; other sizes take the generic kernel
-    const int64_t htiles = (max_unique + kHsRows - 1) / kHsRows;
-    const int64_t hgrid = htiles < num_cus ? (htiles > 0 ? htiles : 1) : num_cus;
-    if ((htiles + hgrid - 1) / hgrid > kHsMaxTiles || n_experts * DL * 2 >= 0x7ff00000ll) return false;
-    hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
-                       (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
-                       (uint16_t*)hout);
-    if (uv == nullptr) return true;  // hidden rows only
+                                 void* uv, int parts, int num_cus, hipStream_t stream) {
+    if (!generate_bf16_ok<DL, DH>(n_experts, max_unique, dl, dh, d2, num_cus)) return false;
+    if (parts & 1) {
+        const int64_t htiles = (max_unique + kHsRows - 1) / kHsRows;
+        const int64_t hgrid = htiles < num_cus ? (htiles > 0 ? htiles : 1) : num_cus;
+        hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
+                           (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
+                           (uint16_t*)hout);
+    }
+    if (uv == nullptr || !(parts & 2)) return true;  // hidden rows only
     // W_v-stationary when d2 splits into 256-column groups that fill the XCDs evenly
     const int n_cg = d2 / kWsCols;
     const int per_xcd = d2 % kWsCols == 0 && n_cg > 0 ? (num_cus / 8) / n_cg : 0;
@@ -801,9 +812,9 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
     const int d2 = vout ? d : 0;
     if (dtype == kBF16) {
         if (launch_generate_bf16<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout,
-                                              vout, num_cus, stream) ||
+                                              vout, 3, num_cus, stream) ||
             launch_generate_bf16<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout,
-                                              vout, num_cus, stream))
+                                              vout, 3, num_cus, stream))
             return (int)hipGetLastError();
     }
     const int R = dtype == kBF16 ? GenTile<uint16_t>::kRows : GenTile<float>::kRows;
@@ -821,6 +832,23 @@ int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq,
                            (float*)hout,
                            (float*)vout);
     return (int)hipGetLastError();
+}
+
+bool generate_split_supported(int64_t n_experts, int64_t max_unique, int dl, int dh, int d, int dtype, int num_cus) {
+    return dtype == kBF16 && (generate_bf16_ok<128, 512>(n_experts, max_unique, dl, dh, d, num_cus) ||
+                              generate_bf16_ok<128, 256>(n_experts, max_unique, dl, dh, d, num_cus));
+}
+
+int launch_generate_part(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
+                         int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d, void* hout,
+                         void* vout, int part, int num_cus, hipStream_t stream) {
+    const void* wv = static_cast<const unsigned char*>(w2) + (size_t)d * dh * 2;
+    if (launch_generate_bf16<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout, vout,
+                                       part, num_cus, stream) ||
+        launch_generate_bf16<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout, vout,
+                                       part, num_cus, stream))
+        return (int)hipGetLastError();
+    return -1;
 }
 
 }  // namespace ethos

@@ -36,6 +36,18 @@ def workspace(nbytes: int, device) -> tuple[torch.Tensor, int]:
     return ws, size
 
 
+def stage_events(events) -> None:
+    """Hand the library torch.cuda.Event objects (already recorded once, so that they exist)
+    to record, in order, at the stage boundaries of this thread's next calls; [] clears."""
+    import ctypes
+
+    handles = [e.cuda_event for e in events]
+    if any(h == 0 for h in handles):
+        raise RuntimeError("stage_events: record each event once before handing it over")
+    arr = (ctypes.c_void_p * max(1, len(handles)))(*handles)
+    check(load().ethos_stage_events(arr, len(handles)), "ethos_stage_events")
+
+
 def key_norm_bounds(sub_keys_1: torch.Tensor, sub_keys_2: torch.Tensor) -> torch.Tensor:
     """fp32 [2, K] upper bounds of the sub-key row norms: fp64 norms of the stored
     values, inflated by 2^-20 and rounded, on the host (once per parameter version)."""
@@ -185,6 +197,43 @@ def apply_hidden(x: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, seg: dict, 
                                    n_heads, top_k, d, dh, code, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
     check(rc, "ethos_apply_hidden")
     return out
+
+
+def expert_forward(x: torch.Tensor, latents: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, seg: dict,
+                   gates: torch.Tensor, n_heads: int, top_k: int, hidden_space: bool = False,
+                   wut: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(out [n, d], h [max_unique, d_hidden]): generation, activations and scatter-back
+    (or, hidden_space=True, the hidden-space form) in one call.  `wut`: optional bf16
+    W_u^T [d_hidden, d] (the transpose of w2[:d]) prepared by the caller."""
+    _need(x, "x", dim=2)
+    _need(latents, "latents", x.dtype, 2)
+    _need(w1, "w1", x.dtype, 2)
+    _need(w2, "w2", x.dtype, 2)
+    _need(gates, "gates", x.dtype)
+    n, d = x.shape
+    E, dl = latents.shape
+    dh = w1.shape[0]
+    if w1.shape != (dh, dl) or w2.shape != (2 * d, dh) or gates.numel() != n * n_heads * top_k:
+        raise RuntimeError("expert_forward: inconsistent shapes")
+    if wut is not None:
+        _need(wut, "wut", x.dtype, 2)
+        if wut.shape != (dh, d):
+            raise RuntimeError("expert_forward: wut must be [d_hidden, d_model]")
+    code = dtype_code(x.dtype)
+    order = 1 if hidden_space else 0
+    max_u = seg["max_unique"]
+    ws, ws_bytes = workspace(load().ethos_expert_forward_workspace_bytes(n, n_heads, top_k, max_u, d, dh, code, order),
+                             x.device)
+    h = torch.empty((max_u, dh), dtype=x.dtype, device=x.device)
+    out = torch.empty_like(x)
+    rc = load().ethos_expert_forward(x.data_ptr(), latents.data_ptr(), E, w1.data_ptr(), w2.data_ptr(),
+                                     wut.data_ptr() if wut is not None else None, seg["uniq"].data_ptr(),
+                                     seg["n_unique"].data_ptr(), max_u, seg["perm"].data_ptr(),
+                                     seg["sorted_slot"].data_ptr(), seg["pair_slot"].data_ptr(), gates.data_ptr(), n,
+                                     n_heads, top_k, dl, dh, d, code, order, ws.data_ptr(), ws_bytes, h.data_ptr(),
+                                     out.data_ptr(), _stream())
+    check(rc, "ethos_expert_forward")
+    return out, h
 
 
 def expert_backward(h: torch.Tensor, xp: torch.Tensor, dyb: torch.Tensor, pair_slot: torch.Tensor, gates: torch.Tensor,

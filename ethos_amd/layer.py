@@ -90,7 +90,7 @@ class _ExpertStages(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, gate_path, latents_w, w1_w, w2_w, layer, gates_exact, seg):
         out, h = layer._expert_stages(x, gates_exact, seg)
-        latents, w1, w2 = layer._generator_params(x.dtype, x.device)
+        latents, w1, w2, _ = layer._generator_params(x.dtype, x.device)
         ctx.save_for_backward(x, gates_exact, h, seg["uniq"], seg["pair_slot"], seg["n_unique"], latents, w1, w2)
         ctx.heads, ctx.top_k = layer.num_heads, layer.top_k
         ctx.param_dtypes = (latents_w.dtype, w1_w.dtype, w2_w.dtype)
@@ -303,31 +303,26 @@ class EthosExpertLayer(nn.Module):
         self._gen = None
 
     def _generator_params(self, dtype, device):
+        """(latents, W1, W2, W_u^T): the generator weights in the layer dtype on the device,
+        and (bf16) the transpose of W2's first d_model rows, cached until a weight changes."""
         ps = (self.expert_latents.weight, self.generation_network.net[0].weight, self.generation_network.net[2].weight)
         key = (dtype, device, tuple((p.data_ptr(), p._version) for p in ps))
         if key != self._gen_key:
             if all(p.dtype == dtype and p.device == device and p.is_contiguous() for p in ps):
-                self._gen = tuple(p.detach() for p in ps)
+                gen = tuple(p.detach() for p in ps)
             else:
-                self._gen = tuple(p.detach().to(device=device, dtype=dtype).contiguous() for p in ps)
+                gen = tuple(p.detach().to(device=device, dtype=dtype).contiguous() for p in ps)
+            wut = gen[2][: self.d_model].t().contiguous() if dtype == torch.bfloat16 else None
+            self._gen = gen + (wut,)
             self._gen_key = key
         return self._gen
 
-    def _expert_stages(self, x_flat: torch.Tensor, gates: torch.Tensor, seg: dict, mark=None):
-        """(out, h): generation over the unique experts, then apply + scatter-back in the
-        layer's execution order."""
-        latents, w1, w2 = self._generator_params(x_flat.dtype, x_flat.device)
-        h, v = hip.generate(latents, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2,
-                            with_v=not self.hidden_space)
-        if mark is not None:
-            mark("generate")
-        if self.hidden_space:
-            out = hip.apply_hidden(x_flat, w2, h, seg, gates, self.num_heads, self.top_k)
-        else:
-            out = hip.apply_scatter(x_flat, w2, h, v, seg, gates, self.num_heads, self.top_k)
-        if mark is not None:
-            mark("apply_scatter")
-        return out, h
+    def _expert_stages(self, x_flat: torch.Tensor, gates: torch.Tensor, seg: dict):
+        """(out, h): generation over the unique experts, activations and scatter-back in the
+        layer's execution order, as one library call."""
+        latents, w1, w2, wut = self._generator_params(x_flat.dtype, x_flat.device)
+        return hip.expert_forward(x_flat, latents, w1, w2, seg, gates, self.num_heads, self.top_k,
+                                  hidden_space=self.hidden_space, wut=wut)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.dim() != 3 or x.shape[-1] != self.d_model:
@@ -340,7 +335,9 @@ class EthosExpertLayer(nn.Module):
 
     def forward_flat(self, x_flat: torch.Tensor, mark=None) -> torch.Tensor:
         """The layer on [n_tok, d_model] rows (model.py:288-343).  `mark(stage)`, if given, is
-        called after each of the five stages is enqueued on the current stream."""
+        called after the query projection, the routing and the sort are enqueued on the
+        current stream (the expert stages are one library call; hip.stage_events times the
+        stages inside it)."""
         if _wants_grad(x_flat, self):
             with torch.no_grad():
                 gates, ids = self.router.route(x_flat)
@@ -353,7 +350,7 @@ class EthosExpertLayer(nn.Module):
             seg = hip.sort_segment(ids.view(-1), self.num_experts)
             if mark is not None:
                 mark("sort_segment")
-            out, _ = self._expert_stages(x_flat, gates, seg, mark)
+            out, _ = self._expert_stages(x_flat, gates, seg)
         return out
 
 

@@ -13,6 +13,7 @@
  *   ethos_generate       hypernetwork expert generation over the unique experts
  *   ethos_apply_scatter  per-pair activation and weighted scatter-back into tokens
  *   ethos_apply_hidden   the same, by hidden-space reordering (no v rows)
+ *   ethos_expert_forward generation + apply + scatter-back in one call (either order)
  *   ethos_expert_backward  per-pair part of the expert stages' backward
  *
  * Conventions (every entry point):
@@ -38,7 +39,7 @@
 extern "C" {
 #endif
 
-#define ETHOS_ABI_VERSION 2
+#define ETHOS_ABI_VERSION 3
 
 #define ETHOS_F32 0
 #define ETHOS_BF16 1
@@ -49,6 +50,16 @@ extern "C" {
 #define ETHOS_EALIGN (-4)       /* a pointer is not 16-byte aligned */
 #define ETHOS_EWORKSPACE (-5)   /* workspace too small */
 #define ETHOS_EUNSUPPORTED (-6) /* valid for the reference, outside this build's limits */
+
+/*
+ * Instrumentation, no counterpart in the reference: hand the calling thread a list of
+ * n_events (<= 16) HIP events (hipEvent_t).  Later calls on this thread record them, in
+ * order, on their stream at stage boundaries, until the list is used up; n_events = 0
+ * clears it.  ethos_expert_forward records five per call: after the token projection, the
+ * hidden rows, the activations, the v rows and the scatter-back.  Lets a caller time the
+ * stages inside one call with events on the launch stream.
+ */
+int ethos_stage_events(void* const* events, int32_t n_events);
 
 /* Message for the calling thread's last failed call ("" after a success). */
 const char* ethos_last_error(void);
@@ -186,6 +197,36 @@ int ethos_apply_scatter(const void* x, const void* w2, const void* h, const void
                         const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores, int64_t n_tok,
                         int32_t n_heads, int32_t top_k, int32_t d_model, int32_t d_hidden, int32_t dtype,
                         void* workspace, size_t workspace_bytes, void* out, void* stream);
+
+/* Workspace size for ethos_expert_forward (order 0: layer order, 1: hidden-space order). */
+size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int64_t max_unique,
+                                            int32_t d_model, int32_t d_hidden, int32_t dtype, int32_t order);
+
+/*
+ * The expert stages of one layer call in one entry point: generation over the unique
+ * experts, per-pair activation and weighted scatter-back, on the sorted pairs from
+ * ethos_sort_segment.  Replaces the pair loop of model.py:306-341 with the generator of
+ * model.py:168-179 (weights read at model.py:297-300) -- the work of ethos_generate
+ * followed by ethos_apply_scatter (order 0) or ethos_apply_hidden (order 1), with the same
+ * results, scheduled so that the activations read the hidden rows right after they are
+ * written.
+ *   x, scores, perm, sorted_slot, pair_slot, n_tok, n_heads, top_k   as for ethos_apply_scatter
+ *   latents, n_experts, uniq_ids, n_unique, max_unique, w1, w2       as for ethos_generate
+ *   wut       bf16 only, may be NULL: W_u^T [d_hidden, d_model] (the transpose of the first
+ *             d_model rows of w2) prepared by the caller, e.g. once per weight version;
+ *             NULL transposes it into the workspace on every call
+ *   workspace >= ethos_expert_forward_workspace_bytes(...) bytes (scratch)
+ *   h_out     [max_unique, d_hidden] dtype T: the hidden rows (rows u < U written)
+ *   out       [n_tok, d_model] dtype T
+ * Limits: those of ethos_generate and ethos_apply_scatter; x, w1, w2, wut, workspace, h_out
+ * and out 16-byte aligned.
+ */
+int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
+                         const void* wut, const int32_t* uniq_ids, const int32_t* n_unique, int64_t max_unique,
+                         const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores,
+                         int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_latent, int32_t d_hidden,
+                         int32_t d_model, int32_t dtype, int32_t order, void* workspace, size_t workspace_bytes,
+                         void* h_out, void* out, void* stream);
 
 /* Workspace size for ethos_apply_hidden. */
 size_t ethos_apply_hidden_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_model,

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ethos_abi_version() == 2
+    assert _lib.load().ethos_abi_version() == 3
 
 
 def _rc(fn, *args):
@@ -104,3 +104,31 @@ def test_sort_noalloc_rejects_pairs_beyond_its_static_workspace():
     assert L.ethos_sort_segment_noalloc(None, 100, 262144, 16, 16, 16, 16, 16, 16, None) == -3
     # the static array covers the library's own workspace formula at the limit
     assert L.ethos_sort_workspace_bytes(_lib.NOALLOC_MAX_PAIRS, 262144) <= 20 * 2 ** 20
+
+
+def test_expert_forward_argument_errors():
+    L = _lib.load()
+    args = [16, 16, 256, 16, 16, None, 16, 16, 64, 16, 16, 16, 16, 48, 2, 4, 16, 32, 64]
+    ws = L.ethos_expert_forward_workspace_bytes(48, 2, 4, 64, 64, 32, 1, 0)
+    assert ws > 48 * 32 * 2 + 64 * 64 * 2
+    assert L.ethos_expert_forward_workspace_bytes(48, 2, 4, 64, 64, 32, 1, 1) != ws
+    # unknown dtype, bad order, unsupported d_latent, null pointer, small workspace, misaligned
+    assert L.ethos_expert_forward(*args, 7, 0, 16, ws, 16, 16, None) == -1
+    assert L.ethos_expert_forward(*args, 1, 2, 16, ws, 16, 16, None) == -2
+    bad = list(args)
+    bad[16] = 10
+    assert L.ethos_expert_forward(*bad, 1, 0, 16, ws, 16, 16, None) == -6
+    assert L.ethos_expert_forward(*args, 1, 0, None, ws, 16, 16, None) == -3
+    assert L.ethos_expert_forward(*args, 1, 0, 16, 8, 16, 16, None) == -5
+    assert L.ethos_expert_forward(*args, 1, 0, 16, ws, 18, 16, None) == -4
+    # an empty batch is a no-op success
+    empty = list(args)
+    empty[13] = 0
+    assert L.ethos_expert_forward(*empty, 1, 0, None, 0, None, None, None) == 0
+
+
+def test_stage_events_argument_errors():
+    L = _lib.load()
+    assert L.ethos_stage_events(None, 17) == -2
+    assert L.ethos_stage_events(None, 2) == -2
+    assert L.ethos_stage_events(None, 0) == 0

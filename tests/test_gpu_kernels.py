@@ -416,3 +416,55 @@ def test_apply_hidden_shapes(n_tok, d, dh, dt):
     ref = O.apply_hidden(xp, O.to_f32(h, dt)[:U], w2, to_host(seg["pair_slot"]), g, H, k, dt)
     got = O.to_f32(to_host(out), dt)
     check_out(got, ref, dt, signal=True, nerr_max=2e-3)
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_fp32", "cfg1", "cfg3", "cfg2"])
+@pytest.mark.parametrize("hidden_space", [False, True])
+def test_expert_forward_matches_separate_calls(name, hidden_space):
+    """ethos_expert_forward (one call, activations between the generator's kernels, W_u^T
+    from the caller for bf16) against ethos_generate followed by ethos_apply_scatter /
+    ethos_apply_hidden: bit-identical outputs and hidden rows."""
+    sh, x, P = _setup(name, signal=True)
+    q = O.query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype)
+    gates, ids = O.route(q, P["K1"], P["K2"], sh.top_k, sh.dtype)
+    seg = hip.sort_segment(to_dev(ids.reshape(-1)), sh.num_experts)
+    xd, lat, w1, w2, g = (to_dev(a) for a in (x, P["latents"], P["W1"], P["W2"], gates))
+    h, v = hip.generate(lat, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2, with_v=not hidden_space)
+    if hidden_space:
+        want = hip.apply_hidden(xd, w2, h, seg, g, sh.num_heads, sh.top_k)
+    else:
+        want = hip.apply_scatter(xd, w2, h, v, seg, g, sh.num_heads, sh.top_k)
+    wut = w2[: sh.d_model].t().contiguous() if sh.dtype == "bf16" else None
+    got, h2 = hip.expert_forward(xd, lat, w1, w2, seg, g, sh.num_heads, sh.top_k, hidden_space=hidden_space, wut=wut)
+    got_nowut, _ = hip.expert_forward(xd, lat, w1, w2, seg, g, sh.num_heads, sh.top_k, hidden_space=hidden_space)
+    torch.cuda.synchronize()
+    U = int(seg["n_unique"].item())
+    assert np.array_equal(to_host(h2)[:U], to_host(h)[:U])
+    assert np.array_equal(to_host(got), to_host(want))
+    assert np.array_equal(to_host(got_nowut), to_host(want))
+
+
+def test_stage_events_recorded_in_expert_forward():
+    """Five events per ethos_expert_forward call, recorded in order on the launch stream."""
+    sh, x, P = _setup("cfg3", signal=True)
+    q = O.query_proj(x, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype)
+    gates, ids = O.route(q, P["K1"], P["K2"], sh.top_k, sh.dtype)
+    seg = hip.sort_segment(to_dev(ids.reshape(-1)), sh.num_experts)
+    args = [to_dev(a) for a in (x, P["latents"], P["W1"], P["W2"])]
+    g = to_dev(gates)
+    start = torch.cuda.Event(enable_timing=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    for e in evs:
+        e.record()
+    torch.cuda.synchronize()
+    start.record()
+    hip.stage_events(evs)
+    hip.expert_forward(*args, seg, g, sh.num_heads, sh.top_k)
+    hip.stage_events([])
+    end = torch.cuda.Event(enable_timing=True)
+    end.record()
+    torch.cuda.synchronize()
+    marks = [start] + evs + [end]
+    gaps = [a.elapsed_time(b) for a, b in zip(marks, marks[1:])]
+    assert all(t >= 0 for t in gaps), gaps
+    assert sum(gaps[:-1]) > 0
