@@ -316,6 +316,176 @@ int launch_sort_empty(int32_t* seg_off, int32_t* n_unique, hipStream_t stream) {
     return (int)hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------
+// Small batches (n <= kSmallMax pairs): the whole reordering in one workgroup.  Each pair
+// becomes one 32-bit word, key << vb | pair index (vb bits for the index), so a stable LSD
+// radix sort of the key digits orders the words by (expert id, pair id) -- the order of
+// the multi-kernel path -- and carries the pair index along.  The words live in LDS (two
+// buffers).  The 64-word chunks are split evenly over 16 waves in order, and every pass
+// is: per-wave digit ranks by multisplit (as sort_downsweep), a scan of the per-wave digit
+// counts in (digit, wave) order, a scatter between the buffers.  Segmentation works chunk
+// by chunk: head flags as a ballot per chunk, a scan of the chunks' head counts, then
+// every output written with coalesced stores (pair_slot scattered by pair).
+// ---------------------------------------------------------------------------------
+constexpr int kSmallWaves = 16;
+constexpr int kSmallMax = 16384;
+constexpr int kSmallChunks = kSmallMax / 64;                 // 256
+constexpr int kSmallPer = kSmallChunks / kSmallWaves;        // chunks per wave at most
+
+__global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int32_t* __restrict__ ids, int n,
+                                                                      int key_bits_, int vb, int passes,
+                                                                      int32_t* __restrict__ perm,
+                                                                      int32_t* __restrict__ uniq,
+                                                                      int32_t* __restrict__ seg_off,
+                                                                      int32_t* __restrict__ pair_slot,
+                                                                      int32_t* __restrict__ sorted_slot,
+                                                                      int32_t* __restrict__ n_unique,
+                                                                      int32_t max_unique) {
+    __shared__ uint32_t buf[2][kSmallMax];
+    __shared__ uint16_t cnt[kSmallWaves][kRadix];  // per-wave digit counts, then bases (< 2^14)
+    __shared__ uint64_t cmask[kSmallChunks];       // head flags per chunk
+    __shared__ uint32_t cbase[kSmallChunks];       // heads before each chunk
+    __shared__ uint32_t wsum[kSmallWaves];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t kmax = (1u << key_bits_) - 1u;
+    const int n_chunks = (n + 63) / 64;
+    const int cpw = (n_chunks + kSmallWaves - 1) / kSmallWaves;  // chunks per wave (<= kSmallPer)
+    const int c0 = wave * cpw;
+    {
+        // all of the thread's ids in flight at once (one workgroup: latency, not bandwidth)
+        constexpr int kIn = kSmallMax / (kSmallWaves * 64);
+        uint32_t k[kIn];
+#pragma unroll
+        for (int j = 0; j < kIn; ++j) {
+            const int i = tid + j * kSmallWaves * 64;
+            k[j] = i < n ? (uint32_t)ids[i] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kIn; ++j) {
+            const int i = tid + j * kSmallWaves * 64;
+            const uint32_t kk = k[j] > kmax ? kmax : k[j];  // ids outside [0, 2^key_bits) (a caller error) stay in range
+            if (i < n) buf[0][i] = (kk << vb) | (uint32_t)i;
+        }
+    }
+    int cur = 0;
+    for (int p = 0; p < passes; ++p) {
+        const int shift = vb + kRadixBits * p;
+        for (int e = tid; e < kSmallWaves * kRadix; e += kSmallWaves * 64) cnt[e / kRadix][e % kRadix] = 0;
+        __syncthreads();
+        uint32_t word[kSmallPer], rank[kSmallPer];
+#pragma unroll
+        for (int j = 0; j < kSmallPer; ++j) {
+            const int idx = (c0 + j) * 64 + lane;
+            const bool v = j < cpw && idx < n;
+            word[j] = v ? buf[cur][idx] : 0u;
+            const uint32_t dg = (word[j] >> shift) & (kRadix - 1);
+            const uint64_t peers = peer_mask(dg, __ballot(v));
+            const uint32_t below = (uint32_t)__popcll(peers & lanemask_lt(lane));
+            uint32_t start = 0;
+            if (v) start = cnt[wave][dg];
+            __builtin_amdgcn_wave_barrier();
+            rank[j] = start + below;
+            if (v && lane == 63 - __clzll((long long)peers)) cnt[wave][dg] = (uint16_t)(start + __popcll(peers));
+            __builtin_amdgcn_wave_barrier();
+        }
+        __syncthreads();
+        // digit d (threads 0 .. 511): bases of (d, wave) in digit-major, wave-minor order
+        uint32_t tot = 0, inc = 0;
+        if (tid < kRadix) {
+#pragma unroll
+            for (int w = 0; w < kSmallWaves; ++w) tot += cnt[w][tid];
+            inc = tot;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t u = __shfl_up(inc, off, 64);
+                if (lane >= off) inc += u;
+            }
+            if (lane == 63) wsum[wave] = inc;
+        }
+        __syncthreads();
+        if (tid < kRadix) {
+            uint32_t run = inc - tot;
+#pragma unroll
+            for (int w = 0; w < kRadix / 64; ++w) run += w < wave ? wsum[w] : 0u;
+#pragma unroll
+            for (int w = 0; w < kSmallWaves; ++w) {
+                const uint32_t c = cnt[w][tid];
+                cnt[w][tid] = (uint16_t)run;
+                run += c;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kSmallPer; ++j) {
+            const int idx = (c0 + j) * 64 + lane;
+            if (j < cpw && idx < n) buf[cur ^ 1][cnt[wave][(word[j] >> shift) & (kRadix - 1)] + rank[j]] = word[j];
+        }
+        cur ^= 1;
+        __syncthreads();
+    }
+    // segments: head flags per chunk
+    const uint32_t* w_ = buf[cur];
+    for (int c = wave; c < n_chunks; c += kSmallWaves) {
+        const int i = c * 64 + lane;
+        const bool head = i < n && (i == 0 || (w_[i] >> vb) != (w_[i - 1] >> vb));
+        const uint64_t m = __ballot(head);
+        if (lane == 0) cmask[c] = m;
+    }
+    __syncthreads();
+    // heads before each chunk: one wave scans the chunk counts (4 per lane)
+    if (wave == 0) {
+        uint32_t v[kSmallChunks / 64], sum = 0;
+#pragma unroll
+        for (int j = 0; j < kSmallChunks / 64; ++j) {
+            const int c = lane * (kSmallChunks / 64) + j;
+            v[j] = c < n_chunks ? (uint32_t)__popcll(cmask[c]) : 0u;
+            sum += v[j];
+        }
+        uint32_t inc = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t u = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += u;
+        }
+        uint32_t run = inc - sum;
+#pragma unroll
+        for (int j = 0; j < kSmallChunks / 64; ++j) {
+            const int c = lane * (kSmallChunks / 64) + j;
+            if (c < kSmallChunks) cbase[c] = run;
+            run += v[j];
+        }
+        if (lane == 63) wsum[0] = inc;  // all heads
+    }
+    __syncthreads();
+    const int32_t u_all = (int32_t)wsum[0];
+    const int32_t u_clamped = u_all < max_unique ? u_all : max_unique;
+    const uint32_t imask = (1u << vb) - 1u;
+    for (int c = wave; c < n_chunks; c += kSmallWaves) {
+        const int i = c * 64 + lane;
+        if (i < n) {
+            const uint64_t m = cmask[c];
+            const uint32_t wd = w_[i];
+            // slot of position i: heads at positions <= i, minus one
+            const int32_t slot = (int32_t)(cbase[c] + (uint32_t)__popcll(m & (lanemask_lt(lane) | (1ull << lane)))) - 1;
+            if ((m >> lane) & 1ull) {
+                if (slot < max_unique) {
+                    uniq[slot] = (int32_t)(wd >> vb);
+                    seg_off[slot] = i;
+                }
+            }
+            const int32_t sc = slot < max_unique ? slot : max_unique - 1;
+            const int32_t pi = (int32_t)(wd & imask);
+            perm[i] = pi;
+            sorted_slot[i] = sc;
+            pair_slot[pi] = sc;
+        }
+    }
+    if (tid == 0) {
+        *n_unique = u_clamped;
+        seg_off[u_clamped] = n;
+    }
+}
+
 static int key_bits(int64_t n_experts) {
     int b = 0;
     while (b < 32 && ((int64_t)1 << b) < n_experts) ++b;
@@ -331,6 +501,16 @@ size_t sort_workspace_bytes(int64_t n) {
 int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,
                         int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
                         hipStream_t stream) {
+    const int bits = key_bits(n_experts);
+    const int passes = bits <= kRadixBits ? 1 : (bits + kRadixBits - 1) / kRadixBits;
+    int vb = 0;
+    while (vb < 31 && ((int64_t)1 << vb) < n) ++vb;
+    if (n <= kSmallMax && bits + vb <= 32) {
+        hipLaunchKernelGGL(sort_small_kernel, dim3(1), dim3(kSmallWaves * 64), 0, stream, ids, (int)n, bits, vb,
+                           passes, perm, uniq, seg_off, pair_slot, sorted_slot, n_unique,
+                           (int32_t)(n < n_experts ? n : n_experts));
+        return (int)hipGetLastError();
+    }
     const int n_tiles = (int)((n + kSortTile - 1) / kSortTile);
     uint32_t* w = reinterpret_cast<uint32_t*>(ws);
     uint32_t* kbuf[2] = {w, w + n};
@@ -338,8 +518,6 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
     uint32_t* hist = w + 4 * n;
     uint32_t* total = hist + (size_t)kRadix * n_tiles;
     uint32_t* tcnt = total + kRadix;
-    const int bits = key_bits(n_experts);
-    const int passes = bits <= kRadixBits ? 1 : (bits + kRadixBits - 1) / kRadixBits;
     hipError_t err;
     for (int p = 0; p < passes; ++p) {
         const uint32_t* kin = p == 0 ? reinterpret_cast<const uint32_t*>(ids) : kbuf[(p - 1) & 1];

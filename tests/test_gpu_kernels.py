@@ -81,7 +81,9 @@ def test_route_ties_break_to_lowest_index():
                                          (8192, 4096, "rand"), (70000, 262144, "rand"), (524288, 262144, "rand"),
                                          (30000, 262144, "same"), (50000, 262144, "skew"), (4097, 7, "rand"),
                                          (12345, 262144, "max"), (300000, 262144, "rand"),
-                                         (2000003, 262144, "rand")])
+                                         (2000003, 262144, "rand"), (16384, 262144, "skew"),
+                                         (16385, 262144, "skew"), (16384, 7, "rand"), (2, 262144, "same"),
+                                         (8192, 262144, "max")])
 def test_sort_segment_exact(n, E, pattern):
     rng = np.random.default_rng(n + E)
     if pattern == "same":
