@@ -63,7 +63,8 @@ template <> struct Elem<uint16_t> {
     __device__ __forceinline__ static double to_f64(uint16_t v) { return (double)bf16_bits_to_f32(v); }
     __device__ __forceinline__ static uint16_t from_f32(float v) { return f32_to_bf16_bits(v); }
     __device__ __forceinline__ static uint16_t from_f64(double v) { return f32_to_bf16_bits(f64_to_f32_odd(v)); }
-    __device__ __forceinline__ static float round32(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+    // through the hardware conversion (round to nearest even), as round32x2
+    __device__ __forceinline__ static float round32(float v) { return __uint_as_float(pack_bf16x2(v, v) << 16); }
     // two values at once through the hardware conversion (round to nearest even)
     __device__ __forceinline__ static void round32x2(float& a, float& b);
     __device__ __forceinline__ static float round64(double v) { return bf16_bits_to_f32(from_f64(v)); }
@@ -205,6 +206,14 @@ __device__ __forceinline__ uint32_t gelu_bf16x2_lut(uint32_t pk, uint32_t lut_by
 
 // ---------------------------------------------------------------- wave reductions (DPP)
 // dpp_ctrl encodings (GCN/CDNA DPP): quad_perm, row_half_mirror, row_mirror.
+// Lane mask of a predicate: the compare writes the scalar mask directly (HIP's __ballot
+// takes an int and adds a select and a second compare).
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+// Number of set bits of m below the calling lane (v_mbcnt).
+__device__ __forceinline__ int count_below(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 constexpr int kDppXor1 = 0xb1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4e;        // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;

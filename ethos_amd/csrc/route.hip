@@ -36,8 +36,11 @@
 namespace ethos {
 
 constexpr int kRtWaves = 8;                            // two workgroups per CU: four waves per SIMD
-constexpr int kRtRows = 32;                            // rows per workgroup (one MFMA row block)
-constexpr int kRtRowsPerWave = kRtRows / kRtWaves;
+constexpr int kRtRows = 32;                            // rows of the MFMA tile (and LDS row slots)
+// rows per wave: 4 (32 rows per workgroup) for large batches; 1 (8 rows per workgroup,
+// the MFMA tile's other rows zero) for small ones, which spreads them over 4x as many
+// workgroups and cuts each wave's sequential work by 4
+constexpr int kRtSmallRows = 4096;                     // batches up to this many rows take 1 row per wave
 constexpr int kRtMaxKc = 32;                           // k_cand <= 32, top_k <= 32
 constexpr int kRtMaxK = 512;                           // sub-keys per table
 constexpr int kRtSlots = kRtMaxK / kWave;              // approximate scores per lane per row
@@ -51,31 +54,34 @@ __device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
     return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
-// v of lane (lane ^ mask), mask a compile-time constant after inlining: DPP quad
-// permutes for 1 and 2, ds_swizzle (xor mode, within 32 lanes) up to 31, and
-// v_permlane32_swap for the half-wave exchange; no LDS addressing.
+// v of lane (lane ^ mask), mask a compile-time constant after inlining, with VALU lane
+// exchanges only (no LDS round trip): DPP quad permutes for 1 and 2, a half-row mirror
+// (lane ^ 7) or row mirror (lane ^ 15) composed with a second DPP move for 4 and 8,
+// v_permlane16_swap for 16 and v_permlane32_swap for 32.
 template <int kCtrl>
 __device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {  // every lane reads: no "old" operand
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kCtrl, 0xf, 0xf, true);
 }
+constexpr int kDppXor3 = 0x1b;  // quad_perm [3,2,1,0]
 
 __device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v, int mask) {
-    if (mask == 1) return dpp_mov<kDppXor1>(v);
-    if (mask == 2) return dpp_mov<kDppXor2>(v);
     uint32_t r = v;
     if (mask & 32) {
         const auto sw = __builtin_amdgcn_permlane32_swap(r, r, false, false);
         r = (__lane_id() & 32) ? sw[0] : sw[1];
     }
-    switch (mask & 31) {
+    if (mask & 16) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(r, r, false, false);
+        r = (__lane_id() & 16) ? sw[0] : sw[1];
+    }
+    switch (mask & 15) {
         case 0: break;
         case 1: r = dpp_mov<kDppXor1>(r); break;
         case 2: r = dpp_mov<kDppXor2>(r); break;
-        case 4: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (4 << 10) | 0x1f); break;
-        case 8: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (8 << 10) | 0x1f); break;
-        case 16: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (16 << 10) | 0x1f); break;
-        case 31: r = (uint32_t)__builtin_amdgcn_ds_swizzle((int)r, (31 << 10) | 0x1f); break;
-        default: r = (uint32_t)__shfl_xor((int)r, mask & 31, kWave); break;
+        case 4: r = dpp_mov<kDppXor3>(dpp_mov<kDppRowHalfMirror>(r)); break;  // (l ^ 7) ^ 3
+        case 8: r = dpp_mov<kDppRowHalfMirror>(dpp_mov<kDppRowMirror>(r)); break;  // (l ^ 15) ^ 7
+        case 15: r = dpp_mov<kDppRowMirror>(r); break;
+        default: r = (uint32_t)__shfl_xor((int)r, mask & 15, kWave); break;
     }
     return r;
 }
@@ -96,19 +102,73 @@ __device__ __forceinline__ uint32_t shfl_xor_v<uint32_t>(uint32_t v, int mask) {
     return xor_lane_u32(v, mask);
 }
 
+// Lanes of a bitonic stage (partner distance j, block size k) that keep the larger of
+// their own and their partner's value: (lane & j) == 0 exactly when (lane & k) == 0.  A
+// compile-time constant after unrolling.
+__host__ __device__ constexpr uint64_t bitonic_keep_max(int j, int k) {
+    uint64_t m = 0;
+    for (int l = 0; l < 64; ++l)
+        if (((l & j) == 0) == ((l & k) == 0)) m |= 1ull << l;
+    return m;
+}
+
+// Per-lane select by a wave-uniform lane mask: lane l gets t if bit l of m is set, else f.
+__device__ __forceinline__ uint32_t select_by_mask(uint32_t f, uint32_t t, uint64_t m) {
+    uint32_t r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(f), "v"(t), "s"(m));
+    return r;
+}
+__device__ __forceinline__ uint64_t select_by_mask(uint64_t f, uint64_t t, uint64_t m) {
+    const uint32_t lo = select_by_mask((uint32_t)f, (uint32_t)t, m);
+    const uint32_t hi = select_by_mask((uint32_t)(f >> 32), (uint32_t)(t >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// One compare-exchange stage: every lane takes its partner's value p when p is larger
+// and the lane keeps the maximum, or when p is not larger and it keeps the minimum;
+// the comparison mask and the constant keep mask combine in scalar registers.
+// For partner distance 16 or 32 one v_permlane{16,32}_swap of v with itself leaves every
+// lane holding its own and its partner's value, in an order that differs between lanes;
+// keeping the larger or smaller of the two is symmetric, so the order does not matter.
+template <int kJ>
+__device__ __forceinline__ void swap_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+    if constexpr (kJ == 16) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        a = sw[0];
+        b = sw[1];
+    } else {
+        const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        a = sw[0];
+        b = sw[1];
+    }
+}
+template <int kJ>
+__device__ __forceinline__ void swap_pair(uint64_t v, uint64_t& a, uint64_t& b) {
+    uint32_t al, bl, ah, bh;
+    swap_pair<kJ>((uint32_t)v, al, bl);
+    swap_pair<kJ>((uint32_t)(v >> 32), ah, bh);
+    a = ((uint64_t)ah << 32) | al;
+    b = ((uint64_t)bh << 32) | bl;
+}
+
+template <typename V>
+__device__ __forceinline__ V bitonic_stage(V v, int j, uint64_t keep_max) {
+    if (j == 16 || j == 32) {
+        V a, b;
+        if (j == 16) swap_pair<16>(v, a, b);
+        else swap_pair<32>(v, a, b);
+        return select_by_mask(b, a, ~(ballot(a > b) ^ keep_max));
+    }
+    const V p = shfl_xor_v<V>(v, j);
+    return select_by_mask(v, p, ~(ballot(p > v) ^ keep_max));
+}
+
 template <typename V>
 __device__ __forceinline__ V wave_sort_desc(V v, int lane) {
 #pragma unroll
     for (int k = 2; k <= kWave; k <<= 1) {
 #pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const V p = shfl_xor_v<V>(v, j);
-            const bool desc = (lane & k) == 0;
-            const bool lower = (lane & j) == 0;
-            const bool keep_max = lower == desc;
-            // take the partner's value when it is larger (keep_max) or not larger
-            v = (p > v) == keep_max ? p : v;
-        }
+        for (int j = k >> 1; j > 0; j >>= 1) v = bitonic_stage<V>(v, j, bitonic_keep_max(j, k));
     }
     return v;
 }
@@ -117,14 +177,32 @@ __device__ __forceinline__ V wave_sort_desc(V v, int lane) {
 // of their union, sorted descending.
 __device__ __forceinline__ uint64_t wave_merge_desc(uint64_t run, uint64_t chunk, int lane) {
     const uint64_t rev = shfl_xor_u64(chunk, kWave - 1);  // chunk[63 - lane]
-    uint64_t v = run > rev ? run : rev;                    // bitonic top-64
+    uint64_t v = select_by_mask(rev, run, ballot(run > rev));  // bitonic top-64
 #pragma unroll
-    for (int j = kWave >> 1; j > 0; j >>= 1) {
-        const uint64_t p = shfl_xor_u64(v, j);
-        const bool lower = (lane & j) == 0;
-        v = (p > v) == lower ? p : v;
-    }
+    for (int j = kWave >> 1; j > 0; j >>= 1) v = bitonic_stage<uint64_t>(v, j, bitonic_keep_max(j, 2 * kWave));
     return v;
+}
+
+// 32-bit form of a canonical key whose score is a bf16 value and whose index is below
+// 2^16: the upper 16 bits of ord32(score) (its lower 16 bits are all zero or all one
+// for such a score), then 0xffff - index.  Same order as the 64-bit key; 0 <-> 0 (no
+// key; a finite score never maps to 0).
+__device__ __forceinline__ uint32_t key32_of(uint64_t k) {
+    return k == 0ull ? 0u : ((uint32_t)(k >> 48) << 16) | (0xffffu - key_idx(k));
+}
+__device__ __forceinline__ uint64_t key64_of32(uint32_t k) {
+    if (k == 0u) return 0ull;
+    const uint32_t o16 = k >> 16;
+    const uint32_t o32 = (o16 << 16) | ((o16 & 0x8000u) ? 0u : 0xffffu);
+    return ((uint64_t)o32 << 32) | (uint64_t)(~(0xffffu - (k & 0xffffu)));
+}
+
+// Descending sort of one canonical key per lane; keys of bf16 scores sort in their
+// 32-bit form (half the lane exchanges).
+template <typename T>
+__device__ __forceinline__ uint64_t wave_sort_keys(uint64_t k, int lane) {
+    if constexpr (sizeof(T) == 2) return key64_of32(wave_sort_desc<uint32_t>(key32_of(k), lane));
+    else return wave_sort_desc<uint64_t>(k, lane);
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
@@ -142,7 +220,9 @@ template <typename T> struct KeyVec;
 template <> struct KeyVec<uint16_t> {
     static constexpr int kN = 8;
     __device__ __forceinline__ static void load(const uint16_t* p, double* d) {
-        const uint4 r = *reinterpret_cast<const uint4*>(p);
+        from_raw(*reinterpret_cast<const uint4*>(p), d);
+    }
+    __device__ __forceinline__ static void from_raw(const uint4 r, double* d) {
         const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -154,11 +234,13 @@ template <> struct KeyVec<uint16_t> {
 template <> struct KeyVec<float> {
     static constexpr int kN = 4;
     __device__ __forceinline__ static void load(const float* p, double* d) {
-        const float4 r = *reinterpret_cast<const float4*>(p);
-        d[0] = r.x;
-        d[1] = r.y;
-        d[2] = r.z;
-        d[3] = r.w;
+        from_raw(*reinterpret_cast<const uint4*>(p), d);
+    }
+    __device__ __forceinline__ static void from_raw(const uint4 r, double* d) {
+        d[0] = __uint_as_float(r.x);
+        d[1] = __uint_as_float(r.y);
+        d[2] = __uint_as_float(r.z);
+        d[3] = __uint_as_float(r.w);
     }
 };
 
@@ -194,11 +276,28 @@ __host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2, int elem_
 
 // Exact score key of sub-key j: the fp64 FMA chain over the query half qh (staged in
 // LDS) and key row j (global, L2-resident), index order, rounded once to T.
-template <typename T>
+// The key row's 16-byte vectors are loaded kG at a time ahead of their FMAs, so that
+// their L2 latencies overlap.
+template <typename T, int kG>
 __device__ __forceinline__ uint64_t exact_key(const T* qh, const T* __restrict__ keys, int dh2, int j) {
+    constexpr int kN = KeyVec<T>::kN;
     const T* kr = keys + (int64_t)j * dh2;
     double acc = 0.0;
-    for (int i = 0; i < dh2; i += KeyVec<T>::kN) {
+    int i0 = 0;
+    for (; i0 + kG * kN <= dh2; i0 += kG * kN) {
+        uint4 raw[kG];
+#pragma unroll
+        for (int g = 0; g < kG; ++g) raw[g] = *reinterpret_cast<const uint4*>(kr + i0 + g * kN);
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+            double qv[kN], kv[kN];
+            KeyVec<T>::load(qh + i0 + g * kN, qv);
+            KeyVec<T>::from_raw(raw[g], kv);
+#pragma unroll
+            for (int t = 0; t < kN; ++t) acc = fma(qv[t], kv[t], acc);
+        }
+    }
+    for (int i = i0; i < dh2; i += kN) {
         double qv[KeyVec<T>::kN], kv[KeyVec<T>::kN];
         KeyVec<T>::load(qh + i, qv);
         KeyVec<T>::load(kr + i, kv);
@@ -212,7 +311,7 @@ __device__ __forceinline__ uint64_t exact_key(const T* qh, const T* __restrict__
 // when the slot still needs the exact chain.
 constexpr uint32_t kRtPending = 0xffffffffu;
 
-template <typename T>
+template <typename T, int RPW>
 __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
                                                     const T* __restrict__ keys2, const float* __restrict__ key_norms,
                                                     int64_t rows, int dq, int K, int top_k, int kc,
@@ -229,11 +328,14 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
     float* kn = reinterpret_cast<float*>(smem + L.kn_off);
     // lst[rr][half]: the canonical top-k_cand list of this wave's row rr and query half,
     // entry i held by lane i
-    uint64_t lst[kRtRowsPerWave][2];
+    constexpr int kRowsWG = kRtWaves * RPW;  // rows of this workgroup (<= kRtRows)
+    // key vectors in flight per exact chain (one row per wave leaves registers for more)
+    constexpr int kExG = RPW == 1 ? 8 : 2;
+    uint64_t lst[RPW][2];
 #pragma unroll
-    for (int rr = 0; rr < kRtRowsPerWave; ++rr) lst[rr][0] = lst[rr][1] = 0;
+    for (int rr = 0; rr < RPW; ++rr) lst[rr][0] = lst[rr][1] = 0;
 
-    const int64_t row0 = (int64_t)blockIdx.x * kRtRows;
+    const int64_t row0 = (int64_t)blockIdx.x * kRowsWG;
     const int nkb = kpad / 32;
     const float gamma = (float)(dh2 + 16) * 0x1p-22f * 1.01f;
 
@@ -257,24 +359,54 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         kn[e] = nrm;
     }
 
+    const int qs_ld = L.qs_pitch / (int)sizeof(T);  // staged query row pitch (elements)
     for (int half = 0; half < 2; ++half) {
         const T* keys = half ? keys2 : keys1;
+        // 0. stage the query halves of the tile's rows in LDS, one 16-byte vector per
+        //    thread and step; rows past the batch or past this workgroup's rows are zero
+        {
+            constexpr int kV = 16 / (int)sizeof(T);
+            const int vpr = dh2 / kV;
+            for (int e = tid; e < kRtRows * vpr; e += kRtWaves * 64) {
+                const int lr = e / vpr, c = e - lr * vpr;
+                const int64_t r = row0 + lr;
+                uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                if (lr < kRowsWG && r < rows) v = *reinterpret_cast<const uint4*>(q + r * dq + half * dh2 + c * kV);
+                *reinterpret_cast<uint4*>(smem + L.qs_off + (size_t)lr * L.qs_pitch + (size_t)c * 16) = v;
+            }
+        }
+        __syncthreads();
+        const T* qtile = reinterpret_cast<const T*>(smem + L.qs_off);
+
         // 1. approximate scores for the 32-row tile: wave w takes key blocks w, w + 8, ...
+        //    The key fragments of kU reduction steps are loaded before their MFMAs, so
+        //    their L2 latencies overlap.
+        constexpr int kU = sizeof(T) == 2 ? (RPW == 1 ? 4 : 1) : (RPW == 1 ? 16 : 8);
         for (int kb0 = wave; kb0 < nkb; kb0 += 2 * kRtWaves) {
             f32x16_t acc[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c) acc[c] = f32x16_zero();
-            const int64_t arow = row0 + lrow;
-            for (int k0 = 0; k0 < dh2; k0 += M::kK) {
-                const typename M::frag a = arow < rows ? M::load(q + arow * dq + half * dh2 + k0 + lk) : M::zero();
+            for (int k0 = 0; k0 < dh2; k0 += kU * M::kK) {
+                typename M::frag a[kU], b[2][kU];
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const int kb = kb0 + kRtWaves * c;
-                    if (kb < nkb) {
-                        const int j = kb * 32 + lrow;
-                        const typename M::frag b = j < K ? M::load(keys + (int64_t)j * dh2 + k0 + lk) : M::zero();
-                        acc[c] = M::mma(a, b, acc[c]);
+                for (int u = 0; u < kU; ++u) {
+                    const int kk = k0 + u * M::kK;
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const int j = (kb0 + kRtWaves * c) * 32 + lrow;
+                        b[c][u] = kk < dh2 && j < K ? M::load(keys + (int64_t)j * dh2 + kk + lk) : M::zero();
                     }
+                }
+#pragma unroll
+                for (int u = 0; u < kU; ++u) {
+                    const int kk = k0 + u * M::kK;
+                    a[u] = kk < dh2 ? M::load(qtile + lrow * qs_ld + kk + lk) : M::zero();
+                }
+#pragma unroll
+                for (int u = 0; u < kU; ++u) {
+#pragma unroll
+                    for (int c = 0; c < 2; ++c)
+                        if (kb0 + kRtWaves * c < nkb) acc[c] = M::mma(a[u], b[c][u], acc[c]);
                 }
             }
 #pragma unroll
@@ -297,29 +429,28 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         //    exactly in full in step 4.
         // zero for every row slot, including the slots past the last row of a partial
         // tile (the loop below stops at that row, and step 3 sums all of n_pend)
-        int n_cand[kRtRowsPerWave], n_pend[kRtRowsPerWave];
+        int n_cand[RPW], n_pend[RPW];
 #pragma unroll
-        for (int rr = 0; rr < kRtRowsPerWave; ++rr) n_cand[rr] = n_pend[rr] = 0;
+        for (int rr = 0; rr < RPW; ++rr) n_cand[rr] = n_pend[rr] = 0;
         uint32_t slow_rows = 0;
-        const uint64_t below = (1ull << lane) - 1ull;
 #pragma unroll
-        for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
-            const int lr = wave * kRtRowsPerWave + rr;
+        for (int rr = 0; rr < RPW; ++rr) {
+            const int lr = wave * RPW + rr;
             const int64_t r = row0 + lr;
             if (r >= rows) break;
-            // stage the query half in LDS (16 bytes per lane) and bound its norm
-            T* qs = reinterpret_cast<T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
+            // bound the norm of the staged query half
+            const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
             float sq = 0.0f;
             for (int i = lane * KeyVec<T>::kN; i < dh2; i += kWave * KeyVec<T>::kN) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(q + r * dq + half * dh2 + i);
-                *reinterpret_cast<uint4*>(qs + i) = raw;
                 double v[KeyVec<T>::kN];
                 KeyVec<T>::load(qs + i, v);
 #pragma unroll
                 for (int t = 0; t < KeyVec<T>::kN; ++t) sq = __builtin_fmaf((float)v[t], (float)v[t], sq);
             }
-            const float qn = sqrtf(wave_sum(sq)) * (1.0f + 0x1p-12f);
+            // (v_sqrt_f32 is within 1 ulp for a normal argument; the offset keeps it normal)
+            const float qn = __builtin_amdgcn_sqrtf(wave_sum(sq) + 0x1p-100f) * (1.0f + 0x1p-12f);
 
+            const float gq = gamma * qn;
             // up: upper bounds of the scores (filter); cs: certified scores or kRtPending
             float up[kRtSlots];   // RN_T of the upper bounds
             uint32_t cs[kRtSlots];
@@ -332,7 +463,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
                 cs[m] = kRtPending;
                 if (j < K) {
                     const float sj = S[lr * pitch + j];
-                    const float marg = gamma * qn * kn[half * kpad + j] + fabsf(sj) * 0x1p-21f + 0x1p-120f;
+                    const float marg = __builtin_fmaf(fabsf(sj), 0x1p-21f, __builtin_fmaf(gq, kn[half * kpad + j], 0x1p-120f));
                     float lo_f = sj - marg, hi_f = sj + marg;
                     Elem<T>::round32x2(lo_f, hi_f);  // RN_T of both ends (rounding is monotone)
                     up[m] = hi_f;
@@ -351,7 +482,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
 #pragma unroll
             for (int b = 31; b >= 16; --b) {
                 const uint32_t cand_o = o | (1u << b);
-                if ((int)__popcll(__ballot(lkey >= cand_o)) >= kc) o = cand_o;
+                if ((int)__popcll(ballot(lkey >= cand_o)) >= kc) o = cand_o;
             }
             const float tau_s = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
             const float tau = tau_s - emax * (1.0f + 0x1p-20f) - fabsf(tau_s) * 0x1p-21f;
@@ -363,7 +494,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             for (int m = 0; m < kRtSlots; ++m) {
                 const bool f = lane + m * kWave < K && up[m] >= thr;
                 fbits |= (uint32_t)f << m;
-                n += (int)__popcll(__ballot(f));
+                n += (int)__popcll(ballot(f));
             }
             n_cand[rr] = n;
             // the row's scores are in registers now: its LDS row holds the candidates
@@ -374,8 +505,8 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
 #pragma unroll
                 for (int m = 0; m < kRtSlots; ++m) {
                     const bool f = (fbits >> m) & 1u;
-                    const uint64_t bal = __ballot(f);
-                    if (f) ck[pos + __popcll(bal & below)] = ((uint64_t)cs[m] << 32) | (uint32_t)(lane + m * kWave);
+                    const uint64_t bal = ballot(f);
+                    if (f) ck[pos + count_below(bal)] = ((uint64_t)cs[m] << 32) | (uint32_t)(lane + m * kWave);
                     pos += (int)__popcll(bal);
                 }
                 __builtin_amdgcn_wave_barrier();
@@ -384,9 +515,9 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
                 const uint64_t e = lane < n ? ck[lane] : 0ull;
                 const uint32_t sc = (uint32_t)(e >> 32), j = (uint32_t)e;
                 const bool pend = lane < n && sc == kRtPending;
-                const uint64_t bal = __ballot(pend);
+                const uint64_t bal = ballot(pend);
                 if (lane < n) {
-                    if (pend) reinterpret_cast<uint32_t*>(S + lr * pitch + kRtPendOff)[__popcll(bal & below)] = (j << 8) | (uint32_t)lane;
+                    if (pend) reinterpret_cast<uint32_t*>(S + lr * pitch + kRtPendOff)[count_below(bal)] = (j << 8) | (uint32_t)lane;
                     else ck[lane] = make_key(__uint_as_float(sc), j);
                 }
                 n_pend[rr] = (int)__popcll(bal);
@@ -396,8 +527,8 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
 #pragma unroll
                 for (int m = 0; m < kRtSlots; ++m) {
                     const bool f = (fbits >> m) & 1u;
-                    const uint64_t bal = __ballot(f);
-                    if (f) cand[pos + __popcll(bal & below)] = lane + m * kWave;
+                    const uint64_t bal = ballot(f);
+                    if (f) cand[pos + count_below(bal)] = lane + m * kWave;
                     pos += (int)__popcll(bal);
                 }
                 slow_rows |= 1u << rr;
@@ -408,25 +539,25 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         // 3. exact scores of the pending candidates of all the wave's rows, one per lane,
         //    written to their slots
         {
-            int p_end[kRtRowsPerWave];
+            int p_end[RPW];
             int nq = 0;
 #pragma unroll
-            for (int rr = 0; rr < kRtRowsPerWave; ++rr) p_end[rr] = (nq += n_pend[rr]);
+            for (int rr = 0; rr < RPW; ++rr) p_end[rr] = (nq += n_pend[rr]);
             for (int c0 = 0; c0 < nq; c0 += kWave) {
                 const int idx = c0 + lane;
                 if (idx < nq) {
                     int rr = 0, start = 0;
 #pragma unroll
-                    for (int t = 0; t < kRtRowsPerWave - 1; ++t) {
+                    for (int t = 0; t < RPW - 1; ++t) {
                         if (idx >= p_end[t]) {
                             rr = t + 1;
                             start = p_end[t];
                         }
                     }
-                    const int lr = wave * kRtRowsPerWave + rr;
+                    const int lr = wave * RPW + rr;
                     const uint32_t e = reinterpret_cast<const uint32_t*>(S + lr * pitch + kRtPendOff)[idx - start];
                     const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
-                    reinterpret_cast<uint64_t*>(S + lr * pitch)[e & 0xffu] = exact_key<T>(qs, keys, dh2, (int)(e >> 8));
+                    reinterpret_cast<uint64_t*>(S + lr * pitch)[e & 0xffu] = exact_key<T, kExG>(qs, keys, dh2, (int)(e >> 8));
                 }
             }
         }
@@ -434,21 +565,21 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
 
         // 4. canonical top-k_cand list of each row
 #pragma unroll
-        for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
-            const int lr = wave * kRtRowsPerWave + rr;
+        for (int rr = 0; rr < RPW; ++rr) {
+            const int lr = wave * RPW + rr;
             const int64_t r = row0 + lr;
             if (r >= rows) break;
             const int n = n_cand[rr];
             uint64_t run = 0;
             if (!((slow_rows >> rr) & 1u)) {
                 const uint64_t* ck = reinterpret_cast<const uint64_t*>(S + lr * pitch);
-                run = wave_sort_desc<uint64_t>(lane < n ? ck[lane] : 0ull, lane);
+                run = wave_sort_keys<T>(lane < n ? ck[lane] : 0ull, lane);
             } else {
                 const int32_t* cand = reinterpret_cast<const int32_t*>(S + lr * pitch);
                 const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
                 for (int c0 = 0; c0 < n; c0 += kWave) {
                     const int idx = c0 + lane;
-                    uint64_t key = idx < n ? exact_key<T>(qs, keys, dh2, cand[idx]) : 0ull;
+                    uint64_t key = idx < n ? exact_key<T, kExG>(qs, keys, dh2, cand[idx]) : 0ull;
                     key = wave_sort_desc<uint64_t>(key, lane);
                     run = c0 == 0 ? key : wave_merge_desc(run, key, lane);
                 }
@@ -467,27 +598,34 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
     // staircase, and an outside pair can enter the top-k only by tying theta (it may
     // win the tie on its expert id).  So: rank the staircase, then merge in the rare
     // outside pairs equal to theta.
+    // Staircase pair t of this lane: entry lane + 64 t of the list of (a, b), a-major, with
+    // b < nb(a) = min(top_k / (a + 1), kc).  nb(a) does not increase with a, so one
+    // wave-uniform pass finds it without divisions.
     int st_a[kRtStSlots], st_b[kRtStSlots];
 #pragma unroll
     for (int t = 0; t < kRtStSlots; ++t) {
-        int idx = lane + t * kWave, a = 0;
         st_a[t] = -1;
         st_b[t] = 0;
-        for (; a < kc; ++a) {
-            int nb = top_k / (a + 1);
-            nb = nb < kc ? nb : kc;
+    }
+    {
+        int nb = top_k < kc ? top_k : kc, cum = 0;
+        for (int a = 0; a < kc; ++a) {
+            while (nb > 0 && nb * (a + 1) > top_k) --nb;
             if (nb == 0) break;
-            if (idx < nb) {
-                st_a[t] = a;
-                st_b[t] = idx;
-                break;
+#pragma unroll
+            for (int t = 0; t < kRtStSlots; ++t) {
+                const int idx = lane + t * kWave;
+                if (idx >= cum && idx < cum + nb) {
+                    st_a[t] = a;
+                    st_b[t] = idx - cum;
+                }
             }
-            idx -= nb;
+            cum += nb;
         }
     }
 #pragma unroll
-    for (int rr = 0; rr < kRtRowsPerWave; ++rr) {
-        const int lr = wave * kRtRowsPerWave + rr;
+    for (int rr = 0; rr < RPW; ++rr) {
+        const int lr = wave * RPW + rr;
         const int64_t r = row0 + lr;
         if (r >= rows) break;
         const uint64_t L1 = lst[rr][0], L2 = lst[rr][1];
@@ -500,7 +638,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         uint64_t run = 0;
 #pragma unroll
         for (int t = 0; t < kRtStSlots; ++t) {
-            if (t > 0 && __ballot(st_a[t] >= 0) == 0) break;
+            if (t > 0 && ballot(st_a[t] >= 0) == 0) break;
             const uint64_t pk = pair_key(st_a[t] >= 0 ? st_a[t] : 0, st_b[t]);
             uint64_t key = st_a[t] >= 0 ? pk : 0ull;
             key = wave_sort_desc<uint64_t>(key, lane);
@@ -513,14 +651,14 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         Elem<T>::round32x2(ca, cb);
         const bool in_a = lane < kc && ca >= theta;
         const bool in_b = lane < kc && cb >= theta;
-        const int na = (int)__popcll(__ballot(in_a)), nb = (int)__popcll(__ballot(in_b));
+        const int na = (int)__popcll(ballot(in_a)), nb = (int)__popcll(ballot(in_b));
         for (int p0 = 0; p0 < na * nb; p0 += kWave) {
             const int p = p0 + lane;
             const bool in = p < na * nb;
             const int a = in ? p / nb : 0, b = in ? p - (p / nb) * nb : 0;
             uint64_t key = pair_key(a, b);
             const bool tie = in && (a + 1) * (b + 1) > top_k && key_score(key) == theta;
-            if (__ballot(tie) == 0) continue;
+            if (ballot(tie) == 0) continue;
             key = wave_sort_desc<uint64_t>(tie ? key : 0ull, lane);
             run = wave_merge_desc(run, key, lane);
         }
@@ -547,14 +685,26 @@ int launch_route(const void* q, const void* k1, const void* k2, const float* key
                  int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream) {
     const int dh2 = dq / 2;
     const size_t smem = route_smem_bytes(K, dh2, dtype == kBF16 ? 2 : 4);
-    dim3 grid((unsigned)((rows + kRtRows - 1) / kRtRows));
-    if (dtype == kBF16)
-        hipLaunchKernelGGL(route_kernel<uint16_t>, grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
-                           (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
-                           (uint16_t*)gates, ids);
-    else
-        hipLaunchKernelGGL(route_kernel<float>, grid, dim3(kRtWaves * 64), smem, stream, (const float*)q, (const float*)k1,
-                           (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
+    const bool small = rows <= kRtSmallRows;
+    const int per_wg = kRtWaves * (small ? 1 : 4);
+    dim3 grid((unsigned)((rows + per_wg - 1) / per_wg));
+    if (dtype == kBF16) {
+        if (small)
+            hipLaunchKernelGGL((route_kernel<uint16_t, 1>), grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
+                               (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
+                               (uint16_t*)gates, ids);
+        else
+            hipLaunchKernelGGL((route_kernel<uint16_t, 4>), grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
+                               (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
+                               (uint16_t*)gates, ids);
+    } else {
+        if (small)
+            hipLaunchKernelGGL((route_kernel<float, 1>), grid, dim3(kRtWaves * 64), smem, stream, (const float*)q,
+                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
+        else
+            hipLaunchKernelGGL((route_kernel<float, 4>), grid, dim3(kRtWaves * 64), smem, stream, (const float*)q,
+                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
+    }
     return (int)hipGetLastError();
 }
 

@@ -49,11 +49,12 @@ def test_route_bit_exact(name):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "fp32"])
-@pytest.mark.parametrize("rows", [1, 17, 80, 95, 200])
+@pytest.mark.parametrize("rows", [1, 17, 80, 95, 200, 4096, 4097, 4123])
 def test_route_partial_tiles_bit_exact(rows, dt):
-    """Row counts that leave the last 32-row workgroup partly empty (one wave with live and
-    dead rows, whole waves of dead rows): a regression test for per-row counters that were
-    left unset past the last row."""
+    """Row counts that leave the last workgroup partly empty, for both row layouts (up to
+    4096 rows: one row per wave, 8 per workgroup; above: four per wave, 32 per workgroup,
+    with one wave holding live and dead rows and whole waves of dead rows): a regression
+    test for per-row counters that were left unset past the last row."""
     rng = np.random.default_rng(rows)
     K, dh2, top_k = 16 if rows < 100 else 512, 16 if rows < 100 else 128, 4 if rows < 100 else 16
     q, k1, k2 = _stress_case("zipf", rng, rows, K, dh2, dt)
