@@ -56,6 +56,10 @@ template <> struct Elem<float> {
     __device__ __forceinline__ static float round32(float v) { return v; }
     __device__ __forceinline__ static void round32x2(float& a, float& b) {}
     __device__ __forceinline__ static float round64(double v) { return (float)v; }
+    // a float c <= every x with RN_T(x) >= t, for t a T value: the spacing below t is at
+    // most |t| 2^-23, so RN(t - |t| 2^-23) <= t - ulp is below the midpoint between t and
+    // its predecessor; 2^-126 covers t = 0 and subnormal t
+    __device__ __forceinline__ static float round_down_cut(float t) { return (t - fabsf(t) * 0x1p-23f) - 0x1p-126f; }
 };
 template <> struct Elem<uint16_t> {
     static constexpr DType kDType = kBF16;
@@ -68,6 +72,10 @@ template <> struct Elem<uint16_t> {
     // two values at once through the hardware conversion (round to nearest even)
     __device__ __forceinline__ static void round32x2(float& a, float& b);
     __device__ __forceinline__ static float round64(double v) { return bf16_bits_to_f32(from_f64(v)); }
+    // a float c <= every x with RN_T(x) >= t, for t a bf16 value: the bf16 spacing below
+    // t is at most |t| 2^-7, so t - |t| 2^-7 (exact in fp32) is at most the midpoint
+    // between t and its predecessor; 2^-126 covers t = 0 and subnormal t
+    __device__ __forceinline__ static float round_down_cut(float t) { return (t - fabsf(t) * 0x1p-7f) - 0x1p-126f; }
 };
 
 __device__ __forceinline__ void Elem<uint16_t>::round32x2(float& a, float& b) {

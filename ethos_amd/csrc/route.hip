@@ -22,10 +22,13 @@
 //      truncating fp32 add), by Cauchy-Schwarz on sum |q_i k_ij|.
 //   2. tau_s = the k_cand-th largest of the 64 per-lane maxima of s~ is at most the
 //      k_cand-th largest s~, so at least k_cand keys have s >= tau_s - max_j e_j =: tau.
-//      A key whose upper bound rounds below RN_T(tau) rounds strictly below k_cand
-//      other keys and cannot be selected: it is dropped.
-//   3. The survivors (about 40 of 512) are scored exactly (the fp64 chain) one per
-//      lane and ranked with 64-lane bitonic sort / merge networks on canonical keys.
+//      A key whose exact score rounds below RN_T(tau) rounds strictly below k_cand
+//      other keys and cannot be selected; a key is dropped when even s~ plus its
+//      margin lies below the interval that rounds to RN_T(tau).
+//   3. The survivors (about 40 of 512) whose interval [s~ - e, s~ + e] rounds to one T
+//      value have it as their exact score; the others are scored exactly (the fp64
+//      chain), one per lane.  The survivors are ranked with 64-lane bitonic sort /
+//      merge networks on canonical keys.
 // The output therefore equals exhaustive exact scoring bit for bit.
 #pragma clang fp contract(off)
 
@@ -420,19 +423,39 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         }
         __syncthreads();
 
-        // 2. per row: certified candidate filter.  A candidate whose certified interval
-        //    [s~ - e, s~ + e] rounds to a single T value has that value as its exact score:
-        //    rounding is monotone and the fp64 chain lies inside the interval (its own
-        //    error is below 2^-45 ||q|| ||k||, far inside the 1% slack of e).  The others
-        //    go on the row's pending list, and step 3 scores the pending lists of all the
-        //    wave's rows together.  A row with more than 64 candidates (rare) is scored
-        //    exactly in full in step 4.
+        // 2. per row: candidate filter, then certification of the survivors.
+        //    Filter: with the query-half norm bound qn >= ||q|| and the sub-key norm bounds
+        //    kn_j >= ||k_j||, every approximate score satisfies |s~_j| <= (qn + e'_j) kn_j
+        //    (e'_j = gamma qn), so the margin m_j = gamma qn kn_j + |s~_j| 2^-21 + 2^-120
+        //    is at most m'_j = gamma qn kn_j + A and at most E = gamma qn kn_max + A, with
+        //    A = (qn + gamma qn) kn_max 2^-21 + 2^-120 the same for the whole row.  A key
+        //    whose upper bound s~_j + m_j rounds to a T value below RN_T(tau) cannot be
+        //    selected; every such key has s~_j + gamma qn kn_j < cut - A, where cut is at
+        //    most the lower end of the interval that rounds to RN_T(tau) (the filter keeps
+        //    a superset of the keys that can be selected).
+        //    Certification: a survivor whose interval [s~ - m, s~ + m] rounds to a single T
+        //    value has that value as its exact score: rounding is monotone and the fp64
+        //    chain lies inside the interval (its own error is below 2^-45 ||q|| ||k||, far
+        //    inside the 1% slack of the margin).  The others go on the row's pending list,
+        //    and step 3 scores the pending lists of all the wave's rows together.  A row
+        //    with more than 64 survivors (rare) is scored exactly in full in step 4.
         // zero for every row slot, including the slots past the last row of a partial
         // tile (the loop below stops at that row, and step 3 sums all of n_pend)
         int n_cand[RPW], n_pend[RPW];
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) n_cand[rr] = n_pend[rr] = 0;
         uint32_t slow_rows = 0;
+        // largest sub-key norm bound of this half (wave-uniform)
+        float kn_max;
+        {
+            uint32_t kb = 0;
+#pragma unroll
+            for (int m = 0; m < kRtSlots; ++m) {
+                const int j = lane + m * kWave;
+                if (j < K) kb = max(kb, __float_as_uint(kn[half * kpad + j]));
+            }
+            kn_max = __uint_as_float(wave_max_u32(kb));
+        }
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) {
             const int lr = wave * RPW + rr;
@@ -449,32 +472,19 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             }
             // (v_sqrt_f32 is within 1 ulp for a normal argument; the offset keeps it normal)
             const float qn = __builtin_amdgcn_sqrtf(wave_sum(sq) + 0x1p-100f) * (1.0f + 0x1p-12f);
-
             const float gq = gamma * qn;
-            // up: upper bounds of the scores (filter); cs: certified scores or kRtPending
-            float up[kRtSlots];   // RN_T of the upper bounds
-            uint32_t cs[kRtSlots];
+            const float A = (qn + gq) * kn_max * 0x1p-21f * (1.0f + 0x1p-20f) + 0x1p-120f;
+            const float E = __builtin_fmaf(gq, kn_max, A) * (1.0f + 0x1p-20f);
+
+            // approximate scores of the row (registers) and the lane maxima
+            float sv[kRtSlots];
             float lane_max = -__builtin_huge_valf();
-            uint32_t emax_bits = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
                 const int j = lane + m * kWave;
-                up[m] = -__builtin_huge_valf();
-                cs[m] = kRtPending;
-                if (j < K) {
-                    const float sj = S[lr * pitch + j];
-                    const float marg = __builtin_fmaf(fabsf(sj), 0x1p-21f, __builtin_fmaf(gq, kn[half * kpad + j], 0x1p-120f));
-                    float lo_f = sj - marg, hi_f = sj + marg;
-                    Elem<T>::round32x2(lo_f, hi_f);  // RN_T of both ends (rounding is monotone)
-                    up[m] = hi_f;
-                    const uint32_t lo = __float_as_uint(lo_f);
-                    const uint32_t hi = __float_as_uint(hi_f);
-                    if (lo == hi && (lo & 0x7f800000u) != 0x7f800000u) cs[m] = lo;
-                    lane_max = fmaxf(lane_max, sj);
-                    emax_bits = max(emax_bits, __float_as_uint(marg));
-                }
+                sv[m] = j < K ? S[lr * pitch + j] : -__builtin_huge_valf();
+                lane_max = fmaxf(lane_max, sv[m]);
             }
-            const float emax = __uint_as_float(wave_max_u32(emax_bits));
             // o: the largest value with 16 low zero bits such that at least kc lane maxima
             // are >= o (as ordered keys); it is at most the kc-th largest lane maximum
             const uint32_t lkey = lane < K ? ord32(lane_max) : 0u;
@@ -485,51 +495,60 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
                 if ((int)__popcll(ballot(lkey >= cand_o)) >= kc) o = cand_o;
             }
             const float tau_s = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
-            const float tau = tau_s - emax * (1.0f + 0x1p-20f) - fabsf(tau_s) * 0x1p-21f;
-            const float thr = Elem<T>::round32(tau);
+            const float tau = tau_s - E - fabsf(tau_s) * 0x1p-21f;
+            const float cut = Elem<T>::round_down_cut(Elem<T>::round32(tau)) - A;
 
-            uint32_t fbits = 0;
+            // the row's scores are in registers now: its LDS row takes the survivors
+            // (approximate score bits << 32 | sub-key), in slot order
+            __builtin_amdgcn_wave_barrier();
+            uint64_t* ck = reinterpret_cast<uint64_t*>(S + lr * pitch);
+            int32_t* cand = reinterpret_cast<int32_t*>(S + lr * pitch);
+            bool f[kRtSlots];
+            uint64_t fb[kRtSlots];
             int n = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
-                const bool f = lane + m * kWave < K && up[m] >= thr;
-                fbits |= (uint32_t)f << m;
-                n += (int)__popcll(ballot(f));
+                const int j = lane + m * kWave;
+                f[m] = j < K && __builtin_fmaf(gq, kn[half * kpad + j], sv[m]) >= cut;
+                fb[m] = ballot(f[m]);
+                n += (int)__popcll(fb[m]);
             }
             n_cand[rr] = n;
-            // the row's scores are in registers now: its LDS row holds the candidates
-            __builtin_amdgcn_wave_barrier();
             if (n <= kWave) {
-                uint64_t* ck = reinterpret_cast<uint64_t*>(S + lr * pitch);
                 int pos = 0;
 #pragma unroll
                 for (int m = 0; m < kRtSlots; ++m) {
-                    const bool f = (fbits >> m) & 1u;
-                    const uint64_t bal = ballot(f);
-                    if (f) ck[pos + count_below(bal)] = ((uint64_t)cs[m] << 32) | (uint32_t)(lane + m * kWave);
-                    pos += (int)__popcll(bal);
+                    if (f[m])
+                        ck[pos + count_below(fb[m])] = ((uint64_t)__float_as_uint(sv[m]) << 32) | (uint32_t)(lane + m * kWave);
+                    pos += (int)__popcll(fb[m]);
                 }
                 __builtin_amdgcn_wave_barrier();
-                // certified slots become final keys; the others join the pending list as
-                // (sub-key << 8 | slot)
+                // certify each survivor; certified ones become final keys, the others join
+                // the pending list as (sub-key << 8 | slot)
                 const uint64_t e = lane < n ? ck[lane] : 0ull;
-                const uint32_t sc = (uint32_t)(e >> 32), j = (uint32_t)e;
-                const bool pend = lane < n && sc == kRtPending;
+                const float sj = __uint_as_float((uint32_t)(e >> 32));
+                const uint32_t j = (uint32_t)e;
+                bool pend = false;
+                uint32_t lo = 0;
+                if (lane < n) {
+                    const float marg = __builtin_fmaf(fabsf(sj), 0x1p-21f, __builtin_fmaf(gq, kn[half * kpad + j], 0x1p-120f));
+                    float lo_f = sj - marg, hi_f = sj + marg;
+                    Elem<T>::round32x2(lo_f, hi_f);  // RN_T of both ends (rounding is monotone)
+                    lo = __float_as_uint(lo_f);
+                    pend = !(lo == __float_as_uint(hi_f) && (lo & 0x7f800000u) != 0x7f800000u);
+                }
                 const uint64_t bal = ballot(pend);
                 if (lane < n) {
                     if (pend) reinterpret_cast<uint32_t*>(S + lr * pitch + kRtPendOff)[count_below(bal)] = (j << 8) | (uint32_t)lane;
-                    else ck[lane] = make_key(__uint_as_float(sc), j);
+                    else ck[lane] = make_key(__uint_as_float(lo), j);
                 }
                 n_pend[rr] = (int)__popcll(bal);
             } else {
-                int32_t* cand = reinterpret_cast<int32_t*>(S + lr * pitch);
                 int pos = 0;
 #pragma unroll
                 for (int m = 0; m < kRtSlots; ++m) {
-                    const bool f = (fbits >> m) & 1u;
-                    const uint64_t bal = ballot(f);
-                    if (f) cand[pos + count_below(bal)] = lane + m * kWave;
-                    pos += (int)__popcll(bal);
+                    if (f[m]) cand[pos + count_below(fb[m])] = lane + m * kWave;
+                    pos += (int)__popcll(fb[m]);
                 }
                 slow_rows |= 1u << rr;
             }
