@@ -265,10 +265,19 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
 // P = pieces per lane: dh <= 64 P elements (bf16) or 32 P (fp32).
 constexpr int kAct8Waves = 4;
 
+// Token order for the activations, taken when the hidden rows of all unique experts fit
+// in a cache (at most this many bytes): one wave per token holds the token's projection in
+// registers and reads the hidden rows of its H*k pairs, which stay cache-resident, instead
+// of gathering one projection row per pair.  Same lanes, same per-lane dot products and
+// same reduction as the expert-order walk, so the results are bit-identical.
+constexpr int64_t kActTokenOrderMaxHBytes = 8 << 20;
+
 template <typename T, int P>
 __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
                                                                      const int32_t* __restrict__ perm,
                                                                      const int32_t* __restrict__ sorted_slot,
+                                                                     const int32_t* __restrict__ pair_slot,
+                                                                     const int32_t* __restrict__ n_unique,
                                                                      const T* __restrict__ gates, int64_t n_pairs,
                                                                      int hk, int dh, float* __restrict__ act) {
     constexpr int N = Vec16<T>::kN;
@@ -278,6 +287,52 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
     const int part = lane & 7, slot = lane >> 3;
     const int64_t wave_id = (int64_t)blockIdx.x * kAct8Waves + wave;
     const int64_t n_waves = (int64_t)gridDim.x * kAct8Waves;
+    if (n_unique != nullptr && pair_slot != nullptr &&
+        (int64_t)*n_unique * dh * (int64_t)sizeof(T) <= kActTokenOrderMaxHBytes) {
+        const int64_t n_tok = n_pairs / hk;
+        for (int64_t t = wave_id; t < n_tok; t += n_waves) {
+            const T* xr = xp + t * dh;
+            Raw xv[P];
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                const int e = (part + 8 * i) * N;
+                xv[i] = e < dh ? *reinterpret_cast<const Raw*>(xr + e) : Raw{};
+            }
+            const int64_t pbase = t * hk;
+            for (int j0 = 0; j0 < hk; j0 += 64) {
+                const int cnt = hk - j0 < 64 ? hk - j0 : 64;
+                const int my_s = lane < cnt ? pair_slot[pbase + j0 + lane] : 0;
+                for (int g = 0; g < cnt; g += 8) {
+                    // this lane's pair of the group (a tail group repeats the last pair)
+                    const int src = g + slot < cnt ? g + slot : cnt - 1;
+                    const int sl = __shfl(my_s, src, 64);
+                    const T* hr = hid + (int64_t)sl * dh;
+                    Raw hv[P];
+#pragma unroll
+                    for (int i = 0; i < P; ++i) {
+                        const int e = (part + 8 * i) * N;
+                        hv[i] = e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
+                    }
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < P; ++i) acc = dot_raw(hv[i], xv[i], acc);
+                    acc += dpp_f32<kDppXor1>(acc);
+                    acc += dpp_f32<kDppXor2>(acc);
+                    acc += dpp_f32<kDppRowHalfMirror>(acc);
+                    if (part == 0) dots[wave][g + slot] = acc;
+                }
+                __builtin_amdgcn_wave_barrier();
+                if (lane < cnt) {
+                    const int64_t p = pbase + j0 + lane;
+                    const float gt = Elem<T>::to_f32(gates[p]);
+                    const float a = Elem<T>::round32(gelu_erf(Elem<T>::round32(dots[wave][lane])));
+                    act[p] = Elem<T>::round32(a * gt);
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+        return;
+    }
     const int64_t n_chunks = (n_pairs + 63) / 64;
     for (int64_t chunk = wave_id; chunk < n_chunks; chunk += n_waves) {
         const int64_t i0 = chunk * 64;
@@ -594,26 +649,29 @@ static void launch_scatter_t(const void* v, const int32_t* pair_slot, const floa
 
 template <typename T, int P>
 static void launch_act8_t(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
-                          const void* gates, int64_t n_pairs, int hk, int dh, float* act, int num_cus,
-                          hipStream_t stream) {
+                          const int32_t* pair_slot, const int32_t* n_unique, const void* gates, int64_t n_pairs,
+                          int hk, int dh, float* act, int num_cus, hipStream_t stream) {
     const int64_t cap = (int64_t)num_cus * 16;
     int64_t g1 = ((n_pairs + 63) / 64 + kAct8Waves - 1) / kAct8Waves;
     g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
     hipLaunchKernelGGL((apply_act8_kernel<T, P>), dim3((unsigned)g1), dim3(kAct8Waves * 64), 0, stream, (const T*)xp,
-                       (const T*)hid, perm, sorted_slot, (const T*)gates, n_pairs, hk, dh, act);
+                       (const T*)hid, perm, sorted_slot, pair_slot, n_unique, (const T*)gates, n_pairs, hk, dh, act);
 }
 
 // Per-pair activations a_p (phase 1): 8 lanes per pair for rows of up to 64 pieces of 16
 // bytes (d_hidden <= 512 bf16 / 256 fp32), one wave per pair beyond; -1 past the limits.
+// With pair_slot and the device count n_unique given, the 8-lane kernel takes token order
+// when the hidden rows are few (kActTokenOrderMaxHBytes).
 static int launch_act(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
-                      const void* gates, int64_t n_pairs, int hk, int dh, int dtype, float* act, int num_cus,
-                      hipStream_t stream) {
+                      const int32_t* pair_slot, const int32_t* n_unique, const void* gates, int64_t n_pairs, int hk,
+                      int dh, int dtype, float* act, int num_cus, hipStream_t stream) {
     const int pieces = (dh + (dtype == kBF16 ? 8 : 4) - 1) / (dtype == kBF16 ? 8 : 4);
     const int pp = (pieces + 7) / 8;
     const int P = pp <= 1 ? 1 : pp <= 2 ? 2 : pp <= 4 ? 4 : pp <= 8 ? 8 : 0;
 #define ETHOS_ACT8_CASE(TT, PP)                                                                                \
     if (P == PP) {                                                                                             \
-        launch_act8_t<TT, PP>(xp, hid, perm, sorted_slot, gates, n_pairs, hk, dh, act, num_cus, stream);        \
+        launch_act8_t<TT, PP>(xp, hid, perm, sorted_slot, pair_slot, n_unique, gates, n_pairs, hk, dh, act,     \
+                              num_cus, stream);                                                                \
         return 0;                                                                                              \
     }
     if (dtype == kBF16) {
@@ -724,7 +782,8 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
                         : nullptr;
     if (apply_chunks(dh, dtype) > 8 || apply_chunks(d, dtype) > 8) return -1;
     launch_token_proj(x, w2, nullptr, n_tok, H, k, d, dh, dtype, ws, stream);
-    launch_act(xp, hid, perm, sorted_slot, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus, stream);
+    launch_act(xp, hid, perm, sorted_slot, nullptr, nullptr, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus,
+               stream);
     launch_scatter(v, pair_slot, act, n_tok, H, k, d, dtype, headbuf, out, num_cus, stream);
     return (int)hipGetLastError();
 }
@@ -768,7 +827,8 @@ int launch_apply_hidden(const void* x, const void* w2, const void* hid, const in
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
     if (apply_chunks(dh, dtype) > 8) return -1;
     launch_token_proj(x, w2, nullptr, n_tok, H, k, d, dh, dtype, ws, stream);
-    launch_act(xp, hid, perm, sorted_slot, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus, stream);
+    launch_act(xp, hid, perm, sorted_slot, nullptr, nullptr, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus,
+               stream);
     return launch_hidden_tail(w2, hid, pair_slot, act, n_tok, H, k, d, dh, dtype, ws, out, num_cus, stream);
 }
 
@@ -878,7 +938,8 @@ int launch_expert_forward(const void* x, const void* latents, int64_t n_experts,
                                   num_cus, stream);
     if (rc != 0) return rc;
     stage_mark(stream);
-    launch_act(xp, hout, perm, sorted_slot, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus, stream);
+    launch_act(xp, hout, perm, sorted_slot, pair_slot, n_unique, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus,
+               stream);
     stage_mark(stream);
     if (order == 1) {
         stage_mark(stream);
