@@ -480,6 +480,47 @@ __global__ __launch_bounds__(256) void qproj_fixup_kernel(const uint16_t* __rest
         const int t = e / ncols, c = e - t * ncols;
         const uint16_t* xr = x + (int64_t)t * d;
         const uint16_t* wr = w + (int64_t)c * d;
+        // Exactness test.  Every product is an integer multiple of 2^L, L the smallest
+        // lowest-bit exponent of the non-zero products (a bf16 value with biased exponent
+        // b is a multiple of 2^(max(b, 1) - 134)), and so is every partial sum, in any
+        // order, of magnitude at most S = sum |x_i w_i|.  When S < 2^(L + 53) every such
+        // sum is exact in fp64: the chain never rounds and equals the wave's sum in any
+        // order.  (S is taken with a factor-2 margin for the rounding of its own sum;
+        // a non-finite product makes S non-finite and fails the test.)
+        double ls = 0.0, la = 0.0;
+        int lmin = 0x7fffffff;
+        for (int g = lane; g < d / 8; g += kWave) {
+            const uint4 xa = *reinterpret_cast<const uint4*>(xr + 8 * g);
+            const uint4 wa = *reinterpret_cast<const uint4*>(wr + 8 * g);
+            const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
+            const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t xb = (xv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                const uint32_t wb = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                const double pj = (double)__uint_as_float(xb << 16) * (double)__uint_as_float(wb << 16);
+                if (pj != 0.0) {
+                    const int lx = max((int)((xb >> 7) & 0xffu), 1) - 134;
+                    const int lw = max((int)((wb >> 7) & 0xffu), 1) - 134;
+                    lmin = min(lmin, lx + lw);
+                }
+                ls += pj;
+                la += fabs(pj);
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            ls += __shfl_xor(ls, m, kWave);
+            la += __shfl_xor(la, m, kWave);
+            lmin = min(lmin, __shfl_xor(lmin, m, kWave));
+        }
+        if (lmin == 0x7fffffff || la < ldexp(1.0, lmin + 52)) {
+            if (lane == 0) {
+                const float ql = Elem<uint16_t>::round64(ls + (double)bf16_bits_to_f32(bias[c]));
+                q[e] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
+            }
+            continue;
+        }
         double acc = 0.0;
         for (int k0 = 0; k0 < d; k0 += kFixChunk) {
             const int len = min(kFixChunk, d - k0);  // a multiple of 8
