@@ -119,30 +119,78 @@ size_t ethos_query_proj_workspace_bytes(int64_t n_tok, int32_t d_model, int32_t 
     return b < 256 ? 256 : b;
 }
 
-int ethos_query_proj(const void* x, const void* wq, const void* bq, const float* bn_alpha, const float* bn_beta,
-                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace,
-                     size_t workspace_bytes, void* q_out, void* stream) {
+static int query_proj_impl(const char* name, const void* x, const void* wq, const void* prepared, const void* bq,
+                           const float* bn_alpha, const float* bn_beta, int64_t n_tok, int32_t d_model,
+                           int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace, size_t workspace_bytes,
+                           void* q_out, void* stream) {
     g_err[0] = 0;
-    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_query_proj: unknown dtype %d", dtype);
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "%s: unknown dtype %d", name, dtype);
     if (n_tok < 0 || d_model <= 0 || n_heads <= 0 || d_query <= 0)
-        return fail(ETHOS_ESIZE, "ethos_query_proj: bad sizes n_tok=%lld d_model=%d n_heads=%d d_query=%d",
+        return fail(ETHOS_ESIZE, "%s: bad sizes n_tok=%lld d_model=%d n_heads=%d d_query=%d", name,
                     (long long)n_tok, d_model, n_heads, d_query);
     if ((int64_t)n_heads * d_query > INT32_MAX / 2 || n_tok * (int64_t)n_heads * d_query > INT32_MAX)
-        return fail(ETHOS_ESIZE, "ethos_query_proj: n_tok * n_heads * d_query exceeds int32");
+        return fail(ETHOS_ESIZE, "%s: n_tok * n_heads * d_query exceeds int32", name);
     if (n_tok == 0) return 0;
-    if (!x || !wq || !bq || !bn_alpha || !bn_beta || !q_out)
-        return fail(ETHOS_ENULL, "ethos_query_proj: null pointer");
+    if (!x || !wq || !bq || !bn_alpha || !bn_beta || !q_out) return fail(ETHOS_ENULL, "%s: null pointer", name);
     const size_t need = ethos_query_proj_workspace_bytes(n_tok, d_model, n_heads, d_query, dtype);
     if (dtype == ETHOS_BF16) {
         if (!workspace || workspace_bytes < need)
-            return fail(ETHOS_EWORKSPACE, "ethos_query_proj: workspace of %zu bytes, %zu needed", workspace_bytes,
-                        need);
-        if (!aligned16(workspace) || !aligned16(x) || !aligned16(wq) || (d_model % 8))
-            return fail(ETHOS_EALIGN, "ethos_query_proj: x, wq, workspace 16-byte aligned and d_model %% 8 == 0");
+            return fail(ETHOS_EWORKSPACE, "%s: workspace of %zu bytes, %zu needed", name, workspace_bytes, need);
+        if (!aligned16(workspace) || !aligned16(x) || !aligned16(wq) || (prepared && !aligned16(prepared)) ||
+            (d_model % 8))
+            return fail(ETHOS_EALIGN, "%s: x, wq, prepared, workspace 16-byte aligned and d_model %% 8 == 0", name);
     }
-    return hip_status(ethos::launch_qproj(x, wq, bq, bn_alpha, bn_beta, n_tok, d_model, n_heads * d_query, dtype,
-                                          workspace, q_out, num_cus(), (hipStream_t)stream),
-                      "ethos_query_proj");
+    if (ethos::qproj_weights_bytes(n_heads * d_query, d_model, dtype) == 0) prepared = nullptr;
+    return hip_status(ethos::launch_qproj(x, wq, prepared, bq, bn_alpha, bn_beta, n_tok, d_model, n_heads * d_query,
+                                          dtype, workspace, q_out, num_cus(), (hipStream_t)stream),
+                      name);
+}
+
+int ethos_query_proj(const void* x, const void* wq, const void* bq, const float* bn_alpha, const float* bn_beta,
+                     int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace,
+                     size_t workspace_bytes, void* q_out, void* stream) {
+    return query_proj_impl("ethos_query_proj", x, wq, nullptr, bq, bn_alpha, bn_beta, n_tok, d_model, n_heads,
+                           d_query, dtype, workspace, workspace_bytes, q_out, stream);
+}
+
+size_t ethos_query_proj_weights_bytes(int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype) {
+    if (d_model <= 0 || n_heads <= 0 || d_query <= 0 || !dtype_ok(dtype)) return 0;
+    return ethos::qproj_weights_bytes(n_heads * d_query, d_model, dtype);
+}
+
+int ethos_query_proj_prepare(const void* wq, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype,
+                             void* prepared, size_t prepared_bytes, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_query_proj_prepare: unknown dtype %d", dtype);
+    if (d_model <= 0 || n_heads <= 0 || d_query <= 0 || (int64_t)n_heads * d_query > INT32_MAX / 2)
+        return fail(ETHOS_ESIZE, "ethos_query_proj_prepare: bad sizes d_model=%d n_heads=%d d_query=%d", d_model,
+                    n_heads, d_query);
+    const size_t need = ethos_query_proj_weights_bytes(d_model, n_heads, d_query, dtype);
+    if (need == 0) return 0;
+    if (!wq || !prepared) return fail(ETHOS_ENULL, "ethos_query_proj_prepare: null pointer");
+    if (prepared_bytes < need)
+        return fail(ETHOS_EWORKSPACE, "ethos_query_proj_prepare: %zu bytes, %zu needed", prepared_bytes, need);
+    if (!aligned16(wq) || !aligned16(prepared) || (d_model % 8))
+        return fail(ETHOS_EALIGN, "ethos_query_proj_prepare: wq, prepared 16-byte aligned and d_model %% 8 == 0");
+    return hip_status(ethos::launch_qproj_prepare(wq, n_heads * d_query, d_model, dtype, prepared,
+                                                  (hipStream_t)stream),
+                      "ethos_query_proj_prepare");
+}
+
+int ethos_query_proj_prepared(const void* x, const void* wq, const void* prepared, size_t prepared_bytes,
+                              const void* bq, const float* bn_alpha, const float* bn_beta, int64_t n_tok,
+                              int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace,
+                              size_t workspace_bytes, void* q_out, void* stream) {
+    const size_t need = ethos_query_proj_weights_bytes(d_model, n_heads, d_query, dtype);
+    if (need > 0 && n_tok > 0) {
+        g_err[0] = 0;
+        if (!prepared) return fail(ETHOS_ENULL, "ethos_query_proj_prepared: null prepared weights");
+        if (prepared_bytes < need)
+            return fail(ETHOS_EWORKSPACE, "ethos_query_proj_prepared: prepared weights of %zu bytes, %zu needed",
+                        prepared_bytes, need);
+    }
+    return query_proj_impl("ethos_query_proj_prepared", x, wq, prepared, bq, bn_alpha, bn_beta, n_tok, d_model,
+                           n_heads, d_query, dtype, workspace, workspace_bytes, q_out, stream);
 }
 
 int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, const float* key_norms,

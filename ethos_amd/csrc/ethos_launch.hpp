@@ -12,8 +12,11 @@ namespace ethos {
 void stage_mark(hipStream_t stream);
 
 size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int d, int dtype);
-int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
-                 int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream);
+size_t qproj_weights_bytes(int ncols, int d, int dtype);
+int launch_qproj_prepare(const void* w, int ncols, int d, int dtype, void* prepared, hipStream_t stream);
+int launch_qproj(const void* x, const void* w, const void* prepared, const void* b, const float* alpha,
+                 const float* beta, int64_t n_tok, int d, int ncols, int dtype, void* ws, void* q, int num_cus,
+                 hipStream_t stream);
 
 size_t route_smem_bytes(int K, int dh2, int elem_bytes);
 bool route_supported(int K, int dh2, int dtype);

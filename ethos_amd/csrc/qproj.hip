@@ -142,18 +142,18 @@ __host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols, 
 
 __device__ __forceinline__ uint32_t qp_wave_max_u32(uint32_t v) { return (uint32_t)wave_max_u64((uint64_t)v); }
 
-// One wave per row of x (rows < n_tok) or Wq: digit planes and the row's format.  The
-// first thread also resets the uncertain-element count (read by the kernels after this one
-// on the same stream).
+// One wave per row of x (rows < n_tok) or Wq (the n_rows - n_tok rows after them): digit
+// planes and the row's format.  The first thread also resets the uncertain-element count,
+// if given (read by the kernels after this one on the same stream).
 __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ w, int n_tok, int ncols,
-                                                           int d, int8_t* __restrict__ xdig,
-                                                           int8_t* __restrict__ wdig, QRowMeta* __restrict__ meta,
-                                                           int32_t* __restrict__ count) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) *count = 0;
+                                                           int64_t n_rows, int d, int8_t* __restrict__ xdig,
+                                                           int8_t* __restrict__ wdig, QRowMeta* __restrict__ xmeta,
+                                                           QRowMeta* __restrict__ wmeta, int32_t* __restrict__ count) {
+    if (count != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *count = 0;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= (int64_t)n_tok + ncols) return;
+    if (row >= n_rows) return;
     const bool is_x = row < n_tok;
     const int64_t r = is_x ? row : row - n_tok;
     const uint16_t* src = (is_x ? x : w) + r * d;
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
         mt.n_inex = bad ? -1 : total_inex;
         mt.l1 = l1;
         mt.amax = amax;
-        meta[row] = mt;
+        (is_x ? xmeta : wmeta)[r] = mt;
     }
 }
 
@@ -265,7 +265,8 @@ __device__ __forceinline__ int qi_slot(int row, int piece) { return piece ^ ((ro
 template <int kWaves, int kCB, int kStages>
 __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __restrict__ xdig,
                                                                  const int8_t* __restrict__ wdig,
-                                                                 const QRowMeta* __restrict__ meta,
+                                                                 const QRowMeta* __restrict__ xmeta,
+                                                                 const QRowMeta* __restrict__ wmeta,
                                                                  const uint16_t* __restrict__ bias,
                                                                  const float* __restrict__ alpha,
                                                                  const float* __restrict__ beta, int n_tok, int d,
@@ -323,7 +324,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     static_assert(kStages >= 2 && kStages <= 4, "waits cover at most two chunks in flight past the current one");
 
     if (tid < kQiRows && t0 + tid < n_tok) {
-        const QRowMeta m = meta[t0 + tid];
+        const QRowMeta m = xmeta[t0 + tid];
         xpf[tid] = make_float4(ldexpf(m.amax, -m.e), ldexpf(m.l1, -m.e), (float)m.n_inex * 0x1p-21f, 0.0f);
         xpi[tid] = make_int2(m.e, m.n_inex);
     }
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     double b = 0.0;
     float al = 0.0f, be = 0.0f;
     if (col_ok) {
-        const QRowMeta m = meta[n_tok + c];
+        const QRowMeta m = wmeta[c];
         ew = m.e;
         nw = m.n_inex;
         aw = ldexpf(m.amax, -m.e);
@@ -554,18 +555,47 @@ size_t qproj_workspace_bytes(int64_t n_tok, int ncols, int d, int dtype) {
     return dtype == kBF16 && d <= kQiMaxD ? qproj_ws_bytes(n_tok, ncols, d) : 0;
 }
 
-int launch_qproj(const void* x, const void* w, const void* b, const float* alpha, const float* beta, int64_t n_tok,
-                 int d, int ncols, int dtype, void* ws, void* q, int num_cus, hipStream_t stream) {
+// Prepared weights: Wq's digit planes [3][ncols][dpad] and row formats [ncols], computed
+// once (launch_qproj_prepare) and read by every later projection with the same Wq.
+size_t qproj_weights_bytes(int ncols, int d, int dtype) {
+    if (dtype != kBF16 || d > kQiMaxD) return 0;
+    return qproj_align(3 * (size_t)ncols * qproj_dpad(d)) + qproj_align(sizeof(QRowMeta) * (size_t)ncols);
+}
+
+static void prepared_parts(const void* prepared, int ncols, int d, const int8_t** wdig, const QRowMeta** wmeta) {
+    const unsigned char* p = static_cast<const unsigned char*>(prepared);
+    *wdig = reinterpret_cast<const int8_t*>(p);
+    *wmeta = reinterpret_cast<const QRowMeta*>(p + qproj_align(3 * (size_t)ncols * qproj_dpad(d)));
+}
+
+int launch_qproj_prepare(const void* w, int ncols, int d, int dtype, void* prepared, hipStream_t stream) {
+    if (qproj_weights_bytes(ncols, d, dtype) == 0) return 0;
+    const int8_t* wdig;
+    const QRowMeta* wmeta;
+    prepared_parts(prepared, ncols, d, &wdig, &wmeta);
+    hipLaunchKernelGGL(qproj_digits_kernel, dim3((unsigned)((ncols + 3) / 4)), dim3(256), 0, stream, nullptr,
+                       (const uint16_t*)w, 0, ncols, (int64_t)ncols, d, nullptr, const_cast<int8_t*>(wdig), nullptr,
+                       const_cast<QRowMeta*>(wmeta), nullptr);
+    return (int)hipGetLastError();
+}
+
+int launch_qproj(const void* x, const void* w, const void* prepared, const void* b, const float* alpha,
+                 const float* beta, int64_t n_tok, int d, int ncols, int dtype, void* ws, void* q, int num_cus,
+                 hipStream_t stream) {
     if (dtype == kBF16 && d <= kQiMaxD) {
         const QprojWs W = qproj_ws(ws, n_tok, ncols, d);
-        const int64_t rows = n_tok + ncols;
+        const int8_t* wdig = W.wdig;
+        const QRowMeta* wmeta = W.meta + n_tok;
+        // with prepared weights only the rows of x are converted
+        const int64_t rows = prepared ? n_tok : n_tok + ncols;
+        if (prepared) prepared_parts(prepared, ncols, d, &wdig, &wmeta);
         hipLaunchKernelGGL(qproj_digits_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream,
-                           (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, d, W.xdig, W.wdig, W.meta,
-                           W.count);
+                           (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, rows, d, W.xdig, W.wdig, W.meta,
+                           W.meta + n_tok, W.count);
         using C = QiLaunch;
         dim3 grid((ncols + C::kCols - 1) / C::kCols, (unsigned)((n_tok + C::kRows - 1) / C::kRows));
         hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages>), grid, dim3(C::kWaves * 64), C::kSmem,
-                           stream, W.xdig, W.wdig, W.meta, (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols,
+                           stream, W.xdig, wdig, W.meta, wmeta, (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols,
                            W.count, W.list, (uint16_t*)q);
         hipLaunchKernelGGL(qproj_fixup_kernel, dim3((unsigned)num_cus * 4), dim3(256), 0, stream, (const uint16_t*)x,
                            (const uint16_t*)w, (const uint16_t*)b, alpha, beta, d, ncols, W.count, W.list,

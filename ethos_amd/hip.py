@@ -60,9 +60,24 @@ def key_norm_bounds(sub_keys_1: torch.Tensor, sub_keys_2: torch.Tensor) -> torch
     return torch.from_numpy(np.stack(rows)).contiguous()
 
 
+def query_proj_prepare(wq: torch.Tensor) -> torch.Tensor | None:
+    """The prepared form of wq [H, dq, d] for query_proj(..., prepared=...) (a uint8 device
+    buffer), or None when the dtype has nothing to prepare (fp32)."""
+    _need(wq, "wq", dim=3)
+    H, dq, d = wq.shape
+    n = load().ethos_query_proj_weights_bytes(d, H, dq, dtype_code(wq.dtype))
+    if n == 0:
+        return None
+    buf = torch.empty(n, dtype=torch.uint8, device=wq.device)
+    rc = load().ethos_query_proj_prepare(wq.data_ptr(), d, H, dq, dtype_code(wq.dtype), buf.data_ptr(), n, _stream())
+    check(rc, "ethos_query_proj_prepare")
+    return buf
+
+
 def query_proj(x: torch.Tensor, wq: torch.Tensor, bq: torch.Tensor, bn_alpha: torch.Tensor, bn_beta: torch.Tensor,
-               out: torch.Tensor | None = None) -> torch.Tensor:
-    """x [n, d], wq [H, dq, d], bq [H, dq], bn_alpha/beta [H, dq] fp32 -> q [n, H, dq]."""
+               out: torch.Tensor | None = None, prepared: torch.Tensor | None = None) -> torch.Tensor:
+    """x [n, d], wq [H, dq, d], bq [H, dq], bn_alpha/beta [H, dq] fp32 -> q [n, H, dq].
+    prepared: query_proj_prepare(wq) of the same wq, or None."""
     _need(x, "x", dim=2)
     _need(wq, "wq", x.dtype, 3)
     _need(bq, "bq", x.dtype, 2)
@@ -75,6 +90,14 @@ def query_proj(x: torch.Tensor, wq: torch.Tensor, bq: torch.Tensor, bn_alpha: to
     if out is None:
         out = torch.empty((n, H, dq), dtype=x.dtype, device=x.device)
     ws, ws_bytes = workspace(load().ethos_query_proj_workspace_bytes(n, d, H, dq, dtype_code(x.dtype)), x.device)
+    if prepared is not None:
+        _need(prepared, "prepared", torch.uint8, 1)
+        rc = load().ethos_query_proj_prepared(x.data_ptr(), wq.data_ptr(), prepared.data_ptr(), prepared.numel(),
+                                              bq.data_ptr(),
+                                              bn_alpha.data_ptr(), bn_beta.data_ptr(), n, d, H, dq,
+                                              dtype_code(x.dtype), ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
+        check(rc, "ethos_query_proj_prepared")
+        return out
     rc = load().ethos_query_proj(x.data_ptr(), wq.data_ptr(), bq.data_ptr(), bn_alpha.data_ptr(), bn_beta.data_ptr(),
                                  n, d, H, dq, dtype_code(x.dtype), ws.data_ptr(), ws_bytes, out.data_ptr(), _stream())
     check(rc, "ethos_query_proj")

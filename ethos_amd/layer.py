@@ -162,6 +162,7 @@ class ProductKeyRouter(nn.Module):
         self._cache_key = None
         self._cache = None
         self._key_norms = None
+        self._wq_prepared = None
 
     # -- parameter packing (cached until a parameter changes) ---------------------
     def _packed(self, dtype: torch.dtype, device: torch.device):
@@ -182,6 +183,9 @@ class ProductKeyRouter(nn.Module):
             alpha = torch.from_numpy(np.stack(alpha)).contiguous().to(device)
             beta = torch.from_numpy(np.stack(beta)).contiguous().to(device)
             self._key_norms = hip.key_norm_bounds(k1, k2).to(device)
+            # the projection weights' prepared form (bf16: digit planes), reused by every call
+            # until a parameter changes
+            self._wq_prepared = hip.query_proj_prepare(wq) if wq.is_cuda else None
             self._cache = (wq, bq, k1, k2, alpha, beta)
             self._cache_key = key
         return self._cache
@@ -193,13 +197,13 @@ class ProductKeyRouter(nn.Module):
         """Per-head queries after BatchNorm, [n, H, d_query] (model.py:215-216)."""
         wq, bq, _, _, alpha, beta = self._packed(x_flat.dtype, x_flat.device)
         if not self._bn_uses_batch_stats():
-            return hip.query_proj(x_flat, wq, bq, alpha, beta)
+            return hip.query_proj(x_flat, wq, bq, alpha, beta, prepared=self._wq_prepared)
         # Training-mode BatchNorm normalises with batch statistics and updates the
         # running stats: project with an identity affine, then apply torch's batch_norm
         # per head on the projected queries.
         ones = torch.ones_like(alpha)
         zeros = torch.zeros_like(beta)
-        q_lin = hip.query_proj(x_flat, wq, bq, ones, zeros)
+        q_lin = hip.query_proj(x_flat, wq, bq, ones, zeros, prepared=self._wq_prepared)
         outs = []
         for h, m in enumerate(self.query_norms):
             outs.append(F.batch_norm(q_lin[:, h], m.running_mean, m.running_var,

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define ETHOS_ABI_VERSION 3
+#define ETHOS_ABI_VERSION 4
 
 #define ETHOS_F32 0
 #define ETHOS_BF16 1
@@ -89,6 +89,28 @@ size_t ethos_query_proj_workspace_bytes(int64_t n_tok, int32_t d_model, int32_t 
 int ethos_query_proj(const void* x, const void* wq, const void* bq, const float* bn_alpha, const float* bn_beta,
                      int64_t n_tok, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace,
                      size_t workspace_bytes, void* q_out, void* stream);
+
+/*
+ * The same projection with the weight-dependent part computed once.  The reference
+ * re-reads query_projs[h].weight on every call (model.py:215); these split that work off
+ * for callers that keep the weights between calls (the module does, per parameter version).
+ *   ethos_query_proj_weights_bytes: size of the prepared form of wq (0 for fp32: nothing to
+ *     prepare, and ethos_query_proj_prepared then equals ethos_query_proj).
+ *   ethos_query_proj_prepare: writes the prepared form of wq (for bf16: its int8 digit
+ *     planes and per-row formats) into `prepared` (>= that many bytes, 16-byte aligned).
+ *   ethos_query_proj_prepared: ethos_query_proj with `prepared` (prepared_bytes long) from
+ *     the same wq; bit-identical results.  wq is still read (for the exact recomputation of
+ *     uncertain elements).
+ */
+size_t ethos_query_proj_weights_bytes(int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype);
+
+int ethos_query_proj_prepare(const void* wq, int32_t d_model, int32_t n_heads, int32_t d_query, int32_t dtype,
+                             void* prepared, size_t prepared_bytes, void* stream);
+
+int ethos_query_proj_prepared(const void* x, const void* wq, const void* prepared, size_t prepared_bytes,
+                              const void* bq, const float* bn_alpha, const float* bn_beta, int64_t n_tok, int32_t d_model,
+                              int32_t n_heads, int32_t d_query, int32_t dtype, void* workspace,
+                              size_t workspace_bytes, void* q_out, void* stream);
 
 /*
  * Product-key routing of n_rows independent query rows (row = token * n_heads + head).

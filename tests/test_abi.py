@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ethos_abi_version() == 3
+    assert _lib.load().ethos_abi_version() == 4
 
 
 def _rc(fn, *args):
@@ -53,6 +53,14 @@ def test_argument_errors_are_codes():
     assert L.ethos_query_proj(None, 16, 16, 16, 16, 4, 8, 2, 8, 1, 16, 4096, 16, None) == -3
     # bf16 needs its workspace
     assert L.ethos_query_proj(16, 16, 16, 16, 16, 4, 64, 2, 8, 1, 16, 8, 16, None) == -5
+    # prepared weights: missing, or smaller than their size (bf16); fp32 has nothing to prepare
+    need = L.ethos_query_proj_weights_bytes(64, 2, 8, 1)
+    assert need > 0 and L.ethos_query_proj_weights_bytes(64, 2, 8, 0) == 0
+    assert L.ethos_query_proj_prepared(16, 16, None, 0, 16, 16, 16, 4, 64, 2, 8, 1, 16, 1 << 30, 16, None) == -3
+    assert L.ethos_query_proj_prepared(16, 16, 16, need - 1, 16, 16, 16, 4, 64, 2, 8, 1, 16, 1 << 30, 16, None) == -5
+    assert L.ethos_query_proj_prepare(16, 64, 2, 8, 1, 16, need - 1, None) == -5
+    assert L.ethos_query_proj_prepare(None, 64, 2, 8, 1, 16, need, None) == -3
+    assert L.ethos_query_proj_prepare(None, 64, 2, 8, 0, None, 0, None) == 0
     # workspace too small
     assert L.ethos_sort_segment(1, 100, 16, 16, 8, 16, 16, 16, 16, 16, 16, None) == -5
     # misaligned apply pointers

@@ -36,6 +36,21 @@ def test_query_proj_bit_exact(name):
     assert np.array_equal(to_host(q), q_ref)
 
 
+@pytest.mark.parametrize("name", SMALL + ["cfg3"])
+def test_query_proj_prepared_weights_bit_exact(name):
+    """Weights prepared once (digit planes for bf16; nothing for fp32) and reused by two
+    projections of different batches: both equal the oracle bit for bit."""
+    sh, x, P = _setup(name)
+    wq, bq, a, b = (to_dev(P[k]) for k in ("Wq", "bq", "alpha", "beta"))
+    prep = hip.query_proj_prepare(wq)
+    assert (prep is None) == (sh.dtype == "fp32")
+    for rows in (slice(None), slice(0, max(1, x.shape[0] // 3))):
+        xs = np.ascontiguousarray(x[rows])
+        q = hip.query_proj(to_dev(xs), wq, bq, a, b, prepared=prep)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(q), O.query_proj(xs, P["Wq"], P["bq"], P["alpha"], P["beta"], sh.dtype))
+
+
 @pytest.mark.parametrize("name", SMALL + ["cfg3", "yaml"])
 def test_route_bit_exact(name):
     sh, x, P = _setup(name)
@@ -361,9 +376,12 @@ def test_query_proj_certified_fallback_bit_exact(kind):
         beta[:, ::4] = -0.0
         beta[:, 1::4] = 0.0
     q_ref = O.query_proj(x, w, b, alpha, beta, "bf16")
-    q = hip.query_proj(to_dev(x), to_dev(w), to_dev(b), to_dev(alpha), to_dev(beta))
+    wd = to_dev(w)
+    q = hip.query_proj(to_dev(x), wd, to_dev(b), to_dev(alpha), to_dev(beta))
+    qp = hip.query_proj(to_dev(x), wd, to_dev(b), to_dev(alpha), to_dev(beta), prepared=hip.query_proj_prepare(wd))
     torch.cuda.synchronize()
     assert np.array_equal(to_host(q), q_ref), f"{np.sum(to_host(q) != q_ref)} elements differ"
+    assert np.array_equal(to_host(qp), q_ref), f"prepared weights: {np.sum(to_host(qp) != q_ref)} elements differ"
 
 
 @pytest.mark.parametrize("name,signal", [("tiny", False), ("tiny", True), ("tiny_fp32", True), ("cfg1", False),
