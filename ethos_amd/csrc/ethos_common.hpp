@@ -52,6 +52,7 @@ template <> struct Elem<float> {
     __device__ __forceinline__ static double to_f64(float v) { return (double)v; }
     __device__ __forceinline__ static float from_f32(float v) { return v; }
     __device__ __forceinline__ static float from_f64(double v) { return (float)v; }
+    __device__ __forceinline__ static float from_f32_rne(float v) { return v; }
     // round a float to T and return the T value as float
     __device__ __forceinline__ static float round32(float v) { return v; }
     __device__ __forceinline__ static void round32x2(float& a, float& b) {}
@@ -67,6 +68,9 @@ template <> struct Elem<uint16_t> {
     __device__ __forceinline__ static double to_f64(uint16_t v) { return (double)bf16_bits_to_f32(v); }
     __device__ __forceinline__ static uint16_t from_f32(float v) { return f32_to_bf16_bits(v); }
     __device__ __forceinline__ static uint16_t from_f64(double v) { return f32_to_bf16_bits(f64_to_f32_odd(v)); }
+    // from_f32 through the hardware conversion (round to nearest even; the same bits for
+    // every non-NaN input)
+    __device__ __forceinline__ static uint16_t from_f32_rne(float v) { return (uint16_t)(pack_bf16x2(v, v) & 0xffffu); }
     // through the hardware conversion (round to nearest even), as round32x2
     __device__ __forceinline__ static float round32(float v) { return __uint_as_float(pack_bf16x2(v, v) << 16); }
     // two values at once through the hardware conversion (round to nearest even)

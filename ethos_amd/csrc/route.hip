@@ -626,10 +626,14 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         st_a[t] = -1;
         st_b[t] = 0;
     }
+    // fr_b: the first column outside the staircase in row a = lane (a <= top_k, a < kc), or
+    // -1 when the row has none: the largest pair of the row outside the staircase
+    int fr_b = -1;
     {
         int nb = top_k < kc ? top_k : kc, cum = 0;
         for (int a = 0; a < kc; ++a) {
             while (nb > 0 && nb * (a + 1) > top_k) --nb;
+            if (lane == a && nb < kc) fr_b = nb;
             if (nb == 0) break;
 #pragma unroll
             for (int t = 0; t < kRtStSlots; ++t) {
@@ -671,6 +675,12 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         const bool in_a = lane < kc && ca >= theta;
         const bool in_b = lane < kc && cb >= theta;
         const int na = (int)__popcll(ballot(in_a)), nb = (int)__popcll(ballot(in_b));
+        // No pair outside the staircase exceeds theta, and within a row they do not
+        // increase with b (rows beyond top_k are bounded by row top_k), so unless one of
+        // the rows' first outside pairs equals theta there is no tie to merge in.
+        const uint64_t fk = shfl_u64(L2, fr_b >= 0 ? fr_b : 0);
+        const bool fr_tie = fr_b >= 0 && Elem<T>::round32(key_score(L1) + key_score(fk)) == theta;
+        if (ballot(fr_tie) != 0)
         for (int p0 = 0; p0 < na * nb; p0 += kWave) {
             const int p = p0 + lane;
             const bool in = p < na * nb;
@@ -688,7 +698,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         for (int i = 0; i < top_k; ++i) sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ex), i));
         if (lane < top_k) {
             out_ids[r * top_k + lane] = (int32_t)key_idx(run);
-            out_gates[r * top_k + lane] = Elem<T>::from_f32(ex / sum);
+            out_gates[r * top_k + lane] = Elem<T>::from_f32_rne(ex / sum);
         }
     }
 }
