@@ -385,8 +385,28 @@ size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int3
     return ethos::expert_forward_workspace_bytes(n_tok, n_heads, top_k, max_unique, d_model, d_hidden, dtype, order);
 }
 
+int ethos_token_proj(const void* x, const void* w2, const void* wut, int64_t n_tok, int32_t d_model,
+                     int32_t d_hidden, int32_t dtype, void* xp_out, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_token_proj: unknown dtype %d", dtype);
+    const int vec = dtype == ETHOS_BF16 ? 8 : 4;
+    if (n_tok < 0 || d_model <= 0 || d_hidden <= 0 || n_tok > INT32_MAX)
+        return fail(ETHOS_ESIZE, "ethos_token_proj: bad sizes");
+    if (d_model % vec || d_hidden % vec)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_token_proj: d_model and d_hidden must be multiples of %d", vec);
+    if (n_tok == 0) return 0;
+    if (!x || !w2 || !xp_out) return fail(ETHOS_ENULL, "ethos_token_proj: null pointer");
+    if (!aligned16(x) || !aligned16(w2) || (wut && !aligned16(wut)) || !aligned16(xp_out))
+        return fail(ETHOS_EALIGN, "ethos_token_proj: x, w2, wut and xp_out must be 16-byte aligned");
+    const int rc = ethos::launch_token_proj_out(x, w2, dtype == ETHOS_BF16 ? wut : nullptr, n_tok, d_model, d_hidden,
+                                                dtype, xp_out, (hipStream_t)stream);
+    if (rc < 0) return fail(ETHOS_ENULL, "ethos_token_proj: bf16 needs wut (W_u^T)");
+    return hip_status(rc, "ethos_token_proj");
+}
+
 int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                         const void* wut, const int32_t* uniq_ids, const int32_t* n_unique, int64_t max_unique,
+                         const void* wut, const void* xp, const int32_t* uniq_ids, const int32_t* n_unique,
+                         int64_t max_unique,
                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores,
                          int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_latent, int32_t d_hidden,
                          int32_t d_model, int32_t dtype, int32_t order, void* workspace, size_t workspace_bytes,
@@ -418,12 +438,12 @@ int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, 
     if (workspace_bytes < need)
         return fail(ETHOS_EWORKSPACE, "ethos_expert_forward: workspace of %zu bytes, %zu needed", workspace_bytes,
                     need);
-    if (!aligned16(x) || !aligned16(w1) || !aligned16(w2) || (wut && !aligned16(wut)) || !aligned16(workspace) ||
-        !aligned16(h_out) || !aligned16(out))
-        return fail(ETHOS_EALIGN, "ethos_expert_forward: x, w1, w2, wut, workspace, h_out and out must be 16-byte "
-                                  "aligned");
+    if (!aligned16(x) || !aligned16(w1) || !aligned16(w2) || (wut && !aligned16(wut)) || (xp && !aligned16(xp)) ||
+        !aligned16(workspace) || !aligned16(h_out) || !aligned16(out))
+        return fail(ETHOS_EALIGN, "ethos_expert_forward: x, w1, w2, wut, xp, workspace, h_out and out must be "
+                                  "16-byte aligned");
     const int rc = ethos::launch_expert_forward(x, latents, n_experts, w1, w2, dtype == ETHOS_BF16 ? wut : nullptr,
-                                                uniq_ids, n_unique, max_unique, perm, sorted_slot, pair_slot, scores,
+                                                xp, uniq_ids, n_unique, max_unique, perm, sorted_slot, pair_slot, scores,
                                                 n_tok, n_heads, top_k, d_latent, d_hidden, d_model, dtype, order,
                                                 workspace, h_out, out, num_cus(), (hipStream_t)stream);
     if (rc < 0) return fail(ETHOS_EUNSUPPORTED, "ethos_expert_forward: shape not supported");

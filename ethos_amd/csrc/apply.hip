@@ -771,6 +771,14 @@ static void launch_token_proj(const void* x, const void* w2, const void* wut_in,
                            (int)n_tok, d, dh, (float*)xp);
 }
 
+int launch_token_proj_out(const void* x, const void* w2, const void* wut, int64_t n_tok, int d, int dh, int dtype,
+                          void* xp, hipStream_t stream) {
+    // the bf16 MFMA form reads W_u^T; without it the kernel would transpose into scratch
+    if (dtype == kBF16 && d % kTpK == 0 && dh % 8 == 0 && wut == nullptr) return -1;
+    launch_token_proj(x, w2, wut, n_tok, 1, 1, d, dh, dtype, xp, stream);
+    return (int)hipGetLastError();
+}
+
 int launch_apply(const void* x, const void* w2, const void* hid, const void* v, const int32_t* perm,
                  const int32_t* sorted_slot, const int32_t* pair_slot, const void* gates, int64_t n_tok, int H, int k,
                  int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream) {
@@ -902,7 +910,8 @@ size_t expert_forward_workspace_bytes(int64_t n_tok, int H, int k, int64_t max_u
 }
 
 int launch_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                          const void* wut, const int32_t* uniq, const int32_t* n_unique, int64_t max_unique,
+                          const void* wut, const void* xp_in, const int32_t* uniq, const int32_t* n_unique,
+                          int64_t max_unique,
                           const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot,
                           const void* gates, int64_t n_tok, int H, int k, int dl, int dh, int d, int dtype, int order,
                           void* ws, void* hout, void* out, int num_cus, hipStream_t stream) {
@@ -930,9 +939,11 @@ int launch_expert_forward(const void* x, const void* latents, int64_t n_experts,
         stage_mark(stream);
         return rc;
     }
-    void* xp = ws;
+    // the token projection, unless the caller computed it (e.g. on another stream, while
+    // the routing ran)
+    void* xp = xp_in ? const_cast<void*>(xp_in) : ws;
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
-    launch_token_proj(x, w2, wut, n_tok, H, k, d, dh, dtype, ws, stream);
+    if (!xp_in) launch_token_proj(x, w2, wut, n_tok, H, k, d, dh, dtype, ws, stream);
     stage_mark(stream);
     int rc = launch_generate_part(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d, hout, v, 1,
                                   num_cus, stream);

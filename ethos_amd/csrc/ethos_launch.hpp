@@ -55,8 +55,12 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
                  int d, int dh, int dtype, void* ws, void* out, int num_cus, hipStream_t stream);
 size_t expert_forward_workspace_bytes(int64_t n_tok, int H, int k, int64_t max_unique, int d, int dh, int dtype,
                                       int order);
+// xp = RN_T(x W_u) into xp [n_tok, dh]; bf16 MFMA shapes need wut (-1 without it).
+int launch_token_proj_out(const void* x, const void* w2, const void* wut, int64_t n_tok, int d, int dh, int dtype,
+                          void* xp, hipStream_t stream);
 int launch_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                          const void* wut, const int32_t* uniq, const int32_t* n_unique, int64_t max_unique,
+                          const void* wut, const void* xp_in, const int32_t* uniq, const int32_t* n_unique,
+                          int64_t max_unique,
                           const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot,
                           const void* gates, int64_t n_tok, int H, int k, int dl, int dh, int d, int dtype, int order,
                           void* ws, void* hout, void* out, int num_cus, hipStream_t stream);

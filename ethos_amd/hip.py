@@ -222,12 +222,33 @@ def apply_hidden(x: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, seg: dict, 
     return out
 
 
+def token_proj(x: torch.Tensor, w2: torch.Tensor, wut: torch.Tensor | None = None) -> torch.Tensor:
+    """x_proj [n, d_hidden] = RN(x W_u), W_u = w2[:d] ([d, d_hidden]); bf16 needs wut = W_u^T
+    ([d_hidden, d]) for d % 64 == 0."""
+    _need(x, "x", dim=2)
+    _need(w2, "w2", x.dtype, 2)
+    n, d = x.shape
+    dh = w2.shape[1]
+    if w2.shape[0] != 2 * d:
+        raise RuntimeError("token_proj: w2 must be [2 d_model, d_hidden]")
+    if wut is not None:
+        _need(wut, "wut", x.dtype, 2)
+        if wut.shape != (dh, d):
+            raise RuntimeError("token_proj: wut must be [d_hidden, d_model]")
+    xp = torch.empty((n, dh), dtype=x.dtype, device=x.device)
+    rc = load().ethos_token_proj(x.data_ptr(), w2.data_ptr(), wut.data_ptr() if wut is not None else None, n, d, dh,
+                                 dtype_code(x.dtype), xp.data_ptr(), _stream())
+    check(rc, "ethos_token_proj")
+    return xp
+
+
 def expert_forward(x: torch.Tensor, latents: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, seg: dict,
                    gates: torch.Tensor, n_heads: int, top_k: int, hidden_space: bool = False,
-                   wut: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                   wut: torch.Tensor | None = None, xp: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """(out [n, d], h [max_unique, d_hidden]): generation, activations and scatter-back
     (or, hidden_space=True, the hidden-space form) in one call.  `wut`: optional bf16
-    W_u^T [d_hidden, d] (the transpose of w2[:d]) prepared by the caller."""
+    W_u^T [d_hidden, d] (the transpose of w2[:d]) prepared by the caller; `xp`: optional
+    token projection from token_proj (then not recomputed)."""
     _need(x, "x", dim=2)
     _need(latents, "latents", x.dtype, 2)
     _need(w1, "w1", x.dtype, 2)
@@ -242,6 +263,10 @@ def expert_forward(x: torch.Tensor, latents: torch.Tensor, w1: torch.Tensor, w2:
         _need(wut, "wut", x.dtype, 2)
         if wut.shape != (dh, d):
             raise RuntimeError("expert_forward: wut must be [d_hidden, d_model]")
+    if xp is not None:
+        _need(xp, "xp", x.dtype, 2)
+        if xp.shape != (n, dh):
+            raise RuntimeError("expert_forward: xp must be [n_tok, d_hidden]")
     code = dtype_code(x.dtype)
     order = 1 if hidden_space else 0
     max_u = seg["max_unique"]
@@ -250,7 +275,8 @@ def expert_forward(x: torch.Tensor, latents: torch.Tensor, w1: torch.Tensor, w2:
     h = torch.empty((max_u, dh), dtype=x.dtype, device=x.device)
     out = torch.empty_like(x)
     rc = load().ethos_expert_forward(x.data_ptr(), latents.data_ptr(), E, w1.data_ptr(), w2.data_ptr(),
-                                     wut.data_ptr() if wut is not None else None, seg["uniq"].data_ptr(),
+                                     wut.data_ptr() if wut is not None else None,
+                                     xp.data_ptr() if xp is not None else None, seg["uniq"].data_ptr(),
                                      seg["n_unique"].data_ptr(), max_u, seg["perm"].data_ptr(),
                                      seg["sorted_slot"].data_ptr(), seg["pair_slot"].data_ptr(), gates.data_ptr(), n,
                                      n_heads, top_k, dl, dh, d, code, order, ws.data_ptr(), ws_bytes, h.data_ptr(),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define ETHOS_ABI_VERSION 4
+#define ETHOS_ABI_VERSION 5
 
 #define ETHOS_F32 0
 #define ETHOS_BF16 1
@@ -220,6 +220,16 @@ int ethos_apply_scatter(const void* x, const void* w2, const void* h, const void
                         int32_t n_heads, int32_t top_k, int32_t d_model, int32_t d_hidden, int32_t dtype,
                         void* workspace, size_t workspace_bytes, void* out, void* stream);
 
+/*
+ * The token projection of the expert apply, x_proj = RN_T(x W_u) with W_u the first d_model
+ * rows of w2 (generation_network.net.2.weight), once per token -- the reference forms it
+ * inside the pair loop (model.py:326).  For ethos_expert_forward's xp argument.
+ *   x [n_tok, d_model], w2 [2 d_model, d_hidden], wut [d_hidden, d_model] (bf16: required
+ *   for d_model % 64 == 0; the transpose of w2's first d_model rows), xp_out [n_tok, d_hidden]
+ */
+int ethos_token_proj(const void* x, const void* w2, const void* wut, int64_t n_tok, int32_t d_model,
+                     int32_t d_hidden, int32_t dtype, void* xp_out, void* stream);
+
 /* Workspace size for ethos_expert_forward (order 0: layer order, 1: hidden-space order). */
 size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int64_t max_unique,
                                             int32_t d_model, int32_t d_hidden, int32_t dtype, int32_t order);
@@ -237,6 +247,9 @@ size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int3
  *   wut       bf16 only, may be NULL: W_u^T [d_hidden, d_model] (the transpose of the first
  *             d_model rows of w2) prepared by the caller, e.g. once per weight version;
  *             NULL transposes it into the workspace on every call
+ *   xp        may be NULL: the token projection [n_tok, d_hidden] dtype T from
+ *             ethos_token_proj (computed by the caller, e.g. on a second stream while the
+ *             routing runs); NULL computes it here
  *   workspace >= ethos_expert_forward_workspace_bytes(...) bytes (scratch)
  *   h_out     [max_unique, d_hidden] dtype T: the hidden rows (rows u < U written)
  *   out       [n_tok, d_model] dtype T
@@ -244,7 +257,8 @@ size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int3
  * and out 16-byte aligned.
  */
 int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                         const void* wut, const int32_t* uniq_ids, const int32_t* n_unique, int64_t max_unique,
+                         const void* wut, const void* xp, const int32_t* uniq_ids, const int32_t* n_unique,
+                         int64_t max_unique,
                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores,
                          int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_latent, int32_t d_hidden,
                          int32_t d_model, int32_t dtype, int32_t order, void* workspace, size_t workspace_bytes,

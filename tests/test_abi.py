@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ethos_abi_version() == 4
+    assert _lib.load().ethos_abi_version() == 5
 
 
 def _rc(fn, *args):
@@ -116,7 +116,7 @@ def test_sort_noalloc_rejects_pairs_beyond_its_static_workspace():
 
 def test_expert_forward_argument_errors():
     L = _lib.load()
-    args = [16, 16, 256, 16, 16, None, 16, 16, 64, 16, 16, 16, 16, 48, 2, 4, 16, 32, 64]
+    args = [16, 16, 256, 16, 16, None, None, 16, 16, 64, 16, 16, 16, 16, 48, 2, 4, 16, 32, 64]
     ws = L.ethos_expert_forward_workspace_bytes(48, 2, 4, 64, 64, 32, 1, 0)
     assert ws > 48 * 32 * 2 + 64 * 64 * 2
     assert L.ethos_expert_forward_workspace_bytes(48, 2, 4, 64, 64, 32, 1, 1) != ws
@@ -124,15 +124,31 @@ def test_expert_forward_argument_errors():
     assert L.ethos_expert_forward(*args, 7, 0, 16, ws, 16, 16, None) == -1
     assert L.ethos_expert_forward(*args, 1, 2, 16, ws, 16, 16, None) == -2
     bad = list(args)
-    bad[16] = 10
+    bad[17] = 10
     assert L.ethos_expert_forward(*bad, 1, 0, 16, ws, 16, 16, None) == -6
     assert L.ethos_expert_forward(*args, 1, 0, None, ws, 16, 16, None) == -3
     assert L.ethos_expert_forward(*args, 1, 0, 16, 8, 16, 16, None) == -5
     assert L.ethos_expert_forward(*args, 1, 0, 16, ws, 18, 16, None) == -4
     # an empty batch is a no-op success
     empty = list(args)
-    empty[13] = 0
+    empty[14] = 0
     assert L.ethos_expert_forward(*empty, 1, 0, None, 0, None, None, None) == 0
+    # a misaligned caller-provided token projection
+    misx = list(args)
+    misx[6] = 18
+    assert L.ethos_expert_forward(*misx, 1, 0, 16, ws, 16, 16, None) == -4
+
+
+def test_token_proj_argument_errors():
+    L = _lib.load()
+    assert L.ethos_token_proj(16, 16, 16, 4, 64, 32, 7, 16, None) == -1
+    assert L.ethos_token_proj(16, 16, 16, -1, 64, 32, 1, 16, None) == -2
+    assert L.ethos_token_proj(16, 16, 16, 4, 60, 32, 1, 16, None) == -6
+    assert L.ethos_token_proj(None, 16, 16, 4, 64, 32, 1, 16, None) == -3
+    assert L.ethos_token_proj(16, 16, 16, 4, 64, 32, 1, 18, None) == -4
+    # bf16 with d_model % 64 == 0 needs W_u^T
+    assert L.ethos_token_proj(16, 16, None, 4, 64, 32, 1, 16, None) == -3
+    assert L.ethos_token_proj(None, None, None, 0, 64, 32, 1, None, None) == 0
 
 
 def test_stage_events_argument_errors():

@@ -458,11 +458,25 @@ def test_expert_forward_matches_separate_calls(name, hidden_space):
     wut = w2[: sh.d_model].t().contiguous() if sh.dtype == "bf16" else None
     got, h2 = hip.expert_forward(xd, lat, w1, w2, seg, g, sh.num_heads, sh.top_k, hidden_space=hidden_space, wut=wut)
     got_nowut, _ = hip.expert_forward(xd, lat, w1, w2, seg, g, sh.num_heads, sh.top_k, hidden_space=hidden_space)
+    # the token projection computed beforehand (ethos_token_proj) and passed in
+    xp = hip.token_proj(xd, w2, wut)
+    got_xp, _ = hip.expert_forward(xd, lat, w1, w2, seg, g, sh.num_heads, sh.top_k, hidden_space=hidden_space,
+                                   wut=wut, xp=xp)
     torch.cuda.synchronize()
     U = int(seg["n_unique"].item())
     assert np.array_equal(to_host(h2)[:U], to_host(h)[:U])
     assert np.array_equal(to_host(got), to_host(want))
     assert np.array_equal(to_host(got_nowut), to_host(want))
+    assert np.array_equal(to_host(got_xp), to_host(want))
+    # x_proj itself: fp32 MFMA accumulation rounded once, against the oracle's fp64 product
+    # rounded once -- one rounding step apart, plus the fp32 accumulation error on
+    # cancelling sums
+    xr = O.to_f32(O.token_proj(x, P["W2"], sh.dtype), sh.dtype)
+    xg = O.to_f32(to_host(xp), sh.dtype)
+    ulp = 2.0 ** -7 if sh.dtype == "bf16" else 2.0 ** -22
+    bad = np.abs(xg - xr) > ulp * np.abs(xr) + 2.0 ** -16 * np.abs(xr).max()
+    assert not bad.any(), (f"{bad.sum()} of {bad.size}; shapes {xg.shape} {xr.shape}; first {np.argwhere(bad)[:3]} "
+                           f"got {xg[bad][:3]} want {xr[bad][:3]}")
 
 
 def test_stage_events_recorded_in_expert_forward():
