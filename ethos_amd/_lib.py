@@ -44,8 +44,9 @@ SIGNATURES = {
     "ethos_expert_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                              _vp]),
     "ethos_expert_forward_workspace_bytes": (_sz, [_i64, _i32, _i32, _i64, _i32, _i32, _i32, _i32]),
-    "ethos_expert_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
-                                            _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _vp, _vp]),
+    "ethos_expert_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                                            _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _vp,
+                                            _vp]),
     "ethos_token_proj": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp]),
     "ethos_apply_hidden_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ethos_apply_hidden": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,

@@ -405,8 +405,8 @@ int ethos_token_proj(const void* x, const void* w2, const void* wut, int64_t n_t
 }
 
 int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                         const void* wut, const void* xp, const int32_t* uniq_ids, const int32_t* n_unique,
-                         int64_t max_unique,
+                         const void* wut, const void* xp, const int32_t* uniq_ids, const int32_t* seg_off,
+                         const int32_t* n_unique, int64_t max_unique,
                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores,
                          int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_latent, int32_t d_hidden,
                          int32_t d_model, int32_t dtype, int32_t order, void* workspace, size_t workspace_bytes,
@@ -430,8 +430,8 @@ int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, 
                     d_model);
     if (n_tok == 0) return 0;
     if (max_unique < 1) return fail(ETHOS_ESIZE, "ethos_expert_forward: max_unique must be >= 1 for a nonempty batch");
-    if (!x || !latents || !w1 || !w2 || !uniq_ids || !n_unique || !perm || !sorted_slot || !pair_slot || !scores ||
-        !workspace || !h_out || !out)
+    if (!x || !latents || !w1 || !w2 || !uniq_ids || !seg_off || !n_unique || !perm || !sorted_slot || !pair_slot ||
+        !scores || !workspace || !h_out || !out)
         return fail(ETHOS_ENULL, "ethos_expert_forward: null pointer");
     const size_t need = ethos::expert_forward_workspace_bytes(n_tok, n_heads, top_k, max_unique, d_model, d_hidden,
                                                               dtype, order);
@@ -443,7 +443,8 @@ int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, 
         return fail(ETHOS_EALIGN, "ethos_expert_forward: x, w1, w2, wut, xp, workspace, h_out and out must be "
                                   "16-byte aligned");
     const int rc = ethos::launch_expert_forward(x, latents, n_experts, w1, w2, dtype == ETHOS_BF16 ? wut : nullptr,
-                                                xp, uniq_ids, n_unique, max_unique, perm, sorted_slot, pair_slot, scores,
+                                                xp, uniq_ids, seg_off, n_unique, max_unique, perm, sorted_slot,
+                                                pair_slot, scores,
                                                 n_tok, n_heads, top_k, d_latent, d_hidden, d_model, dtype, order,
                                                 workspace, h_out, out, num_cus(), (hipStream_t)stream);
     if (rc < 0) return fail(ETHOS_EUNSUPPORTED, "ethos_expert_forward: shape not supported");

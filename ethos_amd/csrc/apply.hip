@@ -190,22 +190,6 @@ __global__ __launch_bounds__(256) void token_proj_kernel(const T* __restrict__ x
 
 constexpr int kActGroup = 4;  // pairs whose loads are in flight together
 
-// a . b + acc over one lane's raw slice (fp32 accumulation; bf16 pairs by v_dot2c_f32_bf16)
-typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float dot_raw(const uint4& a, const uint4& b, float acc) {
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.x), __builtin_bit_cast(bf16x2_v, b.x), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.y), __builtin_bit_cast(bf16x2_v, b.y), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.z), __builtin_bit_cast(bf16x2_v, b.z), acc, false);
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.w), __builtin_bit_cast(bf16x2_v, b.w), acc,
-                                           false);
-}
-__device__ __forceinline__ float dot_raw(const float4& a, const float4& b, float acc) {
-    acc = __builtin_fmaf(a.x, b.x, acc);
-    acc = __builtin_fmaf(a.y, b.y, acc);
-    acc = __builtin_fmaf(a.z, b.z, acc);
-    return __builtin_fmaf(a.w, b.w, acc);
-}
-
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
                                                         const int32_t* __restrict__ perm,
@@ -260,17 +244,13 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
 // and works through them 8 at a time: lane l serves pair l / 8 of the group and holds the
 // 16-byte pieces (l % 8) + 8 i, i < P, of its h row and its xp row, so each load
 // instruction reads 8 whole 128-byte lines.  Per lane: P pieces of dot products in fp32,
-// then a 3-step reduction over the pair's 8 lanes; the 64 dot products wait in LDS and
-// the epilogue (rounding, GELU, gate) runs once per 64 pairs, one pair per lane.
-// P = pieces per lane: dh <= 64 P elements (bf16) or 32 P (fp32).
+// then a 3-step reduction over the pair's 8 lanes (act_reduce8); the 64 dot products wait
+// in LDS and the epilogue (act_epilogue: rounding, GELU, gate) runs once per 64 pairs, one
+// pair per lane.  P = pieces per lane: dh <= 64 P elements (bf16) or 32 P (fp32).
+// With seg_off given (after the hidden-row kernel has computed the activations of the
+// tiles it could), the expert-order walk takes only the pairs of tiles of kActTileRows
+// unique experts with more than kActFusedCap pairs; chunks without such pairs are skipped.
 constexpr int kAct8Waves = 4;
-
-// Token order for the activations, taken when the hidden rows of all unique experts fit
-// in a cache (at most this many bytes): one wave per token holds the token's projection in
-// registers and reads the hidden rows of its H*k pairs, which stay cache-resident, instead
-// of gathering one projection row per pair.  Same lanes, same per-lane dot products and
-// same reduction as the expert-order walk, so the results are bit-identical.
-constexpr int64_t kActTokenOrderMaxHBytes = 8 << 20;
 
 template <typename T, int P>
 __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
@@ -278,6 +258,7 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
                                                                      const int32_t* __restrict__ sorted_slot,
                                                                      const int32_t* __restrict__ pair_slot,
                                                                      const int32_t* __restrict__ n_unique,
+                                                                     const int32_t* __restrict__ seg_off,
                                                                      const T* __restrict__ gates, int64_t n_pairs,
                                                                      int hk, int dh, float* __restrict__ act) {
     constexpr int N = Vec16<T>::kN;
@@ -316,17 +297,13 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
                     float acc = 0.0f;
 #pragma unroll
                     for (int i = 0; i < P; ++i) acc = dot_raw(hv[i], xv[i], acc);
-                    acc += dpp_f32<kDppXor1>(acc);
-                    acc += dpp_f32<kDppXor2>(acc);
-                    acc += dpp_f32<kDppRowHalfMirror>(acc);
+                    acc = act_reduce8(acc);
                     if (part == 0) dots[wave][g + slot] = acc;
                 }
                 __builtin_amdgcn_wave_barrier();
                 if (lane < cnt) {
                     const int64_t p = pbase + j0 + lane;
-                    const float gt = Elem<T>::to_f32(gates[p]);
-                    const float a = Elem<T>::round32(gelu_erf(Elem<T>::round32(dots[wave][lane])));
-                    act[p] = Elem<T>::round32(a * gt);
+                    act[p] = act_epilogue<T>(dots[wave][lane], Elem<T>::to_f32(gates[p]));
                 }
                 __builtin_amdgcn_wave_barrier();
             }
@@ -334,11 +311,20 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
         return;
     }
     const int64_t n_chunks = (n_pairs + 63) / 64;
+    const int U = seg_off != nullptr ? *n_unique : 0;
     for (int64_t chunk = wave_id; chunk < n_chunks; chunk += n_waves) {
         const int64_t i0 = chunk * 64;
         const int cnt = (int)min((int64_t)64, n_pairs - i0);
-        const int my_p = lane < cnt ? perm[i0 + lane] : 0;
         const int my_s = lane < cnt ? sorted_slot[i0 + lane] : 0;
+        bool mine = lane < cnt;
+        if (seg_off != nullptr && mine) {
+            // pairs of tiles within the cap were done by the hidden-row kernel
+            const int t0 = my_s - my_s % kActTileRows;
+            const int t1 = t0 + kActTileRows < U ? t0 + kActTileRows : U;
+            mine = (int64_t)seg_off[t1] - (int64_t)seg_off[t0] > kActFusedCap;
+        }
+        if (ballot(mine) == 0) continue;
+        const int my_p = mine ? perm[i0 + lane] : 0;
         for (int g = 0; g < cnt; g += 8) {
             // this lane's pair of the group (a tail group repeats the last pair)
             const int src = g + slot < cnt ? g + slot : cnt - 1;
@@ -357,17 +343,11 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
 #pragma unroll
             for (int i = 0; i < P; ++i) acc = dot_raw(hv[i], xv[i], acc);
             // sum over the pair's 8 lanes (lanes 8 slot .. 8 slot + 7)
-            acc += dpp_f32<kDppXor1>(acc);
-            acc += dpp_f32<kDppXor2>(acc);
-            acc += dpp_f32<kDppRowHalfMirror>(acc);
+            acc = act_reduce8(acc);
             if (part == 0) dots[wave][g + slot] = acc;
         }
         __builtin_amdgcn_wave_barrier();
-        if (lane < cnt) {
-            const float g = Elem<T>::to_f32(gates[my_p]);
-            const float a = Elem<T>::round32(gelu_erf(Elem<T>::round32(dots[wave][lane])));
-            act[my_p] = Elem<T>::round32(a * g);
-        }
+        if (mine) act[my_p] = act_epilogue<T>(dots[wave][lane], Elem<T>::to_f32(gates[my_p]));
         __builtin_amdgcn_wave_barrier();
     }
 }
@@ -649,29 +629,31 @@ static void launch_scatter_t(const void* v, const int32_t* pair_slot, const floa
 
 template <typename T, int P>
 static void launch_act8_t(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
-                          const int32_t* pair_slot, const int32_t* n_unique, const void* gates, int64_t n_pairs,
-                          int hk, int dh, float* act, int num_cus, hipStream_t stream) {
+                          const int32_t* pair_slot, const int32_t* n_unique, const int32_t* seg_off, const void* gates,
+                          int64_t n_pairs, int hk, int dh, float* act, int num_cus, hipStream_t stream) {
     const int64_t cap = (int64_t)num_cus * 16;
     int64_t g1 = ((n_pairs + 63) / 64 + kAct8Waves - 1) / kAct8Waves;
     g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
     hipLaunchKernelGGL((apply_act8_kernel<T, P>), dim3((unsigned)g1), dim3(kAct8Waves * 64), 0, stream, (const T*)xp,
-                       (const T*)hid, perm, sorted_slot, pair_slot, n_unique, (const T*)gates, n_pairs, hk, dh, act);
+                       (const T*)hid, perm, sorted_slot, pair_slot, n_unique, seg_off, (const T*)gates, n_pairs, hk, dh,
+                       act);
 }
 
 // Per-pair activations a_p (phase 1): 8 lanes per pair for rows of up to 64 pieces of 16
 // bytes (d_hidden <= 512 bf16 / 256 fp32), one wave per pair beyond; -1 past the limits.
 // With pair_slot and the device count n_unique given, the 8-lane kernel takes token order
-// when the hidden rows are few (kActTokenOrderMaxHBytes).
+// when the hidden rows are few (kActTokenOrderMaxHBytes).  With seg_off given too, only
+// the pairs the hidden-row kernel left (tiles over kActFusedCap pairs) are computed.
 static int launch_act(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
-                      const int32_t* pair_slot, const int32_t* n_unique, const void* gates, int64_t n_pairs, int hk,
-                      int dh, int dtype, float* act, int num_cus, hipStream_t stream) {
+                      const int32_t* pair_slot, const int32_t* n_unique, const int32_t* seg_off, const void* gates,
+                      int64_t n_pairs, int hk, int dh, int dtype, float* act, int num_cus, hipStream_t stream) {
     const int pieces = (dh + (dtype == kBF16 ? 8 : 4) - 1) / (dtype == kBF16 ? 8 : 4);
     const int pp = (pieces + 7) / 8;
     const int P = pp <= 1 ? 1 : pp <= 2 ? 2 : pp <= 4 ? 4 : pp <= 8 ? 8 : 0;
 #define ETHOS_ACT8_CASE(TT, PP)                                                                                \
     if (P == PP) {                                                                                             \
-        launch_act8_t<TT, PP>(xp, hid, perm, sorted_slot, pair_slot, n_unique, gates, n_pairs, hk, dh, act,     \
-                              num_cus, stream);                                                                \
+        launch_act8_t<TT, PP>(xp, hid, perm, sorted_slot, pair_slot, n_unique, seg_off, gates, n_pairs, hk, dh, \
+                              act, num_cus, stream);                                                           \
         return 0;                                                                                              \
     }
     if (dtype == kBF16) {
@@ -681,6 +663,7 @@ static int launch_act(const void* xp, const void* hid, const int32_t* perm, cons
         ETHOS_ACT8_CASE(float, 1) ETHOS_ACT8_CASE(float, 2) ETHOS_ACT8_CASE(float, 4) ETHOS_ACT8_CASE(float, 8)
     }
 #undef ETHOS_ACT8_CASE
+    if (seg_off != nullptr) return -1;  // the remainder walk exists in the 8-lane kernel only
     const int c = apply_chunks(dh, dtype);
     const int ch = c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : c <= 8 ? 8 : 0;
 #define ETHOS_ACT_CASE(TT, CC)                                                                                 \
@@ -790,8 +773,8 @@ int launch_apply(const void* x, const void* w2, const void* hid, const void* v, 
                         : nullptr;
     if (apply_chunks(dh, dtype) > 8 || apply_chunks(d, dtype) > 8) return -1;
     launch_token_proj(x, w2, nullptr, n_tok, H, k, d, dh, dtype, ws, stream);
-    launch_act(xp, hid, perm, sorted_slot, nullptr, nullptr, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus,
-               stream);
+    launch_act(xp, hid, perm, sorted_slot, nullptr, nullptr, nullptr, gates, n_tok * H * k, H * k, dh, dtype, act,
+               num_cus, stream);
     launch_scatter(v, pair_slot, act, n_tok, H, k, d, dtype, headbuf, out, num_cus, stream);
     return (int)hipGetLastError();
 }
@@ -835,8 +818,8 @@ int launch_apply_hidden(const void* x, const void* w2, const void* hid, const in
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
     if (apply_chunks(dh, dtype) > 8) return -1;
     launch_token_proj(x, w2, nullptr, n_tok, H, k, d, dh, dtype, ws, stream);
-    launch_act(xp, hid, perm, sorted_slot, nullptr, nullptr, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus,
-               stream);
+    launch_act(xp, hid, perm, sorted_slot, nullptr, nullptr, nullptr, gates, n_tok * H * k, H * k, dh, dtype, act,
+               num_cus, stream);
     return launch_hidden_tail(w2, hid, pair_slot, act, n_tok, H, k, d, dh, dtype, ws, out, num_cus, stream);
 }
 
@@ -891,9 +874,10 @@ static int launch_hidden_tail(const void* w2, const void* hid, const int32_t* pa
 // The expert stages as one call (generation, apply, scatter-back) on the sorted pairs.
 // Order 0 (the layer's rounding points): xp, h rows, activations, v rows, scatter-back;
 // order 1 (hidden-space reordering): xp, h rows, activations, per-token hidden sums,
-// projection back.  With the two-kernel bf16 generator the activations run between its
-// kernels, while the freshly written h rows are still in the memory-side cache; other
-// shapes generate first (one kernel) and apply after.
+// projection back.  With the two-kernel bf16 generator the hidden-row kernel computes the
+// activations of its tiles' pairs from the rows it has just staged in LDS (so h is not
+// read back for them), and the activation kernel takes what it leaves; other shapes
+// generate first (one kernel) and apply after.
 // Workspace: the apply workspace of the order, then (order 0) v [max_unique, d].
 // ---------------------------------------------------------------------------------
 static size_t order_ws_bytes(int64_t n_tok, int H, int k, int d, int dh, int dtype, int order) {
@@ -910,8 +894,8 @@ size_t expert_forward_workspace_bytes(int64_t n_tok, int H, int k, int64_t max_u
 }
 
 int launch_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                          const void* wut, const void* xp_in, const int32_t* uniq, const int32_t* n_unique,
-                          int64_t max_unique,
+                          const void* wut, const void* xp_in, const int32_t* uniq, const int32_t* seg_off,
+                          const int32_t* n_unique, int64_t max_unique,
                           const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot,
                           const void* gates, int64_t n_tok, int H, int k, int dl, int dh, int d, int dtype, int order,
                           void* ws, void* hout, void* out, int num_cus, hipStream_t stream) {
@@ -945,12 +929,16 @@ int launch_expert_forward(const void* x, const void* latents, int64_t n_experts,
     float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + align256((size_t)n_tok * dh * eb));
     if (!xp_in) launch_token_proj(x, w2, wut, n_tok, H, k, d, dh, dtype, ws, stream);
     stage_mark(stream);
-    int rc = launch_generate_part(latents, n_experts, uniq, n_unique, max_unique, w1, w2, dl, dh, d, hout, v, 1,
-                                  num_cus, stream);
+    // the hidden rows, with the activations of every tile of at most kActFusedCap pairs
+    // computed while its rows are in LDS; then the activation kernel for the rest (the
+    // pairs of larger tiles, or all pairs in token order when the hidden rows are few)
+    int rc = launch_hidden_act(latents, n_experts, uniq, n_unique, max_unique, w1, dl, dh, hout, xp, perm,
+                               sorted_slot, seg_off, gates, H * k, act, num_cus, stream);
     if (rc != 0) return rc;
     stage_mark(stream);
-    launch_act(xp, hout, perm, sorted_slot, pair_slot, n_unique, gates, n_tok * H * k, H * k, dh, dtype, act, num_cus,
-               stream);
+    rc = launch_act(xp, hout, perm, sorted_slot, pair_slot, n_unique, seg_off, gates, n_tok * H * k, H * k, dh, dtype,
+                    act, num_cus, stream);
+    if (rc != 0) return rc;
     stage_mark(stream);
     if (order == 1) {
         stage_mark(stream);

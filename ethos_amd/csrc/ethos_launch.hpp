@@ -41,6 +41,14 @@ int launch_generate_part(const void* latents, int64_t n_experts, const int32_t* 
                          int64_t max_unique, const void* w1, const void* w2, int dl, int dh, int d, void* hout,
                          void* vout, int part, int num_cus, hipStream_t stream);
 
+// The bf16 hidden rows (part 1) with the activations of their pairs computed in the same
+// kernel for tiles of at most kActFusedCap pairs (act[p] for those pairs; the rest are left
+// for the activation kernel with seg_off); -1 when not supported.
+int launch_hidden_act(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
+                      int64_t max_unique, const void* w1, int dl, int dh, void* hout, const void* xp,
+                      const int32_t* perm, const int32_t* sorted_slot, const int32_t* seg_off, const void* gates, int hk,
+                      float* act, int num_cus, hipStream_t stream);
+
 int apply_chunks(int d, int dtype);
 int launch_expert_backward(const void* hid, const float* xp, const float* dyb, const int32_t* pair_slot,
                            const void* gates, int64_t n_tok, int H, int k, int dh, int dtype, float* dg, float* hacc,
@@ -59,8 +67,8 @@ size_t expert_forward_workspace_bytes(int64_t n_tok, int H, int k, int64_t max_u
 int launch_token_proj_out(const void* x, const void* w2, const void* wut, int64_t n_tok, int d, int dh, int dtype,
                           void* xp, hipStream_t stream);
 int launch_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                          const void* wut, const void* xp_in, const int32_t* uniq, const int32_t* n_unique,
-                          int64_t max_unique,
+                          const void* wut, const void* xp_in, const int32_t* uniq, const int32_t* seg_off,
+                          const int32_t* n_unique, int64_t max_unique,
                           const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot,
                           const void* gates, int64_t n_tok, int H, int k, int dl, int dh, int d, int dtype, int order,
                           void* ws, void* hout, void* out, int num_cus, hipStream_t stream);

@@ -37,6 +37,55 @@ template <> struct Vec16<float> {
     __device__ __forceinline__ static raw pack(const float* f) { return make_float4(f[0], f[1], f[2], f[3]); }
 };
 
+// a . b + acc over one lane's raw slice (fp32 accumulation; bf16 pairs by v_dot2c_f32_bf16)
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot_raw(const uint4& a, const uint4& b, float acc) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.x), __builtin_bit_cast(bf16x2_v, b.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.y), __builtin_bit_cast(bf16x2_v, b.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.z), __builtin_bit_cast(bf16x2_v, b.z), acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.w), __builtin_bit_cast(bf16x2_v, b.w), acc,
+                                           false);
+}
+__device__ __forceinline__ float dot_raw(const float4& a, const float4& b, float acc) {
+    acc = __builtin_fmaf(a.x, b.x, acc);
+    acc = __builtin_fmaf(a.y, b.y, acc);
+    acc = __builtin_fmaf(a.z, b.z, acc);
+    return __builtin_fmaf(a.w, b.w, acc);
+}
+
+// Per-pair activations a_p = RN_T(RN_T(gelu(RN_T(h_s . xp_t))) g_p), the arithmetic every
+// activation kernel shares: the pair's 8 lanes hold pieces part + 8 i (i < P) of both rows
+// (16 bytes each), each lane sums its pieces in order with dot_raw, and the 8 lanes reduce
+// by three DPP steps (xor 1, xor 2, half-row mirror).  Kernels that follow this recipe give
+// bit-identical activations whatever order they visit the pairs in.
+__device__ __forceinline__ float act_reduce8(float acc) {
+    acc += dpp_f32<kDppXor1>(acc);
+    acc += dpp_f32<kDppXor2>(acc);
+    acc += dpp_f32<kDppRowHalfMirror>(acc);
+    return acc;
+}
+template <typename T>
+__device__ __forceinline__ float act_epilogue(float dot, float gate) {
+    const float a = Elem<T>::round32(gelu_erf(Elem<T>::round32(dot)));
+    return Elem<T>::round32(a * gate);
+}
+
+// Token order for the activations, taken when the hidden rows of all unique experts fit
+// in a cache (at most this many bytes): one wave per token holds the token's projection in
+// registers and reads the hidden rows of its H*k pairs, which stay cache-resident, instead
+// of gathering one projection row per pair.  Same lanes, same per-lane dot products and
+// same reduction as the expert-order walk, so the results are bit-identical.
+constexpr int64_t kActTokenOrderMaxHBytes = 8 << 20;
+
+// Activations inside the bf16 hidden-row kernel: when the expert order applies (more
+// hidden-row bytes than kActTokenOrderMaxHBytes), the hidden-row kernel computes the
+// activations of every tile of kActTileRows unique experts whose pairs number at most
+// kActFusedCap, from the tile's rows while they are still in LDS.  The pairs of larger
+// tiles (a few hot experts) are left to the activation kernel, which spreads them over
+// the whole GPU instead of one workgroup.
+constexpr int kActTileRows = 64;
+constexpr int64_t kActFusedCap = 2048;
+
 // Load a d-long row into per-lane registers: element e = c*64*N + lane*N + v.
 template <typename T, int CH>
 __device__ __forceinline__ void load_row(const T* __restrict__ row, int d, int lane, float (&f)[CH * Vec16<T>::kN]) {

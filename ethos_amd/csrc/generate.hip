@@ -19,6 +19,7 @@
 #include "ethos_common.hpp"
 #include "ethos_launch.hpp"
 #include "ethos_mfma.hpp"
+#include "ethos_rows.hpp"
 
 namespace ethos {
 
@@ -181,13 +182,117 @@ __device__ const uint16_t kGeluLut[kGeluLutSize] = {
 // ---------------------------------------------------------------------------------
 constexpr int kHsRows = 64;       // experts per tile
 constexpr int kHsMaxTiles = 32;   // tiles per workgroup whose ids fit the LDS id table
+static_assert(kHsRows == kActTileRows, "activation tiles are the hidden-row tiles");
 
-template <int DL, int DH>
+// What the hidden-row kernel needs to compute the activations of a tile's pairs
+// (a_p = RN(RN(gelu(RN(h_s . xp_t))) g_p), the apply's phase 1) while the tile's rows are
+// in LDS.
+struct HiddenActArgs {
+    const uint16_t* xp;          // [n_tok, DH] token projections x W_u
+    const int32_t* perm;         // sorted position -> pair
+    const int32_t* sorted_slot;  // sorted position -> unique slot
+    const int32_t* seg_off;      // [U + 1] first sorted position of each unique slot
+    const uint16_t* gates;       // [n_pairs]
+    int hk;                      // pairs per token (heads x top_k)
+    float* act;                  // [n_pairs] activations (fp32 holding bf16 values)
+};
+
+// A tile's activations: its sorted positions and this lane's pair of the first round,
+// loaded at the top of the tile's iteration, so that the loads have landed by the time
+// the tile's rows are staged.
+struct ActMeta {
+    int64_t s0, s1;  // the tile's pairs: sorted positions s0 .. s1 - 1
+    int p, s;        // this lane's pair of the first round and its row in the tile
+    bool valid;
+};
+
+template <int kWaves>
+__device__ __forceinline__ int64_t act_position(int64_t r0, int wave, int lane) {
+    return r0 + 8 * (wave + kWaves * (lane >> 3)) + (lane & 7);
+}
+
+template <int kWaves>
+__device__ __forceinline__ ActMeta act_meta(const HiddenActArgs& A, int64_t row0, int live, int wave, int lane) {
+    ActMeta m;
+    m.s0 = A.seg_off[row0];
+    m.s1 = A.seg_off[row0 + live];
+    const int64_t j = act_position<kWaves>(m.s0, wave, lane);
+    m.valid = j < m.s1 && m.s1 - m.s0 <= kActFusedCap;
+    m.p = m.valid ? A.perm[j] : 0;
+    m.s = m.valid ? A.sorted_slot[j] - (int)row0 : 0;
+    return m;
+}
+
+// The activations of one tile's pairs (sorted positions s0 .. s1 - 1) from the tile's
+// staged hidden rows, when they number at most kActFusedCap (larger tiles are left to the
+// activation kernel).  Rounds of 64 pairs per wave: lane l of wave w holds the metadata of
+// sorted position r0 + 8 (w + waves (l / 8)) + l % 8 (act_position), so the wave's groups
+// of 8 consecutive pairs interleave with the other waves' and a tile's ~170 pairs spread
+// over all waves.  Per group, lane (q, part) serves the group's pair q with the pieces
+// part + 8 i of the pair's xp row (global) and hidden row (staged: piece part + 8 i is
+// 16-byte group `part` of wave area i), with the arithmetic of apply_act8_kernel
+// (dot_raw in piece order, act_reduce8, act_epilogue), so the activations are
+// bit-identical to it.  Two groups' xp rows are requested before either is summed.
+template <int DH, int kWaves>
+__device__ __forceinline__ void tile_activations(const HiddenActArgs& A, const u32x4_t (*stg)[kHsRows * 8],
+                                                 float* dsm, int64_t row0, const ActMeta& m, int wave, int lane) {
+    constexpr int P = DH / 64;
+    if (m.s1 - m.s0 > kActFusedCap) return;
+    const int part = lane & 7, q = lane >> 3;
+    auto piece = [&](int sl, int i) { return __builtin_bit_cast(uint4, stg[i][sl * 8 + (part ^ (sl & 7))]); };
+    for (int64_t r0 = m.s0; r0 < m.s1; r0 += 64 * kWaves) {
+        int my_p = m.p, my_s = m.s;
+        bool valid = m.valid;
+        if (r0 != m.s0) {
+            const int64_t j = act_position<kWaves>(r0, wave, lane);
+            valid = j < m.s1;
+            my_p = valid ? A.perm[j] : 0;
+            my_s = valid ? A.sorted_slot[j] - (int)row0 : 0;
+        }
+        my_s = my_s < 0 ? 0 : (my_s < kHsRows ? my_s : kHsRows - 1);  // stays inside the tile on any input
+        const uint16_t my_g = valid ? A.gates[my_p] : (uint16_t)0;
+        // this wave's groups of the round: group gi starts at r0 + 8 (wave + waves gi)
+        const int64_t left = m.s1 - r0 - 8 * wave;
+        const int ng = left <= 0 ? 0 : (int)min((int64_t)8, (left + 8 * kWaves - 1) / (8 * kWaves));
+        for (int gi = 0; gi < ng; gi += 2) {
+            const bool two = gi + 1 < ng;
+            const int sa = gi * 8 + q, sb = sa + 8;
+            const int pa = __shfl(my_p, sa, 64), la = __shfl(my_s, sa, 64);
+            const int pb = __shfl(my_p, two ? sb : sa, 64), lb = __shfl(my_s, two ? sb : sa, 64);
+            const uint16_t* xra = A.xp + (int64_t)(pa / A.hk) * DH;
+            const uint16_t* xrb = A.xp + (int64_t)(pb / A.hk) * DH;
+            uint4 xa[P], xb[P];
+#pragma unroll
+            for (int i = 0; i < P; ++i) xa[i] = *reinterpret_cast<const uint4*>(xra + (part + 8 * i) * 8);
+            if (two) {
+#pragma unroll
+                for (int i = 0; i < P; ++i) xb[i] = *reinterpret_cast<const uint4*>(xrb + (part + 8 * i) * 8);
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < P; ++i) acc = dot_raw(piece(la, i), xa[i], acc);
+            acc = act_reduce8(acc);
+            if (part == 0) dsm[sa] = acc;
+            if (two) {
+                acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < P; ++i) acc = dot_raw(piece(lb, i), xb[i], acc);
+                acc = act_reduce8(acc);
+                if (part == 0) dsm[sb] = acc;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (valid) A.act[my_p] = act_epilogue<uint16_t>(dsm[lane], bf16_bits_to_f32(my_g));
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+template <int DL, int DH, bool kAct>
 __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __restrict__ latents, int64_t n_experts,
                                                             const int32_t* __restrict__ uniq,
                                                             const int32_t* __restrict__ n_unique, int64_t max_unique,
                                                             const uint16_t* __restrict__ w1,
-                                                            uint16_t* __restrict__ hout) {
+                                                            uint16_t* __restrict__ hout, HiddenActArgs A) {
     constexpr int kWaves = DH / 64;
     constexpr int KS1 = DL / 16;                 // k-steps
     constexpr int PPR = DL / 8;                  // 16-byte pieces per latent row
@@ -200,6 +305,7 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
     __shared__ uint4 zs[2][kHsRows * PPR];
     __shared__ u32x4_t stg[kWaves][kHsRows * 8];
     __shared__ int32_t ids_s[kHsMaxTiles][kHsRows];
+    __shared__ float dsm[kAct ? kWaves : 1][64];  // per-wave dot products of the activations
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
@@ -207,6 +313,8 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
     const int n_tiles = (U + kHsRows - 1) / kHsRows;
     const int G = gridDim.x;
     const int hid0 = wave * 64;
+    // activations here unless the token order applies (few hidden-row bytes)
+    const bool act_on = kAct && (int64_t)U * DH * (int64_t)sizeof(uint16_t) > kActTokenOrderMaxHBytes;
 
     // the GELU table and this workgroup's tile ids (-1 past U or for ids outside the table)
     for (int e = tid; e < kGeluMcSize; e += DH) gmc[e] = gelu_mc_entry(e, kGeluLut);
@@ -269,6 +377,12 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
     for (int64_t t = blockIdx.x; t < n_tiles; t += G, ++i) {
         __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this tile's rows have landed
         __syncthreads();
+        const int64_t row0 = t * kHsRows;
+        const int live = U - (int)row0 < kHsRows ? U - (int)row0 : kHsRows;
+        ActMeta meta{};
+        if constexpr (kAct) {
+            if (act_on) meta = act_meta<kWaves>(A, row0, live, wave, lane);
+        }
         u32x4_t outv[kNSt];
 #pragma unroll
         for (int k = 0; k < kNSt; ++k) {
@@ -324,11 +438,17 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
                         gelu_bf16x2_mc(pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3]), mc_bytes)};
                 }
         }
-        const int64_t row0 = t * kHsRows;
-        const int live = U - (int)row0 < kHsRows ? U - (int)row0 : kHsRows;
         hr_prev = __builtin_amdgcn_make_buffer_rsrc(hout + row0 * DH, (short)0, live * DH * (int)sizeof(uint16_t),
                                                     0x00020000);
         have_prev = true;
+        if constexpr (kAct) {
+            if (act_on) {
+                // every wave's rows of this tile are staged; the next tile's staging writes
+                // wait for the barrier at the top of the next iteration
+                __syncthreads();
+                tile_activations<DH, kWaves>(A, stg, dsm[wave], row0, meta, wave, lane);
+            }
+        }
     }
     if (have_prev) {
 #pragma unroll
@@ -772,9 +892,9 @@ static bool launch_generate_bf16(const void* latents, int64_t n_experts, const i
     if (parts & 1) {
         const int64_t htiles = (max_unique + kHsRows - 1) / kHsRows;
         const int64_t hgrid = htiles < num_cus ? (htiles > 0 ? htiles : 1) : num_cus;
-        hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
+        hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH, false>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
                            (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
-                           (uint16_t*)hout);
+                           (uint16_t*)hout, HiddenActArgs{});
     }
     if (uv == nullptr || !(parts & 2)) return true;  // hidden rows only
     // W_v-stationary when d2 splits into 256-column groups that fill the XCDs evenly
@@ -847,6 +967,37 @@ int launch_generate_part(const void* latents, int64_t n_experts, const int32_t* 
                                        part, num_cus, stream) ||
         launch_generate_bf16<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, wv, dl, dh, d, hout, vout,
                                        part, num_cus, stream))
+        return (int)hipGetLastError();
+    return -1;
+}
+
+// The hidden rows with the activations of their pairs (tiles of at most kActFusedCap
+// pairs; see tile_activations) in one kernel; the activation kernel with seg_off then
+// takes the pairs of larger tiles.  -1 (nothing launched) for shapes without the two-kernel
+// bf16 generator.
+template <int DL, int DH>
+static bool launch_hidden_act_t(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
+                                int64_t max_unique, const void* w1, int dl, int dh, void* hout,
+                                const HiddenActArgs& A, int num_cus, hipStream_t stream) {
+    if (dl != DL || dh != DH) return false;
+    const int64_t htiles = (max_unique + kHsRows - 1) / kHsRows;
+    const int64_t hgrid = htiles < num_cus ? (htiles > 0 ? htiles : 1) : num_cus;
+    if ((htiles + hgrid - 1) / hgrid > kHsMaxTiles || n_experts * DL * 2 >= 0x7ff00000ll) return false;
+    hipLaunchKernelGGL((hidden_ws_bf16_kernel<DL, DH, true>), dim3((unsigned)hgrid), dim3(DH), 0, stream,
+                       (const uint16_t*)latents, n_experts, uniq, n_unique, max_unique, (const uint16_t*)w1,
+                       (uint16_t*)hout, A);
+    return true;
+}
+
+int launch_hidden_act(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
+                      int64_t max_unique, const void* w1, int dl, int dh, void* hout, const void* xp,
+                      const int32_t* perm, const int32_t* sorted_slot, const int32_t* seg_off, const void* gates, int hk,
+                      float* act, int num_cus, hipStream_t stream) {
+    const HiddenActArgs A{(const uint16_t*)xp, perm, sorted_slot, seg_off, (const uint16_t*)gates, hk, act};
+    if (launch_hidden_act_t<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, dl, dh, hout, A, num_cus,
+                                      stream) ||
+        launch_hidden_act_t<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, dl, dh, hout, A, num_cus,
+                                      stream))
         return (int)hipGetLastError();
     return -1;
 }

@@ -277,7 +277,7 @@ def expert_forward(x: torch.Tensor, latents: torch.Tensor, w1: torch.Tensor, w2:
     rc = load().ethos_expert_forward(x.data_ptr(), latents.data_ptr(), E, w1.data_ptr(), w2.data_ptr(),
                                      wut.data_ptr() if wut is not None else None,
                                      xp.data_ptr() if xp is not None else None, seg["uniq"].data_ptr(),
-                                     seg["n_unique"].data_ptr(), max_u, seg["perm"].data_ptr(),
+                                     seg["seg_off"].data_ptr(), seg["n_unique"].data_ptr(), max_u, seg["perm"].data_ptr(),
                                      seg["sorted_slot"].data_ptr(), seg["pair_slot"].data_ptr(), gates.data_ptr(), n,
                                      n_heads, top_k, dl, dh, d, code, order, ws.data_ptr(), ws_bytes, h.data_ptr(),
                                      out.data_ptr(), _stream())

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define ETHOS_ABI_VERSION 5
+#define ETHOS_ABI_VERSION 6
 
 #define ETHOS_F32 0
 #define ETHOS_BF16 1
@@ -240,10 +240,12 @@ size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int3
  * ethos_sort_segment.  Replaces the pair loop of model.py:306-341 with the generator of
  * model.py:168-179 (weights read at model.py:297-300) -- the work of ethos_generate
  * followed by ethos_apply_scatter (order 0) or ethos_apply_hidden (order 1), with the same
- * results, scheduled so that the activations read the hidden rows right after they are
- * written.
+ * results (bit-identical), scheduled so that the activations are computed from the hidden
+ * rows while they are on chip.
  *   x, scores, perm, sorted_slot, pair_slot, n_tok, n_heads, top_k   as for ethos_apply_scatter
  *   latents, n_experts, uniq_ids, n_unique, max_unique, w1, w2       as for ethos_generate
+ *   seg_off   [max_unique + 1] int32 from ethos_sort_segment (first sorted position of
+ *             each unique expert; seg_off[U] = number of pairs)
  *   wut       bf16 only, may be NULL: W_u^T [d_hidden, d_model] (the transpose of the first
  *             d_model rows of w2) prepared by the caller, e.g. once per weight version;
  *             NULL transposes it into the workspace on every call
@@ -257,8 +259,8 @@ size_t ethos_expert_forward_workspace_bytes(int64_t n_tok, int32_t n_heads, int3
  * and out 16-byte aligned.
  */
 int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, const void* w1, const void* w2,
-                         const void* wut, const void* xp, const int32_t* uniq_ids, const int32_t* n_unique,
-                         int64_t max_unique,
+                         const void* wut, const void* xp, const int32_t* uniq_ids, const int32_t* seg_off,
+                         const int32_t* n_unique, int64_t max_unique,
                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* pair_slot, const void* scores,
                          int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_latent, int32_t d_hidden,
                          int32_t d_model, int32_t dtype, int32_t order, void* workspace, size_t workspace_bytes,

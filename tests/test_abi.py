@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ethos_abi_version() == 5
+    assert _lib.load().ethos_abi_version() == 6
 
 
 def _rc(fn, *args):
@@ -116,7 +116,7 @@ def test_sort_noalloc_rejects_pairs_beyond_its_static_workspace():
 
 def test_expert_forward_argument_errors():
     L = _lib.load()
-    args = [16, 16, 256, 16, 16, None, None, 16, 16, 64, 16, 16, 16, 16, 48, 2, 4, 16, 32, 64]
+    args = [16, 16, 256, 16, 16, None, None, 16, 16, 16, 64, 16, 16, 16, 16, 48, 2, 4, 16, 32, 64]
     ws = L.ethos_expert_forward_workspace_bytes(48, 2, 4, 64, 64, 32, 1, 0)
     assert ws > 48 * 32 * 2 + 64 * 64 * 2
     assert L.ethos_expert_forward_workspace_bytes(48, 2, 4, 64, 64, 32, 1, 1) != ws
@@ -124,14 +124,17 @@ def test_expert_forward_argument_errors():
     assert L.ethos_expert_forward(*args, 7, 0, 16, ws, 16, 16, None) == -1
     assert L.ethos_expert_forward(*args, 1, 2, 16, ws, 16, 16, None) == -2
     bad = list(args)
-    bad[17] = 10
+    bad[18] = 10
     assert L.ethos_expert_forward(*bad, 1, 0, 16, ws, 16, 16, None) == -6
     assert L.ethos_expert_forward(*args, 1, 0, None, ws, 16, 16, None) == -3
+    noseg = list(args)
+    noseg[8] = None  # seg_off
+    assert L.ethos_expert_forward(*noseg, 1, 0, 16, ws, 16, 16, None) == -3
     assert L.ethos_expert_forward(*args, 1, 0, 16, 8, 16, 16, None) == -5
     assert L.ethos_expert_forward(*args, 1, 0, 16, ws, 18, 16, None) == -4
     # an empty batch is a no-op success
     empty = list(args)
-    empty[14] = 0
+    empty[15] = 0
     assert L.ethos_expert_forward(*empty, 1, 0, None, 0, None, None, None) == 0
     # a misaligned caller-provided token projection
     misx = list(args)

@@ -479,6 +479,54 @@ def test_expert_forward_matches_separate_calls(name, hidden_space):
                            f"got {xg[bad][:3]} want {xr[bad][:3]}")
 
 
+@pytest.mark.parametrize("hidden_space", [False, True])
+def test_expert_forward_hot_experts(hidden_space):
+    """Routing with four hot experts among ~10^5 others (1,024 tokens, 131,072 pairs): the
+    hidden-row kernel computes the activations of tiles of at most 2,048 pairs (64 unique
+    experts per tile) and the activation kernel the pairs of larger tiles.  Here two tiles
+    are over that cap (3,277 and 2,149 pairs of one expert) and one just under it.  The one
+    call must equal generate + apply bit for bit, and the apply must meet the oracle on a
+    token sample (given the same hidden and v rows)."""
+    sh = SHAPES["cfg2"].with_tokens(1024)
+    xt, sd = make_inputs(sh, signal=True)
+    P = O.unpack_state(sd, sh.num_heads)
+    x = O.from_torch(xt)
+    n, H, k, E = sh.n_tok, sh.num_heads, sh.top_k, sh.num_experts
+    rng = np.random.default_rng(5)
+    ids = rng.integers(0, E, size=n * H * k).astype(np.int32)
+    p = np.arange(ids.size)
+    for mod, rem, e in ((40, 0, 7777), (61, 3, 150000), (70, 1, 100000), (300, 2, 200000)):
+        ids[p % mod == rem] = e
+    gates = O.f32_to_bf16_bits((rng.random(ids.size) / 16).astype(np.float32)).reshape(n, H, k)
+    seg = hip.sort_segment(to_dev(ids), E)
+    U = int(seg["n_unique"].item())
+    off = to_host(seg["seg_off"])[: U + 1].astype(np.int64)
+    tile_pairs = off[np.minimum(np.arange(0, U, 64) + 64, U)] - off[np.arange(0, U, 64)]
+    assert U * sh.d_hidden * 2 > 8 << 20, "the activations must take the expert order"
+    assert (tile_pairs > 2048).sum() == 2 and ((tile_pairs > 1800) & (tile_pairs <= 2048)).sum() >= 1, tile_pairs.max()
+    xd, lat, w1, w2, g = (to_dev(a) for a in (x, P["latents"], P["W1"], P["W2"], gates))
+    h, v = hip.generate(lat, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2, with_v=not hidden_space)
+    if hidden_space:
+        want = hip.apply_hidden(xd, w2, h, seg, g, H, k)
+    else:
+        want = hip.apply_scatter(xd, w2, h, v, seg, g, H, k)
+    wut = w2[: sh.d_model].t().contiguous()
+    got, h2 = hip.expert_forward(xd, lat, w1, w2, seg, g, H, k, hidden_space=hidden_space, wut=wut)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(h2)[:U], to_host(h)[:U])
+    assert np.array_equal(to_host(got), to_host(want))
+    # the apply against the oracle on tokens that use the hot experts (and others)
+    tokens = np.array([0, 1, 5, 17, 300, 511, 777, 1023])
+    xp = O.token_proj(x, P["W2"], sh.dtype)
+    hh = O.to_f32(to_host(h), sh.dtype)[:U]
+    slot = to_host(seg["pair_slot"])
+    if hidden_space:
+        ref = O.apply_hidden(xp, hh, P["W2"], slot, gates, H, k, sh.dtype, tokens=tokens)
+    else:
+        ref = O.apply(xp, hh, O.to_f32(to_host(v), sh.dtype)[:U], slot, gates, H, k, sh.dtype, tokens=tokens)
+    check_out(O.to_f32(to_host(got), sh.dtype)[tokens], ref, sh.dtype, signal=True, nerr_max=2e-3)
+
+
 def test_stage_events_recorded_in_expert_forward():
     """Five events per ethos_expert_forward call, recorded in order on the launch stream."""
     sh, x, P = _setup("cfg3", signal=True)
