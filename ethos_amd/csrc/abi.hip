@@ -50,8 +50,7 @@ bool dtype_ok(int dtype) { return dtype == ETHOS_F32 || dtype == ETHOS_BF16; }
 // device data, sized for ETHOS_NOALLOC_MAX_PAIRS pairs.  Its name is only a host-side
 // stand-in; kernels receive the device address that hipGetSymbolAddress returns for the
 // current device (g_scratch_ptr), looked up once per device on the first call there.
-constexpr size_t kScratchWords = (size_t)4 * ETHOS_NOALLOC_MAX_PAIRS + (size_t)512 * (ETHOS_NOALLOC_MAX_PAIRS / 1024) +
-                                 512 + ETHOS_NOALLOC_MAX_PAIRS / 1024 + 64;
+constexpr size_t kScratchWords = ethos::sort_workspace_words(ETHOS_NOALLOC_MAX_PAIRS);
 static __device__ __align__(256) uint32_t scratch[kScratchWords];
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 

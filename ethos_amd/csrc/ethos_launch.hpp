@@ -23,6 +23,12 @@ bool route_supported(int K, int dh2, int dtype);
 int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, int64_t rows, int dq, int K,
                  int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream);
 
+// The sort's workspace: keys and values twice (4 n words), then per (digit, tile of
+// kSortTileKeys keys) four counters, and two per-digit totals.
+constexpr int kSortTileKeys = 4096;
+constexpr size_t sort_workspace_words(int64_t n) {
+    return (size_t)4 * (size_t)n + (size_t)4 * 512 * (size_t)((n + kSortTileKeys - 1) / kSortTileKeys) + 2 * 512 + 64;
+}
 size_t sort_workspace_bytes(int64_t n);
 int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,
                         int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,

@@ -1,21 +1,31 @@
 // Reordering of (token, head, k) pairs by expert id: an LSD radix sort of the expert
-// ids carrying the pair index, followed by segmentation into unique experts.
+// ids carrying the pair index, with the segmentation into unique experts done in its
+// last pass.
 // (No reference code: the reference loops over pairs in token order, model.py:306-334;
 // the paper's Algorithm 1 reorders by expert, paper/ETHOS.pdf p.10.)
 //
-// Sort: 9-bit digits, ceil(bits / 9) passes over keys < n_experts (two for 262,144
-// experts).  Each pass is
-//   upsweep     per-tile digit histogram                 -> hist[digit][tile]
-//   scan_tiles  per digit, exclusive scan over the tiles  -> hist[digit][tile], total[digit]
-//   downsweep   stable scatter: digit base (scan of the totals, in LDS) + tile prefix +
-//               rank inside the tile by wave-level multisplit
-// A tile is 1024 keys = 4 waves x 4 chunks of 64 consecutive keys.  Inside a wave, the
-// lanes holding the same digit are found with nine ballots ("peer mask"); the rank of a
-// key is (keys of that digit in earlier waves) + (in earlier chunks of its wave) + (peers
-// in lower lanes), which keeps the order of equal keys.  No global atomics; LDS counters
-// are updated by one leader lane per digit.
+// Sort: 9-bit digits, P = ceil(bits / 9) passes over keys < n_experts (two for 262,144
+// experts), over tiles of 8192 keys (one workgroup of 16 waves each).  A pass is
+//   count/stats  per-tile digit counts (last pass: also per digit the number of distinct
+//                keys, and the lower bits of the first and last key)
+//   scan         per digit, exclusive prefix over the tiles (last pass: also of the new
+//                distinct keys, and the lower bits of the last earlier key)
+//   down         stable scatter: digit base (scan of the totals) + tile prefix + rank in
+//                the tile by wave-level multisplit
+// Inside a wave, the lanes holding the same digit are found with nine ballots ("peer
+// mask"); the rank of a key is (keys of that digit in earlier waves) + (in earlier chunks
+// of its wave) + (peers in lower lanes), which keeps the order of equal keys.  No global
+// atomics and no waiting between workgroups; LDS counters are updated by one leader lane
+// per digit.
 //
-// Segment: flags[i] = (i == 0 || key[i] != key[i-1]); slot = inclusive scan - 1.
+// Segmentation (last pass).  Equal keys are adjacent in the final order, and inside a
+// tile's group of one digit the keys come in the order of their lower bits (the earlier
+// passes' order), so the tile can rank its keys locally (LDS) and tell its heads (first
+// key of a segment): a key differs from the one before it in the tile's group, or, for
+// the group's first key, from the last key of that digit in earlier tiles (the scan's
+// prefix maximum of the tiles' last lower bits; keys of one digit are non-decreasing over
+// the tiles).  Slot = (new distinct keys of smaller digits and of this digit in earlier
+// tiles) + (heads so far in the group) - 1.
 // Outputs: perm (pair ids by expert), uniq (expert id per slot), seg_off (U + 1),
 // pair_slot[p] (slot of pair p), sorted_slot[i] (slot of position i), n_unique.
 #include "ethos_common.hpp"
@@ -23,11 +33,8 @@
 
 namespace ethos {
 
-constexpr int kSortChunks = 4;                  // chunks of 64 keys per wave
-constexpr int kSortTile = 4 * kSortChunks * 64; // 1024 keys
 constexpr int kRadixBits = 9;
 constexpr int kRadix = 1 << kRadixBits;
-constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ uint64_t peer_mask(uint32_t digit, uint64_t valid) {
     uint64_t peers = valid;
@@ -42,77 +49,61 @@ __device__ __forceinline__ uint64_t peer_mask(uint32_t digit, uint64_t valid) {
 
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
 
-__global__ __launch_bounds__(256) void sort_upsweep(const uint32_t* __restrict__ keys, int64_t n, int shift,
-                                                    uint32_t* __restrict__ hist, int n_tiles) {
-    __shared__ uint32_t cnt[4][kRadix];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < 4 * kRadix; i += 256) cnt[i / kRadix][i % kRadix] = 0;
-    __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortChunks * 64);
+// ---------------------------------------------------------------------------------
+// Tile passes: a tile is kTile = kSortTileKeys (4096) consecutive keys, one workgroup of
+// kTW = 16 waves; wave w owns chunks w kTC .. w kTC + kTC - 1 of 64 keys (kTC = 4).
+// Every kernel issues its per-digit table loads first, so that they overlap the key loads.
+// ---------------------------------------------------------------------------------
+constexpr int kTW = 16;
+constexpr int kTThreads = kTW * 64;
+constexpr int kTile = kSortTileKeys;
+constexpr int kTC = kTile / (kTW * 64);
+constexpr int kTPer = kTile / kTThreads;  // tile-local positions per thread in the segment phase
+static_assert(kTC * kTW * 64 == kTile && kTPer == 4, "tile shape");
+
+// Exclusive scans of NV values per thread over threads 0 .. 511 (waves 0 .. 7; the other
+// threads pass zeros), in one pass.  Every thread of the workgroup calls it (it holds
+// barriers); tot[] receives the sums.  wsum: 8 NV words of LDS.
+template <int NV>
+__device__ __forceinline__ void scan512(const uint32_t (&v)[NV], uint32_t (&ex)[NV], uint32_t (&tot)[NV],
+                                        uint32_t* wsum) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t inc[NV];
 #pragma unroll
-    for (int c = 0; c < kSortChunks; ++c) {
-        const int64_t idx = base + c * 64 + lane;
-        const bool v = idx < n;
-        const uint32_t key = v ? keys[idx] : 0u;
-        const uint32_t dg = (key >> shift) & (kRadix - 1);
-        const uint64_t peers = peer_mask(dg, __ballot(v));
-        if (v && lane == 63 - __clzll((long long)peers)) cnt[wave][dg] += (uint32_t)__popcll(peers);
+    for (int c = 0; c < NV; ++c) inc[c] = v[c];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const uint32_t u = __shfl_up(inc[c], off, 64);
+            if (lane >= off) inc[c] += u;
+        }
+    }
+    if (wave < kRadix / 64 && lane == 63) {
+#pragma unroll
+        for (int c = 0; c < NV; ++c) wsum[wave * NV + c] = inc[c];
     }
     __syncthreads();
-    for (int d = tid; d < kRadix; d += 256)
-        hist[(int64_t)d * n_tiles + blockIdx.x] = cnt[0][d] + cnt[1][d] + cnt[2][d] + cnt[3][d];
-}
-
-// One wave per digit: exclusive scan of hist[digit][0 .. n_tiles) in place, the digit's
-// total to total[digit].
-__global__ __launch_bounds__(256) void sort_scan_tiles(uint32_t* __restrict__ hist, int n_tiles,
-                                                       uint32_t* __restrict__ total) {
-    const int lane = threadIdx.x & 63;
-    const int d = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (d >= kRadix) return;
-    uint32_t* row = hist + (int64_t)d * n_tiles;
-    uint32_t carry = 0;
-    for (int t0 = 0; t0 < n_tiles; t0 += 64 * 8) {
-        uint32_t v[8], s = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int t = t0 + lane * 8 + j;
-            v[j] = t < n_tiles ? row[t] : 0u;
-            s += v[j];
-        }
-        uint32_t inc = s;
+    for (int c = 0; c < NV; ++c) {
+        uint32_t pre = 0, t = 0;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t u = __shfl_up(inc, off, 64);
-            if (lane >= off) inc += u;
+        for (int w = 0; w < kRadix / 64; ++w) {
+            const uint32_t x = wsum[w * NV + c];
+            pre += w < wave ? x : 0u;
+            t += x;
         }
-        uint32_t run = carry + inc - s;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int t = t0 + lane * 8 + j;
-            if (t < n_tiles) row[t] = run;
-            run += v[j];
-        }
-        carry += __shfl(inc, 63, 64);
+        ex[c] = pre + inc[c] - v[c];
+        tot[c] = t;
     }
-    if (lane == 0) total[d] = carry;
+    __syncthreads();  // wsum may be reused by the caller
 }
 
-template <bool kFirst>
-__global__ __launch_bounds__(256) void sort_downsweep(const uint32_t* __restrict__ keys_in,
-                                                      const uint32_t* __restrict__ vals_in,
-                                                      uint32_t* __restrict__ keys_out,
-                                                      uint32_t* __restrict__ vals_out, int64_t n, int shift,
-                                                      const uint32_t* __restrict__ hist,
-                                                      const uint32_t* __restrict__ total, int n_tiles) {
-    __shared__ uint32_t cnt[4][kRadix];
-    __shared__ uint32_t wsum[4];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < 4 * kRadix; i += 256) cnt[i / kRadix][i % kRadix] = 0;
-    // digit bases: exclusive scan of the digit totals (two digits per thread)
-    const uint32_t ta = total[2 * tid], tb = total[2 * tid + 1];
-    const uint32_t s = ta + tb;
-    uint32_t inc = s;
+// Exclusive scan of one value per thread over the workgroup's 1024 threads; tot gets the
+// sum.  wsum: kTW words of LDS.
+__device__ __forceinline__ uint32_t scan1024(uint32_t v, uint32_t* wsum, uint32_t& tot) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t inc = v;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
         const uint32_t u = __shfl_up(inc, off, 64);
@@ -120,189 +111,424 @@ __global__ __launch_bounds__(256) void sort_downsweep(const uint32_t* __restrict
     }
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
-    uint32_t wpre = 0;
+    uint32_t pre = 0, t = 0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) wpre += w < wave ? wsum[w] : 0u;
-    const uint32_t base_a = wpre + inc - s, base_b = base_a + ta;
+    for (int w = 0; w < kTW; ++w) {
+        const uint32_t x = wsum[w];
+        pre += w < wave ? x : 0u;
+        t += x;
+    }
+    __syncthreads();
+    tot = t;
+    return pre + inc - v;
+}
 
-    const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortChunks * 64);
-    uint32_t key[kSortChunks], val[kSortChunks], rank[kSortChunks];
+// Phase A of a tile pass: load the wave's chunks (key; value = the key's index on the first
+// pass) and rank them by digit in order.  wcnt[w][d] must be zero on entry; on exit it holds
+// wave w's count of digit d, and rank[j] the number of keys of the same digit before chunk
+// j's key in wave w.
+template <bool kFirst>
+__device__ __forceinline__ void tile_load(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+                                          int64_t n, uint32_t (&key)[kTC], uint32_t (&val)[kTC]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
 #pragma unroll
-    for (int c = 0; c < kSortChunks; ++c) {
-        const int64_t idx = base + c * 64 + lane;
+    for (int j = 0; j < kTC; ++j) {
+        const int64_t idx = base + j * 64 + lane;
         const bool v = idx < n;
-        key[c] = v ? keys_in[idx] : 0u;
-        val[c] = v ? (kFirst ? (uint32_t)idx : vals_in[idx]) : 0u;
-        const uint32_t dg = (key[c] >> shift) & (kRadix - 1);
+        key[j] = v ? keys[idx] : 0u;
+        val[j] = v ? (kFirst ? (uint32_t)idx : vals[idx]) : 0u;
+    }
+}
+__device__ __forceinline__ void tile_rank(int64_t n, int shift, uint32_t (*wcnt)[kRadix], const uint32_t (&key)[kTC],
+                                          uint32_t (&rank)[kTC]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+#pragma unroll
+    for (int j = 0; j < kTC; ++j) {
+        const bool v = base + j * 64 + lane < n;
+        const uint32_t dg = (key[j] >> shift) & (kRadix - 1);
         const uint64_t peers = peer_mask(dg, __ballot(v));
         const uint32_t below = (uint32_t)__popcll(peers & lanemask_lt(lane));
         uint32_t start = 0;
-        if (v) start = cnt[wave][dg];
+        if (v) start = wcnt[wave][dg];
         __builtin_amdgcn_wave_barrier();
-        rank[c] = start + below;
-        if (v && lane == 63 - __clzll((long long)peers)) cnt[wave][dg] = start + (uint32_t)__popcll(peers);
+        rank[j] = start + below;
+        if (v && lane == 63 - __clzll((long long)peers)) wcnt[wave][dg] = start + (uint32_t)__popcll(peers);
         __builtin_amdgcn_wave_barrier();
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int d = 2 * tid + j;
-        uint32_t run = (j ? base_b : base_a) + hist[(int64_t)d * n_tiles + blockIdx.x];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const uint32_t c = cnt[w][d];
-            cnt[w][d] = run;
-            run += c;
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < kSortChunks; ++c) {
-        const int64_t idx = base + c * 64 + lane;
-        if (idx < n) {
-            const uint32_t dg = (key[c] >> shift) & (kRadix - 1);
-            const uint32_t pos = cnt[wave][dg] + rank[c];
-            keys_out[pos] = key[c];
-            vals_out[pos] = val[c];
-        }
     }
 }
 
-// Exclusive scan of n uint32 in place by one workgroup; total -> *total (if given).
-// Exclusive scan of a[0..n) in place, one workgroup.  Each thread holds 16 consecutive
-// values in registers (four 16-byte loads issued together); thread sums are scanned
-// across the wave with shuffles and across the 16 waves through LDS; chunks of 16384
-// values are chained by a carry.  *total (if given) receives the sum of all values.
-constexpr int kScanPer = 16;
-constexpr int kScanChunk = kScanThreads * kScanPer;
+// After phase A (and a barrier): thread d < 512 turns wcnt[.][d] into the exclusive prefix
+// over the waves and returns the tile's count of digit d (0 for the other threads).
+__device__ __forceinline__ uint32_t tile_digit_counts(uint32_t (*wcnt)[kRadix]) {
+    const int d = threadIdx.x;
+    if (d >= kRadix) return 0u;
+    uint32_t run = 0;
+#pragma unroll
+    for (int w = 0; w < kTW; ++w) {
+        const uint32_t c = wcnt[w][d];
+        wcnt[w][d] = run;
+        run += c;
+    }
+    return run;
+}
 
-__global__ __launch_bounds__(kScanThreads) void scan_exclusive(uint32_t* __restrict__ a, int64_t n,
-                                                               int32_t* __restrict__ total) {
-    __shared__ uint32_t wsum[kScanThreads / 64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool vec = ((uintptr_t)a & 15) == 0;
-    uint32_t carry = 0;
-    for (int64_t base = 0; base < n; base += kScanChunk) {
-        const int64_t lo = base + (int64_t)tid * kScanPer;
-        const bool full = vec && lo + kScanPer <= n;
-        uint32_t v[kScanPer];
-        if (full) {
+__device__ __forceinline__ void zero_wcnt(uint32_t (*wcnt)[kRadix]) {
+    uint4* w = reinterpret_cast<uint4*>(&wcnt[0][0]);
+    for (int e = threadIdx.x; e < kTW * kRadix / 4; e += kTThreads) w[e] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Per-tile digit counts of one (non-last) pass: cnt[d * n_tiles + tile].
+__global__ __launch_bounds__(kTThreads) void tsort_count(const uint32_t* __restrict__ keys, int64_t n, int shift,
+                                                         int n_tiles, uint32_t* __restrict__ cnt) {
+    __shared__ uint32_t c[kRadix];
+    const int tid = threadIdx.x;
+    const int64_t base = (int64_t)blockIdx.x * kTile + tid;
+    uint32_t k[kTPer];
 #pragma unroll
-            for (int j = 0; j < kScanPer / 4; ++j) {
-                const uint4 q = reinterpret_cast<const uint4*>(a + lo)[j];
-                v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
-            }
-        } else {
+    for (int j = 0; j < kTPer; ++j) k[j] = base + j * kTThreads < n ? keys[base + j * kTThreads] : 0u;
+    if (tid < kRadix) c[tid] = 0;
+    __syncthreads();
 #pragma unroll
-            for (int j = 0; j < kScanPer; ++j) v[j] = lo + j < n ? a[lo + j] : 0u;
+    for (int j = 0; j < kTPer; ++j)
+        if (base + j * kTThreads < n) atomicAdd(&c[(k[j] >> shift) & (kRadix - 1)], 1u);
+    __syncthreads();
+    if (tid < kRadix) cnt[(int64_t)tid * n_tiles + blockIdx.x] = c[tid];
+}
+
+// Per-tile statistics of the last pass (keys sorted by their lower bits lo = key & lomask),
+// for each digit d of the tile: cnt (keys), dist (distinct keys), flo / llo (lower bits of
+// the digit's first and last key in the tile's order, i.e. the smallest and largest).
+// Keys of at most 18 bits (two passes): distinct keys counted with a bitmap of all keys in
+// LDS (a key's bit is set by one of its copies first, whichever), flo / llo by atomic
+// min / max.
+__global__ __launch_bounds__(kTThreads) void tsort_stats_map(const uint32_t* __restrict__ keys, int64_t n, int shift,
+                                                             uint32_t mkmask, int n_tiles, uint32_t* __restrict__ cnt,
+                                                             uint32_t* __restrict__ dist, uint32_t* __restrict__ flo,
+                                                             uint32_t* __restrict__ llo) {
+    constexpr int kMapWords = (1 << (2 * kRadixBits)) / 32;
+    __shared__ uint4 seen[kMapWords / 4];
+    __shared__ uint32_t c[kRadix], dc[kRadix], mn[kRadix], mx[kRadix];
+    const int tid = threadIdx.x;
+    const int64_t base = (int64_t)blockIdx.x * kTile + tid;
+    uint32_t k[kTPer];
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) k[j] = base + j * kTThreads < n ? keys[base + j * kTThreads] & mkmask : 0u;
+    for (int e = tid; e < kMapWords / 4; e += kTThreads) seen[e] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < kRadix) {
+        c[tid] = dc[tid] = mx[tid] = 0u;
+        mn[tid] = 0xffffffffu;
+    }
+    __syncthreads();
+    uint32_t* sw = reinterpret_cast<uint32_t*>(seen);
+    const uint32_t lomask = (1u << shift) - 1u;
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) {
+        if (base + j * kTThreads < n) {
+            const uint32_t d = (k[j] >> shift) & (kRadix - 1), lo = k[j] & lomask;
+            const uint32_t bit = 1u << (k[j] & 31u);
+            atomicAdd(&c[d], 1u);
+            atomicMin(&mn[d], lo);
+            atomicMax(&mx[d], lo);
+            if (!(atomicOr(&sw[(k[j] >> 5) & (kMapWords - 1)], bit) & bit)) atomicAdd(&dc[d], 1u);
         }
-        uint32_t s = 0;
+    }
+    __syncthreads();
+    if (tid < kRadix) {
+        const int64_t o = (int64_t)tid * n_tiles + blockIdx.x;
+        const uint32_t cc = c[tid];
+        cnt[o] = cc;
+        dist[o] = dc[tid];
+        flo[o] = cc ? mn[tid] : 0u;
+        llo[o] = cc ? mx[tid] : 0u;
+    }
+}
+
+// The same statistics for wider keys (three or more passes): the tile's keys are ranked by
+// digit into LDS, where equal keys are adjacent.
+__global__ __launch_bounds__(kTThreads) void tsort_stats(const uint32_t* __restrict__ keys, int64_t n, int shift,
+                                                         uint32_t mkmask, int n_tiles, uint32_t* __restrict__ cnt,
+                                                         uint32_t* __restrict__ dist, uint32_t* __restrict__ flo,
+                                                         uint32_t* __restrict__ llo) {
+    __shared__ uint32_t wcnt[kTW][kRadix];
+    __shared__ uint32_t sk[kTile];
+    __shared__ uint32_t lstart[kRadix], dcnt[kRadix], wsum[8];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    uint32_t key[kTC], val[kTC], rank[kTC];
+    tile_load<true>(keys, nullptr, n, key, val);
+    zero_wcnt(wcnt);
+    if (tid < kRadix) dcnt[tid] = 0;
+    __syncthreads();
+    tile_rank(n, shift, wcnt, key, rank);
+    __syncthreads();
+    const uint32_t tcv[1] = {tile_digit_counts(wcnt)};
+    uint32_t ls[1], tile_n[1];
+    scan512<1>(tcv, ls, tile_n, wsum);
+    if (tid < kRadix) lstart[tid] = ls[0];
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
 #pragma unroll
-        for (int j = 0; j < kScanPer; ++j) s += v[j];
-        // inclusive wave scan of the thread sums
-        uint32_t inc = s;
+    for (int j = 0; j < kTC; ++j) {
+        if (base + j * 64 + (tid & 63) < n) {
+            const uint32_t d = (key[j] >> shift) & (kRadix - 1);
+            const uint32_t lp = lstart[d] + wcnt[wave][d] + rank[j];
+            if (lp < (uint32_t)kTile) sk[lp] = key[j] & mkmask;
+        }
+    }
+    __syncthreads();
+    for (int p = tid; p < (int)tile_n[0]; p += kTThreads) {
+        const uint32_t k = sk[p];
+        const uint32_t d = (k >> shift) & (kRadix - 1);
+        if (p == (int)lstart[d] || k != sk[p - 1]) atomicAdd(&dcnt[d], 1u);
+    }
+    __syncthreads();
+    if (tid < kRadix) {
+        const int64_t o = (int64_t)tid * n_tiles + blockIdx.x;
+        const uint32_t lomask = (1u << shift) - 1u, tc = tcv[0];
+        cnt[o] = tc;
+        dist[o] = dcnt[tid];
+        flo[o] = tc ? sk[ls[0]] & lomask : 0u;
+        llo[o] = tc ? sk[ls[0] + tc - 1] & lomask : 0u;
+    }
+}
+
+// One wave per digit: exclusive prefix of the digit's tile counts over the tiles (in
+// place), the total to tot[d].  Last pass (kLast): also the lower bits of the last key of
+// the digit in earlier tiles, as llo + 1 (0: none; in place of llo), by a prefix maximum
+// (the keys of one digit do not decrease over the tiles), and the exclusive prefix of the
+// new distinct keys, dist - [the tile's first key equals that last key] (in place of dist),
+// its total to stot[d].
+template <bool kLast>
+__global__ __launch_bounds__(256) void tsort_scan(uint32_t* __restrict__ cnt, uint32_t* __restrict__ dist,
+                                                  const uint32_t* __restrict__ flo, uint32_t* __restrict__ llo,
+                                                  int n_tiles, uint32_t* __restrict__ tot,
+                                                  uint32_t* __restrict__ stot) {
+    const int lane = threadIdx.x & 63;
+    const int d = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (d >= kRadix) return;
+    uint32_t* crow = cnt + (int64_t)d * n_tiles;
+    uint32_t* drow = dist + (int64_t)d * n_tiles;
+    const uint32_t* frow = flo + (int64_t)d * n_tiles;
+    uint32_t* lrow = llo + (int64_t)d * n_tiles;
+    uint32_t carry_c = 0, carry_s = 0, carry_l = 0;
+    constexpr int kPer = 8;
+    for (int t0 = 0; t0 < n_tiles; t0 += 64 * kPer) {
+        uint32_t c[kPer], ds[kPer], fl[kPer], le[kPer];
+        uint32_t sc = 0, ml = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int t = t0 + lane * kPer + j;
+            const bool v = t < n_tiles;
+            c[j] = v ? crow[t] : 0u;
+            sc += c[j];
+            if (kLast) {
+                ds[j] = v ? drow[t] : 0u;
+                fl[j] = v ? frow[t] : 0u;
+                le[j] = v && c[j] ? lrow[t] + 1u : 0u;
+                ml = max(ml, le[j]);
+            }
+        }
+        // inclusive wave scans of the lane totals (sum of counts; max of the last keys)
+        uint32_t ic = sc, il = ml;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t t = __shfl_up(inc, off, 64);
-            if (lane >= off) inc += t;
-        }
-        if (lane == 63) wsum[wave] = inc;
-        __syncthreads();
-        uint32_t wpre = 0, chunk_total = 0;
-#pragma unroll
-        for (int w = 0; w < kScanThreads / 64; ++w) {
-            const uint32_t t = wsum[w];
-            wpre += w < wave ? t : 0u;
-            chunk_total += t;
-        }
-        __syncthreads();  // wsum is rewritten by the next chunk
-        uint32_t run = carry + wpre + inc - s;
-#pragma unroll
-        for (int j = 0; j < kScanPer; ++j) {
-            const uint32_t t = v[j];
-            v[j] = run;
-            run += t;
-        }
-        if (full) {
-#pragma unroll
-            for (int j = 0; j < kScanPer / 4; ++j)
-                reinterpret_cast<uint4*>(a + lo)[j] = make_uint4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < kScanPer; ++j)
-                if (lo + j < n) a[lo + j] = v[j];
-        }
-        carry += chunk_total;
-    }
-    if (tid == 0 && total) *total = (int32_t)carry;
-}
-
-// Head count per tile (items thread-contiguous: thread t owns 4 consecutive keys).
-constexpr int kSegPer = kSortTile / 256;  // keys per thread in the segment kernels
-
-__global__ __launch_bounds__(256) void seg_count(const uint32_t* __restrict__ keys, int64_t n,
-                                                 uint32_t* __restrict__ tile_cnt) {
-    __shared__ uint32_t red[256];
-    const int tid = threadIdx.x;
-    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * kSegPer;
-    uint32_t c = 0;
-    for (int i = 0; i < kSegPer; ++i) {
-        const int64_t idx = lo + i;
-        if (idx < n && (idx == 0 || keys[idx] != keys[idx - 1])) ++c;
-    }
-    red[tid] = c;
-    __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (tid < off) red[tid] += red[tid + off];
-        __syncthreads();
-    }
-    if (tid == 0) tile_cnt[blockIdx.x] = red[0];
-}
-
-__global__ __launch_bounds__(256) void seg_write(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ perm,
-                                                 int64_t n, const uint32_t* __restrict__ tile_base,
-                                                 int32_t* __restrict__ uniq, int32_t* __restrict__ seg_off,
-                                                 int32_t* __restrict__ pair_slot, int32_t* __restrict__ sorted_slot,
-                                                 int32_t* __restrict__ n_unique, int32_t max_unique) {
-    __shared__ uint32_t part[256];
-    const int tid = threadIdx.x;
-    const int64_t lo = (int64_t)blockIdx.x * kSortTile + tid * kSegPer;
-    uint32_t c = 0;
-    for (int i = 0; i < kSegPer; ++i) {
-        const int64_t idx = lo + i;
-        if (idx < n && (idx == 0 || keys[idx] != keys[idx - 1])) ++c;
-    }
-    part[tid] = c;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-        const uint32_t v = tid >= off ? part[tid - off] : 0u;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
-    }
-    // slot of the item just before this thread's first head
-    int32_t slot = (int32_t)(tile_base[blockIdx.x] + part[tid] - c) - 1;
-    for (int i = 0; i < kSegPer; ++i) {
-        const int64_t idx = lo + i;
-        if (idx >= n) break;
-        const uint32_t k = keys[idx];
-        if (idx == 0 || k != keys[idx - 1]) {
-            ++slot;
-            if (slot < max_unique) {
-                uniq[slot] = (int32_t)k;
-                seg_off[slot] = (int32_t)idx;
+            const uint32_t u = __shfl_up(ic, off, 64);
+            const uint32_t w = __shfl_up(il, off, 64);
+            if (lane >= off) {
+                ic += u;
+                il = max(il, w);
             }
         }
-        // Ids >= n_experts (a caller error) could make more slots than the buffers hold;
-        // clamp so every later kernel stays in bounds.
-        const int32_t s = slot < max_unique ? slot : max_unique - 1;
-        sorted_slot[idx] = s;
-        pair_slot[perm[idx]] = s;
-        if (idx == n - 1) {
-            const int32_t u = *n_unique < max_unique ? *n_unique : max_unique;
-            *n_unique = u;
-            seg_off[u] = (int32_t)n;
+        uint32_t run_c = carry_c + ic - sc;
+        uint32_t run_l = max(carry_l, (uint32_t)__shfl_up(il, 1, 64));
+        if (lane == 0) run_l = carry_l;
+        uint32_t nd[kPer], sn = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int t = t0 + lane * kPer + j;
+            if (t < n_tiles) crow[t] = run_c;
+            run_c += c[j];
+            if (kLast) {
+                nd[j] = ds[j] - (c[j] && run_l != 0u && fl[j] + 1u == run_l ? 1u : 0u);
+                sn += nd[j];
+                if (t < n_tiles) lrow[t] = run_l;
+                run_l = max(run_l, le[j]);
+            }
         }
+        carry_c += __shfl(ic, 63, 64);
+        if (kLast) {
+            uint32_t is = sn;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t u = __shfl_up(is, off, 64);
+                if (lane >= off) is += u;
+            }
+            uint32_t run_s = carry_s + is - sn;
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const int t = t0 + lane * kPer + j;
+                if (t < n_tiles) drow[t] = run_s;
+                run_s += nd[j];
+            }
+            carry_s += __shfl(is, 63, 64);
+            carry_l = max(carry_l, __shfl(il, 63, 64));
+        }
+    }
+    if (lane == 0) {
+        tot[d] = carry_c;
+        if (kLast) stot[d] = carry_s;
+    }
+}
+
+// Scatter of one non-last pass: key and value of each element to digit base + tile prefix
+// + rank.
+template <bool kFirst>
+__global__ __launch_bounds__(kTThreads) void tsort_down(const uint32_t* __restrict__ keys_in,
+                                                        const uint32_t* __restrict__ vals_in,
+                                                        uint32_t* __restrict__ keys_out,
+                                                        uint32_t* __restrict__ vals_out, int64_t n, int shift,
+                                                        int n_tiles, const uint32_t* __restrict__ pre,
+                                                        const uint32_t* __restrict__ tot) {
+    __shared__ uint32_t wcnt[kTW][kRadix];
+    __shared__ uint32_t gbase[kRadix], wsum[8];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t my_pre = tid < kRadix ? pre[(int64_t)tid * n_tiles + blockIdx.x] : 0u;
+    const uint32_t my_tot[1] = {tid < kRadix ? tot[tid] : 0u};
+    uint32_t key[kTC], val[kTC], rank[kTC];
+    tile_load<kFirst>(keys_in, vals_in, n, key, val);
+    zero_wcnt(wcnt);
+    __syncthreads();
+    tile_rank(n, shift, wcnt, key, rank);
+    __syncthreads();
+    tile_digit_counts(wcnt);
+    uint32_t db[1], all[1];
+    scan512<1>(my_tot, db, all, wsum);
+    if (tid < kRadix) gbase[tid] = db[0] + my_pre;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+#pragma unroll
+    for (int j = 0; j < kTC; ++j) {
+        if (base + j * 64 + (tid & 63) < n) {
+            const uint32_t d = (key[j] >> shift) & (kRadix - 1);
+            const uint32_t pos = gbase[d] + wcnt[wave][d] + rank[j];
+            if (pos < (uint64_t)n) {  // always, for ids from one consistent pass
+                keys_out[pos] = key[j];
+                vals_out[pos] = val[j];
+            }
+        }
+    }
+}
+
+// The last pass with the segmentation: the tile's keys and values ranked by digit into LDS,
+// then each thread takes kTPer consecutive positions of that order: head flags, their
+// prefix over the tile (one scan), slots, and every output.
+template <bool kFirst>
+__global__ __launch_bounds__(kTThreads) void tsort_down_last(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n, int shift,
+    uint32_t mkmask, int n_tiles, const uint32_t* __restrict__ pre, const uint32_t* __restrict__ spre,
+    const uint32_t* __restrict__ plast, const uint32_t* __restrict__ tot, const uint32_t* __restrict__ stot,
+    int32_t* __restrict__ perm, int32_t* __restrict__ uniq, int32_t* __restrict__ seg_off,
+    int32_t* __restrict__ pair_slot, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ n_unique,
+    int32_t max_unique) {
+    __shared__ uint32_t wcnt[kTW][kRadix];
+    __shared__ __align__(16) uint32_t sk[kTile];
+    __shared__ __align__(16) uint32_t sv[kTile];
+    __shared__ uint32_t gbase[kRadix], sbase[kRadix], lst[kRadix], lstart[kRadix], hstart[kRadix];
+    __shared__ uint32_t wsum[3 * 8];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t o = (int64_t)tid * n_tiles + blockIdx.x;
+    const bool dl = tid < kRadix;
+    const uint32_t my_pre = dl ? pre[o] : 0u, my_spre = dl ? spre[o] : 0u, my_plast = dl ? plast[o] : 0u;
+    uint32_t tv[3] = {dl ? tot[tid] : 0u, dl ? stot[tid] : 0u, 0u};
+    uint32_t key[kTC], val[kTC], rank[kTC];
+    tile_load<kFirst>(keys_in, vals_in, n, key, val);
+    zero_wcnt(wcnt);
+    __syncthreads();
+    tile_rank(n, shift, wcnt, key, rank);
+    __syncthreads();
+    tv[2] = tile_digit_counts(wcnt);
+    uint32_t ex[3], sums[3];
+    scan512<3>(tv, ex, sums, wsum);
+    const uint32_t u_all = sums[1], tile_n = sums[2];
+    if (dl) {
+        gbase[tid] = ex[0] + my_pre;
+        sbase[tid] = ex[1] + my_spre;
+        lst[tid] = my_plast;
+        lstart[tid] = ex[2];
+    }
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+#pragma unroll
+    for (int j = 0; j < kTC; ++j) {
+        if (base + j * 64 + lane < n) {
+            const uint32_t d = (key[j] >> shift) & (kRadix - 1);
+            const uint32_t lp = lstart[d] + wcnt[wave][d] + rank[j];
+            if (lp < (uint32_t)kTile) {
+                sk[lp] = key[j];
+                sv[lp] = val[j];
+            }
+        }
+    }
+    __syncthreads();
+    // heads: a key differs from the one before it in its digit's group; a group's first key
+    // continues the last earlier key of its digit when their lower bits agree (lst holds
+    // those bits + 1, 0 for none)
+    const uint32_t lomask = (1u << shift) - 1u;
+    const int p0 = tid * kTPer;
+    const uint4 k4 = reinterpret_cast<const uint4*>(sk)[tid];
+    const uint4 v4 = reinterpret_cast<const uint4*>(sv)[tid];
+    const uint32_t kk[kTPer] = {k4.x, k4.y, k4.z, k4.w}, vv[kTPer] = {v4.x, v4.y, v4.z, v4.w};
+    uint32_t prev = p0 > 0 ? sk[p0 - 1] : 0u;
+    uint32_t dd[kTPer];
+    bool st[kTPer], head[kTPer];
+    uint32_t nh = 0;
+#pragma unroll
+    for (int i = 0; i < kTPer; ++i) {
+        const int p = p0 + i;
+        const bool valid = p < (int)tile_n;
+        dd[i] = (kk[i] >> shift) & (kRadix - 1);
+        st[i] = valid && p == (int)lstart[dd[i]];
+        head[i] = valid && (st[i] ? (lst[dd[i]] == 0u || (kk[i] & lomask) + 1u != lst[dd[i]])
+                                  : ((kk[i] ^ prev) & mkmask) != 0u);
+        prev = kk[i];
+        nh += head[i] ? 1u : 0u;
+    }
+    uint32_t all_heads;
+    uint32_t run = scan1024(nh, wsum, all_heads);
+    (void)all_heads;
+#pragma unroll
+    for (int i = 0; i < kTPer; ++i) {
+        if (st[i]) hstart[dd[i]] = run;
+        run += head[i] ? 1u : 0u;
+    }
+    __syncthreads();
+    run -= nh;
+#pragma unroll
+    for (int i = 0; i < kTPer; ++i) {
+        const int p = p0 + i;
+        if (p >= (int)tile_n) break;
+        const uint32_t d = dd[i];
+        run += head[i] ? 1u : 0u;
+        const int32_t slot = (int32_t)(sbase[d] + run - hstart[d]) - 1;
+        // ids outside [0, n_experts) (a caller error) could make more slots than the buffers
+        // hold: clamp so that every later kernel stays in bounds
+        const int32_t sc = slot < 0 ? 0 : (slot < max_unique ? slot : max_unique - 1);
+        const uint32_t pos = gbase[d] + (uint32_t)p - lstart[d];
+        if (pos < (uint64_t)n) {
+            perm[pos] = (int32_t)vv[i];
+            sorted_slot[pos] = sc;
+        }
+        if (vv[i] < (uint64_t)n) pair_slot[vv[i]] = sc;
+        if (head[i] && slot >= 0 && slot < max_unique) {
+            uniq[slot] = (int32_t)kk[i];
+            seg_off[slot] = (int32_t)pos;
+        }
+    }
+    if (blockIdx.x == 0 && tid == 0) {
+        const int32_t u = (int32_t)u_all < max_unique ? (int32_t)u_all : max_unique;
+        *n_unique = u;
+        seg_off[u] = (int32_t)n;
     }
 }
 
@@ -492,11 +718,7 @@ static int key_bits(int64_t n_experts) {
     return b;
 }
 
-size_t sort_workspace_bytes(int64_t n) {
-    const int64_t tiles = (n + kSortTile - 1) / kSortTile;
-    const size_t words = (size_t)4 * n + (size_t)kRadix * tiles + kRadix + (size_t)tiles + 64;
-    return words * sizeof(uint32_t);
-}
+size_t sort_workspace_bytes(int64_t n) { return sort_workspace_words(n) * sizeof(uint32_t); }
 
 int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,
                         int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
@@ -505,42 +727,61 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
     const int passes = bits <= kRadixBits ? 1 : (bits + kRadixBits - 1) / kRadixBits;
     int vb = 0;
     while (vb < 31 && ((int64_t)1 << vb) < n) ++vb;
+    const int32_t max_unique = (int32_t)(n < n_experts ? n : n_experts);
     if (n <= kSmallMax && bits + vb <= 32) {
         hipLaunchKernelGGL(sort_small_kernel, dim3(1), dim3(kSmallWaves * 64), 0, stream, ids, (int)n, bits, vb,
-                           passes, perm, uniq, seg_off, pair_slot, sorted_slot, n_unique,
-                           (int32_t)(n < n_experts ? n : n_experts));
+                           passes, perm, uniq, seg_off, pair_slot, sorted_slot, n_unique, max_unique);
         return (int)hipGetLastError();
     }
-    const int n_tiles = (int)((n + kSortTile - 1) / kSortTile);
+    const int n_tiles = (int)((n + kTile - 1) / kTile);
     uint32_t* w = reinterpret_cast<uint32_t*>(ws);
     uint32_t* kbuf[2] = {w, w + n};
     uint32_t* vbuf[2] = {w + 2 * n, w + 3 * n};
-    uint32_t* hist = w + 4 * n;
-    uint32_t* total = hist + (size_t)kRadix * n_tiles;
-    uint32_t* tcnt = total + kRadix;
-    hipError_t err;
+    uint32_t* cnt = w + 4 * n;
+    uint32_t* dist = cnt + (size_t)kRadix * n_tiles;
+    uint32_t* flo = dist + (size_t)kRadix * n_tiles;
+    uint32_t* llo = flo + (size_t)kRadix * n_tiles;
+    uint32_t* tot = llo + (size_t)kRadix * n_tiles;
+    uint32_t* stot = tot + kRadix;
+    // keys compare on the bits the passes sort (those of ids below n_experts)
+    const uint32_t mkmask = kRadixBits * passes >= 32 ? 0xffffffffu : (1u << (kRadixBits * passes)) - 1u;
+    const dim3 tg((unsigned)n_tiles), tb(kTThreads), sg((unsigned)(kRadix / 4)), sb(256);
     for (int p = 0; p < passes; ++p) {
         const uint32_t* kin = p == 0 ? reinterpret_cast<const uint32_t*>(ids) : kbuf[(p - 1) & 1];
         const uint32_t* vin = p == 0 ? nullptr : vbuf[(p - 1) & 1];
-        uint32_t* kout = kbuf[p & 1];
-        uint32_t* vout = p == passes - 1 ? reinterpret_cast<uint32_t*>(perm) : vbuf[p & 1];
         const int shift = kRadixBits * p;
-        hipLaunchKernelGGL(sort_upsweep, dim3(n_tiles), dim3(256), 0, stream, kin, n, shift, hist, n_tiles);
-        hipLaunchKernelGGL(sort_scan_tiles, dim3(kRadix / 4), dim3(256), 0, stream, hist, n_tiles, total);
-        if (p == 0)
-            hipLaunchKernelGGL(sort_downsweep<true>, dim3(n_tiles), dim3(256), 0, stream, kin, vin, kout, vout, n,
-                               shift, (const uint32_t*)hist, (const uint32_t*)total, n_tiles);
-        else
-            hipLaunchKernelGGL(sort_downsweep<false>, dim3(n_tiles), dim3(256), 0, stream, kin, vin, kout, vout, n,
-                               shift, (const uint32_t*)hist, (const uint32_t*)total, n_tiles);
-        if ((err = hipGetLastError()) != hipSuccess) return (int)err;
+        if (p < passes - 1) {
+            hipLaunchKernelGGL(tsort_count, tg, tb, 0, stream, kin, n, shift, n_tiles, cnt);
+            hipLaunchKernelGGL(tsort_scan<false>, sg, sb, 0, stream, cnt, dist, flo, llo, n_tiles, tot, stot);
+            if (p == 0)
+                hipLaunchKernelGGL(tsort_down<true>, tg, tb, 0, stream, kin, vin, kbuf[p & 1], vbuf[p & 1], n, shift,
+                                   n_tiles, (const uint32_t*)cnt, (const uint32_t*)tot);
+            else
+                hipLaunchKernelGGL(tsort_down<false>, tg, tb, 0, stream, kin, vin, kbuf[p & 1], vbuf[p & 1], n, shift,
+                                   n_tiles, (const uint32_t*)cnt, (const uint32_t*)tot);
+        } else {
+            if (passes <= 2)
+                hipLaunchKernelGGL(tsort_stats_map, tg, tb, 0, stream, kin, n, shift, mkmask, n_tiles, cnt, dist, flo,
+                                   llo);
+            else
+                hipLaunchKernelGGL(tsort_stats, tg, tb, 0, stream, kin, n, shift, mkmask, n_tiles, cnt, dist, flo,
+                                   llo);
+            hipLaunchKernelGGL(tsort_scan<true>, sg, sb, 0, stream, cnt, dist, flo, llo, n_tiles, tot, stot);
+            if (p == 0)
+                hipLaunchKernelGGL(tsort_down_last<true>, tg, tb, 0, stream, kin, vin, n, shift, mkmask, n_tiles,
+                                   (const uint32_t*)cnt, (const uint32_t*)dist, (const uint32_t*)llo,
+                                   (const uint32_t*)tot, (const uint32_t*)stot, perm, uniq, seg_off, pair_slot,
+                                   sorted_slot, n_unique, max_unique);
+            else
+                hipLaunchKernelGGL(tsort_down_last<false>, tg, tb, 0, stream, kin, vin, n, shift, mkmask, n_tiles,
+                                   (const uint32_t*)cnt, (const uint32_t*)dist, (const uint32_t*)llo,
+                                   (const uint32_t*)tot, (const uint32_t*)stot, perm, uniq, seg_off, pair_slot,
+                                   sorted_slot, n_unique, max_unique);
+        }
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return (int)err;
     }
-    const uint32_t* sorted = kbuf[(passes - 1) & 1];
-    hipLaunchKernelGGL(seg_count, dim3(n_tiles), dim3(256), 0, stream, sorted, n, tcnt);
-    hipLaunchKernelGGL(scan_exclusive, dim3(1), dim3(kScanThreads), 0, stream, tcnt, (int64_t)n_tiles, n_unique);
-    hipLaunchKernelGGL(seg_write, dim3(n_tiles), dim3(256), 0, stream, sorted, (const uint32_t*)perm, n, tcnt, uniq,
-                       seg_off, pair_slot, sorted_slot, n_unique, (int32_t)(n < n_experts ? n : n_experts));
-    return (int)hipGetLastError();
+    return 0;
 }
 
 }  // namespace ethos

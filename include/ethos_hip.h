@@ -158,7 +158,7 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
  * ethos_sort_segment without a caller workspace, for callers that cannot allocate device
  * memory (code under HIP graph capture, fixed-memory serving loops).  It has no
  * counterpart in the reference.  The sort workspace is a static array in the library's
- * device data, one per GPU, sized for ETHOS_NOALLOC_MAX_PAIRS pairs (about 19 MiB, held
+ * device data, one per GPU, sized for ETHOS_NOALLOC_MAX_PAIRS pairs (about 18 MiB, held
  * from the first call on a GPU until the process ends); larger n_pairs returns
  * ETHOS_ESIZE.  Every other argument and every output is as for ethos_sort_segment, and
  * the outputs are bit-identical to it.  All calls on one GPU share that array: calls that

@@ -99,10 +99,21 @@ def test_route_ties_break_to_lowest_index():
                                          (12345, 262144, "max"), (300000, 262144, "rand"),
                                          (2000003, 262144, "rand"), (16384, 262144, "skew"),
                                          (16385, 262144, "skew"), (16384, 7, "rand"), (2, 262144, "same"),
-                                         (8192, 262144, "max")])
+                                         (8192, 262144, "max"), (70000, 7, "rand"), (100000, 4096, "rand"),
+                                         (60000, 2 ** 21, "rand"), (300000, 262144, "hot2d"),
+                                         (65536, 262144, "same"), (24577, 262144, "rand")])
 def test_sort_segment_exact(n, E, pattern):
+    """The sort against the oracle's counting sort: one pass (E = 7), two (4,096 and 262,144
+    experts) and three (2^21) over tiles of 8,192 pairs; batches up to 16,384 pairs take the
+    single-workgroup sort.  Patterns: uniform ids, one id everywhere (one segment spanning
+    every tile), Zipf-skewed ids, half the pairs on the largest id, and ids whose two
+    9-bit digits are both Zipf-skewed (hot experts whose segments cross tile boundaries)."""
     rng = np.random.default_rng(n + E)
-    if pattern == "same":
+    if pattern == "hot2d":
+        a = np.minimum(rng.zipf(1.1, n), 192) - 1
+        b = np.minimum(rng.zipf(1.1, n), 192) - 1
+        ids = (a * 512 + b).astype(np.int32)
+    elif pattern == "same":
         ids = np.full(n, 12345, np.int32)
     elif pattern == "skew":
         ids = np.minimum((rng.zipf(1.3, n) - 1), E - 1).astype(np.int32)
