@@ -232,8 +232,10 @@ __device__ __forceinline__ ActMeta act_meta(const HiddenActArgs& A, int64_t row0
 // part + 8 i of the pair's xp row (global) and hidden row (staged: piece part + 8 i is
 // 16-byte group `part` of wave area i), with the arithmetic of apply_act8_kernel
 // (dot_raw in piece order, act_reduce8, act_epilogue), so the activations are
-// bit-identical to it.  Two groups' xp rows are requested before either is summed.
-template <int DH, int kWaves>
+// bit-identical to it.  The xp rows of three groups (a batch) are requested before any is
+// summed, so a tile of ~170 pairs (at most three groups per wave) costs one round trip to
+// memory.
+template <int DH, int kWaves, int kBatch = 3>
 __device__ __forceinline__ void tile_activations(const HiddenActArgs& A, const u32x4_t (*stg)[kHsRows * 8],
                                                  float* dsm, int64_t row0, const ActMeta& m, int wave, int lane) {
     constexpr int P = DH / 64;
@@ -254,31 +256,30 @@ __device__ __forceinline__ void tile_activations(const HiddenActArgs& A, const u
         // this wave's groups of the round: group gi starts at r0 + 8 (wave + waves gi)
         const int64_t left = m.s1 - r0 - 8 * wave;
         const int ng = left <= 0 ? 0 : (int)min((int64_t)8, (left + 8 * kWaves - 1) / (8 * kWaves));
-        for (int gi = 0; gi < ng; gi += 2) {
-            const bool two = gi + 1 < ng;
-            const int sa = gi * 8 + q, sb = sa + 8;
-            const int pa = __shfl(my_p, sa, 64), la = __shfl(my_s, sa, 64);
-            const int pb = __shfl(my_p, two ? sb : sa, 64), lb = __shfl(my_s, two ? sb : sa, 64);
-            const uint16_t* xra = A.xp + (int64_t)(pa / A.hk) * DH;
-            const uint16_t* xrb = A.xp + (int64_t)(pb / A.hk) * DH;
-            uint4 xa[P], xb[P];
+        for (int g0 = 0; g0 < ng; g0 += kBatch) {
+            // every group of the batch has its xp row requested before any is summed
+            uint4 xv[kBatch][P];
+            int sl[kBatch];
 #pragma unroll
-            for (int i = 0; i < P; ++i) xa[i] = *reinterpret_cast<const uint4*>(xra + (part + 8 * i) * 8);
-            if (two) {
+            for (int b = 0; b < kBatch; ++b) {
+                const int src = (g0 + b < ng ? g0 + b : g0) * 8 + q;
+                const int pb = __shfl(my_p, src, 64);
+                sl[b] = __shfl(my_s, src, 64);
+                if (g0 + b < ng) {
+                    const uint16_t* xr = A.xp + (int64_t)(pb / A.hk) * DH;
 #pragma unroll
-                for (int i = 0; i < P; ++i) xb[i] = *reinterpret_cast<const uint4*>(xrb + (part + 8 * i) * 8);
+                    for (int i = 0; i < P; ++i) xv[b][i] = *reinterpret_cast<const uint4*>(xr + (part + 8 * i) * 8);
+                }
             }
-            float acc = 0.0f;
 #pragma unroll
-            for (int i = 0; i < P; ++i) acc = dot_raw(piece(la, i), xa[i], acc);
-            acc = act_reduce8(acc);
-            if (part == 0) dsm[sa] = acc;
-            if (two) {
-                acc = 0.0f;
+            for (int b = 0; b < kBatch; ++b) {
+                if (g0 + b < ng) {
+                    float acc = 0.0f;
 #pragma unroll
-                for (int i = 0; i < P; ++i) acc = dot_raw(piece(lb, i), xb[i], acc);
-                acc = act_reduce8(acc);
-                if (part == 0) dsm[sb] = acc;
+                    for (int i = 0; i < P; ++i) acc = dot_raw(piece(sl[b], i), xv[b][i], acc);
+                    acc = act_reduce8(acc);
+                    if (part == 0) dsm[(g0 + b) * 8 + q] = acc;
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();
