@@ -113,6 +113,32 @@ def timed_steps(m, x_flat, steps: int) -> tuple[float, dict]:
     return elapsed / steps * 1e3, per
 
 
+def hidden_rows_alone_ms(m, x_flat, reps: int = 20) -> float | None:
+    """Mean time of the hidden-row kernel without its activation phase (ethos_generate with
+    no v rows) on this batch's unique experts, timed with HIP events on the launch stream
+    after the timed steps; None when the layer does not use the two-kernel generator."""
+    from ethos_amd import hip
+
+    if x_flat.dtype != torch.bfloat16:
+        return None
+    with torch.no_grad():
+        _, ids = m.router.route(x_flat)
+        seg = hip.sort_segment(ids.view(-1), m.num_experts)
+        lat, w1, w2, _ = m._generator_params(x_flat.dtype, x_flat.device)
+        run = lambda: hip.generate(lat, seg["uniq"], seg["n_unique"], seg["max_unique"], w1, w2,  # noqa: E731
+                                   with_v=False)
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
 def unique_experts(m, x_flat) -> int:
     from ethos_amd import hip
 
@@ -154,11 +180,17 @@ def host_cpu() -> dict:
     """The host's CPU model (/proc/cpuinfo, else lscpu), its logical CPU count and the CPUs
     this process may run on."""
     model = None
+    ident = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "model name" and model is None:
+                    model = val.strip()
+                elif key in ("cpu family", "model", "stepping") and key not in ident:
+                    ident[key] = val.strip()
+                if line.strip() == "":  # the first processor's block is enough
                     break
     except OSError:
         pass
@@ -172,7 +204,8 @@ def host_cpu() -> dict:
                 model = val.strip()
     except (OSError, ValueError, subprocess.SubprocessError):
         pass
-    return {"cpu_model": model or "unknown", "logical_cpus": os.cpu_count(),
+    cpu_id = " ".join(f"{k} {ident[k]}" for k in ("cpu family", "model", "stepping") if k in ident)
+    return {"cpu_model": model or "unknown", "cpu_id": cpu_id or "unknown", "logical_cpus": os.cpu_count(),
             "cpus_available": len(os.sched_getaffinity(0))}
 
 
@@ -204,6 +237,7 @@ def cpu_baseline(sh, x_cpu, sd_cpu, n_tokens: int) -> dict:
         "cores": threads,
         "kind": "port",
         "cpu_model": host["cpu_model"],
+        "cpu_id": host["cpu_id"],
         "logical_cpus": host["logical_cpus"],
         "sample": f"first {n_tokens} of the {sh.n_tok} tokens of the same workload, full reference loop "
                   f"({n_tokens * sh.num_heads * sh.top_k} (token, head, k) iterations), {dt:.1f} s on "
@@ -337,8 +371,21 @@ def main():
         log(f"[bench] timing {args.steps} steps")
         ms, st = timed_steps(m, x_flat, args.steps)
         p50 = st.pop("_p50")
-        sub_us = {k: round(v * 1e3, 2) for k, v in st.pop("_kernels").items()}
+        launch_ms = st.pop("_kernels")
+        sub_us = {k: round(v * 1e3, 2) for k, v in launch_ms.items()}
         U = unique_experts(m, x_flat)
+        # The hidden-row kernel also computes the activations of its tiles' pairs.  Its time is
+        # split into the hidden rows (the same kernel without the activation phase, timed on
+        # its own) and the activations (the rest, added to the activation kernel's).
+        alone = hidden_rows_alone_ms(m, x_flat)
+        split = None
+        if alone is not None and launch_ms["hidden_rows"] > alone:
+            act_part = launch_ms["hidden_rows"] - alone
+            st["generate"] -= act_part
+            st["apply_scatter"] += act_part
+            split = {"hidden_rows_alone_us": round(alone * 1e3, 2), "activation_phase_us": round(act_part * 1e3, 2),
+                     "note": "hidden_rows in stage_us is the kernel with its activation phase; generate counts "
+                             "hidden_rows_alone_us, apply_scatter counts activation_phase_us"}
     work = stage_work(sh, U)
     kernels = {}
     for k, ms_k in st.items():
@@ -415,6 +462,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "stage_us": sub_us,
+        "hidden_rows_split": split,
         "alternatives": alternatives,
         "cpu_baseline": cpu,
         "decode_64_tokens": decode,
