@@ -961,7 +961,8 @@ int launch_expert_forward(const void* x, const void* latents, int64_t n_experts,
     // computed while its rows are in LDS; then the activation kernel for the rest (the
     // pairs of larger tiles, or all pairs in token order when the hidden rows are few)
     int rc = launch_hidden_act(latents, n_experts, uniq, n_unique, max_unique, w1, dl, dh, hout, xp, perm,
-                               sorted_slot, seg_off, gates, H * k, act, num_cus, stream);
+                               sorted_slot, seg_off, gates, H * k, act, n_tok * H * k, num_cus,
+                               stream);
     if (rc != 0) return rc;
     stage_mark(stream);
     rc = launch_act(xp, hout, perm, sorted_slot, pair_slot, n_unique, seg_off, gates, n_tok * H * k, H * k, dh, dtype,

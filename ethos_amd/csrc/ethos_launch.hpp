@@ -53,7 +53,7 @@ int launch_generate_part(const void* latents, int64_t n_experts, const int32_t* 
 int launch_hidden_act(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                       int64_t max_unique, const void* w1, int dl, int dh, void* hout, const void* xp,
                       const int32_t* perm, const int32_t* sorted_slot, const int32_t* seg_off, const void* gates, int hk,
-                      float* act, int num_cus, hipStream_t stream);
+                      float* act, int64_t n_pairs, int num_cus, hipStream_t stream);
 
 int apply_chunks(int d, int dtype);
 int launch_expert_backward(const void* hid, const float* xp, const float* dyb, const int32_t* pair_slot,

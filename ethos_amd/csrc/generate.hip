@@ -195,11 +195,13 @@ struct HiddenActArgs {
     const uint16_t* gates;       // [n_pairs]
     int hk;                      // pairs per token (heads x top_k)
     float* act;                  // [n_pairs] activations (fp32 holding bf16 values)
+    int64_t n_pairs;             // entries of perm, sorted_slot, gates and act
 };
 
-// A tile's activations: its sorted positions and this lane's pair of the first round,
-// loaded at the top of the tile's iteration, so that the loads have landed by the time
-// the tile's rows are staged.
+// A tile's activations: its sorted positions and this lane's pair of the first round.
+// The tile's seg_off bounds are loaded one tile ahead and its pair and row at the top of
+// the tile's iteration, with no branch between a load and its use, so that all of them
+// have landed by the time the tile's rows are staged.
 struct ActMeta {
     int64_t s0, s1;  // the tile's pairs: sorted positions s0 .. s1 - 1
     int p, s;        // this lane's pair of the first round and its row in the tile
@@ -211,15 +213,21 @@ __device__ __forceinline__ int64_t act_position(int64_t r0, int wave, int lane) 
     return r0 + 8 * (wave + kWaves * (lane >> 3)) + (lane & 7);
 }
 
+// sorted position j clamped to the pair arrays, so that its loads need no branch
+__device__ __forceinline__ int64_t act_index(const HiddenActArgs& A, int64_t j) {
+    return j < 0 ? 0 : (j < A.n_pairs ? j : A.n_pairs - 1);
+}
+
 template <int kWaves>
-__device__ __forceinline__ ActMeta act_meta(const HiddenActArgs& A, int64_t row0, int live, int wave, int lane) {
+__device__ __forceinline__ ActMeta act_meta(const HiddenActArgs& A, int64_t row0, int64_t s0, int64_t s1, int wave,
+                                            int lane) {
     ActMeta m;
-    m.s0 = A.seg_off[row0];
-    m.s1 = A.seg_off[row0 + live];
-    const int64_t j = act_position<kWaves>(m.s0, wave, lane);
-    m.valid = j < m.s1 && m.s1 - m.s0 <= kActFusedCap;
-    m.p = m.valid ? A.perm[j] : 0;
-    m.s = m.valid ? A.sorted_slot[j] - (int)row0 : 0;
+    m.s0 = s0;
+    m.s1 = s1;
+    const int64_t j = act_position<kWaves>(s0, wave, lane), jc = act_index(A, j);
+    m.valid = j < s1 && s1 - s0 <= kActFusedCap;
+    m.p = A.perm[jc];
+    m.s = A.sorted_slot[jc] - (int)row0;
     return m;
 }
 
@@ -246,44 +254,45 @@ __device__ __forceinline__ void tile_activations(const HiddenActArgs& A, const u
         int my_p = m.p, my_s = m.s;
         bool valid = m.valid;
         if (r0 != m.s0) {
-            const int64_t j = act_position<kWaves>(r0, wave, lane);
+            const int64_t j = act_position<kWaves>(r0, wave, lane), jc = act_index(A, j);
             valid = j < m.s1;
-            my_p = valid ? A.perm[j] : 0;
-            my_s = valid ? A.sorted_slot[j] - (int)row0 : 0;
+            my_p = A.perm[jc];
+            my_s = A.sorted_slot[jc] - (int)row0;
         }
         my_s = my_s < 0 ? 0 : (my_s < kHsRows ? my_s : kHsRows - 1);  // stays inside the tile on any input
-        const uint16_t my_g = valid ? A.gates[my_p] : (uint16_t)0;
+        // the gate is requested with the xp rows and used by the epilogue
+        const uint16_t g_raw = A.gates[my_p];
+        const int my_t = my_p / A.hk;  // the pair's token
         // this wave's groups of the round: group gi starts at r0 + 8 (wave + waves gi)
         const int64_t left = m.s1 - r0 - 8 * wave;
-        const int ng = left <= 0 ? 0 : (int)min((int64_t)8, (left + 8 * kWaves - 1) / (8 * kWaves));
+        const int ng =
+            __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : (int)min((int64_t)8, (left + 8 * kWaves - 1) / (8 * kWaves)));
         for (int g0 = 0; g0 < ng; g0 += kBatch) {
-            // every group of the batch has its xp row requested before any is summed
+            // Every group of the batch has its xp row requested before any is summed.  The
+            // loads and sums are unconditional (a group past ng repeats group g0, whose
+            // result is not kept), so no branch separates a load from its use.
             uint4 xv[kBatch][P];
             int sl[kBatch];
 #pragma unroll
             for (int b = 0; b < kBatch; ++b) {
                 const int src = (g0 + b < ng ? g0 + b : g0) * 8 + q;
-                const int pb = __shfl(my_p, src, 64);
+                const int tb = __shfl(my_t, src, 64);
                 sl[b] = __shfl(my_s, src, 64);
-                if (g0 + b < ng) {
-                    const uint16_t* xr = A.xp + (int64_t)(pb / A.hk) * DH;
+                const uint16_t* xr = A.xp + (int64_t)tb * DH;
 #pragma unroll
-                    for (int i = 0; i < P; ++i) xv[b][i] = *reinterpret_cast<const uint4*>(xr + (part + 8 * i) * 8);
-                }
+                for (int i = 0; i < P; ++i) xv[b][i] = *reinterpret_cast<const uint4*>(xr + (part + 8 * i) * 8);
             }
 #pragma unroll
             for (int b = 0; b < kBatch; ++b) {
-                if (g0 + b < ng) {
-                    float acc = 0.0f;
+                float acc = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < P; ++i) acc = dot_raw(piece(sl[b], i), xv[b][i], acc);
-                    acc = act_reduce8(acc);
-                    if (part == 0) dsm[(g0 + b) * 8 + q] = acc;
-                }
+                for (int i = 0; i < P; ++i) acc = dot_raw(piece(sl[b], i), xv[b][i], acc);
+                acc = act_reduce8(acc);
+                if (part == 0 && g0 + b < ng) dsm[(g0 + b) * 8 + q] = acc;
             }
         }
         __builtin_amdgcn_wave_barrier();
-        if (valid) A.act[my_p] = act_epilogue<uint16_t>(dsm[lane], bf16_bits_to_f32(my_g));
+        if (valid) A.act[my_p] = act_epilogue<uint16_t>(dsm[lane], bf16_bits_to_f32(g_raw));
         __builtin_amdgcn_wave_barrier();
     }
 }
@@ -374,6 +383,17 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
 
     __amdgpu_buffer_rsrc_t hr_prev = __builtin_amdgcn_make_buffer_rsrc(hout, (short)0, 0, 0x00020000);
     bool have_prev = false;
+    // seg_off bounds of tile t: loaded one tile ahead (tile t is clamped to the last tile)
+    auto seg_bounds = [&](int64_t t, int32_t& b0, int32_t& b1) {
+        const int64_t tc = t < n_tiles ? t : n_tiles - 1;
+        const int64_t r0 = tc * kHsRows;
+        b0 = A.seg_off[r0];
+        b1 = A.seg_off[r0 + (U - (int)r0 < kHsRows ? U - (int)r0 : kHsRows)];
+    };
+    int32_t nb0 = 0, nb1 = 0;
+    if constexpr (kAct) {
+        if (act_on && (int)blockIdx.x < n_tiles) seg_bounds(blockIdx.x, nb0, nb1);
+    }
     int i = 0;
     for (int64_t t = blockIdx.x; t < n_tiles; t += G, ++i) {
         __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this tile's rows have landed
@@ -382,7 +402,11 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
         const int live = U - (int)row0 < kHsRows ? U - (int)row0 : kHsRows;
         ActMeta meta{};
         if constexpr (kAct) {
-            if (act_on) meta = act_meta<kWaves>(A, row0, live, wave, lane);
+            if (act_on) {
+                const int32_t b0 = __builtin_amdgcn_readfirstlane(nb0), b1 = __builtin_amdgcn_readfirstlane(nb1);
+                seg_bounds(t + G, nb0, nb1);
+                meta = act_meta<kWaves>(A, row0, b0, b1, wave, lane);
+            }
         }
         u32x4_t outv[kNSt];
 #pragma unroll
@@ -993,8 +1017,9 @@ static bool launch_hidden_act_t(const void* latents, int64_t n_experts, const in
 int launch_hidden_act(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,
                       int64_t max_unique, const void* w1, int dl, int dh, void* hout, const void* xp,
                       const int32_t* perm, const int32_t* sorted_slot, const int32_t* seg_off, const void* gates, int hk,
-                      float* act, int num_cus, hipStream_t stream) {
-    const HiddenActArgs A{(const uint16_t*)xp, perm, sorted_slot, seg_off, (const uint16_t*)gates, hk, act};
+                      float* act, int64_t n_pairs, int num_cus, hipStream_t stream) {
+    if (n_pairs <= 0) return -1;
+    const HiddenActArgs A{(const uint16_t*)xp, perm, sorted_slot, seg_off, (const uint16_t*)gates, hk, act, n_pairs};
     if (launch_hidden_act_t<128, 512>(latents, n_experts, uniq, n_unique, max_unique, w1, dl, dh, hout, A, num_cus,
                                       stream) ||
         launch_hidden_act_t<128, 256>(latents, n_experts, uniq, n_unique, max_unique, w1, dl, dh, hout, A, num_cus,
