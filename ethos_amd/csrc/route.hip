@@ -247,6 +247,31 @@ template <> struct KeyVec<float> {
     }
 };
 
+// 16 bytes of a query row -> floats (bf16 and fp32 elements are exact in float).
+template <typename T> struct QVecF;
+template <> struct QVecF<uint16_t> {
+    static constexpr int kN = 8;
+    __device__ __forceinline__ static void load(const uint16_t* p, float* f) {
+        const uint4 r = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+};
+template <> struct QVecF<float> {
+    static constexpr int kN = 4;
+    __device__ __forceinline__ static void load(const float* p, float* f) {
+        const float4 r = *reinterpret_cast<const float4*>(p);
+        f[0] = r.x;
+        f[1] = r.y;
+        f[2] = r.z;
+        f[3] = r.w;
+    }
+};
+
 struct RouteSmem {
     size_t s_off, kn_off, qs_off, total;
     int qs_pitch;  // bytes per staged query-half row
@@ -445,33 +470,55 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) n_cand[rr] = n_pend[rr] = 0;
         uint32_t slow_rows = 0;
-        // largest sub-key norm bound of this half (wave-uniform)
+        // this lane's sub-key norm bounds (keys lane + 64 m) and their largest value over
+        // the half (wave-uniform)
+        float knr[kRtSlots];
         float kn_max;
         {
             uint32_t kb = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
                 const int j = lane + m * kWave;
-                if (j < K) kb = max(kb, __float_as_uint(kn[half * kpad + j]));
+                knr[m] = j < K ? kn[half * kpad + j] : 0.0f;
+                kb = max(kb, __float_as_uint(knr[m]));
             }
             kn_max = __uint_as_float(wave_max_u32(kb));
+        }
+        // sums of squares of the wave's staged query halves, all its rows at once: 64 / RPW
+        // lanes per row (one DPP row of 16 lanes when a wave has four rows); every lane of
+        // a row's group receives the row's sum
+        float sq_row = 0.0f;
+        {
+            constexpr int kLPR = kWave / RPW;
+            constexpr int kN = QVecF<T>::kN;
+            static_assert(RPW == 1 || RPW == 4, "row groups of 64 or 16 lanes");
+            const int lr = wave * RPW + lane / kLPR;
+            const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
+            for (int i = (lane % kLPR) * kN; i < dh2; i += kLPR * kN) {
+                float v[kN];
+                QVecF<T>::load(qs + i, v);
+#pragma unroll
+                for (int t = 0; t < kN; ++t) sq_row = __builtin_fmaf(v[t], v[t], sq_row);
+            }
+            if constexpr (RPW == 1) {
+                sq_row = wave_sum(sq_row);
+            } else {
+                sq_row += dpp_f32<kDppXor1>(sq_row);
+                sq_row += dpp_f32<kDppXor2>(sq_row);
+                sq_row += dpp_f32<kDppRowHalfMirror>(sq_row);
+                sq_row += dpp_f32<kDppRowMirror>(sq_row);
+            }
         }
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) {
             const int lr = wave * RPW + rr;
             const int64_t r = row0 + lr;
             if (r >= rows) break;
-            // bound the norm of the staged query half
-            const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
-            float sq = 0.0f;
-            for (int i = lane * KeyVec<T>::kN; i < dh2; i += kWave * KeyVec<T>::kN) {
-                double v[KeyVec<T>::kN];
-                KeyVec<T>::load(qs + i, v);
-#pragma unroll
-                for (int t = 0; t < KeyVec<T>::kN; ++t) sq = __builtin_fmaf((float)v[t], (float)v[t], sq);
-            }
-            // (v_sqrt_f32 is within 1 ulp for a normal argument; the offset keeps it normal)
-            const float qn = __builtin_amdgcn_sqrtf(wave_sum(sq) + 0x1p-100f) * (1.0f + 0x1p-12f);
+            // bound the norm of the staged query half (the 2^-12 slack covers the fp32
+            // rounding of the sum of squares; v_sqrt_f32 is within 1 ulp for a normal
+            // argument, and the offset keeps it normal)
+            const float sq = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sq_row), rr * (kWave / RPW)));
+            const float qn = __builtin_amdgcn_sqrtf(sq + 0x1p-100f) * (1.0f + 0x1p-12f);
             const float gq = gamma * qn;
             const float A = (qn + gq) * kn_max * 0x1p-21f * (1.0f + 0x1p-20f) + 0x1p-120f;
             const float E = __builtin_fmaf(gq, kn_max, A) * (1.0f + 0x1p-20f);
@@ -509,7 +556,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
                 const int j = lane + m * kWave;
-                f[m] = j < K && __builtin_fmaf(gq, kn[half * kpad + j], sv[m]) >= cut;
+                f[m] = j < K && __builtin_fmaf(gq, knr[m], sv[m]) >= cut;
                 fb[m] = ballot(f[m]);
                 n += (int)__popcll(fb[m]);
             }
