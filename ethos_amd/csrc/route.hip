@@ -45,6 +45,7 @@ constexpr int kRtRows = 32;                            // rows of the MFMA tile 
 // workgroups and cuts each wave's sequential work by 4
 constexpr int kRtSmallRows = 4096;                     // batches up to this many rows take 1 row per wave
 constexpr int kRtMaxKc = 32;                           // k_cand <= 32, top_k <= 32
+static_assert(kRtMaxKc <= kWave, "candidate lists hold one entry per lane");
 constexpr int kRtMaxK = 512;                           // sub-keys per table
 constexpr int kRtSlots = kRtMaxK / kWave;              // approximate scores per lane per row
 constexpr int kRtStSlots = 2;                          // staircase pairs per lane (<= 119 for top_k <= 32)
@@ -334,10 +335,6 @@ __device__ __forceinline__ uint64_t exact_key(const T* qh, const T* __restrict__
     }
     return make_key(Elem<T>::round64(acc), (uint32_t)j);
 }
-
-// Certified score of a candidate slot, or this pattern (a NaN, never a certified score)
-// when the slot still needs the exact chain.
-constexpr uint32_t kRtPending = 0xffffffffu;
 
 template <typename T, int RPW>
 __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
