@@ -148,18 +148,62 @@ def unique_experts(m, x_flat) -> int:
         return int(seg["n_unique"].item())
 
 
+def load_profile_json(kind: str, config: str):
+    """The machine-readable block of a committed rocprofv3 summary (profiles/<kind>_<config>.md),
+    or None."""
+    path = os.path.join(REPO, "profiles", f"{kind}_{config}.md")
+    if not os.path.exists(path):
+        return None
+    try:
+        return json.loads(open(path).read().split("```json", 1)[1].split("```", 1)[0])
+    except (IndexError, ValueError):
+        return None
+
+
 def load_traffic(config: str, stage: str):
     """HBM bytes per launch of `stage` from the committed rocprofv3 --pmc summary (FETCH_SIZE +
     WRITE_SIZE, scaled by the same counters on a plain copy of known size), or None."""
-    path = os.path.join(REPO, "profiles", f"hbm_traffic_{config}.md")
-    if not os.path.exists(path):
-        return None
-    text = open(path).read()
+    js = load_profile_json("hbm_traffic", config)
     try:
-        block = text.split("```json", 1)[1].split("```", 1)[0]
-        return json.loads(block)["stages"][stage]["traffic_bytes"]
-    except (IndexError, KeyError, ValueError):
+        return js["stages"][stage]["traffic_bytes"]
+    except (TypeError, KeyError):
         return None
+
+
+# Kernels behind the counter figures, named as rocprofv3 names them in the summaries.
+SCATTER_KERNELS = ["void ethos::apply_scatter_kernel<u16, 2>"]
+SORT_KERNELS = ["ethos::tsort_count", "void ethos::tsort_scan<false>", "void ethos::tsort_down<true>",
+                "ethos::tsort_stats_map", "void ethos::tsort_scan<true>", "void ethos::tsort_down_last<false>"]
+GEMM_KERNELS = {"v_rows": "void ethos::expand_ws_bf16_kernel<512>",
+                "hidden_rows_alone": "void ethos::hidden_ws_bf16_kernel<128, 512, false>",
+                "hidden_rows_with_activations": "void ethos::hidden_ws_bf16_kernel<128, 512, true>"}
+
+
+def counter_figures(config: str, stage_us: dict) -> dict | None:
+    """Per-kernel evidence from the committed rocprofv3 counter summaries: HBM bytes per launch
+    (FETCH_SIZE + WRITE_SIZE, copy-calibrated) of the gather/scatter and sort kernels over their
+    launch time measured in this run, and the MFMA-busy fraction of the generator GEMMs
+    (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs)."""
+    hbm, mf = load_profile_json("hbm_traffic", config), load_profile_json("mfma_counters", config)
+    out = {}
+    if hbm and "kernels" in hbm:
+        for stage, names in (("scatter_back", SCATTER_KERNELS), ("sort_segment", SORT_KERNELS)):
+            ks = [k for k in names if k in hbm["kernels"]]
+            us = stage_us.get(stage)
+            if ks and us:
+                b = sum(hbm["kernels"][k]["read_bytes"] + hbm["kernels"][k]["write_bytes"] for k in ks)
+                gbs = b / (us * 1e-6) / 1e9
+                out[stage] = dict(kernels=ks, hbm_bytes=b, us=us, achieved_GBps=round(gbs, 1), peak_GBps=HBM_PEAK_GBS,
+                                  frac=round(gbs / HBM_PEAK_GBS, 4))
+    if mf and "kernels" in mf:
+        for name, k in GEMM_KERNELS.items():
+            if k in mf["kernels"]:
+                out[name] = dict(kernel=k, mfma_busy=mf["kernels"][k]["mfma_busy"])
+    if not out:
+        return None
+    out["source"] = (f"profiles/hbm_traffic_{config}.md and profiles/mfma_counters_{config}.md (rocprofv3 counters); "
+                     "times from this run")
+    return out
 
 
 def copy_probe(mib: int) -> None:
@@ -461,6 +505,7 @@ def main():
         "unique_experts": U,
         "roofline": roofline,
         "kernels": kernels,
+        "counters": counter_figures(args.config, sub_us),
         "stage_us": sub_us,
         "hidden_rows_split": split,
         "alternatives": alternatives,
