@@ -201,13 +201,24 @@ __device__ __forceinline__ uint64_t key64_of32(uint32_t k) {
     return ((uint64_t)o32 << 32) | (uint64_t)(~(0xffffu - (k & 0xffffu)));
 }
 
-// Descending sort of one canonical key per lane; keys of bf16 scores sort in their
-// 32-bit form (half the lane exchanges).
-template <typename T>
-__device__ __forceinline__ uint64_t wave_sort_keys(uint64_t k, int lane) {
-    if constexpr (sizeof(T) == 2) return key64_of32(wave_sort_desc<uint32_t>(key32_of(k), lane));
-    else return wave_sort_desc<uint64_t>(k, lane);
-}
+// A row's candidate list as held between the halves: for bf16 scores the 32-bit key form
+// (half the registers), else the canonical key.
+template <typename T> struct ListKey {
+    using type = uint64_t;
+    __device__ __forceinline__ static uint64_t pack(uint64_t k) { return k; }
+    __device__ __forceinline__ static uint64_t unpack(uint64_t k) { return k; }
+    // descending sort of one key per lane, in list form
+    __device__ __forceinline__ static uint64_t sort(uint64_t k, int lane) { return wave_sort_desc<uint64_t>(k, lane); }
+};
+template <> struct ListKey<uint16_t> {
+    using type = uint32_t;
+    __device__ __forceinline__ static uint32_t pack(uint64_t k) { return key32_of(k); }
+    __device__ __forceinline__ static uint64_t unpack(uint32_t k) { return key64_of32(k); }
+    // keys of bf16 scores sort in their 32-bit form (half the lane exchanges)
+    __device__ __forceinline__ static uint32_t sort(uint64_t k, int lane) {
+        return wave_sort_desc<uint32_t>(key32_of(k), lane);
+    }
+};
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = max(v, dpp_u32<kDppXor1>(v));
@@ -356,7 +367,8 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
     constexpr int kRowsWG = kRtWaves * RPW;  // rows of this workgroup (<= kRtRows)
     // key vectors in flight per exact chain (one row per wave leaves registers for more)
     constexpr int kExG = RPW == 1 ? 8 : 2;
-    uint64_t lst[RPW][2];
+    using LK = ListKey<T>;
+    typename LK::type lst[RPW][2];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) lst[rr][0] = lst[rr][1] = 0;
 
@@ -633,11 +645,12 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             const int64_t r = row0 + lr;
             if (r >= rows) break;
             const int n = n_cand[rr];
-            uint64_t run = 0;
+            typename LK::type run_l;
             if (!((slow_rows >> rr) & 1u)) {
                 const uint64_t* ck = reinterpret_cast<const uint64_t*>(S + lr * pitch);
-                run = wave_sort_keys<T>(lane < n ? ck[lane] : 0ull, lane);
+                run_l = LK::sort(lane < n ? ck[lane] : 0ull, lane);
             } else {
+                uint64_t run = 0;
                 const int32_t* cand = reinterpret_cast<const int32_t*>(S + lr * pitch);
                 const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
                 for (int c0 = 0; c0 < n; c0 += kWave) {
@@ -646,9 +659,10 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
                     key = wave_sort_desc<uint64_t>(key, lane);
                     run = c0 == 0 ? key : wave_merge_desc(run, key, lane);
                 }
+                run_l = LK::pack(run);
             }
-            if (half == 0) lst[rr][0] = run;
-            else lst[rr][1] = run;
+            if (half == 0) lst[rr][0] = run_l;
+            else lst[rr][1] = run_l;
         }
         __syncthreads();
     }
@@ -695,7 +709,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         const int lr = wave * RPW + rr;
         const int64_t r = row0 + lr;
         if (r >= rows) break;
-        const uint64_t L1 = lst[rr][0], L2 = lst[rr][1];
+        const uint64_t L1 = LK::unpack(lst[rr][0]), L2 = LK::unpack(lst[rr][1]);
         // (lane shuffles: call with every lane active, then select)
         auto pair_key = [&](int a, int b) {
             const uint64_t ka = shfl_u64(L1, a), kb = shfl_u64(L2, b);
