@@ -709,6 +709,12 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
 // others find it in that XCD's L2.  Operands and k-steps are those of
 // expand_bf16_kernel (A = W_v rows, B = hidden rows, k-steps in order), so v is
 // bit-identical to it; the difference is that no tile waits for its hidden rows.
+//
+// Most of each tile's epilogue is carried out during the next tile's MFMAs: right after
+// its k-steps a tile's sums are rounded to bf16 pairs in registers (32 registers, no LDS
+// work), the next tile's MFMAs start at once, and the 32 remaining operations of the
+// epilogue (16 staging writes, then 8 read-backs of whole 128-byte rows each followed by
+// its store) are spread evenly over that tile's k-steps.
 // ---------------------------------------------------------------------------------
 constexpr int kWsCols = 256;  // output columns per workgroup, 64 per wave
 constexpr int kWsRows = 64;   // experts per tile
@@ -723,34 +729,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int LA = 4;                                // fragment reads run LA k-steps ahead
     constexpr int kCS = kCopiesW / 4;                    // k-steps that issue copies (4 each)
     constexpr int kNSt = 8;                              // v-row stores per wave and tile
-    // the previous tile's stores go out every kStride k-steps after the copies, spread over
-    // the tile's MFMAs
-    constexpr int kStride = (KS2 - 1 - kCS) / (kNSt - 1) > 0 ? (KS2 - 1 - kCS) / (kNSt - 1) : 1;
-    static_assert(GPR >= 16 && (GPR & (GPR - 1)) == 0 && kCopiesW % 4 == 0 && kCS + kStride * (kNSt - 1) < KS2,
+    constexpr int kEpi = 16 + 2 * kNSt;                  // epilogue operations per tile
+    static_assert(GPR >= 16 && (GPR & (GPR - 1)) == 0 && kCopiesW % 4 == 0 && kEpi % KS2 == 0 && kCS <= KS2,
                   "tile staging shape");
-    // Hidden tiles: row r's 16-byte group g sits at slot g ^ (r % 16) of the row, so a
-    // fragment read (one group, 16 consecutive rows per 256 bytes of banks) is
-    // conflict-free.
+    constexpr int kOps = kEpi / KS2;                     // epilogue operations per k-step
     __shared__ uint4 hs[2][kWsRows * GPR];
-    // Output staging, per wave: 64 experts x 64 columns of bf16; expert r's 128-byte
-    // row holds its 16-byte group q at slot q ^ (r % 8).
     __shared__ u32x4_t stg[4][kWsRows * 8];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
-    // the h and v outputs hold max_unique rows
     const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
     const int n_tiles = (U + kWsRows - 1) / kWsRows;
-    // Workgroup b runs on XCD b % 8.  Slots b / 8 of one XCD are taken n_cg at a time:
-    // the members of one group, column groups 0 .. n_cg - 1.  (The launch makes the
-    // grid a multiple of 8 n_cg.)
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int per_xcd = ((int)gridDim.x >> 3) / n_cg;
     const int cg = slot % n_cg, grp = xcd * per_xcd + slot / n_cg;
     const int n_groups = 8 * per_xcd;
-    const int col0 = cg * kWsCols + wave * 64;  // the wave's first output column
+    const int col0 = cg * kWsCols + wave * 64;
 
-    // the wave's W_v rows: A fragment (cb, s) = W_v[col0 + 32 cb + l32][16 s + 8 h ..]
     bf16x8_t wf[2][KS2];
     {
         const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
@@ -763,10 +758,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
                                   wr, ((col0 + 32 * cb + l32) * DH + 16 * s + 8 * h) * (int)sizeof(uint16_t), 0, 0));
     }
-    // Copy instruction j = 4 it + wave of a tile moves LDS slots 64 j .. 64 j + 63 (lane
-    // i: slot f = 64 j + i, row f / GPR, slot f % GPR of that row, which holds global
-    // group (f % GPR) ^ (row % 16)).  Rows at or past U read as zero (the descriptor
-    // covers rows below U only).
     auto copy = [&](int64_t tile, int buf, int it) {
         const int64_t row0 = tile * kWsRows;
         const int64_t live = U - row0;
@@ -777,43 +768,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const int r = f / GPR, gs = f % GPR;
         lds_dma16(rs, (r * DH + 8 * (gs ^ (r & 15))) * (int)sizeof(uint16_t), 0, lds_addr(&hs[buf][64 * j]));
     };
-    // B fragment (mb, s) of the current tile: row 32 mb + l32, group 2 s + h, at slot
-    // (2 s + h) ^ (l32 % 16) = ((2 (s % 8) + h) ^ (l32 % 16)) + 16 (s / 8)
     int bq_off[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) bq_off[q] = l32 * GPR + ((2 * q + h) ^ (l32 & 15));
-    // lane's store k covers staged row 8 k + lane / 8, 16-byte group lane % 8
     const int st_voff = ((lane >> 3) * d2 + col0 + 8 * (lane & 7)) * (int)sizeof(uint16_t);
     constexpr int kOOB = 0x40000000;  // a byte offset past any tile's rows (and kOOB + 56 d2 * 2 < 2^31)
     u32x4_t* my = stg[wave];
     u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
-    // s_waitcnt vmcnt(8) (gfx9 immediate: vmcnt [3:0] and [15:14], expcnt [6:4],
-    // lgkmcnt [11:8]; expcnt 7 and lgkmcnt 15 do not wait)
     constexpr int kWaitVm8 = 0x0f78;
     constexpr int kWaitVm0 = 0x0f70;
+    // the store descriptor of a tile's rows (rows below max_unique)
+    auto tile_rsrc = [&](int64_t t) {
+        const int64_t row0 = t * kWsRows;
+        const int64_t rows_left = max_unique - row0;
+        const int tile_rows = rows_left < kWsRows ? (int)rows_left : kWsRows;
+        return __builtin_amdgcn_make_buffer_rsrc(uv + row0 * d2, (short)0, tile_rows * d2 * (int)sizeof(uint16_t),
+                                                 0x00020000);
+    };
+    // A tile's sums as bf16 pairs: pk[e] (e = 8 mb + 4 cb + a4) holds columns
+    // col0 + 32 cb + 8 a4 + 4 h .. + 3 of expert 32 mb + l32, i.e. 8-byte half h of 16-byte
+    // group 4 cb + a4 of staged row 32 mb + l32.
+    u32x2_t pk[16];
+    u32x4_t ov[kNSt];
+    // epilogue operation e of the tile held in pk: e < 16 stages pk[e]; then, for k = 0 .. 7,
+    // e = 16 + 2 k reads back staged row group k (rows 8 k .. 8 k + 7) and e + 1 stores it
+    auto epi = [&](int e, __amdgpu_buffer_rsrc_t rsrc, int st_base) {
+        if (e < 16) {
+            const int mb = e / 8, q = e % 8;
+            const int r = mb * 32 + l32;
+            my2[r * 16 + (q ^ (r & 7)) * 2 + h] = pk[e];
+        } else if ((e - 16) % 2 == 0) {
+            const int k = (e - 16) / 2, r = 8 * k + (lane >> 3);
+            ov[k] = my[r * 8 + ((lane & 7) ^ (r & 7))];
+        } else {
+            const int k = (e - 16) / 2;
+            __builtin_amdgcn_raw_buffer_store_b128(ov[k], rsrc, st_base + k * 8 * d2 * 2, 0, 2);
+        }
+    };
 
     if (grp < n_tiles) {
 #pragma unroll
         for (int it = 0; it < kCopiesW; ++it) copy(grp, 0, it);
     }
-    // the W_v rows and the first tile
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
-    // stores of the previous tile's staged rows go through that tile's descriptor
-    // (rows below max_unique)
-    __amdgpu_buffer_rsrc_t uvr_prev = __builtin_amdgcn_make_buffer_rsrc(uv, (short)0, 0, 0x00020000);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) pk[e] = u32x2_t{0u, 0u};
+    // The previous tile's epilogue goes out during this tile's k-steps.  The first tile has
+    // no previous one: its epilogue stores go to an offset past the descriptor (no memory is
+    // written), so that every tile issues its eight stores after its copies and the
+    // vmcnt(8) at the top of the next tile covers the copies.
+    __amdgpu_buffer_rsrc_t prev_rsrc = tile_rsrc(0);
     bool have_prev = false;
     int i = 0;
     for (int64_t t = grp; t < n_tiles; t += n_groups, ++i) {
         __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this tile's copies have landed
         __syncthreads();
         const int64_t t_next = t + n_groups;
-        u32x4_t outv[kNSt];
-#pragma unroll
-        for (int k = 0; k < kNSt; ++k) {
-            const int r = 8 * k + (lane >> 3);
-            outv[k] = my[r * 8 + ((lane & 7) ^ (r & 7))];
-        }
         const int st_base = have_prev ? st_voff : kOOB;
         const uint4* cur = hs[i & 1];
         auto bfrag = [&](int s, int mb) {
@@ -844,56 +855,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 for (int mb = 0; mb < 2; ++mb)
                     acc[mb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cb][s], bfr[s % (LA + 1)][mb],
                                                                          acc[mb][cb], 0, 0, 0);
-            // copies of the next tile, four per k-step
             if (s < kCS && t_next < n_tiles) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) copy(t_next, (i + 1) & 1, 4 * s + j);
             }
-            // the previous tile's rows, one store every kStride k-steps
-            if (s >= kCS && (s - kCS) % kStride == 0 && (s - kCS) / kStride < kNSt)
-                __builtin_amdgcn_raw_buffer_store_b128(outv[(s - kCS) / kStride], uvr_prev,
-                                                       st_base + ((s - kCS) / kStride) * 8 * d2 * 2, 0, 2);
+#pragma unroll
+            for (int o = 0; o < kOps; ++o) epi(s * kOps + o, prev_rsrc, st_base);
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, kNSt + 2 * LA, 0);
+        // per k-step: its MFMAs, then the fragment reads LA k-steps ahead, then its
+        // epilogue operations (staging write, read-back or store)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * LA, 0);
 #pragma unroll
         for (int s = 0; s < KS2; ++s) {
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
             if (s + LA < KS2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            if (s >= kCS && (s - kCS) % kStride == 0 && (s - kCS) / kStride < kNSt)
-                __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
-        }
-        // acc[mb][cb][i]: column col0 + 32 cb + 8 (i/4) + 4h + i%4 of expert 32 mb + l32
-        // of the tile, i.e. 8-byte half h of 16-byte group 4 cb + i/4 of staged row
-        // 32 mb + l32
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-            const int r = mb * 32 + l32;
+            for (int o = 0; o < kOps; ++o) {
+                const int e = s * kOps + o;
+                if (e < 16)
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                else if ((e - 16) % 2 == 0)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                else
+                    __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
+            }
+        }
+        // this tile's sums, rounded (acc[mb][cb][i]: column col0 + 32 cb + 8 (i/4) + 4h + i%4
+        // of expert 32 mb + l32)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-                    const int q = 4 * cb + a4;
-                    my2[r * 16 + (q ^ (r & 7)) * 2 + h] =
-                        u32x2_t{pack_bf16x2(acc[mb][cb][4 * a4], acc[mb][cb][4 * a4 + 1]),
-                                pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3])};
-                }
-        }
-        const int64_t row0 = t * kWsRows;
-        const int64_t rows_left = max_unique - row0;
-        const int tile_rows = rows_left < kWsRows ? (int)rows_left : kWsRows;
-        uvr_prev = __builtin_amdgcn_make_buffer_rsrc(uv + row0 * d2, (short)0,
-                                                     tile_rows * d2 * (int)sizeof(uint16_t), 0x00020000);
+                for (int a4 = 0; a4 < 4; ++a4)
+                    pk[8 * mb + 4 * cb + a4] = u32x2_t{pack_bf16x2(acc[mb][cb][4 * a4], acc[mb][cb][4 * a4 + 1]),
+                                                       pack_bf16x2(acc[mb][cb][4 * a4 + 2], acc[mb][cb][4 * a4 + 3])};
+        prev_rsrc = tile_rsrc(t);
         have_prev = true;
     }
-    // the last tile's rows (the staging writes above are this wave's own LDS operations,
-    // which complete in order)
+    // the last tile's epilogue
     if (have_prev) {
 #pragma unroll
-        for (int k = 0; k < kNSt; ++k) {
-            const int r = 8 * k + (lane >> 3);
-            __builtin_amdgcn_raw_buffer_store_b128(my[r * 8 + ((lane & 7) ^ (r & 7))], uvr_prev,
-                                                   st_voff + k * 8 * d2 * 2, 0, 2);
-        }
+        for (int e = 0; e < kEpi; ++e) epi(e, prev_rsrc, st_voff);
     }
 }
 

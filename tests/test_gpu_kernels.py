@@ -302,6 +302,27 @@ def test_generate_shapes(dl, dh, d, U):
     _check_rows(v[:U], v_ref, "bf16")
 
 
+@pytest.mark.parametrize("dh", [512, 256])
+def test_generate_v_row_kernels_agree(dh):
+    """The v-row kernel for widths that are multiples of 256 columns (W_v rows resident,
+    each tile's epilogue during the next tile's products) and the one for other widths
+    (hidden rows resident) use the same operands and k order per output column, so a
+    320-wide model with W_v's first 320 rows gives the 1024-wide model's first 320 columns
+    bit for bit."""
+    rng = np.random.default_rng(dh)
+    E, dl, d, U = 3000, 128, 1024, 2500
+    lat = O.f32_to_bf16_bits(rng.standard_normal((E, dl)).astype(np.float32))
+    w1 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (dh, dl)) * 4 / np.sqrt(dl)).astype(np.float32))
+    w2 = O.f32_to_bf16_bits((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(dh)).astype(np.float32))
+    uniq = np.sort(rng.choice(E, U, replace=False)).astype(np.int32)
+    dn = 320
+    w2n = np.concatenate([w2[:dn], w2[d:d + dn]])
+    h, v = _generate(lat, uniq, w1, w2, U, "bf16")
+    hn, vn = _generate(lat, uniq, w1, w2n, U, "bf16")
+    assert np.array_equal(h[:U], hn[:U])
+    assert np.array_equal(v[:U, :dn], vn[:U]), int(np.sum(v[:U, :dn] != vn[:U]))
+
+
 @pytest.mark.parametrize("dl,dh,d,dt", [(16, 32, 64, "fp32"), (16, 32, 64, "bf16"), (128, 512, 1024, "bf16"),
                                          (128, 512, 320, "bf16")])
 def test_generate_clamps_unique_count(dl, dh, d, dt):
