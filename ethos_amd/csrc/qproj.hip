@@ -323,12 +323,28 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     };
     static_assert(kStages >= 2 && kStages <= 4, "waits cover at most two chunks in flight past the current one");
 
+    // the first chunk's copies go out before the metadata loads, so that one wait covers both
+    issue(0, 0);
     if (tid < kQiRows && t0 + tid < n_tok) {
         const QRowMeta m = xmeta[t0 + tid];
         xpf[tid] = make_float4(ldexpf(m.amax, -m.e), ldexpf(m.l1, -m.e), (float)m.n_inex * 0x1p-21f, 0.0f);
         xpi[tid] = make_int2(m.e, m.n_inex);
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the meta load is not counted among the copies below
+    // the lane's output columns' formats, bias and BatchNorm coefficients, for the epilogue
+    // (loaded now so that the epilogue does not wait for them)
+    QRowMeta cmeta[kCB];
+    uint16_t cbias[kCB];
+    float calpha[kCB], cbeta[kCB];
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb) {
+        const int c = c0 + wc * 32 * kCB + cb * 32 + l32;
+        const bool ok = c < ncols;
+        cmeta[cb] = ok ? wmeta[c] : QRowMeta{0, -1, 0.0f, 0.0f};
+        cbias[cb] = ok ? bias[c] : (uint16_t)0;
+        calpha[cb] = ok ? alpha[c] : 0.0f;
+        cbeta[cb] = ok ? beta[c] : 0.0f;
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // these loads and the first chunk's copies
 
     i32x16_t acc[kCB][5];
 #pragma unroll
@@ -340,7 +356,6 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
 
     const int arow = wr * 32 + l32;
     const int nch = dpad / kQiKC;
-    issue(0, 0);
 #pragma unroll
     for (int j = 1; j < kStages - 1; ++j)
         if (j < nch) issue(j * kQiKC, j);
@@ -395,15 +410,15 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     double b = 0.0;
     float al = 0.0f, be = 0.0f;
     if (col_ok) {
-        const QRowMeta m = wmeta[c];
+        const QRowMeta m = cmeta[cb];
         ew = m.e;
         nw = m.n_inex;
         aw = ldexpf(m.amax, -m.e);
         lw = ldexpf(m.l1, -m.e);
         mw = (float)m.n_inex * 0x1p-21f;
-        b = (double)bf16_bits_to_f32(bias[c]);
-        al = alpha[c];
-        be = beta[c];
+        b = (double)bf16_bits_to_f32(cbias[cb]);
+        al = calpha[cb];
+        be = cbeta[cb];
     }
     const float dscale = (float)d * 0x1p-52f;  // chain rounding: d 2^-52 A'
     const float dterm = (float)d * 0x1p-12f;
