@@ -733,19 +733,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     static_assert(GPR >= 16 && (GPR & (GPR - 1)) == 0 && kCopiesW % 4 == 0 && kEpi % KS2 == 0 && kCS <= KS2,
                   "tile staging shape");
     constexpr int kOps = kEpi / KS2;                     // epilogue operations per k-step
+    // Hidden tiles: row r's 16-byte group g sits at slot g ^ (r % 16) of the row, so a
+    // fragment read (one group, 16 consecutive rows per 256 bytes of banks) is
+    // conflict-free.
     __shared__ uint4 hs[2][kWsRows * GPR];
+    // Output staging, per wave: 64 experts x 64 columns of bf16; expert r's 128-byte
+    // row holds its 16-byte group q at slot q ^ (r % 8).
     __shared__ u32x4_t stg[4][kWsRows * 8];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
+    // the h and v outputs hold max_unique rows
     const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
     const int n_tiles = (U + kWsRows - 1) / kWsRows;
+    // Workgroup b runs on XCD b % 8.  Slots b / 8 of one XCD are taken n_cg at a time:
+    // the members of one group, column groups 0 .. n_cg - 1.  (The launch makes the
+    // grid a multiple of 8 n_cg.)
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int per_xcd = ((int)gridDim.x >> 3) / n_cg;
     const int cg = slot % n_cg, grp = xcd * per_xcd + slot / n_cg;
     const int n_groups = 8 * per_xcd;
-    const int col0 = cg * kWsCols + wave * 64;
+    const int col0 = cg * kWsCols + wave * 64;  // the wave's first output column
 
+    // the wave's W_v rows: A fragment (cb, s) = W_v[col0 + 32 cb + l32][16 s + 8 h ..]
     bf16x8_t wf[2][KS2];
     {
         const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
@@ -758,6 +768,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
                                   wr, ((col0 + 32 * cb + l32) * DH + 16 * s + 8 * h) * (int)sizeof(uint16_t), 0, 0));
     }
+    // Copy instruction j = 4 it + wave of a tile moves LDS slots 64 j .. 64 j + 63 (lane
+    // i: slot f = 64 j + i, row f / GPR, slot f % GPR of that row, which holds global
+    // group (f % GPR) ^ (row % 16)).  Rows at or past U read as zero (the descriptor
+    // covers rows below U only).
     auto copy = [&](int64_t tile, int buf, int it) {
         const int64_t row0 = tile * kWsRows;
         const int64_t live = U - row0;
@@ -768,13 +782,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const int r = f / GPR, gs = f % GPR;
         lds_dma16(rs, (r * DH + 8 * (gs ^ (r & 15))) * (int)sizeof(uint16_t), 0, lds_addr(&hs[buf][64 * j]));
     };
+    // B fragment (mb, s) of the current tile: row 32 mb + l32, group 2 s + h, at slot
+    // (2 s + h) ^ (l32 % 16) = ((2 (s % 8) + h) ^ (l32 % 16)) + 16 (s / 8)
     int bq_off[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) bq_off[q] = l32 * GPR + ((2 * q + h) ^ (l32 & 15));
+    // lane's store k covers staged row 8 k + lane / 8, 16-byte group lane % 8
     const int st_voff = ((lane >> 3) * d2 + col0 + 8 * (lane & 7)) * (int)sizeof(uint16_t);
     constexpr int kOOB = 0x40000000;  // a byte offset past any tile's rows (and kOOB + 56 d2 * 2 < 2^31)
     u32x4_t* my = stg[wave];
     u32x2_t* my2 = reinterpret_cast<u32x2_t*>(my);
+    // s_waitcnt vmcnt(8) (gfx9 immediate: vmcnt [3:0] and [15:14], expcnt [6:4],
+    // lgkmcnt [11:8]; expcnt 7 and lgkmcnt 15 do not wait)
     constexpr int kWaitVm8 = 0x0f78;
     constexpr int kWaitVm0 = 0x0f70;
     // the store descriptor of a tile's rows (rows below max_unique)
@@ -810,7 +829,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int it = 0; it < kCopiesW; ++it) copy(grp, 0, it);
     }
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // the W_v rows and the first tile
 
 #pragma unroll
     for (int e = 0; e < 16; ++e) pk[e] = u32x2_t{0u, 0u};
