@@ -279,6 +279,7 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
 // tiles it could), the expert-order walk takes only the pairs of tiles of kActTileRows
 // unique experts with more than kActFusedCap pairs; chunks without such pairs are skipped.
 constexpr int kAct8Waves = 4;
+constexpr int64_t kActSmallPairs = 65536;  // batches up to this many pairs take 16-pair token-order units
 
 template <typename T, int P>
 __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
@@ -288,7 +289,8 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
                                                                      const int32_t* __restrict__ n_unique,
                                                                      const int32_t* __restrict__ seg_off,
                                                                      const T* __restrict__ gates, int64_t n_pairs,
-                                                                     int hk, int dh, float* __restrict__ act) {
+                                                                     int hk, int dh, int upairs,
+                                                                     float* __restrict__ act) {
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     __shared__ float dots[kAct8Waves][64];
@@ -298,8 +300,20 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
     const int64_t n_waves = (int64_t)gridDim.x * kAct8Waves;
     if (n_unique != nullptr && pair_slot != nullptr &&
         (int64_t)*n_unique * dh * (int64_t)sizeof(T) <= kActTokenOrderMaxHBytes) {
+        // Units of upairs (<= 64) consecutive pairs of one token, one wave each (small
+        // batches take units smaller than a token's pairs, so that they spread over more
+        // waves).  Two groups' hidden rows are requested before either is summed; the loads
+        // and sums are unconditional (a group past the unit's repeats the pair's first),
+        // so no branch separates a load from its use.
         const int64_t n_tok = n_pairs / hk;
-        for (int64_t t = wave_id; t < n_tok; t += n_waves) {
+        const int cpt = (hk + upairs - 1) / upairs;
+        for (int64_t u = wave_id; u < n_tok * cpt; u += n_waves) {
+            const int64_t t = u / cpt;
+            const int j0 = (int)(u - t * cpt) * upairs;
+            const int cnt = hk - j0 < upairs ? hk - j0 : upairs;
+            const int64_t pbase = t * hk + j0;
+            const int my_s = lane < cnt ? pair_slot[pbase + lane] : 0;
+            const T my_g = lane < cnt ? gates[pbase + lane] : T{};
             const T* xr = xp + t * dh;
             Raw xv[P];
 #pragma unroll
@@ -307,34 +321,33 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
                 const int e = (part + 8 * i) * N;
                 xv[i] = e < dh ? *reinterpret_cast<const Raw*>(xr + e) : Raw{};
             }
-            const int64_t pbase = t * hk;
-            for (int j0 = 0; j0 < hk; j0 += 64) {
-                const int cnt = hk - j0 < 64 ? hk - j0 : 64;
-                const int my_s = lane < cnt ? pair_slot[pbase + j0 + lane] : 0;
-                for (int g = 0; g < cnt; g += 8) {
+            const int ng = (cnt + 7) / 8;
+            for (int g0 = 0; g0 < ng; g0 += 2) {
+                Raw hv[2][P];
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
                     // this lane's pair of the group (a tail group repeats the last pair)
-                    const int src = g + slot < cnt ? g + slot : cnt - 1;
-                    const int sl = __shfl(my_s, src, 64);
-                    const T* hr = hid + (int64_t)sl * dh;
-                    Raw hv[P];
+                    const int g = g0 + b < ng ? g0 + b : g0;
+                    const int src = g * 8 + slot < cnt ? g * 8 + slot : cnt - 1;
+                    const T* hr = hid + (int64_t)__shfl(my_s, src, 64) * dh;
 #pragma unroll
                     for (int i = 0; i < P; ++i) {
                         const int e = (part + 8 * i) * N;
-                        hv[i] = e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
+                        hv[b][i] = e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
                     }
+                }
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
                     float acc = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < P; ++i) acc = dot_raw(hv[i], xv[i], acc);
+                    for (int i = 0; i < P; ++i) acc = dot_raw(hv[b][i], xv[i], acc);
                     acc = act_reduce8(acc);
-                    if (part == 0) dots[wave][g + slot] = acc;
+                    if (part == 0 && g0 + b < ng) dots[wave][(g0 + b) * 8 + slot] = acc;
                 }
-                __builtin_amdgcn_wave_barrier();
-                if (lane < cnt) {
-                    const int64_t p = pbase + j0 + lane;
-                    act[p] = act_epilogue<T>(dots[wave][lane], Elem<T>::to_f32(gates[p]));
-                }
-                __builtin_amdgcn_wave_barrier();
             }
+            __builtin_amdgcn_wave_barrier();
+            if (lane < cnt) act[pbase + lane] = act_epilogue<T>(dots[wave][lane], Elem<T>::to_f32(my_g));
+            __builtin_amdgcn_wave_barrier();
         }
         return;
     }
@@ -659,12 +672,14 @@ template <typename T, int P>
 static void launch_act8_t(const void* xp, const void* hid, const int32_t* perm, const int32_t* sorted_slot,
                           const int32_t* pair_slot, const int32_t* n_unique, const int32_t* seg_off, const void* gates,
                           int64_t n_pairs, int hk, int dh, float* act, int num_cus, hipStream_t stream) {
+    // token-order units: 16 pairs for small batches (more waves than tokens), else 64
+    const int upairs = n_pairs <= kActSmallPairs ? 16 : 64;
     const int64_t cap = (int64_t)num_cus * 16;
-    int64_t g1 = ((n_pairs + 63) / 64 + kAct8Waves - 1) / kAct8Waves;
+    int64_t g1 = ((n_pairs + upairs - 1) / upairs + kAct8Waves - 1) / kAct8Waves;
     g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
     hipLaunchKernelGGL((apply_act8_kernel<T, P>), dim3((unsigned)g1), dim3(kAct8Waves * 64), 0, stream, (const T*)xp,
                        (const T*)hid, perm, sorted_slot, pair_slot, n_unique, seg_off, (const T*)gates, n_pairs, hk, dh,
-                       act);
+                       upairs, act);
 }
 
 // Per-pair activations a_p (phase 1): 8 lanes per pair for rows of up to 64 pieces of 16
