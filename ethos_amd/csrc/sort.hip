@@ -434,6 +434,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
     __shared__ uint32_t wcnt[kTW][kRadix];
     __shared__ __align__(16) uint32_t sk[kTile];
     __shared__ __align__(16) uint32_t sv[kTile];
+    __shared__ __align__(16) uint32_t sslot[kTile];  // slot + 1 of each position, bit 31: a head
     __shared__ uint32_t gbase[kRadix], sbase[kRadix], lst[kRadix], lstart[kRadix], hstart[kRadix];
     __shared__ uint32_t wsum[3 * 8];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -477,8 +478,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
     const uint32_t lomask = (1u << shift) - 1u;
     const int p0 = tid * kTPer;
     const uint4 k4 = reinterpret_cast<const uint4*>(sk)[tid];
-    const uint4 v4 = reinterpret_cast<const uint4*>(sv)[tid];
-    const uint32_t kk[kTPer] = {k4.x, k4.y, k4.z, k4.w}, vv[kTPer] = {v4.x, v4.y, v4.z, v4.w};
+    const uint32_t kk[kTPer] = {k4.x, k4.y, k4.z, k4.w};
     uint32_t prev = p0 > 0 ? sk[p0 - 1] : 0u;
     uint32_t dd[kTPer];
     bool st[kTPer], head[kTPer];
@@ -503,6 +503,9 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
         run += head[i] ? 1u : 0u;
     }
     __syncthreads();
+    // each position's slot (and head flag) into LDS, then the outputs with position
+    // p = tid + 1024 j per thread, so that consecutive lanes write consecutive positions of a
+    // digit's group
     run -= nh;
 #pragma unroll
     for (int i = 0; i < kTPer; ++i) {
@@ -511,17 +514,27 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
         const uint32_t d = dd[i];
         run += head[i] ? 1u : 0u;
         const int32_t slot = (int32_t)(sbase[d] + run - hstart[d]) - 1;
+        sslot[p] = (uint32_t)(slot + 1) | (head[i] ? 0x80000000u : 0u);  // slot + 1 < 2^31
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) {
+        const int p = tid + j * kTThreads;
+        if (p >= (int)tile_n) break;
+        const uint32_t key = sk[p], val = sv[p], sw = sslot[p];
+        const uint32_t d = (key >> shift) & (kRadix - 1);
+        const int32_t slot = (int32_t)(sw & 0x7fffffffu) - 1;
         // ids outside [0, n_experts) (a caller error) could make more slots than the buffers
         // hold: clamp so that every later kernel stays in bounds
         const int32_t sc = slot < 0 ? 0 : (slot < max_unique ? slot : max_unique - 1);
         const uint32_t pos = gbase[d] + (uint32_t)p - lstart[d];
         if (pos < (uint64_t)n) {
-            perm[pos] = (int32_t)vv[i];
+            perm[pos] = (int32_t)val;
             sorted_slot[pos] = sc;
         }
-        if (vv[i] < (uint64_t)n) pair_slot[vv[i]] = sc;
-        if (head[i] && slot >= 0 && slot < max_unique) {
-            uniq[slot] = (int32_t)kk[i];
+        if (val < (uint64_t)n) pair_slot[val] = sc;
+        if ((sw >> 31) && slot >= 0 && slot < max_unique) {
+            uniq[slot] = (int32_t)key;
             seg_off[slot] = (int32_t)pos;
         }
     }
