@@ -391,31 +391,52 @@ __global__ __launch_bounds__(kTThreads) void tsort_down(const uint32_t* __restri
                                                         int n_tiles, const uint32_t* __restrict__ pre,
                                                         const uint32_t* __restrict__ tot) {
     __shared__ uint32_t wcnt[kTW][kRadix];
-    __shared__ uint32_t gbase[kRadix], wsum[8];
+    __shared__ __align__(16) uint32_t sk[kTile];
+    __shared__ __align__(16) uint32_t sv[kTile];
+    __shared__ uint32_t gbase[kRadix], lstart[kRadix], wsum[2 * 8];
     const int tid = threadIdx.x, wave = tid >> 6;
     const uint32_t my_pre = tid < kRadix ? pre[(int64_t)tid * n_tiles + blockIdx.x] : 0u;
-    const uint32_t my_tot[1] = {tid < kRadix ? tot[tid] : 0u};
+    uint32_t tv[2] = {tid < kRadix ? tot[tid] : 0u, 0u};
     uint32_t key[kTC], val[kTC], rank[kTC];
     tile_load<kFirst>(keys_in, vals_in, n, key, val);
     zero_wcnt(wcnt);
     __syncthreads();
     tile_rank(n, shift, wcnt, key, rank);
     __syncthreads();
-    tile_digit_counts(wcnt);
-    uint32_t db[1], all[1];
-    scan512<1>(my_tot, db, all, wsum);
-    if (tid < kRadix) gbase[tid] = db[0] + my_pre;
+    tv[1] = tile_digit_counts(wcnt);
+    uint32_t ex[2], sums[2];
+    scan512<2>(tv, ex, sums, wsum);
+    const uint32_t tile_n = sums[1];
+    if (tid < kRadix) {
+        gbase[tid] = ex[0] + my_pre;
+        lstart[tid] = ex[1];
+    }
     __syncthreads();
+    // the tile ranked by digit into LDS, then written with consecutive positions of a
+    // digit's group on consecutive lanes
     const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
         if (base + j * 64 + (tid & 63) < n) {
             const uint32_t d = (key[j] >> shift) & (kRadix - 1);
-            const uint32_t pos = gbase[d] + wcnt[wave][d] + rank[j];
-            if (pos < (uint64_t)n) {  // always, for ids from one consistent pass
-                keys_out[pos] = key[j];
-                vals_out[pos] = val[j];
+            const uint32_t lp = lstart[d] + wcnt[wave][d] + rank[j];
+            if (lp < (uint32_t)kTile) {
+                sk[lp] = key[j];
+                sv[lp] = val[j];
             }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) {
+        const int p = tid + j * kTThreads;
+        if (p >= (int)tile_n) break;
+        const uint32_t k = sk[p];
+        const uint32_t d = (k >> shift) & (kRadix - 1);
+        const uint32_t pos = gbase[d] + (uint32_t)p - lstart[d];
+        if (pos < (uint64_t)n) {  // always, for ids from one consistent pass
+            keys_out[pos] = k;
+            vals_out[pos] = sv[p];
         }
     }
 }
