@@ -1,6 +1,6 @@
 """Benchmark: ETHOS expert-layer forward tokens/s on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config cfg2]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 20] [--config cfg2]
     python bench.py --config cfg5     # whole language-model forward (12 expert blocks)
 
 A step is one full forward of the drop-in layer (query projection + BatchNorm,
@@ -10,7 +10,7 @@ batch of synthetic input already resident in HBM.  Prints ONE JSON line.
 Besides throughput, the line carries
   roofline      the dominant graded kernel (generator: MFMA, apply/scatter: HBM),
                 algorithmic work per launch / mean launch time measured here with HIP
-                events on the stream the kernels run on;
+                events on the stream the kernels run on (every 4th timed step);
   kernels       the same figures for every stage;
   cpu_baseline  the reference's CPU path (a loop-faithful restatement of
                 model.py:288-343, bit-identical to it on the golden fixtures) timed on a
@@ -70,46 +70,54 @@ STAGES = {"query_proj": ["query_proj"], "route": ["route"], "sort_segment": ["so
           "generate": ["hidden_rows", "v_rows"], "apply_scatter": ["token_proj", "activations", "scatter_back"]}
 
 
-def timed_steps(m, x_flat, steps: int) -> tuple[float, dict]:
+def timed_steps(m, x_flat, steps: int, every: int = 4) -> tuple[float, dict]:
     """Run `steps` layer forwards; return wall ms/step and the mean per-stage ms.
 
-    Stage boundaries are HIP events recorded on the stream every kernel is launched on
-    (torch's current stream, which the library is handed), inside the same timed region:
-    by the layer between its calls, and by the library between the kernels of its
-    expert-stage call.
+    Every step ends with one HIP event on the stream every kernel is launched on (torch's
+    current stream, which the library is handed).  Steps 0, every, 2 every, ... also carry
+    the stage boundaries, inside the same timed region: recorded by the layer between its
+    calls, and by the library between the kernels of its expert-stage call.  A timed event
+    between two kernels holds the GPU for a few microseconds (the nine of a step cost about
+    27 us at 4096 tokens, 20 us at 64), so the other steps carry none; the per-stage means
+    come from the instrumented steps, the p50 step time (`_p50`) from the others.
     """
     from ethos_amd import hip
 
     mk = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    outer = [[mk() for _ in range(len(OUTER) + 1)] for _ in range(steps)]
-    inner = [[mk() for _ in INNER] for _ in range(steps)]
-    for e in (ev for step in inner for ev in step):
+    det = list(range(0, steps, max(1, every)))
+    bounds = [mk() for _ in range(steps + 1)]
+    outer = {i: [mk() for _ in OUTER] for i in det}
+    inner = {i: [mk() for _ in INNER] for i in det}
+    for e in (ev for evs in inner.values() for ev in evs):
         e.record()  # the library records into existing events
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    bounds[0].record()
     for i in range(steps):
-        e = outer[i]
-        e[0].record()
-        pos = iter(range(1, len(OUTER) + 1))
+        if i in outer:
+            pos = iter(outer[i])
 
-        def mark(stage, e=e, pos=pos):
-            e[next(pos)].record()
+            def mark(stage, pos=pos):
+                next(pos).record()
 
-        hip.stage_events(inner[i])
-        m.forward_flat(x_flat, mark)
-    hip.stage_events([])
+            hip.stage_events(inner[i])
+            m.forward_flat(x_flat, mark)
+            hip.stage_events([])
+        else:
+            m.forward_flat(x_flat)
+        bounds[i + 1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    chain = {i: [bounds[i]] + outer[i] + inner[i] for i in det}
     per_k = {}
-    for j, k in enumerate(OUTER):
-        per_k[k] = sum(e[j].elapsed_time(e[j + 1]) for e in outer) / steps
-    for j, k in enumerate(INNER):
-        prev = (lambda i: outer[i][-1]) if j == 0 else (lambda i, j=j: inner[i][j - 1])
-        per_k[k] = sum(prev(i).elapsed_time(inner[i][j]) for i in range(steps)) / steps
+    for j, k in enumerate(OUTER + INNER):
+        per_k[k] = sum(chain[i][j].elapsed_time(chain[i][j + 1]) for i in det) / len(det)
     per = {g: sum(per_k[k] for k in ks) for g, ks in STAGES.items()}
     per["_kernels"] = per_k
-    steps_ms = sorted(outer[i][0].elapsed_time(inner[i][-1]) for i in range(steps))
+    plain = [i for i in range(steps) if i not in outer] or list(range(steps))
+    steps_ms = sorted(bounds[i].elapsed_time(bounds[i + 1]) for i in plain)
     per["_p50"] = steps_ms[len(steps_ms) // 2]
+    per["_instrumented"] = len(det)
     return elapsed / steps * 1e3, per
 
 
@@ -373,8 +381,8 @@ def bench_model(args) -> None:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="token sample for the CPU baseline (0 = skip)")
     ap.add_argument("--no-alternatives", action="store_true",
@@ -415,6 +423,7 @@ def main():
         log(f"[bench] timing {args.steps} steps")
         ms, st = timed_steps(m, x_flat, args.steps)
         p50 = st.pop("_p50")
+        n_instr = st.pop("_instrumented")
         launch_ms = st.pop("_kernels")
         sub_us = {k: round(v * 1e3, 2) for k, v in launch_ms.items()}
         U = unique_experts(m, x_flat)
@@ -464,6 +473,7 @@ def main():
             ms_h, st_h = timed_steps(mh, x_flat, args.steps)
             st_h.pop("_p50")
             st_h.pop("_kernels")
+            st_h.pop("_instrumented")
         del mh
         alternatives = {"hidden_space": dict(
             ms_per_step=round(ms_h, 4), value=round(sh.n_tok / (ms_h * 1e-3), 1), unit="tokens/s",
@@ -507,6 +517,8 @@ def main():
         "kernels": kernels,
         "counters": counter_figures(args.config, sub_us),
         "stage_us": sub_us,
+        "stage_events": f"stage boundaries recorded on {n_instr} of the {args.steps} timed steps "
+                        "(every 4th, from the first); the others carry one event at their end",
         "hidden_rows_split": split,
         "alternatives": alternatives,
         "cpu_baseline": cpu,
@@ -517,7 +529,8 @@ def main():
 
 def decode_latency(args, with_cpu: bool) -> dict:
     """The decode-like layer (64 tokens, the same 262,144-expert layer, bf16): p50 latency
-    of 50 forwards after warmup, and the CPU port on all 64 tokens."""
+    of the 40 of 50 forwards after warmup that carry no stage events (every 5th does), and
+    the CPU port on all 64 tokens."""
     import ethos_amd
     from ethos_amd.workloads import SHAPES, make_inputs
 
@@ -533,9 +546,10 @@ def decode_latency(args, with_cpu: bool) -> dict:
             m.forward_flat(x_flat)
         torch.cuda.synchronize()
         log(f"[bench] timing {steps} forwards of the 64-token layer")
-        ms, st = timed_steps(m, x_flat, steps)
+        ms, st = timed_steps(m, x_flat, steps, every=5)
     p50 = st.pop("_p50")
     st.pop("_kernels")
+    st.pop("_instrumented")
     out = {"workload": "ETHOS expert-layer forward, 64 tokens x d_model 1024, 262144 experts, 8 routing heads, "
                        "top-16, d_query 256, bf16",
            "p50_ms": round(p50, 4), "mean_ms": round(ms, 4), "steps": steps,
