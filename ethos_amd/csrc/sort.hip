@@ -5,13 +5,14 @@
 // the paper's Algorithm 1 reorders by expert, paper/ETHOS.pdf p.10.)
 //
 // Sort: 9-bit digits, P = ceil(bits / 9) passes over keys < n_experts (two for 262,144
-// experts), over tiles of 8192 keys (one workgroup of 16 waves each).  A pass is
+// experts), over tiles of 4096 keys (one workgroup of 16 waves each).  A pass is
 //   count/stats  per-tile digit counts (last pass: also per digit the number of distinct
 //                keys, and the lower bits of the first and last key)
 //   scan         per digit, exclusive prefix over the tiles (last pass: also of the new
 //                distinct keys, and the lower bits of the last earlier key)
 //   down         stable scatter: digit base (scan of the totals) + tile prefix + rank in
-//                the tile by wave-level multisplit
+//                the tile by wave-level multisplit; the tile is first ranked by digit into
+//                LDS, then written with consecutive output positions on consecutive lanes
 // Inside a wave, the lanes holding the same digit are found with nine ballots ("peer
 // mask"); the rank of a key is (keys of that digit in earlier waves) + (in earlier chunks
 // of its wave) + (peers in lower lanes), which keeps the order of equal keys.  No global

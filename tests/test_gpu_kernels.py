@@ -104,7 +104,7 @@ def test_route_ties_break_to_lowest_index():
                                          (65536, 262144, "same"), (24577, 262144, "rand")])
 def test_sort_segment_exact(n, E, pattern):
     """The sort against the oracle's counting sort: one pass (E = 7), two (4,096 and 262,144
-    experts) and three (2^21) over tiles of 8,192 pairs; batches up to 16,384 pairs take the
+    experts) and three (2^21) over tiles of 4,096 pairs; batches up to 16,384 pairs take the
     single-workgroup sort.  Patterns: uniform ids, one id everywhere (one segment spanning
     every tile), Zipf-skewed ids, half the pairs on the largest id, and ids whose two
     9-bit digits are both Zipf-skewed (hot experts whose segments cross tile boundaries)."""
