@@ -296,6 +296,13 @@ __device__ __forceinline__ void lds_dma16(i32x4_t rsrc, int voff, int soff, uint
                  "s"(soff)
                  : "memory");
 }
+// The same with the non-temporal hint, for data read once (it then displaces less of what
+// other loads reuse from L2).
+__device__ __forceinline__ void lds_dma16_nt(i32x4_t rsrc, int voff, int soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds" ::"s"(lds), "v"(voff), "s"(rsrc),
+                 "s"(soff)
+                 : "memory");
+}
 
 template <typename P>
 __device__ __forceinline__ uint32_t lds_addr(P* p) {

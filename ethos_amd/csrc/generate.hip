@@ -365,7 +365,7 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
             const int r = 4 * j + (lane >> 4), sl = lane & 15;
             const int id = ids_s[i_tile][r];
             const int voff = id >= 0 ? (id * DL + 8 * (sl ^ (r & 15))) * (int)sizeof(uint16_t) : kZOOB;
-            lds_dma16(zr, voff, 0, lds_addr(&zs[buf][64 * j]));
+            lds_dma16_nt(zr, voff, 0, lds_addr(&zs[buf][64 * j]));  // each latent row is read once
         }
     };
     // B fragment (mb, s): row 32 mb + l32, piece 2 s + h, at slot (2 s + h) ^ (l32 % 16)
