@@ -262,6 +262,29 @@ constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
 // are in flight while one chunk is multiplied.
 __device__ __forceinline__ int qi_slot(int row, int piece) { return piece ^ ((row >> 2) & 3); }
 
+// Tile order of the i8 product kernel, for the per-XCD L2s (workgroup b runs on XCD
+// b % 8): the tiles are ordered by column group of kQiColGroup column tiles, then row
+// block, then column tile, and XCD x takes the x-th eighth of that order.  So each XCD
+// works on a rectangle of about as many row blocks as column tiles: a row block's x digit
+// planes are read by the consecutive workgroups of its column group on one XCD, and the
+// group's w digit planes (kQiColGroup * 64 columns, 3 MB at d_model 1024) stay in that
+// XCD's L2, instead of every XCD reading every row block.  The grid is padded to a
+// multiple of 8; false for the padding workgroups.
+constexpr int kQiColGroup = 16;
+template <int kRowsT, int kColsT>
+__device__ __forceinline__ bool qi_tile_t(int n_tok, int ncols, int* t0, int* c0) {
+    const int nct = (ncols + kColsT - 1) / kColsT, nrb = (n_tok + kRowsT - 1) / kRowsT;
+    const int total = nct * nrb, per = (total + 7) / 8;
+    const int i = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (i >= total) return false;
+    const int cg = nct < kQiColGroup ? nct : kQiColGroup;  // column tiles per group (the last may be short)
+    const int grp = i / (cg * nrb), r = i - grp * cg * nrb;
+    const int w = nct - grp * cg < cg ? nct - grp * cg : cg;  // this group's column tiles
+    *t0 = (r / w) * kRowsT;
+    *c0 = (grp * cg + r % w) * kColsT;
+    return true;
+}
+
 template <int kWaves, int kCB, int kStages>
 __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __restrict__ xdig,
                                                                  const int8_t* __restrict__ wdig,
@@ -275,6 +298,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
                                                                  uint16_t* __restrict__ q) {
     using C = QiCfg<kWaves, kCB, kStages>;
     constexpr int kQiRows = C::kRows, kQiCols = C::kCols;
+    auto qi_tile = [](int n, int nc, int* t, int* c) { return qi_tile_t<kQiRows, kQiCols>(n, nc, t, c); };
     extern __shared__ __align__(16) unsigned char qsm[];
     int8_t* tiles = reinterpret_cast<int8_t*>(qsm);  // [stage][x planes, w planes][row][64 B]
     // x row formats, scaled by 2^-E_x: {max|x| 2^-E, |x|_1 2^-E, n_inex 2^-21} and {E, n_inex}
@@ -283,7 +307,8 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int wr = wave >> 1, wc = wave & 1;  // rows 32 wr .., columns 32 kCB wc ..
-    const int t0 = blockIdx.y * kQiRows, c0 = blockIdx.x * kQiCols;
+    int t0, c0;
+    if (!qi_tile(n_tok, ncols, &t0, &c0)) return;
     const int dpad = qproj_dpad(d);
     const int64_t xplane = (int64_t)n_tok * dpad, wplane = (int64_t)ncols * dpad;
 
@@ -608,7 +633,8 @@ int launch_qproj(const void* x, const void* w, const void* prepared, const void*
                            (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, rows, d, W.xdig, W.wdig, W.meta,
                            W.meta + n_tok, W.count);
         using C = QiLaunch;
-        dim3 grid((ncols + C::kCols - 1) / C::kCols, (unsigned)((n_tok + C::kRows - 1) / C::kRows));
+        const int64_t tiles = (int64_t)((ncols + C::kCols - 1) / C::kCols) * ((n_tok + C::kRows - 1) / C::kRows);
+        const dim3 grid((unsigned)(8 * ((tiles + 7) / 8)));  // qi_tile_t: XCD-grouped tile order
         hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages>), grid, dim3(C::kWaves * 64), C::kSmem,
                            stream, W.xdig, wdig, W.meta, wmeta, (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols,
                            W.count, W.list, (uint16_t*)q);
