@@ -101,8 +101,10 @@ def timed_steps(m, x_flat, steps: int, every: int = 4) -> tuple[float, dict]:
                 next(pos).record()
 
             hip.stage_events(inner[i])
-            m.forward_flat(x_flat, mark)
-            hip.stage_events([])
+            try:
+                m.forward_flat(x_flat, mark)
+            finally:
+                hip.stage_events([])  # the library holds no event past this step
         else:
             m.forward_flat(x_flat)
         bounds[i + 1].record()
@@ -299,31 +301,35 @@ def cpu_baseline(sh, x_cpu, sd_cpu, n_tokens: int) -> dict:
     }
 
 
-def bench_model(args) -> None:
+def lm_forward(steps: int, warmup: int, alternatives: bool = True) -> dict:
     """Whole ETHOS LM forward (the reference's CompressedMoEModel with the drop-in expert
     layer in every block): 12 blocks, d_model 1024, MLA 16 heads with a 256-wide KV latent,
-    vocabulary 100,277, batch 4 x 2048 uniform token ids, bf16, random init."""
+    vocabulary 100,277, batch 4 x 2048 uniform token ids, bf16, random init.  Returns ms per
+    forward (HIP events around `steps` forwards), the expert layer's share (block 0's layer
+    timed alone on its own input, times the block count) and, with `alternatives`, the same
+    model with the expert layers in hidden-space order."""
     from ethos_amd.model import CompressedMoEModel, init_random_, lm_config
     cfg = lm_config()
     batch, seq = 4, 2048
     log("[bench] building the language model (random init on the host)")
     m = init_random_(CompressedMoEModel(cfg), seed=0).to(torch.bfloat16).cuda().eval()
     ids = torch.randint(0, cfg.vocab_size, (batch, seq), generator=torch.Generator().manual_seed(0)).cuda()
+    out = {}
     with torch.no_grad():
         log("[bench] warmup")
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             m(ids)
         torch.cuda.synchronize()
-        log(f"[bench] timing {args.steps} model forwards")
+        log(f"[bench] timing {steps} model forwards")
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
-        for _ in range(args.steps):
+        for _ in range(steps):
             m(ids)
         e1.record()
         torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) / args.steps * 1e3
-        ms = e0.elapsed_time(e1) / args.steps
+        out["wall_ms"] = (time.perf_counter() - t0) / steps * 1e3
+        out["ms"] = e0.elapsed_time(e1) / steps
         # one block's expert layer alone, on the block's actual input
         inputs = {}
         hk = m.layers[0].mlp.register_forward_pre_hook(lambda mod, a: inputs.__setitem__("x", a[0]))
@@ -334,24 +340,41 @@ def bench_model(args) -> None:
             m.layers[0].mlp(x)
         torch.cuda.synchronize()
         e0.record()
-        for _ in range(args.steps):
+        for _ in range(steps):
             m.layers[0].mlp(x)
         e1.record()
         torch.cuda.synchronize()
-        ms_layer = e0.elapsed_time(e1) / args.steps
-        # the same weights with the expert layers in hidden-space order
-        for layer in m.layers:
-            layer.mlp.hidden_space = True
-        for _ in range(args.warmup):
-            m(ids)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(args.steps):
-            m(ids)
-        e1.record()
-        torch.cuda.synchronize()
-        ms_h = e0.elapsed_time(e1) / args.steps
-    n_tok = batch * seq
+        out["ms_layer"] = e0.elapsed_time(e1) / steps
+        if alternatives:
+            # the same weights with the expert layers in hidden-space order
+            for layer in m.layers:
+                layer.mlp.hidden_space = True
+            for _ in range(warmup):
+                m(ids)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(steps):
+                m(ids)
+            e1.record()
+            torch.cuda.synchronize()
+            out["ms_hidden_space"] = e0.elapsed_time(e1) / steps
+    out.update(cfg=cfg, batch=batch, seq=seq)
+    del m
+    torch.cuda.empty_cache()
+    return out
+
+
+def lm_workload(r: dict) -> str:
+    cfg = r["cfg"]
+    return (f"ETHOS LM forward, {cfg.num_layers} blocks (all expert layers), d_model {cfg.d_model}, MLA "
+            f"{cfg.num_heads} heads kv {cfg.kv_lora_rank}, vocab {cfg.vocab_size}, tokens {r['batch']}x{r['seq']}, bf16")
+
+
+def bench_model(args) -> None:
+    """`--config cfg5`: the whole-model forward as the line's headline."""
+    r = lm_forward(args.steps, args.warmup)
+    cfg, ms = r["cfg"], r["ms"]
+    n_tok = r["batch"] * r["seq"]
     line = {
         "metric": "ETHOS LM forward tokens/sec @1 MI355X",
         "value": round(n_tok / (ms * 1e-3), 1),
@@ -360,22 +383,66 @@ def bench_model(args) -> None:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
-        "wall_ms_per_step": round(wall, 4),
+        "wall_ms_per_step": round(r["wall_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: uniform token ids, random-init weights",
-        "config": {"workload": f"ETHOS LM forward, {cfg.num_layers} blocks (all expert layers), d_model "
-                               f"{cfg.d_model}, MLA {cfg.num_heads} heads kv {cfg.kv_lora_rank}, vocab "
-                               f"{cfg.vocab_size}, tokens {batch}x{seq}, bf16",
-                   "num_layers": cfg.num_layers, "batch": batch, "seq_len": seq, "parallelism": "single GPU"},
-        "expert_layer_ms": round(ms_layer, 4),
-        "expert_layers_share": round(cfg.num_layers * ms_layer / ms, 4),
-        "alternatives": {"hidden_space": dict(ms_per_step=round(ms_h, 4), value=round(n_tok / (ms_h * 1e-3), 1),
+        "config": {"workload": lm_workload(r), "num_layers": cfg.num_layers, "batch": r["batch"], "seq_len": r["seq"],
+                   "parallelism": "single GPU"},
+        "expert_layer_ms": round(r["ms_layer"], 4),
+        "expert_layers_share": round(cfg.num_layers * r["ms_layer"] / ms, 4),
+        "alternatives": {"hidden_space": dict(ms_per_step=round(r["ms_hidden_space"], 4),
+                                              value=round(n_tok / (r["ms_hidden_space"] * 1e-3), 1),
                                               unit="tokens/s")},
     }
     print(json.dumps(line), flush=True)
+
+
+def lm_block(steps: int, warmup: int) -> dict:
+    """The whole-model forward for the default line: tokens/s, ms per forward and the share
+    of the 12 expert layers (no hidden-space alternative, to keep the run short)."""
+    r = lm_forward(steps, warmup, alternatives=False)
+    cfg, ms = r["cfg"], r["ms"]
+    n_tok = r["batch"] * r["seq"]
+    return {"workload": lm_workload(r), "value": round(n_tok / (ms * 1e-3), 1), "unit": "tokens/s",
+            "ms_per_forward": round(ms, 4), "steps": steps, "warmup": warmup,
+            "expert_layer_ms": round(r["ms_layer"], 4),
+            "expert_layers_share": round(cfg.num_layers * r["ms_layer"] / ms, 4)}
+
+
+def skewed_block(steps: int, warmup: int) -> dict:
+    """The large-batch skewed layer (32,768 tokens, sub-key rows scaled by (r+1)^-1.1, the
+    262,144-expert layer, bf16): tokens/s over `steps` forwards, the p50 of the steps that
+    carry no stage events, the stages' means and the unique-expert count."""
+    import ethos_amd
+    from ethos_amd.workloads import SHAPES, make_inputs
+
+    sh = SHAPES["cfg4"]
+    log(f"[bench] building inputs for {sh.name} ({sh.n_tok} tokens, skewed sub-keys)")
+    x_cpu, sd_cpu = make_inputs(sh, seed=0)
+    m = ethos_amd.EthosExpertLayer(sh.config()).to(sh.torch_dtype)
+    m.load_state_dict(sd_cpu)
+    m = m.cuda().eval()
+    x_flat = x_cpu.cuda().view(-1, sh.d_model)
+    with torch.no_grad():
+        for _ in range(warmup):
+            m.forward_flat(x_flat)
+        torch.cuda.synchronize()
+        log(f"[bench] timing {steps} forwards of the {sh.n_tok}-token skewed layer")
+        ms, st = timed_steps(m, x_flat, steps)
+        U = unique_experts(m, x_flat)
+    p50 = st.pop("_p50")
+    st.pop("_instrumented")
+    sub = st.pop("_kernels")
+    del m
+    torch.cuda.empty_cache()
+    return {"workload": f"ETHOS expert-layer forward, {sh.n_tok} tokens x d_model {sh.d_model}, {sh.num_experts} "
+                        f"experts, {sh.num_heads} routing heads, top-{sh.top_k}, Zipf(1.1)-skewed sub-keys, bf16",
+            "value": round(sh.n_tok / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+            "p50_step_ms": round(p50, 4), "steps": steps, "warmup": warmup, "unique_experts": U,
+            "stage_us": {k: round(v * 1e3, 2) for k, v in sub.items()}}
 
 
 def main():
@@ -388,6 +455,8 @@ def main():
     ap.add_argument("--no-alternatives", action="store_true",
                     help="skip the hidden-space timing (profiling runs: keeps per-kernel averages to one order)")
     ap.add_argument("--no-decode", action="store_true", help="skip the 64-token layer's latency measurement")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the 32,768-token skewed layer and the whole-model forward blocks")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain copy of this many MiB (counter calibration for profiling)")
     args = ap.parse_args()
@@ -451,6 +520,16 @@ def main():
             peak = HBM_PEAK_GBS
         kernels[k] = dict(us=round(ms_k * 1e3, 2), bound=w["bound"], achieved=round(ach, 2), peak=peak,
                           unit=w["unit"], frac=round(ach / peak, 4), work=w["work"], parts=STAGES[k])
+    # The generator as launched: the hidden-row kernel with its activation phase plus the
+    # v-row kernel, next to the split figure graded above.
+    if split is not None:
+        raw_ms = launch_ms["hidden_rows"] + launch_ms["v_rows"]
+        ach = work["generate"]["work"] / (raw_ms * 1e-3) / 1e12
+        split["generate_in_pipeline"] = dict(us=round(raw_ms * 1e3, 2), achieved=round(ach, 2),
+                                             peak=BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                                             frac=round(ach / BF16_PEAK_TFLOPS, 4),
+                                             note="hidden-row kernel with its activation phase + v-row kernel, "
+                                                  "as launched in the timed steps")
     graded = {k: kernels[k] for k in ("generate", "apply_scatter")}
     dom = max(graded, key=lambda k: graded[k]["us"])
     kd = kernels[dom]
@@ -489,6 +568,12 @@ def main():
     decode = None
     if args.config == "cfg2" and not args.no_decode:
         decode = decode_latency(args, with_cpu=args.cpu_tokens > 0)
+    skewed = lm = None
+    if args.config == "cfg2" and not args.no_extra:
+        del m
+        torch.cuda.empty_cache()
+        skewed = skewed_block(args.steps, max(args.warmup, 5))
+        lm = lm_block(min(args.steps, 10), 3)
 
     line = {
         "metric": METRIC,
@@ -523,6 +608,8 @@ def main():
         "alternatives": alternatives,
         "cpu_baseline": cpu,
         "decode_64_tokens": decode,
+        "skewed_32768_tokens": skewed,
+        "lm_forward": lm,
     }
     print(json.dumps(line), flush=True)
 
