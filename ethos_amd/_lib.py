@@ -41,8 +41,9 @@ SIGNATURES = {
     "ethos_apply_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "ethos_apply_scatter": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
                                            _vp, _sz, _vp, _vp]),
-    "ethos_expert_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
-                                             _vp]),
+    "ethos_expert_backward_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32]),
+    "ethos_expert_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp,
+                                             _sz, _vp, _vp, _vp, _vp, _vp]),
     "ethos_expert_forward_workspace_bytes": (_sz, [_i64, _i32, _i32, _i64, _i32, _i32, _i32, _i32]),
     "ethos_expert_forward": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
                                             _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _vp,

@@ -450,9 +450,16 @@ int ethos_expert_forward(const void* x, const void* latents, int64_t n_experts, 
     return hip_status(rc, "ethos_expert_forward");
 }
 
+size_t ethos_expert_backward_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden) {
+    if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || d_hidden <= 0) return 0;
+    return ethos::expert_backward_workspace_bytes(n_tok * n_heads * top_k, d_hidden);
+}
+
 int ethos_expert_backward(const void* h, const float* xp, const float* dyb, const int32_t* pair_slot,
-                          const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden,
-                          int32_t dtype, float* dscores, float* hacc, float* dxp, float* dh, void* stream) {
+                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* seg_off, const void* scores,
+                          int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden, int32_t dtype,
+                          void* workspace, size_t workspace_bytes, float* dscores, float* hacc, float* dxp, float* dh,
+                          void* stream) {
     g_err[0] = 0;
     if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_expert_backward: unknown dtype %d", dtype);
     if (n_tok < 0 || n_heads <= 0 || top_k <= 0 || d_hidden <= 0)
@@ -464,11 +471,18 @@ int ethos_expert_backward(const void* h, const float* xp, const float* dyb, cons
     if (n_tok * n_heads * top_k > INT32_MAX || n_tok > INT32_MAX)
         return fail(ETHOS_ESIZE, "ethos_expert_backward: too many pairs");
     if (n_tok == 0) return 0;
-    if (!h || !xp || !dyb || !pair_slot || !scores || !dscores || !hacc || !dxp || !dh)
+    if (!h || !xp || !dyb || !pair_slot || !perm || !sorted_slot || !seg_off || !scores || !workspace || !dscores ||
+        !hacc || !dxp || !dh)
         return fail(ETHOS_ENULL, "ethos_expert_backward: null pointer");
-    if (!aligned16(h)) return fail(ETHOS_EALIGN, "ethos_expert_backward: h must be 16-byte aligned");
-    const int rc = ethos::launch_expert_backward(h, xp, dyb, pair_slot, scores, n_tok, n_heads, top_k, d_hidden, dtype,
-                                                 dscores, hacc, dxp, dh, num_cus(), (hipStream_t)stream);
+    const size_t need = ethos::expert_backward_workspace_bytes(n_tok * n_heads * top_k, d_hidden);
+    if (workspace_bytes < need)
+        return fail(ETHOS_EWORKSPACE, "ethos_expert_backward: workspace of %zu bytes, %zu needed", workspace_bytes,
+                    need);
+    if (!aligned16(h) || !aligned16(workspace))
+        return fail(ETHOS_EALIGN, "ethos_expert_backward: h and workspace must be 16-byte aligned");
+    const int rc = ethos::launch_expert_backward(h, xp, dyb, pair_slot, perm, sorted_slot, seg_off, scores, n_tok,
+                                                 n_heads, top_k, d_hidden, dtype, workspace, dscores, hacc, dxp, dh,
+                                                 num_cus(), (hipStream_t)stream);
     if (rc < 0) return fail(ETHOS_EUNSUPPORTED, "ethos_expert_backward: d_hidden=%d not supported", d_hidden);
     return hip_status(rc, "ethos_expert_backward");
 }

@@ -56,8 +56,12 @@ int launch_hidden_act(const void* latents, int64_t n_experts, const int32_t* uni
                       float* act, int64_t n_pairs, int num_cus, hipStream_t stream);
 
 int apply_chunks(int d, int dtype);
+// The expert stages' backward (per-pair scalars, token sums, then deterministic expert
+// sums over the sorted pairs); ws: expert_backward_workspace_bytes.
+size_t expert_backward_workspace_bytes(int64_t n_pairs, int dh);
 int launch_expert_backward(const void* hid, const float* xp, const float* dyb, const int32_t* pair_slot,
-                           const void* gates, int64_t n_tok, int H, int k, int dh, int dtype, float* dg, float* hacc,
+                           const int32_t* perm, const int32_t* sorted_slot, const int32_t* seg_off, const void* gates,
+                           int64_t n_tok, int H, int k, int dh, int dtype, void* ws, float* dg, float* hacc,
                            float* dxp, float* dhs, int num_cus, hipStream_t stream);
 size_t apply_hidden_workspace_bytes(int64_t n_tok, int H, int k, int d, int dh, int dtype);
 int launch_apply_hidden(const void* x, const void* w2, const void* hid, const int32_t* perm,

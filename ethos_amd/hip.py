@@ -285,13 +285,15 @@ def expert_forward(x: torch.Tensor, latents: torch.Tensor, w1: torch.Tensor, w2:
     return out, h
 
 
-def expert_backward(h: torch.Tensor, xp: torch.Tensor, dyb: torch.Tensor, pair_slot: torch.Tensor, gates: torch.Tensor,
+def expert_backward(h: torch.Tensor, xp: torch.Tensor, dyb: torch.Tensor, seg: dict, gates: torch.Tensor,
                     n_heads: int, top_k: int, U: int):
     """Per-pair part of the expert stages' backward: (dgates [n, H, k], hacc [n, dh], dxp [n, dh],
-    dh [U, dh]), all float32, from xp = x W_u and dyb = (dy / H) W_v^T (float32 [n, dh])."""
+    dh [U, dh]), all float32, from xp = x W_u and dyb = (dy / H) W_v^T (float32 [n, dh]) and the
+    routing's sorted segments `seg` (sort_segment); deterministic (fixed summation orders)."""
     _need(h, "h", dim=2)
     _need(xp, "xp", torch.float32, 2)
     _need(dyb, "dyb", torch.float32, 2)
+    pair_slot = seg["pair_slot"]
     _need(pair_slot, "pair_slot", torch.int32)
     _need(gates, "gates", h.dtype)
     n, dh = xp.shape
@@ -301,9 +303,12 @@ def expert_backward(h: torch.Tensor, xp: torch.Tensor, dyb: torch.Tensor, pair_s
     dg = torch.empty(gates.shape, dtype=torch.float32, device=dev)
     hacc = torch.empty((n, dh), dtype=torch.float32, device=dev)
     dxp = torch.empty((n, dh), dtype=torch.float32, device=dev)
-    dhs = torch.zeros((max(U, 1), dh), dtype=torch.float32, device=dev)
+    dhs = torch.empty((max(U, 1), dh), dtype=torch.float32, device=dev)
+    ws, ws_bytes = workspace(load().ethos_expert_backward_workspace_bytes(n, n_heads, top_k, dh), dev)
     rc = load().ethos_expert_backward(h.data_ptr(), xp.data_ptr(), dyb.data_ptr(), pair_slot.data_ptr(),
-                                      gates.data_ptr(), n, n_heads, top_k, dh, dtype_code(h.dtype), dg.data_ptr(),
-                                      hacc.data_ptr(), dxp.data_ptr(), dhs.data_ptr(), _stream())
+                                      seg["perm"].data_ptr(), seg["sorted_slot"].data_ptr(), seg["seg_off"].data_ptr(),
+                                      gates.data_ptr(), n, n_heads, top_k, dh, dtype_code(h.dtype), ws.data_ptr(),
+                                      ws_bytes, dg.data_ptr(), hacc.data_ptr(), dxp.data_ptr(), dhs.data_ptr(),
+                                      _stream())
     check(rc, "ethos_expert_backward")
     return dg, hacc, dxp, dhs[:U]

@@ -79,8 +79,9 @@ class _ExpertStages(torch.autograd.Function):
     dA = x^T dxp,  dB = dY^T hacc with hacc_t = Σ_p a_p h_s,  dx = dxp A^T;
     dpre = gelu'(pre) dh,  dC = dpre^T z,  dz = dpre C (added into the latent rows of the
     unique experts).  v rows are not needed.  The per-pair terms, the token sums (hacc, dxp)
-    and the expert sums (dh, float atomics) come from one HIP kernel (ethos_expert_backward);
-    the rest are GEMMs.  Both execution orders (scatter of v rows, hidden-space reordering)
+    and the expert sums (dh, summed over each expert's sorted pairs in a fixed order) come
+    from one library call (ethos_expert_backward); the rest are GEMMs.  The backward is
+    deterministic.  Both execution orders (scatter of v rows, hidden-space reordering)
     compute this same function, so they share the backward.
 
     The gates enter as `gates_exact` (the values the forward uses) and `gate_path` (a
@@ -91,7 +92,8 @@ class _ExpertStages(torch.autograd.Function):
     def forward(ctx, x, gate_path, latents_w, w1_w, w2_w, layer, gates_exact, seg):
         out, h = layer._expert_stages(x, gates_exact, seg)
         latents, w1, w2, _ = layer._generator_params(x.dtype, x.device)
-        ctx.save_for_backward(x, gates_exact, h, seg["uniq"], seg["pair_slot"], seg["n_unique"], latents, w1, w2)
+        ctx.save_for_backward(x, gates_exact, h, seg["uniq"], seg["pair_slot"], seg["n_unique"], seg["perm"],
+                              seg["sorted_slot"], seg["seg_off"], latents, w1, w2)
         ctx.heads, ctx.top_k = layer.num_heads, layer.top_k
         ctx.param_dtypes = (latents_w.dtype, w1_w.dtype, w2_w.dtype)
         return out
@@ -100,7 +102,8 @@ class _ExpertStages(torch.autograd.Function):
     def backward(ctx, dy):
         # v_s = h_s B^T never needs forming: dY_t . v_s = (dY_t B) . h_s, the dv_s B term of
         # dh_s is sum_p a_p (dY_t B), and dB = dv^T h = dY^T hacc with hacc_t = sum_p a_p h_s.
-        x, gates, h, uniq, pair_slot, n_unique, latents, w1, w2 = ctx.saved_tensors
+        x, gates, h, uniq, pair_slot, n_unique, perm, sorted_slot, seg_off, latents, w1, w2 = ctx.saved_tensors
+        seg = {"pair_slot": pair_slot, "perm": perm, "sorted_slot": sorted_slot, "seg_off": seg_off}
         H, k = ctx.heads, ctx.top_k
         n, d = x.shape
         f = torch.float32
@@ -110,8 +113,8 @@ class _ExpertStages(torch.autograd.Function):
         xp = xf @ A
         dY = dy.to(f) * (1.0 / H)
         dYB = dY @ B
-        # per-pair terms, token sums and expert sums in one HIP kernel (ethos_expert_backward)
-        dg, hacc, dxp, dh = hip.expert_backward(h, xp, dYB, pair_slot, gates, H, k, U)
+        # per-pair terms, token sums and expert sums (ethos_expert_backward)
+        dg, hacc, dxp, dh = hip.expert_backward(h, xp, dYB, seg, gates, H, k, U)
         dB = dY.T @ hacc
         dA = xf.T @ dxp
         dx = dxp @ A.T

@@ -24,10 +24,8 @@
  *     enqueued), or a positive hipError_t from the launch.  ethos_last_error() gives a
  *     message for the calling thread's last failure.
  *   - dtype: ETHOS_F32 or ETHOS_BF16; tensors of "dtype T" hold that type, row-major.
- *   - The forward entry points are deterministic: the same inputs give bit-identical
- *     outputs on every run (no atomics).  The one exception is ethos_expert_backward,
- *     whose per-expert sums use float atomics and so vary in their last bits from run
- *     to run.
+ *   - Every entry point is deterministic: the same inputs give bit-identical outputs on
+ *     every run (no atomics; every sum has a fixed order).
  */
 #ifndef ETHOS_HIP_H
 #define ETHOS_HIP_H
@@ -39,7 +37,7 @@
 extern "C" {
 #endif
 
-#define ETHOS_ABI_VERSION 6
+#define ETHOS_ABI_VERSION 7
 
 #define ETHOS_F32 0
 #define ETHOS_BF16 1
@@ -298,15 +296,22 @@ int ethos_apply_hidden(const void* x, const void* w2, const void* h, const int32
  *   dscores[p] = gelu(c) da                               float32 [n_tok, n_heads, top_k]
  *   hacc[t]    = sum_p a h_s                              float32 [n_tok, d_hidden]
  *   dxp[t]     = sum_p g gelu'(c) da h_s                  float32 [n_tok, d_hidden]
- *   dh[s]     += a dyb_t + g gelu'(c) da xp_t             float32 [>= U, d_hidden], added
- *                                                          to (zero it first); float atomics,
- *                                                          so the sums' order varies per run
- *   h, pair_slot, scores  as for ethos_apply_scatter (h 16-byte aligned).
+ *   dh[s]      = sum_p a dyb_t + g gelu'(c) da xp_t      float32 [>= U, d_hidden], rows s < U
+ *                                                          written; summed over the expert's
+ *                                                          pairs in sorted order (blocks of 64
+ *                                                          sorted positions, then the blocks'
+ *                                                          parts in order): deterministic
+ *   h, pair_slot, scores            as for ethos_apply_scatter (h 16-byte aligned)
+ *   perm, sorted_slot, seg_off      from ethos_sort_segment on the same routing
+ *   workspace  >= ethos_expert_backward_workspace_bytes(...) bytes, 16-byte aligned (scratch)
  * Limits: d_hidden a multiple of 8 (bf16) or 4 (fp32), <= 4096 (bf16) / 2048 (fp32).
  */
+size_t ethos_expert_backward_workspace_bytes(int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden);
 int ethos_expert_backward(const void* h, const float* xp, const float* dyb, const int32_t* pair_slot,
-                          const void* scores, int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden,
-                          int32_t dtype, float* dscores, float* hacc, float* dxp, float* dh, void* stream);
+                          const int32_t* perm, const int32_t* sorted_slot, const int32_t* seg_off, const void* scores,
+                          int64_t n_tok, int32_t n_heads, int32_t top_k, int32_t d_hidden, int32_t dtype,
+                          void* workspace, size_t workspace_bytes, float* dscores, float* hacc, float* dxp, float* dh,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ethos_abi_version() == 6
+    assert _lib.load().ethos_abi_version() == 7
 
 
 def _rc(fn, *args):
@@ -140,6 +140,28 @@ def test_expert_forward_argument_errors():
     misx = list(args)
     misx[6] = 18
     assert L.ethos_expert_forward(*misx, 1, 0, 16, ws, 16, 16, None) == -4
+
+
+def test_expert_backward_argument_errors():
+    L = _lib.load()
+    ws = L.ethos_expert_backward_workspace_bytes(48, 2, 4, 64)
+    assert ws >= 48 * 2 * 4 * 8  # the per-pair scalars at least
+    assert L.ethos_expert_backward_workspace_bytes(-1, 2, 4, 64) == 0
+    args = [16, 16, 16, 16, 16, 16, 16, 16, 48, 2, 4, 64]
+    outs = [16, 16, 16, 16, None]
+    assert L.ethos_expert_backward(*args, 7, 16, ws, *outs) == -1
+    assert L.ethos_expert_backward(*args, 1, 16, ws - 16, *outs) == -5
+    noperm = list(args)
+    noperm[4] = None
+    assert L.ethos_expert_backward(*noperm, 1, 16, ws, *outs) == -3
+    assert L.ethos_expert_backward(*args, 1, None, ws, *outs) == -3
+    assert L.ethos_expert_backward(*args, 1, 24, ws, *outs) == -4
+    bad = list(args)
+    bad[11] = 60
+    assert L.ethos_expert_backward(*bad, 1, 16, ws, *outs) == -6
+    empty = list(args)
+    empty[8] = 0
+    assert L.ethos_expert_backward(*empty, 1, None, 0, None, None, None, None, None) == 0
 
 
 def test_token_proj_argument_errors():

@@ -74,6 +74,28 @@ def test_grads_match_reference_bf16(train):
         assert ours[k].dtype == torch.bfloat16
 
 
+@pytest.mark.parametrize("name", ["cfg3", "tiny_fp32"])
+def test_backward_deterministic(name):
+    """Two forward + backward passes of the layer on the same input give bit-identical
+    gradients for x and every parameter (the expert sums have a fixed order)."""
+    sh = SHAPES[name]
+    x, sd = make_inputs(sh, signal=True)
+    grads = []
+    for _ in range(2):
+        m = ethos_amd.EthosExpertLayer(sh.config()).to(sh.torch_dtype)
+        m.load_state_dict(sd)
+        m = m.cuda().train()
+        xd = x.cuda().view(sh.batch, -1, sh.d_model).clone().requires_grad_(True)
+        y = m(xd)
+        w = torch.randn(y.shape, generator=torch.Generator().manual_seed(1)).to(y.dtype).cuda()
+        (y.float() * w.float()).sum().backward()
+        torch.cuda.synchronize()
+        grads.append({"x": xd.grad.clone(), **{k: p.grad.clone() for k, p in m.named_parameters()}})
+    assert grads[0].keys() == grads[1].keys()
+    for k in grads[0]:
+        assert torch.equal(grads[0][k], grads[1][k]), f"{name}: gradient of {k} differs between two runs"
+
+
 def test_grad_path_forward_values_unchanged():
     """Autograd on or off, the forward output is the same HIP result bit for bit, and only
     the autograd pass carries a graph; BatchNorm running stats advance once per call."""
@@ -125,21 +147,32 @@ def test_cfg3_backward_runs_and_matches_reference_on_experts():
     assert _nerr(xd.grad.view(-1, sh.d_model).float(), xr.grad) < 3e-2
 
 
-@pytest.mark.parametrize("dt,n,H,k,dh,U", [("bf16", 50, 2, 4, 64, 37), ("bf16", 33, 8, 16, 512, 900),
-                                           ("fp32", 20, 4, 8, 96, 11), ("bf16", 7, 3, 5, 40, 3)])
-def test_expert_backward_entry_point(dt, n, H, k, dh, U):
+@pytest.mark.parametrize("dt,n,H,k,dh,E,hot", [("bf16", 50, 2, 4, 64, 37, 0.0), ("bf16", 33, 8, 16, 512, 900, 0.0),
+                                               ("fp32", 20, 4, 8, 96, 11, 0.0), ("bf16", 7, 3, 5, 40, 3, 0.0),
+                                               ("bf16", 300, 8, 16, 512, 5000, 0.5), ("fp32", 64, 4, 8, 128, 1, 0.0)])
+def test_expert_backward_entry_point(dt, n, H, k, dh, E, hot):
     """ethos_expert_backward through the C-ABI against a float64 torch evaluation of its four
-    outputs (dscores, hacc, dxp, dh), with repeated experts so the expert sums collide."""
+    outputs (dscores, hacc, dxp, dh), on routing sorted by ethos_sort_segment: experts with
+    repeated pairs, a hot expert holding half of 38,400 pairs (a segment across ~300 blocks of
+    the expert-sum pass), and one expert holding every pair.  Two runs are bit-identical."""
     from ethos_amd import hip
     g = torch.Generator().manual_seed(n + dh)
     tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    ids = torch.randint(0, E, (n * H * k,), generator=g, dtype=torch.int32)
+    if hot > 0:
+        ids[torch.rand(ids.numel(), generator=g) < hot] = 7
+    seg = hip.sort_segment(ids.cuda(), E)
+    U = int(seg["n_unique"].item())
+    slot = seg["pair_slot"].cpu()
     h = (torch.randn(U, dh, generator=g) * 0.5).to(tdt)
     xp = torch.randn(n, dh, generator=g)
     dyb = torch.randn(n, dh, generator=g)
-    slot = torch.randint(0, U, (n * H * k,), generator=g, dtype=torch.int32)
     gates = torch.rand(n, H, k, generator=g).to(tdt)
-    dg, hacc, dxp, dhs = hip.expert_backward(h.cuda(), xp.cuda(), dyb.cuda(), slot.cuda(), gates.cuda(), H, k, U)
+    dg, hacc, dxp, dhs = hip.expert_backward(h.cuda(), xp.cuda(), dyb.cuda(), seg, gates.cuda(), H, k, U)
+    again = hip.expert_backward(h.cuda(), xp.cuda(), dyb.cuda(), seg, gates.cuda(), H, k, U)
     torch.cuda.synchronize()
+    for a1, a2, name in zip((dg, hacc, dxp, dhs), again, ("dscores", "hacc", "dxp", "dh")):
+        assert torch.equal(a1, a2), f"{name} differs between two runs"
     hd, x64, y64 = h.double(), xp.double(), dyb.double()
     t = torch.arange(n * H * k) // (H * k)
     hs = hd[slot.long()]

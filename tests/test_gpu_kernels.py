@@ -282,6 +282,9 @@ def test_route_stress_bit_exact(kind, dt):
         torch.cuda.synchronize()
         got = to_host(ids)
         assert np.array_equal(got, ids_ref), f"{kind}/{dt}/{norms}: {np.sum(np.any(got != ids_ref, -1))} rows differ"
+        # the gates too, bit for bit (same ids, same list order, same softmax contract)
+        gg, gr = O.to_f32(to_host(g), dt), O.to_f32(g_ref, dt)
+        assert np.array_equal(gg, gr), f"{kind}/{dt}/{norms}: {np.sum(np.any(gg != gr, -1))} rows' gates differ"
 
 
 @pytest.mark.parametrize("dl,dh,d,U", [(128, 256, 1024, 1000), (128, 512, 512, 300), (128, 512, 1024, 129),

@@ -176,8 +176,10 @@ def test_layer_cfg4_zipf_full_size():
     xs = O.from_torch(x)
     qh = to_host(q)
     sub = np.arange(0, sh.n_tok, 16)
-    q_ref = O.query_proj(xs[sub], P["Wq"], P["bq"], P["alpha"], P["beta"], "bf16")
-    assert np.array_equal(qh[sub], q_ref)
+    # the query projection on every 4th token (8,192 tokens, 16.8 M outputs)
+    qsub = np.arange(0, sh.n_tok, 4)
+    q_ref = O.query_proj(xs[qsub], P["Wq"], P["bq"], P["alpha"], P["beta"], "bf16")
+    assert np.array_equal(qh[qsub], q_ref)
     g_ref, ids_ref = O.route(qh, P["K1"], P["K2"], sh.top_k, "bf16")
     assert np.array_equal(to_host(ids), ids_ref)
     gh = to_host(gates)
