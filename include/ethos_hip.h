@@ -55,7 +55,9 @@ extern "C" {
  * order, on their stream at stage boundaries, until the list is used up; n_events = 0
  * clears it.  ethos_expert_forward records five per call: after the token projection, the
  * hidden rows, the activations, the v rows and the scatter-back.  Lets a caller time the
- * stages inside one call with events on the launch stream.
+ * stages inside one call with events on the launch stream.  The library keeps the raw
+ * handles: the events must stay valid until the list is used up or cleared with
+ * n_events = 0 (a caller whose call fails part-way should clear it before freeing them).
  */
 int ethos_stage_events(void* const* events, int32_t n_events);
 
@@ -156,8 +158,10 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
  * ethos_sort_segment without a caller workspace, for callers that cannot allocate device
  * memory (code under HIP graph capture, fixed-memory serving loops).  It has no
  * counterpart in the reference.  The sort workspace is a static array in the library's
- * device data, one per GPU, sized for ETHOS_NOALLOC_MAX_PAIRS pairs (about 18 MiB, held
- * from the first call on a GPU until the process ends); larger n_pairs returns
+ * device data, one per GPU, sized for ETHOS_NOALLOC_MAX_PAIRS pairs (about 18 MiB, part
+ * of the library's code object: held on a GPU from when the code object is loaded there,
+ * i.e. the first launch of any of the library's kernels on it, until the process ends);
+ * larger n_pairs returns
  * ETHOS_ESIZE.  Every other argument and every output is as for ethos_sort_segment, and
  * the outputs are bit-identical to it.  All calls on one GPU share that array: calls that
  * overlap on one GPU (on different streams, or from different threads) race and must be

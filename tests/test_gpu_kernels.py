@@ -101,15 +101,23 @@ def test_route_ties_break_to_lowest_index():
                                          (16385, 262144, "skew"), (16384, 7, "rand"), (2, 262144, "same"),
                                          (8192, 262144, "max"), (70000, 7, "rand"), (100000, 4096, "rand"),
                                          (60000, 2 ** 21, "rand"), (300000, 262144, "hot2d"),
-                                         (65536, 262144, "same"), (24577, 262144, "rand")])
+                                         (65536, 262144, "same"), (24577, 262144, "rand"),
+                                         (300000, 2 ** 21, "same"), (300000, 2 ** 21, "skew"),
+                                         (300000, 2 ** 21, "hot3d")])
 def test_sort_segment_exact(n, E, pattern):
     """The sort against the oracle's counting sort: one pass (E = 7), two (4,096 and 262,144
     experts) and three (2^21) over tiles of 4,096 pairs; batches up to 16,384 pairs take the
     single-workgroup sort.  Patterns: uniform ids, one id everywhere (one segment spanning
     every tile), Zipf-skewed ids, half the pairs on the largest id, and ids whose two
-    9-bit digits are both Zipf-skewed (hot experts whose segments cross tile boundaries)."""
+    9-bit digits (or, with 2^21 experts, all three digits) are Zipf-skewed (hot experts
+    whose segments cross tile boundaries, in the three-pass path too)."""
     rng = np.random.default_rng(n + E)
-    if pattern == "hot2d":
+    if pattern == "hot3d":
+        a = np.minimum(rng.zipf(1.1, n), 512) - 1
+        b = np.minimum(rng.zipf(1.1, n), 512) - 1
+        c = np.minimum(rng.zipf(1.1, n), 8) - 1
+        ids = ((c << 18) | (b << 9) | a).astype(np.int32)
+    elif pattern == "hot2d":
         a = np.minimum(rng.zipf(1.1, n), 192) - 1
         b = np.minimum(rng.zipf(1.1, n), 192) - 1
         ids = (a * 512 + b).astype(np.int32)

@@ -1,6 +1,8 @@
 """ethos_sort_segment_noalloc (the sort without a caller workspace) against
-ethos_sort_segment through the C-ABI: bit-identical outputs on two calls in a row, the
-second with fewer pairs, so the shared static workspace holds the first call's data."""
+ethos_sort_segment through the C-ABI: bit-identical outputs on three calls in a row, each
+with fewer pairs than the last.  The second (300,000 pairs, another id mix) takes the
+tiled path over the static workspace that still holds the first call's data; the third
+(5,000 pairs) the single-workgroup sort, which does not use the static workspace."""
 import numpy as np
 import pytest
 import torch
@@ -49,11 +51,13 @@ def _no_alloc(ids):
     return r
 
 
-def _ids(n, seed):
-    """Half uniform ids, half drawn from a few hundred hot experts (long segments)."""
+def _ids(n, seed, hot_share=0.5, n_hot=300):
+    """Uniform ids, with a share of the pairs drawn from a few hundred hot experts (long
+    segments)."""
     g = torch.Generator().manual_seed(seed)
-    uni = torch.randint(0, E, (n - n // 2,), generator=g)
-    hot = torch.randint(0, 300, (n // 2,), generator=g) * 871  # ids below 300 * 871 < E
+    nh = int(n * hot_share)
+    uni = torch.randint(0, E, (n - nh,), generator=g)
+    hot = torch.randint(0, n_hot, (nh,), generator=g) * (E // n_hot - 1)  # ids below E
     ids = torch.cat([uni, hot])[torch.randperm(n, generator=g)]
     return ids.to(torch.int32)
 
@@ -70,9 +74,9 @@ def _same(a, b):
 
 def test_sort_noalloc_matches_sort_with_workspace():
     dev = torch.device("cuda")
-    for n, seed in ((_lib.NOALLOC_MAX_PAIRS, 1), (5000, 2)):
+    for n, seed, share, n_hot in ((_lib.NOALLOC_MAX_PAIRS, 1, 0.5, 300), (300000, 3, 0.8, 40), (5000, 2, 0.5, 300)):
         print(f"sort_noalloc: {n} pairs, seed {seed}", flush=True)
-        ids = _ids(n, seed)
+        ids = _ids(n, seed, share, n_hot)
         want = _with_workspace(ids.to(dev))
         got = _no_alloc(ids.to(dev))
         torch.cuda.synchronize()
