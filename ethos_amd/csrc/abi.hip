@@ -47,10 +47,11 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool dtype_ok(int dtype) { return dtype == ETHOS_F32 || dtype == ETHOS_BF16; }
 
 // Sort workspace of ethos_sort_segment_noalloc: one array per GPU, in the code object's
-// device data, sized for ETHOS_NOALLOC_MAX_PAIRS pairs.  Its name is only a host-side
+// device data, sized for ETHOS_NOALLOC_MAX_PAIRS pairs (a batch that size sorts without
+// the expert -> slot table).  Its name is only a host-side
 // stand-in; kernels receive the device address that hipGetSymbolAddress returns for the
 // current device (g_scratch_ptr), looked up once per device on the first call there.
-constexpr size_t kScratchWords = ethos::sort_workspace_words(ETHOS_NOALLOC_MAX_PAIRS);
+constexpr size_t kScratchWords = ethos::sort_workspace_words(ETHOS_NOALLOC_MAX_PAIRS, (int64_t)1 << 18);
 static __device__ __align__(256) uint32_t scratch[kScratchWords];
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
@@ -225,9 +226,8 @@ int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys
 }
 
 size_t ethos_sort_workspace_bytes(int64_t n_pairs, int64_t n_experts) {
-    (void)n_experts;
-    if (n_pairs <= 0) return 256;
-    return ethos::sort_workspace_bytes(n_pairs);
+    if (n_pairs <= 0 || n_experts <= 0) return 256;
+    return ethos::sort_workspace_bytes(n_pairs, n_experts);
 }
 
 int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, void* workspace,
@@ -242,9 +242,9 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
         return hip_status(ethos::launch_sort_empty(seg_off, n_unique, (hipStream_t)stream), "ethos_sort_segment");
     if (!ids || !workspace || !perm || !uniq_ids || !pair_slot || !sorted_slot)
         return fail(ETHOS_ENULL, "ethos_sort_segment: null pointer");
-    if (workspace_bytes < ethos::sort_workspace_bytes(n_pairs))
+    if (workspace_bytes < ethos::sort_workspace_bytes(n_pairs, n_experts))
         return fail(ETHOS_EWORKSPACE, "ethos_sort_segment: workspace of %zu bytes, %zu needed", workspace_bytes,
-                    ethos::sort_workspace_bytes(n_pairs));
+                    ethos::sort_workspace_bytes(n_pairs, n_experts));
     if (!aligned16(workspace)) return fail(ETHOS_EALIGN, "ethos_sort_segment: workspace not 16-byte aligned");
     return hip_status(ethos::launch_sort_segment(ids, n_pairs, n_experts, workspace, perm, uniq_ids, seg_off,
                                                  pair_slot, sorted_slot, n_unique, (hipStream_t)stream),
@@ -268,7 +268,7 @@ int ethos_sort_segment_noalloc(const int32_t* ids, int64_t n_pairs, int64_t n_ex
                           "ethos_sort_segment_noalloc");
     if (!ids || !perm || !uniq_ids || !pair_slot || !sorted_slot)
         return fail(ETHOS_ENULL, "ethos_sort_segment_noalloc: null pointer");
-    if (ethos::sort_workspace_bytes(n_pairs) > sizeof(scratch))
+    if (ethos::sort_workspace_bytes(n_pairs, n_experts) > sizeof(scratch))
         return fail(ETHOS_EWORKSPACE, "ethos_sort_segment_noalloc: static workspace sizing");
     int rc = 0;
     void* ws = scratch_ptr(&rc);

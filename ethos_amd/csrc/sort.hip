@@ -28,7 +28,12 @@
 // the tiles).  Slot = (new distinct keys of smaller digits and of this digit in earlier
 // tiles) + (heads so far in the group) - 1.
 // Outputs: perm (pair ids by expert), uniq (expert id per slot), seg_off (U + 1),
-// pair_slot[p] (slot of pair p), sorted_slot[i] (slot of position i), n_unique.
+// pair_slot[p] (slot of pair p), sorted_slot[i] (slot of position i), n_unique.  The last
+// pass scatters pair_slot by pair (one 4-byte store per pair to a random place).  Above
+// 2^20 pairs with ids of at most 18 bits, where those stores cost more than a launch, it
+// writes an expert -> slot table at the heads instead (one store per unique expert) and a
+// gather over the ids in pair order writes pair_slot with coalesced stores.
+
 #include "ethos_common.hpp"
 #include "ethos_launch.hpp"
 
@@ -64,7 +69,8 @@ static_assert(kTC * kTW * 64 == kTile && kTPer == 4, "tile shape");
 
 // Exclusive scans of NV values per thread over threads 0 .. 511 (waves 0 .. 7; the other
 // threads pass zeros), in one pass.  Every thread of the workgroup calls it (it holds
-// barriers); tot[] receives the sums.  wsum: 8 NV words of LDS.
+// barriers); tot[] receives the sums.  wsum: 8 NV words of LDS.  The waves' totals are read
+// with one LDS load (one per lane) and combined with lane reads into scalar registers.
 template <int NV>
 __device__ __forceinline__ void scan512(const uint32_t (&v)[NV], uint32_t (&ex)[NV], uint32_t (&tot)[NV],
                                         uint32_t* wsum) {
@@ -85,14 +91,17 @@ __device__ __forceinline__ void scan512(const uint32_t (&v)[NV], uint32_t (&ex)[
         for (int c = 0; c < NV; ++c) wsum[wave * NV + c] = inc[c];
     }
     __syncthreads();
+    static_assert(kRadix / 64 * NV <= 64, "one wave total per lane");
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t x = lane < kRadix / 64 * NV ? wsum[lane] : 0u;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
         uint32_t pre = 0, t = 0;
 #pragma unroll
         for (int w = 0; w < kRadix / 64; ++w) {
-            const uint32_t x = wsum[w * NV + c];
-            pre += w < wave ? x : 0u;
-            t += x;
+            const uint32_t y = __builtin_amdgcn_readlane(x, w * NV + c);
+            pre += w < uwave ? y : 0u;
+            t += y;
         }
         ex[c] = pre + inc[c] - v[c];
         tot[c] = t;
@@ -112,12 +121,14 @@ __device__ __forceinline__ uint32_t scan1024(uint32_t v, uint32_t* wsum, uint32_
     }
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t x = lane < kTW ? wsum[lane] : 0u;
     uint32_t pre = 0, t = 0;
 #pragma unroll
     for (int w = 0; w < kTW; ++w) {
-        const uint32_t x = wsum[w];
-        pre += w < wave ? x : 0u;
-        t += x;
+        const uint32_t y = __builtin_amdgcn_readlane(x, w);
+        pre += w < uwave ? y : 0u;
+        t += y;
     }
     __syncthreads();
     tot = t;
@@ -326,7 +337,8 @@ __global__ __launch_bounds__(256) void tsort_scan(uint32_t* __restrict__ cnt, ui
             if (kLast) {
                 ds[j] = v ? drow[t] : 0u;
                 fl[j] = v ? frow[t] : 0u;
-                le[j] = v && c[j] ? lrow[t] + 1u : 0u;
+                const uint32_t l = v ? lrow[t] : 0u;  // loaded with the others, used when c[j] > 0
+                le[j] = c[j] ? l + 1u : 0u;
                 ml = max(ml, le[j]);
             }
         }
@@ -452,11 +464,15 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
     const uint32_t* __restrict__ plast, const uint32_t* __restrict__ tot, const uint32_t* __restrict__ stot,
     int32_t* __restrict__ perm, int32_t* __restrict__ uniq, int32_t* __restrict__ seg_off,
     int32_t* __restrict__ pair_slot, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ n_unique,
-    int32_t max_unique) {
-    __shared__ uint32_t wcnt[kTW][kRadix];
+    int32_t max_unique, int32_t* __restrict__ slot_table) {
+    // wcnt while the tile is ranked; afterwards the same LDS holds sslot, the slot + 1 of each
+    // position (bit 31: a head), so that two workgroups fit a CU
+    __shared__ __align__(16) uint32_t wcnt_sslot[kTW * kRadix];
+    static_assert(kTile <= kTW * kRadix, "sslot aliases wcnt");
+    uint32_t (*wcnt)[kRadix] = reinterpret_cast<uint32_t (*)[kRadix]>(wcnt_sslot);
+    uint32_t* sslot = wcnt_sslot;
     __shared__ __align__(16) uint32_t sk[kTile];
     __shared__ __align__(16) uint32_t sv[kTile];
-    __shared__ __align__(16) uint32_t sslot[kTile];  // slot + 1 of each position, bit 31: a head
     __shared__ uint32_t gbase[kRadix], sbase[kRadix], lst[kRadix], lstart[kRadix], hstart[kRadix];
     __shared__ uint32_t wsum[3 * 8];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -554,17 +570,39 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
             perm[pos] = (int32_t)val;
             sorted_slot[pos] = sc;
         }
-        if (val < (uint64_t)n) pair_slot[val] = sc;
+        if (slot_table) {
+            if (sw >> 31) slot_table[key & mkmask] = sc;
+        } else if (val < (uint64_t)n) {
+            pair_slot[val] = sc;
+        }
         if ((sw >> 31) && slot >= 0 && slot < max_unique) {
             uniq[slot] = (int32_t)key;
             seg_off[slot] = (int32_t)pos;
         }
     }
     if (blockIdx.x == 0 && tid == 0) {
-        const int32_t u = (int32_t)u_all < max_unique ? (int32_t)u_all : max_unique;
+        // unsigned comparison: the count is at most n, and the clamp keeps u in [0, max_unique]
+        const int32_t u = u_all < (uint32_t)max_unique ? (int32_t)u_all : max_unique;
         *n_unique = u;
         seg_off[u] = (int32_t)n;
     }
+}
+
+// pair_slot[p] = slot_table[ids[p] & mkmask]: the slot of pair p's expert, from the table
+// the last pass wrote at the heads (the same clamped slot it gives the pair's sorted
+// position).  Four pairs per thread, 1024 per workgroup, coalesced.
+constexpr int kPsThreads = 256, kPsPer = 4;
+__global__ __launch_bounds__(kPsThreads) void tsort_pair_slot(const uint32_t* __restrict__ ids, int64_t n,
+                                                              uint32_t mkmask,
+                                                              const int32_t* __restrict__ slot_table,
+                                                              int32_t* __restrict__ pair_slot) {
+    const int64_t base = (int64_t)blockIdx.x * (kPsThreads * kPsPer) + threadIdx.x;
+    uint32_t k[kPsPer];
+#pragma unroll
+    for (int j = 0; j < kPsPer; ++j) k[j] = base + j * kPsThreads < n ? ids[base + j * kPsThreads] & mkmask : 0u;
+#pragma unroll
+    for (int j = 0; j < kPsPer; ++j)
+        if (base + j * kPsThreads < n) pair_slot[base + j * kPsThreads] = slot_table[k[j]];
 }
 
 __global__ void seg_empty(int32_t* __restrict__ seg_off, int32_t* __restrict__ n_unique) {
@@ -718,8 +756,8 @@ __global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int3
         if (lane == 63) wsum[0] = inc;  // all heads
     }
     __syncthreads();
-    const int32_t u_all = (int32_t)wsum[0];
-    const int32_t u_clamped = u_all < max_unique ? u_all : max_unique;
+    const uint32_t u_all = wsum[0];
+    const int32_t u_clamped = u_all < (uint32_t)max_unique ? (int32_t)u_all : max_unique;
     const uint32_t imask = (1u << vb) - 1u;
     for (int c = wave; c < n_chunks; c += kSmallWaves) {
         const int i = c * 64 + lane;
@@ -747,19 +785,15 @@ __global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int3
     }
 }
 
-static int key_bits(int64_t n_experts) {
-    int b = 0;
-    while (b < 32 && ((int64_t)1 << b) < n_experts) ++b;
-    return b;
+size_t sort_workspace_bytes(int64_t n, int64_t n_experts) {
+    return sort_workspace_words(n, n_experts) * sizeof(uint32_t);
 }
-
-size_t sort_workspace_bytes(int64_t n) { return sort_workspace_words(n) * sizeof(uint32_t); }
 
 int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,
                         int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
                         hipStream_t stream) {
-    const int bits = key_bits(n_experts);
-    const int passes = bits <= kRadixBits ? 1 : (bits + kRadixBits - 1) / kRadixBits;
+    const int bits = sort_key_bits(n_experts);
+    const int passes = sort_passes(n_experts);
     int vb = 0;
     while (vb < 31 && ((int64_t)1 << vb) < n) ++vb;
     const int32_t max_unique = (int32_t)(n < n_experts ? n : n_experts);
@@ -778,6 +812,9 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
     uint32_t* llo = flo + (size_t)kRadix * n_tiles;
     uint32_t* tot = llo + (size_t)kRadix * n_tiles;
     uint32_t* stot = tot + kRadix;
+    // the expert -> slot table (large batches, ids of at most 18 bits), after the totals and
+    // their padding
+    int32_t* table = sort_table_words(n, n_experts) ? reinterpret_cast<int32_t*>(stot + kRadix + 64) : nullptr;
     // keys compare on the bits the passes sort (those of ids below n_experts)
     const uint32_t mkmask = kRadixBits * passes >= 32 ? 0xffffffffu : (1u << (kRadixBits * passes)) - 1u;
     const dim3 tg((unsigned)n_tiles), tb(kTThreads), sg((unsigned)(kRadix / 4)), sb(256);
@@ -806,12 +843,16 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
                 hipLaunchKernelGGL(tsort_down_last<true>, tg, tb, 0, stream, kin, vin, n, shift, mkmask, n_tiles,
                                    (const uint32_t*)cnt, (const uint32_t*)dist, (const uint32_t*)llo,
                                    (const uint32_t*)tot, (const uint32_t*)stot, perm, uniq, seg_off, pair_slot,
-                                   sorted_slot, n_unique, max_unique);
+                                   sorted_slot, n_unique, max_unique, table);
             else
                 hipLaunchKernelGGL(tsort_down_last<false>, tg, tb, 0, stream, kin, vin, n, shift, mkmask, n_tiles,
                                    (const uint32_t*)cnt, (const uint32_t*)dist, (const uint32_t*)llo,
                                    (const uint32_t*)tot, (const uint32_t*)stot, perm, uniq, seg_off, pair_slot,
-                                   sorted_slot, n_unique, max_unique);
+                                   sorted_slot, n_unique, max_unique, table);
+            if (table)
+                hipLaunchKernelGGL(tsort_pair_slot, dim3((unsigned)((n + kPsThreads * kPsPer - 1) / (kPsThreads * kPsPer))),
+                                   dim3(kPsThreads), 0, stream, reinterpret_cast<const uint32_t*>(ids), n, mkmask,
+                                   (const int32_t*)table, pair_slot);
         }
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return (int)err;

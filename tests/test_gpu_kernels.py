@@ -103,11 +103,14 @@ def test_route_ties_break_to_lowest_index():
                                          (60000, 2 ** 21, "rand"), (300000, 262144, "hot2d"),
                                          (65536, 262144, "same"), (24577, 262144, "rand"),
                                          (300000, 2 ** 21, "same"), (300000, 2 ** 21, "skew"),
-                                         (300000, 2 ** 21, "hot3d")])
+                                         (300000, 2 ** 21, "hot3d"), (2 ** 20, 262144, "same"),
+                                         (2 ** 20 + 1, 262144, "same"), (2 ** 21 + 7, 262144, "hot2d"),
+                                         (2 ** 20 + 3, 7, "rand"), (2 ** 20 + 5, 2 ** 21, "skew")])
 def test_sort_segment_exact(n, E, pattern):
     """The sort against the oracle's counting sort: one pass (E = 7), two (4,096 and 262,144
     experts) and three (2^21) over tiles of 4,096 pairs; batches up to 16,384 pairs take the
-    single-workgroup sort.  Patterns: uniform ids, one id everywhere (one segment spanning
+    single-workgroup sort, batches above 2^20 pairs with ids of at most 18 bits the
+    expert -> slot table for pair_slot.  Patterns: uniform ids, one id everywhere (one segment spanning
     every tile), Zipf-skewed ids, half the pairs on the largest id, and ids whose two
     9-bit digits (or, with 2^21 experts, all three digits) are Zipf-skewed (hot experts
     whose segments cross tile boundaries, in the three-pass path too)."""
