@@ -540,11 +540,56 @@ __global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ in
 }
 
 // Small batches: the scatter-back split by head, so that n_tok * H waves (not n_tok) share
-// the gathers.  apply_scatter_head_kernel writes each (token, head)'s RN_T(sum_k RN_T(a v))
-// to headbuf [n_tok, H, d]; apply_head_sum_kernel adds the heads in order in T and divides
-// by H.  The same operations in the same order as apply_scatter_kernel, so the output is
-// bit-identical.
+// the gathers.  Each (token, head)'s RN_T(sum_k RN_T(a v)) is formed by one wave, then the
+// heads are added in order in T and divided by H: the same operations in the same order as
+// apply_scatter_kernel, so the output is bit-identical.  When a token's H head rows fit in
+// kTokHeadLds bytes of LDS, apply_scatter_tok_kernel does both in one launch (one
+// workgroup per token, its waves taking the heads); otherwise apply_scatter_head_kernel
+// writes the head rows to headbuf [n_tok, H, d] and apply_head_sum_kernel sums them.
 constexpr int64_t kSplitHeadMaxTok = 1024;
+constexpr int kTokWaves = 8;
+constexpr int kTokHeadLds = 64 * 1024;
+
+// The head sum of one (token, head) item, pairs pbase .. pbase + k - 1, into hacc (fp32,
+// this lane's CH chunks of N columns).
+template <typename T, int CH>
+__device__ __forceinline__ void scatter_head_sum(const T* __restrict__ vr_, const int32_t* __restrict__ pair_slot,
+                                                 const float* __restrict__ act, int64_t pbase, int k, int d,
+                                                 int lane, float (&hacc)[CH * Vec16<T>::kN]) {
+    constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
+#pragma unroll
+    for (int e = 0; e < CH * N; ++e) hacc[e] = 0.0f;
+    for (int j0 = 0; j0 < k; j0 += kScatterUnroll) {
+        Raw vr[kScatterUnroll][CH];
+        float a[kScatterUnroll];
+#pragma unroll
+        for (int q = 0; q < kScatterUnroll; ++q) {
+            if (j0 + q < k) {
+                const int s = pair_slot[pbase + j0 + q];
+                a[q] = act[pbase + j0 + q];
+                load_raw<T, CH>(vr_ + (int64_t)s * d, d, lane, vr[q]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kScatterUnroll; ++q) {
+            if (j0 + q < k) {
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    float vf[N];
+                    Vec16<T>::unpack(vr[q][c], vf);
+#pragma unroll
+                    for (int v = 0; v < N; v += 2) {
+                        float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
+                        Elem<T>::round32x2(p0, p1);  // RN_T(a v)
+                        hacc[c * N + v] += p0;
+                        hacc[c * N + v + 1] += p1;
+                    }
+                }
+            }
+        }
+    }
+}
 
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void apply_scatter_head_kernel(const T* __restrict__ vr_,
@@ -558,43 +603,59 @@ __global__ __launch_bounds__(256) void apply_scatter_head_kernel(const T* __rest
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     for (int64_t it = wave_id; it < n_items; it += n_waves) {  // item = t * H + head
         float hacc[CH * N];
-#pragma unroll
-        for (int e = 0; e < CH * N; ++e) hacc[e] = 0.0f;
-        const int64_t pbase = it * k;
-        for (int j0 = 0; j0 < k; j0 += kScatterUnroll) {
-            Raw vr[kScatterUnroll][CH];
-            float a[kScatterUnroll];
-#pragma unroll
-            for (int q = 0; q < kScatterUnroll; ++q) {
-                if (j0 + q < k) {
-                    const int s = pair_slot[pbase + j0 + q];
-                    a[q] = act[pbase + j0 + q];
-                    load_raw<T, CH>(vr_ + (int64_t)s * d, d, lane, vr[q]);
-                }
-            }
-#pragma unroll
-            for (int q = 0; q < kScatterUnroll; ++q) {
-                if (j0 + q < k) {
-#pragma unroll
-                    for (int c = 0; c < CH; ++c) {
-                        float vf[N];
-                        Vec16<T>::unpack(vr[q][c], vf);
-#pragma unroll
-                        for (int v = 0; v < N; v += 2) {
-                            float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
-                            Elem<T>::round32x2(p0, p1);  // RN_T(a v)
-                            hacc[c * N + v] += p0;
-                            hacc[c * N + v + 1] += p1;
-                        }
-                    }
-                }
-            }
-        }
+        scatter_head_sum<T, CH>(vr_, pair_slot, act, it * k, k, d, lane, hacc);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int e = c * 64 * N + lane * N;
             if (e < d) *reinterpret_cast<Raw*>(headbuf + it * d + e) = Vec16<T>::pack(hacc + c * N);  // RN_T
         }
+    }
+}
+
+// One workgroup per token (gridDim.x = n_tok): wave w forms the head rows h = w, w +
+// kTokWaves, ... into LDS (H d elements of T), then the threads add the heads in order for
+// 16-byte column groups and store the token's output row.
+template <typename T, int CH>
+__global__ __launch_bounds__(kTokWaves * 64) void apply_scatter_tok_kernel(const T* __restrict__ vr_,
+                                                                           const int32_t* __restrict__ pair_slot,
+                                                                           const float* __restrict__ act, int H,
+                                                                           int k, int d, T* __restrict__ out) {
+    constexpr int N = Vec16<T>::kN;
+    typedef typename Vec16<T>::raw Raw;
+    extern __shared__ __align__(16) unsigned char tok_lds[];
+    T* hb = reinterpret_cast<T*>(tok_lds);  // [H][d]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t t = blockIdx.x;
+    for (int h = wave; h < H; h += kTokWaves) {
+        float hacc[CH * N];
+        scatter_head_sum<T, CH>(vr_, pair_slot, act, (t * H + h) * k, k, d, lane, hacc);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int e = c * 64 * N + lane * N;
+            if (e < d) *reinterpret_cast<Raw*>(hb + h * d + e) = Vec16<T>::pack(hacc + c * N);  // RN_T
+        }
+    }
+    __syncthreads();
+    const float hdiv = (float)H;
+    for (int g = threadIdx.x; g * N < d; g += kTokWaves * 64) {
+        float o[N];
+#pragma unroll
+        for (int v = 0; v < N; ++v) o[v] = 0.0f;
+        for (int h = 0; h < H; ++h) {
+            float hv[N];
+            Vec16<T>::unpack(*reinterpret_cast<const Raw*>(hb + h * d + g * N), hv);
+#pragma unroll
+            for (int v = 0; v < N; v += 2) {
+                float o0 = o[v] + hv[v], o1 = o[v + 1] + hv[v + 1];
+                Elem<T>::round32x2(o0, o1);  // the running head sum in T
+                o[v] = o0;
+                o[v + 1] = o1;
+            }
+        }
+        float r[N];
+#pragma unroll
+        for (int v = 0; v < N; ++v) r[v] = o[v] / hdiv;
+        *reinterpret_cast<Raw*>(out + t * d + g * N) = Vec16<T>::pack(r);
     }
 }
 
@@ -650,6 +711,12 @@ template <typename T, int CH2>
 static void launch_scatter_t(const void* v, const int32_t* pair_slot, const float* act, int64_t n_tok, int H, int k,
                              int d, void* headbuf, void* out, int num_cus, hipStream_t stream) {
     const int64_t cap = (int64_t)num_cus * 16;
+    const size_t tok_lds = (size_t)H * d * sizeof(T);
+    if (CH2 <= 4 && headbuf != nullptr && tok_lds <= (size_t)kTokHeadLds) {  // (wider rows would spill)
+        hipLaunchKernelGGL((apply_scatter_tok_kernel<T, CH2>), dim3((unsigned)n_tok), dim3(kTokWaves * 64), tok_lds,
+                           stream, (const T*)v, pair_slot, act, H, k, d, (T*)out);
+        return;
+    }
     if (headbuf != nullptr) {
         const int64_t items = n_tok * H;
         int64_t g3 = (items + 3) / 4;

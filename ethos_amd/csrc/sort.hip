@@ -674,8 +674,9 @@ __global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int3
         uint32_t word[kSmallPer], rank[kSmallPer];
 #pragma unroll
         for (int j = 0; j < kSmallPer; ++j) {
+            if (j >= cpw) break;  // wave-uniform: the wave's chunks end here
             const int idx = (c0 + j) * 64 + lane;
-            const bool v = j < cpw && idx < n;
+            const bool v = idx < n;
             word[j] = v ? buf[cur][idx] : 0u;
             const uint32_t dg = (word[j] >> shift) & (kRadix - 1);
             const uint64_t peers = peer_mask(dg, __ballot(v));
@@ -716,8 +717,9 @@ __global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int3
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < kSmallPer; ++j) {
+            if (j >= cpw) break;
             const int idx = (c0 + j) * 64 + lane;
-            if (j < cpw && idx < n) buf[cur ^ 1][cnt[wave][(word[j] >> shift) & (kRadix - 1)] + rank[j]] = word[j];
+            if (idx < n) buf[cur ^ 1][cnt[wave][(word[j] >> shift) & (kRadix - 1)] + rank[j]] = word[j];
         }
         cur ^= 1;
         __syncthreads();

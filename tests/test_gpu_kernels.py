@@ -246,6 +246,36 @@ def test_apply_shapes(n_tok, d, dh, dt):
     check_out(got, ref, dt, signal=True, nerr_max=2e-3)
 
 
+@pytest.mark.parametrize("d,dh,H,dt", [(1024, 128, 8, "bf16"), (4096, 64, 2, "bf16"), (256, 64, 3, "fp32")])
+def test_scatter_paths_bit_identical(d, dh, H, dt):
+    """The scatter-back's three forms give the same bits: up to 1,024 tokens one workgroup
+    per token with the head rows in LDS (d 1024 bf16, d 256 fp32) or, for rows too wide
+    for it, the head kernel plus the head sum (d 4096); above 1,024 tokens one wave per
+    token.  The hidden and v rows are functions of the expert id, so the first 1,024
+    tokens of a 1,025-token call must give the output of a call on those 1,024 tokens."""
+    rng = np.random.default_rng(d + H)
+    k, E = 4, 3000
+    enc = (lambda a: O.f32_to_bf16_bits(a)) if dt == "bf16" else (lambda a: a.astype(np.float32))
+    x = enc(rng.standard_normal((1025, d)).astype(np.float32))
+    w2 = enc((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(d)).astype(np.float32))
+    ids = rng.integers(0, E, (1025, H, k)).astype(np.int32)
+    g = enc(rng.uniform(0, 1, (1025, H, k)).astype(np.float32))
+    h_e = enc(rng.standard_normal((E, dh)).astype(np.float32) * 0.3)
+    v_e = enc(rng.standard_normal((E, d)).astype(np.float32))
+    outs = []
+    for n in (1025, 1024):
+        seg = hip.sort_segment(to_dev(ids[:n].reshape(-1)), E)
+        U = int(seg["n_unique"].item())
+        uniq = to_host(seg["uniq"])[:U]
+        h = np.zeros((seg["max_unique"], dh), h_e.dtype)
+        v = np.zeros((seg["max_unique"], d), v_e.dtype)
+        h[:U], v[:U] = h_e[uniq], v_e[uniq]
+        out = hip.apply_scatter(to_dev(x[:n]), to_dev(w2), to_dev(h), to_dev(v), seg, to_dev(g[:n]), H, k)
+        torch.cuda.synchronize()
+        outs.append(to_host(out))
+    assert np.array_equal(outs[0][:1024], outs[1])
+
+
 def _stress_case(kind, rng, rows, K, dh2, dt):
     """Adversarial query / sub-key sets for the certified routing filter."""
     q = rng.standard_normal((rows, 2 * dh2)).astype(np.float32)
