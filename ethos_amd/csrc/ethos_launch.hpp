@@ -24,10 +24,12 @@ int launch_route(const void* q, const void* k1, const void* k2, const float* key
                  int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream);
 
 // The sort's workspace: keys and values twice (4 n words), then per (digit, tile of
-// kSortTileKeys keys) four counters, two per-digit totals, and, for batches of more than
+// kSortTileKeys keys) four counters (rows of sort_tile_pitch words: the tile count rounded
+// up to a multiple of 8), two per-digit totals, and, for batches of more than
 // kSortTableMinPairs pairs with ids of at most 18 bits (two 9-bit passes), an expert ->
 // slot table of 2^(9 passes) words.
 constexpr int kSortTileKeys = 4096;
+__host__ __device__ constexpr int sort_tile_pitch(int n_tiles) { return (n_tiles + 7) / 8 * 8; }
 constexpr int64_t kSortTableMinPairs = (int64_t)1 << 20;
 constexpr int sort_key_bits(int64_t n_experts) {
     int b = 0;
@@ -42,8 +44,8 @@ constexpr size_t sort_table_words(int64_t n, int64_t n_experts) {
     return n > kSortTableMinPairs && sort_passes(n_experts) <= 2 ? (size_t)1 << (9 * sort_passes(n_experts)) : 0;
 }
 constexpr size_t sort_workspace_words(int64_t n, int64_t n_experts) {
-    return (size_t)4 * (size_t)n + (size_t)4 * 512 * (size_t)((n + kSortTileKeys - 1) / kSortTileKeys) + 2 * 512 + 64 +
-           sort_table_words(n, n_experts);
+    return (size_t)4 * (size_t)n + (size_t)4 * 512 * (size_t)sort_tile_pitch((int)((n + kSortTileKeys - 1) / kSortTileKeys)) +
+           2 * 512 + 64 + sort_table_words(n, n_experts);
 }
 size_t sort_workspace_bytes(int64_t n, int64_t n_experts);
 int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* ws, int32_t* perm, int32_t* uniq,

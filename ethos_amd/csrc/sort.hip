@@ -67,6 +67,19 @@ constexpr int kTC = kTile / (kTW * 64);
 constexpr int kTPer = kTile / kTThreads;  // tile-local positions per thread in the segment phase
 static_assert(kTC * kTW * 64 == kTile && kTPer == 4, "tile shape");
 
+// The tile of this workgroup.  Workgroup b runs on XCD b % 8.  The per-digit statistics
+// are rows of sort_tile_pitch(n_tiles) words, one per tile, so that each aligned group of
+// 8 tiles shares 32-byte sectors; the groups are dealt to the XCDs in turn (group g to XCD
+// g % 8) and a group's 8 tiles run on its XCD, so that their statistics stores merge in
+// that XCD's L2 while runs of hot keys still spread over all XCDs.  The grid is padded to
+// 64 workgroups per 8 groups: -1 for the padding workgroups.
+__device__ __forceinline__ int tsort_tile(int n_tiles) {
+    const int x = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
+    const int t = ((j >> 3) * 8 + x) * 8 + (j & 7);
+    return t < n_tiles ? t : -1;
+}
+static unsigned tsort_grid(int n_tiles) { return 64u * (unsigned)(((n_tiles + 7) / 8 + 7) / 8); }
+
 // Exclusive scans of NV values per thread over threads 0 .. 511 (waves 0 .. 7; the other
 // threads pass zeros), in one pass.  Every thread of the workgroup calls it (it holds
 // barriers); tot[] receives the sums.  wsum: 8 NV words of LDS.  The waves' totals are read
@@ -141,9 +154,9 @@ __device__ __forceinline__ uint32_t scan1024(uint32_t v, uint32_t* wsum, uint32_
 // j's key in wave w.
 template <bool kFirst>
 __device__ __forceinline__ void tile_load(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
-                                          int64_t n, uint32_t (&key)[kTC], uint32_t (&val)[kTC]) {
+                                          int64_t n, int tile, uint32_t (&key)[kTC], uint32_t (&val)[kTC]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+    const int64_t base = (int64_t)tile * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
         const int64_t idx = base + j * 64 + lane;
@@ -152,10 +165,10 @@ __device__ __forceinline__ void tile_load(const uint32_t* __restrict__ keys, con
         val[j] = v ? (kFirst ? (uint32_t)idx : vals[idx]) : 0u;
     }
 }
-__device__ __forceinline__ void tile_rank(int64_t n, int shift, uint32_t (*wcnt)[kRadix], const uint32_t (&key)[kTC],
-                                          uint32_t (&rank)[kTC]) {
+__device__ __forceinline__ void tile_rank(int64_t n, int tile, int shift, uint32_t (*wcnt)[kRadix],
+                                          const uint32_t (&key)[kTC], uint32_t (&rank)[kTC]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+    const int64_t base = (int64_t)tile * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
         const bool v = base + j * 64 + lane < n;
@@ -191,12 +204,14 @@ __device__ __forceinline__ void zero_wcnt(uint32_t (*wcnt)[kRadix]) {
     for (int e = threadIdx.x; e < kTW * kRadix / 4; e += kTThreads) w[e] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// Per-tile digit counts of one (non-last) pass: cnt[d * n_tiles + tile].
+// Per-tile digit counts of one (non-last) pass: cnt[d * sort_tile_pitch(n_tiles) + tile].
 __global__ __launch_bounds__(kTThreads) void tsort_count(const uint32_t* __restrict__ keys, int64_t n, int shift,
                                                          int n_tiles, uint32_t* __restrict__ cnt) {
+    const int tile = tsort_tile(n_tiles);
+    if (tile < 0) return;
     __shared__ uint32_t c[kRadix];
     const int tid = threadIdx.x;
-    const int64_t base = (int64_t)blockIdx.x * kTile + tid;
+    const int64_t base = (int64_t)tile * kTile + tid;
     uint32_t k[kTPer];
 #pragma unroll
     for (int j = 0; j < kTPer; ++j) k[j] = base + j * kTThreads < n ? keys[base + j * kTThreads] : 0u;
@@ -206,7 +221,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_count(const uint32_t* __restr
     for (int j = 0; j < kTPer; ++j)
         if (base + j * kTThreads < n) atomicAdd(&c[(k[j] >> shift) & (kRadix - 1)], 1u);
     __syncthreads();
-    if (tid < kRadix) cnt[(int64_t)tid * n_tiles + blockIdx.x] = c[tid];
+    if (tid < kRadix) cnt[(int64_t)tid * sort_tile_pitch(n_tiles) + tile] = c[tid];
 }
 
 // Per-tile statistics of the last pass (keys sorted by their lower bits lo = key & lomask),
@@ -219,11 +234,13 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats_map(const uint32_t* __r
                                                              uint32_t mkmask, int n_tiles, uint32_t* __restrict__ cnt,
                                                              uint32_t* __restrict__ dist, uint32_t* __restrict__ flo,
                                                              uint32_t* __restrict__ llo) {
+    const int tile = tsort_tile(n_tiles);
+    if (tile < 0) return;
     constexpr int kMapWords = (1 << (2 * kRadixBits)) / 32;
     __shared__ uint4 seen[kMapWords / 4];
     __shared__ uint32_t c[kRadix], dc[kRadix], mn[kRadix], mx[kRadix];
     const int tid = threadIdx.x;
-    const int64_t base = (int64_t)blockIdx.x * kTile + tid;
+    const int64_t base = (int64_t)tile * kTile + tid;
     uint32_t k[kTPer];
 #pragma unroll
     for (int j = 0; j < kTPer; ++j) k[j] = base + j * kTThreads < n ? keys[base + j * kTThreads] & mkmask : 0u;
@@ -248,7 +265,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats_map(const uint32_t* __r
     }
     __syncthreads();
     if (tid < kRadix) {
-        const int64_t o = (int64_t)tid * n_tiles + blockIdx.x;
+        const int64_t o = (int64_t)tid * sort_tile_pitch(n_tiles) + tile;
         const uint32_t cc = c[tid];
         cnt[o] = cc;
         dist[o] = dc[tid];
@@ -263,23 +280,25 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats(const uint32_t* __restr
                                                          uint32_t mkmask, int n_tiles, uint32_t* __restrict__ cnt,
                                                          uint32_t* __restrict__ dist, uint32_t* __restrict__ flo,
                                                          uint32_t* __restrict__ llo) {
+    const int tile = tsort_tile(n_tiles);
+    if (tile < 0) return;
     __shared__ uint32_t wcnt[kTW][kRadix];
     __shared__ uint32_t sk[kTile];
     __shared__ uint32_t lstart[kRadix], dcnt[kRadix], wsum[8];
     const int tid = threadIdx.x, wave = tid >> 6;
     uint32_t key[kTC], val[kTC], rank[kTC];
-    tile_load<true>(keys, nullptr, n, key, val);
+    tile_load<true>(keys, nullptr, n, tile, key, val);
     zero_wcnt(wcnt);
     if (tid < kRadix) dcnt[tid] = 0;
     __syncthreads();
-    tile_rank(n, shift, wcnt, key, rank);
+    tile_rank(n, tile, shift, wcnt, key, rank);
     __syncthreads();
     const uint32_t tcv[1] = {tile_digit_counts(wcnt)};
     uint32_t ls[1], tile_n[1];
     scan512<1>(tcv, ls, tile_n, wsum);
     if (tid < kRadix) lstart[tid] = ls[0];
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+    const int64_t base = (int64_t)tile * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
         if (base + j * 64 + (tid & 63) < n) {
@@ -296,7 +315,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats(const uint32_t* __restr
     }
     __syncthreads();
     if (tid < kRadix) {
-        const int64_t o = (int64_t)tid * n_tiles + blockIdx.x;
+        const int64_t o = (int64_t)tid * sort_tile_pitch(n_tiles) + tile;
         const uint32_t lomask = (1u << shift) - 1u, tc = tcv[0];
         cnt[o] = tc;
         dist[o] = dcnt[tid];
@@ -319,10 +338,11 @@ __global__ __launch_bounds__(256) void tsort_scan(uint32_t* __restrict__ cnt, ui
     const int lane = threadIdx.x & 63;
     const int d = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (d >= kRadix) return;
-    uint32_t* crow = cnt + (int64_t)d * n_tiles;
-    uint32_t* drow = dist + (int64_t)d * n_tiles;
-    const uint32_t* frow = flo + (int64_t)d * n_tiles;
-    uint32_t* lrow = llo + (int64_t)d * n_tiles;
+    const int64_t pitch = sort_tile_pitch(n_tiles);
+    uint32_t* crow = cnt + (int64_t)d * pitch;
+    uint32_t* drow = dist + (int64_t)d * pitch;
+    const uint32_t* frow = flo + (int64_t)d * pitch;
+    uint32_t* lrow = llo + (int64_t)d * pitch;
     uint32_t carry_c = 0, carry_s = 0, carry_l = 0;
     constexpr int kPer = 8;
     for (int t0 = 0; t0 < n_tiles; t0 += 64 * kPer) {
@@ -407,14 +427,16 @@ __global__ __launch_bounds__(kTThreads) void tsort_down(const uint32_t* __restri
     __shared__ __align__(16) uint32_t sk[kTile];
     __shared__ __align__(16) uint32_t sv[kTile];
     __shared__ uint32_t gbase[kRadix], lstart[kRadix], wsum[2 * 8];
+    const int tile = tsort_tile(n_tiles);
+    if (tile < 0) return;
     const int tid = threadIdx.x, wave = tid >> 6;
-    const uint32_t my_pre = tid < kRadix ? pre[(int64_t)tid * n_tiles + blockIdx.x] : 0u;
+    const uint32_t my_pre = tid < kRadix ? pre[(int64_t)tid * sort_tile_pitch(n_tiles) + tile] : 0u;
     uint32_t tv[2] = {tid < kRadix ? tot[tid] : 0u, 0u};
     uint32_t key[kTC], val[kTC], rank[kTC];
-    tile_load<kFirst>(keys_in, vals_in, n, key, val);
+    tile_load<kFirst>(keys_in, vals_in, n, tile, key, val);
     zero_wcnt(wcnt);
     __syncthreads();
-    tile_rank(n, shift, wcnt, key, rank);
+    tile_rank(n, tile, shift, wcnt, key, rank);
     __syncthreads();
     tv[1] = tile_digit_counts(wcnt);
     uint32_t ex[2], sums[2];
@@ -427,7 +449,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_down(const uint32_t* __restri
     __syncthreads();
     // the tile ranked by digit into LDS, then written with consecutive positions of a
     // digit's group on consecutive lanes
-    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+    const int64_t base = (int64_t)tile * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
         if (base + j * 64 + (tid & 63) < n) {
@@ -475,16 +497,18 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
     __shared__ __align__(16) uint32_t sv[kTile];
     __shared__ uint32_t gbase[kRadix], sbase[kRadix], lst[kRadix], lstart[kRadix], hstart[kRadix];
     __shared__ uint32_t wsum[3 * 8];
+    const int tile = tsort_tile(n_tiles);
+    if (tile < 0) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int64_t o = (int64_t)tid * n_tiles + blockIdx.x;
+    const int64_t o = (int64_t)tid * sort_tile_pitch(n_tiles) + tile;
     const bool dl = tid < kRadix;
     const uint32_t my_pre = dl ? pre[o] : 0u, my_spre = dl ? spre[o] : 0u, my_plast = dl ? plast[o] : 0u;
     uint32_t tv[3] = {dl ? tot[tid] : 0u, dl ? stot[tid] : 0u, 0u};
     uint32_t key[kTC], val[kTC], rank[kTC];
-    tile_load<kFirst>(keys_in, vals_in, n, key, val);
+    tile_load<kFirst>(keys_in, vals_in, n, tile, key, val);
     zero_wcnt(wcnt);
     __syncthreads();
-    tile_rank(n, shift, wcnt, key, rank);
+    tile_rank(n, tile, shift, wcnt, key, rank);
     __syncthreads();
     tv[2] = tile_digit_counts(wcnt);
     uint32_t ex[3], sums[3];
@@ -497,7 +521,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
         lstart[tid] = ex[2];
     }
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kTile + wave * (kTC * 64);
+    const int64_t base = (int64_t)tile * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
         if (base + j * 64 + lane < n) {
@@ -580,7 +604,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
             seg_off[slot] = (int32_t)pos;
         }
     }
-    if (blockIdx.x == 0 && tid == 0) {
+    if (tile == 0 && tid == 0) {
         // unsigned comparison: the count is at most n, and the clamp keeps u in [0, max_unique]
         const int32_t u = u_all < (uint32_t)max_unique ? (int32_t)u_all : max_unique;
         *n_unique = u;
@@ -808,18 +832,19 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
     uint32_t* w = reinterpret_cast<uint32_t*>(ws);
     uint32_t* kbuf[2] = {w, w + n};
     uint32_t* vbuf[2] = {w + 2 * n, w + 3 * n};
+    const size_t pitch = (size_t)sort_tile_pitch(n_tiles);
     uint32_t* cnt = w + 4 * n;
-    uint32_t* dist = cnt + (size_t)kRadix * n_tiles;
-    uint32_t* flo = dist + (size_t)kRadix * n_tiles;
-    uint32_t* llo = flo + (size_t)kRadix * n_tiles;
-    uint32_t* tot = llo + (size_t)kRadix * n_tiles;
+    uint32_t* dist = cnt + (size_t)kRadix * pitch;
+    uint32_t* flo = dist + (size_t)kRadix * pitch;
+    uint32_t* llo = flo + (size_t)kRadix * pitch;
+    uint32_t* tot = llo + (size_t)kRadix * pitch;
     uint32_t* stot = tot + kRadix;
     // the expert -> slot table (large batches, ids of at most 18 bits), after the totals and
     // their padding
     int32_t* table = sort_table_words(n, n_experts) ? reinterpret_cast<int32_t*>(stot + kRadix + 64) : nullptr;
     // keys compare on the bits the passes sort (those of ids below n_experts)
     const uint32_t mkmask = kRadixBits * passes >= 32 ? 0xffffffffu : (1u << (kRadixBits * passes)) - 1u;
-    const dim3 tg((unsigned)n_tiles), tb(kTThreads), sg((unsigned)(kRadix / 4)), sb(256);
+    const dim3 tg(tsort_grid(n_tiles)), tb(kTThreads), sg((unsigned)(kRadix / 4)), sb(256);
     for (int p = 0; p < passes; ++p) {
         const uint32_t* kin = p == 0 ? reinterpret_cast<const uint32_t*>(ids) : kbuf[(p - 1) & 1];
         const uint32_t* vin = p == 0 ? nullptr : vbuf[(p - 1) & 1];
