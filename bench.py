@@ -614,6 +614,32 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+def captured_latency(m, x_flat, steps: int) -> dict:
+    """The same forward replayed from a HIP graph (ethos_amd.graphs.CapturedLayer: one input
+    copy and one graph launch per step, the token projection on a second stream inside the
+    graph): p50 of `steps` back-to-back steps, each bracketed by events, and whether the
+    replay's output equals the eager forward's."""
+    from ethos_amd.graphs import CapturedLayer
+
+    cap = CapturedLayer(m, x_flat.shape[0])
+    with torch.no_grad():
+        same = bool(torch.equal(cap(x_flat), m.forward_flat(x_flat)))
+        for _ in range(10):
+            cap(x_flat)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record()
+        for i in range(steps):
+            cap(x_flat)
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+    t = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    p50 = t[len(t) // 2]
+    return {"p50_ms": round(p50, 4), "value": round(x_flat.shape[0] / (p50 * 1e-3), 1),
+            "unit": "tokens/s (at the p50 latency)", "steps": steps, "equals_eager": same,
+            "note": "one input copy and one graph launch per step; token projection on a second stream"}
+
+
 def decode_latency(args, with_cpu: bool) -> dict:
     """The decode-like layer (64 tokens, the same 262,144-expert layer, bf16): p50 latency
     of the 40 of 50 forwards after warmup that carry no stage events (every 5th does), and
@@ -637,11 +663,13 @@ def decode_latency(args, with_cpu: bool) -> dict:
     p50 = st.pop("_p50")
     st.pop("_kernels")
     st.pop("_instrumented")
+    graph = captured_latency(m, x_flat, steps)
     out = {"workload": "ETHOS expert-layer forward, 64 tokens x d_model 1024, 262144 experts, 8 routing heads, "
                        "top-16, d_query 256, bf16",
            "p50_ms": round(p50, 4), "mean_ms": round(ms, 4), "steps": steps,
            "value": round(sh.n_tok / (p50 * 1e-3), 1), "unit": "tokens/s (at the p50 latency)",
-           "stage_us": {k: round(v * 1e3, 2) for k, v in st.items()}}
+           "stage_us": {k: round(v * 1e3, 2) for k, v in st.items()},
+           "graph": graph}
     if with_cpu:
         log("[bench] CPU baseline on the 64-token layer")
         out["cpu_baseline"] = cpu_baseline(sh, x_cpu, sd_cpu, sh.n_tok)

@@ -222,9 +222,10 @@ def apply_hidden(x: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, seg: dict, 
     return out
 
 
-def token_proj(x: torch.Tensor, w2: torch.Tensor, wut: torch.Tensor | None = None) -> torch.Tensor:
+def token_proj(x: torch.Tensor, w2: torch.Tensor, wut: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
     """x_proj [n, d_hidden] = RN(x W_u), W_u = w2[:d] ([d, d_hidden]); bf16 needs wut = W_u^T
-    ([d_hidden, d]) for d % 64 == 0."""
+    ([d_hidden, d]) for d % 64 == 0.  `out`: optional [n, d_hidden] destination."""
     _need(x, "x", dim=2)
     _need(w2, "w2", x.dtype, 2)
     n, d = x.shape
@@ -235,7 +236,11 @@ def token_proj(x: torch.Tensor, w2: torch.Tensor, wut: torch.Tensor | None = Non
         _need(wut, "wut", x.dtype, 2)
         if wut.shape != (dh, d):
             raise RuntimeError("token_proj: wut must be [d_hidden, d_model]")
-    xp = torch.empty((n, dh), dtype=x.dtype, device=x.device)
+    if out is not None:
+        _need(out, "out", x.dtype, 2)
+        if out.shape != (n, dh):
+            raise RuntimeError("token_proj: out must be [n_tok, d_hidden]")
+    xp = torch.empty((n, dh), dtype=x.dtype, device=x.device) if out is None else out
     rc = load().ethos_token_proj(x.data_ptr(), w2.data_ptr(), wut.data_ptr() if wut is not None else None, n, d, dh,
                                  dtype_code(x.dtype), xp.data_ptr(), _stream())
     check(rc, "ethos_token_proj")

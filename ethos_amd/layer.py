@@ -324,12 +324,13 @@ class EthosExpertLayer(nn.Module):
             self._gen_key = key
         return self._gen
 
-    def _expert_stages(self, x_flat: torch.Tensor, gates: torch.Tensor, seg: dict):
+    def _expert_stages(self, x_flat: torch.Tensor, gates: torch.Tensor, seg: dict, xp: torch.Tensor | None = None):
         """(out, h): generation over the unique experts, activations and scatter-back in the
-        layer's execution order, as one library call."""
+        layer's execution order, as one library call (`xp`: the token projection, if already
+        formed)."""
         latents, w1, w2, wut = self._generator_params(x_flat.dtype, x_flat.device)
         return hip.expert_forward(x_flat, latents, w1, w2, seg, gates, self.num_heads, self.top_k,
-                                  hidden_space=self.hidden_space, wut=wut)
+                                  hidden_space=self.hidden_space, wut=wut, xp=xp)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.dim() != 3 or x.shape[-1] != self.d_model:
@@ -340,11 +341,14 @@ class EthosExpertLayer(nn.Module):
             return torch.zeros_like(x)
         return self.forward_flat(x_flat).view(b, s, d)
 
-    def forward_flat(self, x_flat: torch.Tensor, mark=None) -> torch.Tensor:
+    def forward_flat(self, x_flat: torch.Tensor, mark=None, side_stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         """The layer on [n_tok, d_model] rows (model.py:288-343).  `mark(stage)`, if given, is
         called after the query projection, the routing and the sort are enqueued on the
         current stream (the expert stages are one library call; hip.stage_events times the
-        stages inside it)."""
+        stages inside it).  `side_stream`: the token projection x W_u, which needs only x, runs
+        there while the routing and the sort run on the current stream, which waits for it
+        before the expert stages (worth its host cost under graph capture; see
+        ethos_amd.graphs)."""
         if _wants_grad(x_flat, self):
             with torch.no_grad():
                 gates, ids = self.router.route(x_flat)
@@ -353,11 +357,23 @@ class EthosExpertLayer(nn.Module):
             return _ExpertStages.apply(x_flat, g, self.expert_latents.weight, self.generation_network.net[0].weight,
                                        self.generation_network.net[2].weight, self, gates, seg)
         with torch.no_grad():
+            xp = None
+            if side_stream is not None:
+                cur = torch.cuda.current_stream(x_flat.device)
+                _, _, w2, wut = self._generator_params(x_flat.dtype, x_flat.device)
+                # allocated on the current stream, written on the side stream, which the
+                # current stream waits for before any use
+                xp = torch.empty((x_flat.shape[0], self.d_hidden), dtype=x_flat.dtype, device=x_flat.device)
+                side_stream.wait_stream(cur)
+                with torch.cuda.stream(side_stream):
+                    hip.token_proj(x_flat, w2, wut, out=xp)
             gates, ids = self.router.route(x_flat, mark)
             seg = hip.sort_segment(ids.view(-1), self.num_experts)
             if mark is not None:
                 mark("sort_segment")
-            out, _ = self._expert_stages(x_flat, gates, seg)
+            if xp is not None:
+                cur.wait_stream(side_stream)
+            out, _ = self._expert_stages(x_flat, gates, seg, xp=xp)
         return out
 
 
