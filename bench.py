@@ -183,7 +183,8 @@ def load_traffic(config: str, stage: str):
 # Kernels behind the counter figures, named as rocprofv3 names them in the summaries.
 SCATTER_KERNELS = ["void ethos::apply_scatter_kernel<u16, 2>"]
 SORT_KERNELS = ["ethos::tsort_count", "void ethos::tsort_scan<false>", "void ethos::tsort_down<true>",
-                "ethos::tsort_stats_map", "void ethos::tsort_scan<true>", "void ethos::tsort_down_last<false>"]
+                "ethos::tsort_stats_map", "void ethos::tsort_scan<true>", "void ethos::tsort_down_last<false>",
+                "ethos::tsort_pair_slot"]
 GEMM_KERNELS = {"v_rows": "void ethos::expand_ws_bf16_kernel<512>",
                 "hidden_rows_alone": "void ethos::hidden_ws_bf16_kernel<128, 512, false>",
                 "hidden_rows_with_activations": "void ethos::hidden_ws_bf16_kernel<128, 512, true>"}
