@@ -107,12 +107,20 @@ struct QRowMeta {
     float amax;       // upper bound of max |v_i|
 };
 
+// Small batches (at most kQiSplitMaxTok tokens, whose 64 x 64 output tiles would leave most
+// CUs idle) split the reduction into kQiSplit ranges of chunks, one workgroup each; each
+// writes its exact partial digit-product sums P (int64) and a second kernel adds the
+// kQiSplit partials of every element (integers: exact, in any order) and certifies them.
+constexpr int kQiSplit = 8;
+constexpr int64_t kQiSplitMaxTok = 128;
+
 struct QprojWs {
     int32_t* count;   // [1]   uncertain elements
     int32_t* list;    // [n_tok * ncols]
     int8_t* xdig;     // [3][n_tok][dpad]
     int8_t* wdig;     // [3][ncols][dpad]
     QRowMeta* meta;   // [n_tok + ncols]: x rows, then Wq rows
+    int64_t* part;    // [kQiSplit][n_tok][ncols] partial sums (n_tok <= kQiSplitMaxTok only)
 };
 
 __host__ __device__ inline int qproj_dpad(int d) { return (d + kQiKC - 1) / kQiKC * kQiKC; }
@@ -121,8 +129,9 @@ __host__ __device__ inline size_t qproj_align(size_t b) { return (b + 255) & ~(s
 
 __host__ __device__ inline size_t qproj_ws_bytes(int64_t n_tok, int ncols, int d) {
     const size_t rows = (size_t)n_tok + (size_t)ncols;
+    const size_t part = n_tok <= kQiSplitMaxTok ? (size_t)kQiSplit * (size_t)n_tok * (size_t)ncols * 8 : 0;
     return 256 + qproj_align(4 * (size_t)n_tok * ncols) + qproj_align(3 * rows * (size_t)qproj_dpad(d)) +
-           qproj_align(sizeof(QRowMeta) * rows);
+           qproj_align(sizeof(QRowMeta) * rows) + qproj_align(part);
 }
 
 __host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols, int d) {
@@ -137,6 +146,8 @@ __host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols, 
     w.wdig = w.xdig + 3 * (size_t)n_tok * dpad;
     p += qproj_align(3 * ((size_t)n_tok + ncols) * dpad);
     w.meta = reinterpret_cast<QRowMeta*>(p);
+    p += qproj_align(sizeof(QRowMeta) * ((size_t)n_tok + ncols));
+    w.part = n_tok <= kQiSplitMaxTok ? reinterpret_cast<int64_t*>(p) : nullptr;
     return w;
 }
 
@@ -234,6 +245,77 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
 
 typedef int32_t i32x16_t __attribute__((ext_vector_type(16)));
 
+// An x row's format as the certification reads it: {max|x| 2^-E, |x|_1 2^-E, n_inex 2^-21}
+// and {E, n_inex}.
+__device__ __forceinline__ float4 qp_xf(const QRowMeta& m) {
+    return make_float4(ldexpf(m.amax, -m.e), ldexpf(m.l1, -m.e), (float)m.n_inex * 0x1p-21f, 0.0f);
+}
+__device__ __forceinline__ int2 qp_xi(const QRowMeta& m) { return make_int2(m.e, m.n_inex); }
+
+// An output column's format, bias and BatchNorm coefficients.
+struct QColFmt {
+    int ew, nw;        // E_w, n_inex of the Wq row (-1: inf / NaN)
+    float aw, lw, mw;  // max|w| 2^-E_w, |w|_1 2^-E_w, n_inex 2^-21
+    double b;
+    float al, be;
+};
+__device__ __forceinline__ QColFmt qp_col(const QRowMeta& m, uint16_t bias, float alpha, float beta) {
+    QColFmt f;
+    f.ew = m.e;
+    f.nw = m.n_inex;
+    f.aw = ldexpf(m.amax, -m.e);
+    f.lw = ldexpf(m.l1, -m.e);
+    f.mw = (float)m.n_inex * 0x1p-21f;
+    f.b = (double)bf16_bits_to_f32(bias);
+    f.al = alpha;
+    f.be = beta;
+    return f;
+}
+
+// Certify one element from Pd, its digit-product sum P = sum_k 2^(7 (4 - k)) C_k as fp64
+// (exact below 2^53, else rounded at most four times), and write its output bits to *out;
+// false when the element must take the exact chain.  The error bounds are evaluated in fp32
+// scaled by 2^-(E_x + E_w), where every term is O(1) (max|v| 2^-E lies in [1/2, 1), |v|_1
+// 2^-E in [1/2, d]); the 1% slack covers their fp32 rounding.  P's partial sums (scaled to
+// units of P) are integers of magnitude at most B = sum_i (|F_i| + 2^15)(|G_i| + 2^15) <=
+// 2^42 H', where in units of 2^(E_x + E_w) H' = A' + 2^-6 (|x|_1 + |w|_1) + d 2^-12 and A'
+// bounds sum |x_i w_i|.  Below 2^53 (H' < 2^11) P's fp64 form is exact; otherwise its
+// roundings add at most 2^-51 H' to the error.
+__device__ __forceinline__ bool qp_certify(double Pd, float4 xf, int2 xi, const QColFmt& cf, int d, uint16_t* out) {
+    const float dscale = (float)d * 0x1p-52f;  // chain rounding: d 2^-52 A'
+    const float dterm = (float)d * 0x1p-12f;
+    const double V = ldexp(Pd, xi.x + cf.ew - 42);
+    const float As = fminf(xf.x * cf.lw, cf.aw * xf.y);
+    const float Hs = As + 0x1p-6f * (xf.y + cf.lw) + dterm;
+    // Both rows exact in the digit format and H' < 2^11 (with margin for the rounding of
+    // H'): V is exact, and so is every partial sum of the chain (an integer multiple of
+    // 2^(E_x + E_w - 42) below 2^53 of them), so the chain never rounds and equals V (+0 for
+    // a zero sum, as the chain from +0 gives); otherwise the certified interval.
+    const bool exact = (xi.y | cf.nw) == 0 && Hs < 2047.0f;
+    const float Es =
+        1.01f * (__builtin_fmaf(dscale, As, __builtin_fmaf(xf.z, cf.aw, cf.mw * xf.x)) + 0x1p-51f * Hs);
+    const double E = exact ? 0.0 : ldexp((double)Es, xi.x + cf.ew) + 0x1p-50 * (fabs(V) + fabs(cf.b)) + 0x1p-1074;
+    const double sv = V + cf.b;
+    const uint16_t lo = Elem<uint16_t>::from_f64(sv - E);
+    const uint16_t hi = exact ? lo : Elem<uint16_t>::from_f64(sv + E);
+    if (!(xi.y >= 0 && cf.nw >= 0 && lo == hi)) return false;
+    *out = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32(lo), cf.al, cf.be));
+    return true;
+}
+
+// Queue the lanes' uncertain elements e (queue true) on the exact-chain list.
+__device__ __forceinline__ void qp_queue(bool queue, int e, int lane, int32_t* __restrict__ count,
+                                         int32_t* __restrict__ list) {
+    const uint64_t bal = __ballot(queue);
+    if (bal) {
+        const int leader = __builtin_ctzll(bal);
+        int base = 0;
+        if (lane == leader) base = atomicAdd(count, (int)__popcll(bal));
+        base = __shfl(base, leader, 64);
+        if (queue) list[base + (int)__popcll(bal & ((1ull << lane) - 1ull))] = e;
+    }
+}
+
 // Tile configuration: kWaves waves in kWaves / 2 rows x 2 columns, each wave 32 rows x
 // 32 kCB columns; kStages chunk buffers in LDS (kStages - 1 chunks in flight).
 template <int Waves, int CB, int Stages>
@@ -285,7 +367,7 @@ __device__ __forceinline__ bool qi_tile_t(int n_tok, int ncols, int* t0, int* c0
     return true;
 }
 
-template <int kWaves, int kCB, int kStages>
+template <int kWaves, int kCB, int kStages, bool kSplit>
 __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __restrict__ xdig,
                                                                  const int8_t* __restrict__ wdig,
                                                                  const QRowMeta* __restrict__ xmeta,
@@ -295,7 +377,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
                                                                  const float* __restrict__ beta, int n_tok, int d,
                                                                  int ncols, int32_t* __restrict__ count,
                                                                  int32_t* __restrict__ list,
-                                                                 uint16_t* __restrict__ q) {
+                                                                 uint16_t* __restrict__ q, int64_t* __restrict__ part) {
     using C = QiCfg<kWaves, kCB, kStages>;
     constexpr int kQiRows = C::kRows, kQiCols = C::kCols;
     auto qi_tile = [](int n, int nc, int* t, int* c) { return qi_tile_t<kQiRows, kQiCols>(n, nc, t, c); };
@@ -310,6 +392,15 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     int t0, c0;
     if (!qi_tile(n_tok, ncols, &t0, &c0)) return;
     const int dpad = qproj_dpad(d);
+    // the chunks this workgroup reduces: all of them, or (kSplit) range blockIdx.y of
+    // gridDim.y ranges (possibly empty: its partial sums are then zero)
+    const int nch = dpad / kQiKC;
+    int k_lo = 0, k_hi = nch;
+    if constexpr (kSplit) {
+        const int cps = (nch + (int)gridDim.y - 1) / (int)gridDim.y;
+        k_lo = min(nch, (int)blockIdx.y * cps);
+        k_hi = min(nch, k_lo + cps);
+    }
     const int64_t xplane = (int64_t)n_tok * dpad, wplane = (int64_t)ncols * dpad;
 
     // Copies: wave w moves 16-row block w of every x plane and blocks w, w + kWaves, ... of
@@ -349,11 +440,11 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     static_assert(kStages >= 2 && kStages <= 4, "waits cover at most two chunks in flight past the current one");
 
     // the first chunk's copies go out before the metadata loads, so that one wait covers both
-    issue(0, 0);
-    if (tid < kQiRows && t0 + tid < n_tok) {
+    if (k_lo < k_hi) issue(k_lo * kQiKC, 0);
+    if (!kSplit && tid < kQiRows && t0 + tid < n_tok) {
         const QRowMeta m = xmeta[t0 + tid];
-        xpf[tid] = make_float4(ldexpf(m.amax, -m.e), ldexpf(m.l1, -m.e), (float)m.n_inex * 0x1p-21f, 0.0f);
-        xpi[tid] = make_int2(m.e, m.n_inex);
+        xpf[tid] = qp_xf(m);
+        xpi[tid] = qp_xi(m);
     }
     // the lane's output columns' formats, bias and BatchNorm coefficients, for the epilogue
     // (loaded now so that the epilogue does not wait for them)
@@ -363,7 +454,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
 #pragma unroll
     for (int cb = 0; cb < kCB; ++cb) {
         const int c = c0 + wc * 32 * kCB + cb * 32 + l32;
-        const bool ok = c < ncols;
+        const bool ok = !kSplit && c < ncols;
         cmeta[cb] = ok ? wmeta[c] : QRowMeta{0, -1, 0.0f, 0.0f};
         cbias[cb] = ok ? bias[c] : (uint16_t)0;
         calpha[cb] = ok ? alpha[c] : 0.0f;
@@ -380,15 +471,14 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
             for (int i = 0; i < 16; ++i) acc[cb][k][i] = 0;
 
     const int arow = wr * 32 + l32;
-    const int nch = dpad / kQiKC;
 #pragma unroll
     for (int j = 1; j < kStages - 1; ++j)
-        if (j < nch) issue(j * kQiKC, j);
-    for (int kc = 0; kc < nch; ++kc) {
-        const int stage = kc % kStages;
+        if (k_lo + j < k_hi) issue((k_lo + j) * kQiKC, j);
+    for (int kc = k_lo; kc < k_hi; ++kc) {
+        const int stage = (kc - k_lo) % kStages;
         // this wave's copies of chunk kc have landed once at most those of the chunks after
         // it that are already issued (up to kStages - 2 of them, kCopies each) are pending
-        const int ahead = min(kStages - 2, nch - 1 - kc);
+        const int ahead = min(kStages - 2, k_hi - 1 - kc);
         if (kStages == 2 || ahead == 0)
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         else if (ahead == 1)
@@ -397,7 +487,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * C::kCopies));
         __syncthreads();  // every wave's copies of chunk kc landed; chunk kc - 1 fully read
         const int kn = kc + kStages - 1;
-        if (kn < nch) issue(kn * kQiKC, kn % kStages);  // into chunk kc - 1's buffer
+        if (kn < k_hi) issue(kn * kQiKC, (kn - k_lo) % kStages);  // into chunk kc - 1's buffer
 #pragma unroll
         for (int s = 0; s < kQiKC; s += 32) {
             const int piece = s / 16 + h;
@@ -423,30 +513,31 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
         }
     }
 
-    // Certify each element; store it or queue it for the exact chain.  The error bounds are
-    // evaluated in fp32 scaled by 2^-(E_x + E_w), where every term is O(1) (max|v| 2^-E lies
-    // in [1/2, 1), |v|_1 2^-E in [1/2, d]); the 1% slack covers their fp32 rounding.
+    if constexpr (kSplit) {
+        // this range's exact partial sums P = sum_k 2^(7 (4 - k)) C_k (|P| < 2^61), one
+        // int64 per live element
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) {
+            const int c = c0 + wc * 32 * kCB + cb * 32 + l32;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int t = t0 + wr * 32 + mfma32_row(i, lane);
+                if (c < ncols && t < n_tok) {
+                    int64_t P = acc[cb][0][i];
+#pragma unroll
+                    for (int k = 1; k < 5; ++k) P = P * 128 + acc[cb][k][i];
+                    part[((int64_t)blockIdx.y * n_tok + t) * ncols + c] = P;
+                }
+            }
+        }
+        return;
+    }
+    // Certify each element; store it or queue it for the exact chain.
 #pragma unroll
   for (int cb = 0; cb < kCB; ++cb) {
     const int c = c0 + wc * 32 * kCB + cb * 32 + l32;
     const bool col_ok = c < ncols;
-    int ew = 0, nw = -1;
-    float aw = 0.0f, lw = 0.0f, mw = 0.0f;
-    double b = 0.0;
-    float al = 0.0f, be = 0.0f;
-    if (col_ok) {
-        const QRowMeta m = cmeta[cb];
-        ew = m.e;
-        nw = m.n_inex;
-        aw = ldexpf(m.amax, -m.e);
-        lw = ldexpf(m.l1, -m.e);
-        mw = (float)m.n_inex * 0x1p-21f;
-        b = (double)bf16_bits_to_f32(cbias[cb]);
-        al = calpha[cb];
-        be = cbeta[cb];
-    }
-    const float dscale = (float)d * 0x1p-52f;  // chain rounding: d 2^-52 A'
-    const float dterm = (float)d * 0x1p-12f;
+    const QColFmt cf = qp_col(cmeta[cb], cbias[cb], calpha[cb], cbeta[cb]);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int tl = wr * 32 + mfma32_row(i, lane);
@@ -454,48 +545,47 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
         const bool live = col_ok && t < n_tok;
         bool sure = false;
         if (live) {
-            const float4 xf = xpf[tl];
-            const int2 xi = xpi[tl];
-            // P = sum_k 2^(7 (4 - k)) C_k by an fp64 Horner chain on the int32 sums.  Its
-            // partial sums (scaled to units of P) are integers of magnitude at most
-            // B = sum_i (|F_i| + 2^15)(|G_i| + 2^15) <= 2^42 H', where in units of
-            // 2^(E_x + E_w) H' = A' + 2^-6 (|x|_1 + |w|_1) + d 2^-12 and A' bounds
-            // sum |x_i w_i|.  Below 2^53 (H' < 2^11) the chain is exact; otherwise its four
-            // roundings add at most 2^-51 H' to the error.
+            // P by an fp64 Horner chain on the int32 sums (exact below 2^53, else four roundings)
             double Pd = (double)acc[cb][0][i];
             Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][1][i]);
             Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][2][i]);
             Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][3][i]);
             Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][4][i]);
-            const double V = ldexp(Pd, xi.x + ew - 42);
-            const float As = fminf(xf.x * lw, aw * xf.y);
-            const float Hs = As + 0x1p-6f * (xf.y + lw) + dterm;
-            // Both rows exact in the digit format and H' < 2^11 (with margin for the rounding
-            // of H'): V is exact, and so is every partial sum of the chain (an integer multiple
-            // of 2^(E_x + E_w - 42) below 2^53 of them), so the chain never rounds and equals V
-            // (+0 for a zero sum, as the chain from +0 gives); otherwise the certified interval.
-            const bool exact = (xi.y | nw) == 0 && Hs < 2047.0f;
-            const float Es =
-                1.01f * (__builtin_fmaf(dscale, As, __builtin_fmaf(xf.z, aw, mw * xf.x)) + 0x1p-51f * Hs);
-            const double E =
-                exact ? 0.0 : ldexp((double)Es, xi.x + ew) + 0x1p-50 * (fabs(V) + fabs(b)) + 0x1p-1074;
-            const double sv = V + b;
-            const uint16_t lo = Elem<uint16_t>::from_f64(sv - E);
-            const uint16_t hi = exact ? lo : Elem<uint16_t>::from_f64(sv + E);
-            sure = xi.y >= 0 && nw >= 0 && lo == hi;
-            if (sure) q[(int64_t)t * ncols + c] = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32(lo), al, be));
+            uint16_t o;
+            sure = qp_certify(Pd, xpf[tl], xpi[tl], cf, d, &o);
+            if (sure) q[(int64_t)t * ncols + c] = o;
         }
-        const bool queue = live && !sure;
-        const uint64_t bal = __ballot(queue);
-        if (bal) {
-            const int leader = __builtin_ctzll(bal);
-            int base = 0;
-            if (lane == leader) base = atomicAdd(count, (int)__popcll(bal));
-            base = __shfl(base, leader, 64);
-            if (queue) list[base + (int)__popcll(bal & ((1ull << lane) - 1ull))] = t * ncols + c;
-        }
+        qp_queue(live && !sure, t * ncols + c, lane, count, list);
     }
   }
+}
+
+// Split reductions: element e = t ncols + c (one thread each) adds the kQiSplit partial sums
+// of the ranges (int64, exact), converts once to fp64 (exact below 2^53) and is certified
+// as in the product kernel.
+__global__ __launch_bounds__(256) void qproj_split_finish_kernel(const int64_t* __restrict__ part,
+                                                                 const QRowMeta* __restrict__ xmeta,
+                                                                 const QRowMeta* __restrict__ wmeta,
+                                                                 const uint16_t* __restrict__ bias,
+                                                                 const float* __restrict__ alpha,
+                                                                 const float* __restrict__ beta, int n_tok, int d,
+                                                                 int ncols, int n_split, int32_t* __restrict__ count,
+                                                                 int32_t* __restrict__ list, uint16_t* __restrict__ q) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t n_el = (int64_t)n_tok * ncols;
+    const bool live = e < n_el;
+    bool sure = false;
+    if (live) {
+        const int t = (int)(e / ncols), c = (int)(e - (int64_t)t * ncols);
+        int64_t P = 0;
+        for (int s = 0; s < n_split; ++s) P += part[(int64_t)s * n_el + e];
+        const QRowMeta xm = xmeta[t];
+        const QColFmt cf = qp_col(wmeta[c], bias[c], alpha[c], beta[c]);
+        uint16_t o;
+        sure = qp_certify((double)P, qp_xf(xm), qp_xi(xm), cf, d, &o);
+        if (sure) q[e] = o;
+    }
+    qp_queue(live && !sure, (int)e, threadIdx.x & 63, count, list);
 }
 
 // Exact fp64 chain for the queued elements (index order, as the contract defines).  A
@@ -634,10 +724,22 @@ int launch_qproj(const void* x, const void* w, const void* prepared, const void*
                            W.meta + n_tok, W.count);
         using C = QiLaunch;
         const int64_t tiles = (int64_t)((ncols + C::kCols - 1) / C::kCols) * ((n_tok + C::kRows - 1) / C::kRows);
-        const dim3 grid((unsigned)(8 * ((tiles + 7) / 8)));  // qi_tile_t: XCD-grouped tile order
-        hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages>), grid, dim3(C::kWaves * 64), C::kSmem,
-                           stream, W.xdig, wdig, W.meta, wmeta, (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols,
-                           W.count, W.list, (uint16_t*)q);
+        const unsigned tgrid = (unsigned)(8 * ((tiles + 7) / 8));  // qi_tile_t: XCD-grouped tile order
+        if (W.part != nullptr) {
+            hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, true>), dim3(tgrid, kQiSplit),
+                               dim3(C::kWaves * 64), C::kSmem, stream, W.xdig, wdig, W.meta, wmeta,
+                               (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q,
+                               W.part);
+            const int64_t n_el = n_tok * (int64_t)ncols;
+            hipLaunchKernelGGL(qproj_split_finish_kernel, dim3((unsigned)((n_el + 255) / 256)), dim3(256), 0, stream,
+                               (const int64_t*)W.part, (const QRowMeta*)W.meta, wmeta, (const uint16_t*)b, alpha, beta,
+                               (int)n_tok, d, ncols, kQiSplit, W.count, W.list, (uint16_t*)q);
+        } else {
+            hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, false>), dim3(tgrid),
+                               dim3(C::kWaves * 64), C::kSmem, stream, W.xdig, wdig, W.meta, wmeta,
+                               (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q,
+                               (int64_t*)nullptr);
+        }
         hipLaunchKernelGGL(qproj_fixup_kernel, dim3((unsigned)num_cus * 4), dim3(256), 0, stream, (const uint16_t*)x,
                            (const uint16_t*)w, (const uint16_t*)b, alpha, beta, d, ncols, W.count, W.list,
                            (uint16_t*)q);
