@@ -617,9 +617,8 @@ def main():
 
 def captured_latency(m, x_flat, steps: int) -> dict:
     """The same forward replayed from a HIP graph (ethos_amd.graphs.CapturedLayer: one input
-    copy and one graph launch per step, the token projection on a second stream inside the
-    graph): p50 of `steps` back-to-back steps, each bracketed by events, and whether the
-    replay's output equals the eager forward's."""
+    copy and one graph launch per step): p50 of `steps` back-to-back steps, each bracketed by
+    events, and whether the replay's output equals the eager forward's."""
     from ethos_amd.graphs import CapturedLayer
 
     cap = CapturedLayer(m, x_flat.shape[0])
@@ -638,7 +637,7 @@ def captured_latency(m, x_flat, steps: int) -> dict:
     p50 = t[len(t) // 2]
     return {"p50_ms": round(p50, 4), "value": round(x_flat.shape[0] / (p50 * 1e-3), 1),
             "unit": "tokens/s (at the p50 latency)", "steps": steps, "equals_eager": same,
-            "note": "one input copy and one graph launch per step; token projection on a second stream"}
+            "note": "one input copy and one graph launch per step"}
 
 
 def decode_latency(args, with_cpu: bool) -> dict:

@@ -4,9 +4,11 @@ A decode step of the layer is a chain of about ten short kernels (query projecti
 routing, sort, generation, activations, scatter-back) whose host-side launch work is
 comparable to their GPU time at small batches.  `CapturedLayer` records one forward for a
 fixed input shape into a HIP graph (torch.cuda.CUDAGraph) and replays it: per call one
-copy of the input into the captured buffer and one graph launch.  Inside the graph the
-token projection x W_u, which needs only x, runs on a second stream beside the query
-projection, routing and sort, and joins before the expert stages.
+copy of the input into the captured buffer and one graph launch.  Optionally
+(`overlap_token_proj`) the token projection x W_u, which needs only x, runs on a second
+stream inside the graph beside the query projection, routing and sort, and joins before the
+expert stages; on ROCm 7 the fork and join cost more GPU time than the overlap saves (64
+tokens: 0.167 against 0.153 ms per replayed step), so it is off by default.
 
 The replay gives the eager forward's output bit for bit (the same kernels on the same
 inputs).  The graph holds the layer's packed parameters by address: when a parameter or a
@@ -28,7 +30,7 @@ class CapturedLayer:
     Calls on one CapturedLayer must not overlap (one input and one output buffer)."""
 
     def __init__(self, layer: EthosExpertLayer, n_tok: int, dtype: torch.dtype | None = None,
-                 device: torch.device | str | None = None, overlap_token_proj: bool = True, warmup: int = 2):
+                 device: torch.device | str | None = None, overlap_token_proj: bool = False, warmup: int = 2):
         if not isinstance(layer, EthosExpertLayer):
             raise TypeError("CapturedLayer wraps an EthosExpertLayer")
         if layer.training or layer.router._bn_uses_batch_stats():
