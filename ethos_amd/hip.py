@@ -9,8 +9,17 @@ import torch
 from ._lib import check, dtype_code, load
 
 
-def _stream() -> int:
+def _stream_slow() -> int:
     return torch.cuda.current_stream().cuda_stream
+
+
+def _stream_fast() -> int:
+    return torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
+
+
+# The current device's current stream as a hipStream_t; the raw accessor skips the Python
+# device bookkeeping of torch.cuda.current_stream (a few microseconds per call).
+_stream = _stream_fast if hasattr(torch._C, "_cuda_getCurrentRawStream") else _stream_slow
 
 
 def _need(t: torch.Tensor, name: str, dtype=None, dim=None) -> None:

@@ -168,11 +168,19 @@ class ProductKeyRouter(nn.Module):
         self._wq_prepared = None
 
     # -- parameter packing (cached until a parameter changes) ---------------------
+    def _packed_sources(self) -> list:
+        """The tensors the packed form is built from, read from the modules' parameter and
+        buffer dicts directly (this runs on every call; nn.Module attribute lookup is slow)."""
+        ts = []
+        for m in self._modules["query_projs"]._modules.values():
+            ts += (m._parameters["weight"], m._parameters["bias"])
+        ts += (self._modules["sub_keys_1"]._parameters["weight"], self._modules["sub_keys_2"]._parameters["weight"])
+        for m in self._modules["query_norms"]._modules.values():
+            ts += (m._parameters["weight"], m._parameters["bias"], m._buffers["running_mean"], m._buffers["running_var"])
+        return ts
+
     def _packed(self, dtype: torch.dtype, device: torch.device):
-        params = [p for m in self.query_projs for p in (m.weight, m.bias)]
-        params += [self.sub_keys_1.weight, self.sub_keys_2.weight]
-        bn = [t for m in self.query_norms for t in (m.weight, m.bias, m.running_mean, m.running_var)]
-        key = (dtype, device, tuple((t.data_ptr(), t._version) for t in params + bn))
+        key = (dtype, device, tuple((t.data_ptr(), t._version) for t in self._packed_sources() if t is not None))
         if key != self._cache_key:
             wq = torch.stack([m.weight.detach() for m in self.query_projs]).to(device=device, dtype=dtype).contiguous()
             bq = torch.stack([m.bias.detach() for m in self.query_projs]).to(device=device, dtype=dtype).contiguous()
@@ -196,9 +204,10 @@ class ProductKeyRouter(nn.Module):
     def _bn_uses_batch_stats(self) -> bool:
         return any(m.training or not m.track_running_stats for m in self.query_norms)
 
-    def queries(self, x_flat: torch.Tensor) -> torch.Tensor:
-        """Per-head queries after BatchNorm, [n, H, d_query] (model.py:215-216)."""
-        wq, bq, _, _, alpha, beta = self._packed(x_flat.dtype, x_flat.device)
+    def queries(self, x_flat: torch.Tensor, packed=None) -> torch.Tensor:
+        """Per-head queries after BatchNorm, [n, H, d_query] (model.py:215-216).  `packed`:
+        the result of _packed for x_flat's dtype and device, if the caller has it."""
+        wq, bq, _, _, alpha, beta = packed if packed is not None else self._packed(x_flat.dtype, x_flat.device)
         if not self._bn_uses_batch_stats():
             return hip.query_proj(x_flat, wq, bq, alpha, beta, prepared=self._wq_prepared)
         # Training-mode BatchNorm normalises with batch statistics and updates the
@@ -224,8 +233,9 @@ class ProductKeyRouter(nn.Module):
     def route(self, x_flat: torch.Tensor, mark=None):
         """(gates [n, H, k] x.dtype, expert ids [n, H, k] int32).  `mark(stage)`, if given,
         is called after each stage is enqueued (used to place timing events)."""
-        _, _, k1, k2, _, _ = self._packed(x_flat.dtype, x_flat.device)
-        q = self.queries(x_flat)
+        packed = self._packed(x_flat.dtype, x_flat.device)
+        _, _, k1, k2, _, _ = packed
+        q = self.queries(x_flat, packed)
         if mark is not None:
             mark("query_proj")
         out = hip.route_topk(q, k1, k2, self.top_k, key_norms=self._key_norms)

@@ -264,3 +264,13 @@ def test_layer_hidden_space_cfg2_subset():
     sub = np.arange(0, sh.n_tok, 64)
     r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub, q=to_host(q))
     check_out(O.to_f32(to_host(y), "bf16")[sub], r["out"], "bf16", nerr_max=1e-2)
+
+
+def test_library_stream_is_torch_current_stream():
+    """The stream handed to the library is torch's current stream, also inside a stream
+    context (the raw accessor the wrappers use agrees with torch.cuda.current_stream)."""
+    assert hip._stream() == torch.cuda.current_stream().cuda_stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert hip._stream() == s.cuda_stream == torch.cuda.current_stream().cuda_stream
+    assert hip._stream() == torch.cuda.current_stream().cuda_stream
