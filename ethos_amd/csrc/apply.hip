@@ -551,8 +551,9 @@ constexpr int kTokWaves = 8;
 constexpr int kTokHeadLds = 64 * 1024;
 
 // The head sum of one (token, head) item, pairs pbase .. pbase + k - 1, into hacc (fp32,
-// this lane's CH chunks of N columns).
-template <typename T, int CH>
+// this lane's CH chunks of N columns), U v rows in flight (16 per wave in the per-token kernel
+// was slower: 0.142 -> 0.145 ms per 64-token forward, 0.348 -> 0.371 ms at 1,024 tokens).
+template <typename T, int CH, int U = kScatterUnroll>
 __device__ __forceinline__ void scatter_head_sum(const T* __restrict__ vr_, const int32_t* __restrict__ pair_slot,
                                                  const float* __restrict__ act, int64_t pbase, int k, int d,
                                                  int lane, float (&hacc)[CH * Vec16<T>::kN]) {
@@ -560,11 +561,11 @@ __device__ __forceinline__ void scatter_head_sum(const T* __restrict__ vr_, cons
     typedef typename Vec16<T>::raw Raw;
 #pragma unroll
     for (int e = 0; e < CH * N; ++e) hacc[e] = 0.0f;
-    for (int j0 = 0; j0 < k; j0 += kScatterUnroll) {
-        Raw vr[kScatterUnroll][CH];
-        float a[kScatterUnroll];
+    for (int j0 = 0; j0 < k; j0 += U) {
+        Raw vr[U][CH];
+        float a[U];
 #pragma unroll
-        for (int q = 0; q < kScatterUnroll; ++q) {
+        for (int q = 0; q < U; ++q) {
             if (j0 + q < k) {
                 const int s = pair_slot[pbase + j0 + q];
                 a[q] = act[pbase + j0 + q];
@@ -572,7 +573,7 @@ __device__ __forceinline__ void scatter_head_sum(const T* __restrict__ vr_, cons
             }
         }
 #pragma unroll
-        for (int q = 0; q < kScatterUnroll; ++q) {
+        for (int q = 0; q < U; ++q) {
             if (j0 + q < k) {
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {

@@ -740,7 +740,10 @@ int launch_qproj(const void* x, const void* w, const void* prepared, const void*
                                (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q,
                                (int64_t*)nullptr);
         }
-        hipLaunchKernelGGL(qproj_fixup_kernel, dim3((unsigned)num_cus * 4), dim3(256), 0, stream, (const uint16_t*)x,
+        // one wave per queued element, at most one per element of the batch
+        const int64_t fix_wg = (n_tok * (int64_t)ncols + 3) / 4;
+        const unsigned fgrid = (unsigned)(fix_wg < (int64_t)num_cus * 4 ? fix_wg : (int64_t)num_cus * 4);
+        hipLaunchKernelGGL(qproj_fixup_kernel, dim3(fgrid), dim3(256), 0, stream, (const uint16_t*)x,
                            (const uint16_t*)w, (const uint16_t*)b, alpha, beta, d, ncols, W.count, W.list,
                            (uint16_t*)q);
         return (int)hipGetLastError();
