@@ -285,7 +285,7 @@ template <> struct QVecF<float> {
 };
 
 struct RouteSmem {
-    size_t s_off, kn_off, qs_off, total;
+    size_t s_off, kn_off, qs_off, xch_off, total;
     int qs_pitch;  // bytes per staged query-half row
 };
 
@@ -299,17 +299,22 @@ __host__ __device__ inline int route_pitch(int K) {
     return (p > 3 * kWave ? p : 3 * kWave) + 4;
 }
 
-__host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2, int elem_bytes) {
+// hp: the half-parallel form (two groups of kRtWaves waves, one per query half, kRtWaves rows):
+// score rows for the workgroup's rows of both halves, both halves' staged query tiles, and the
+// second half's candidate lists handed to the first group.
+__host__ __device__ inline RouteSmem route_smem_layout(int K, int dh2, int elem_bytes, bool hp = false) {
     RouteSmem L;
     size_t off = 0;
     L.s_off = off;
-    off += (size_t)kRtRows * route_pitch(K) * sizeof(float);
+    off += (size_t)(hp ? 2 * kRtWaves : kRtRows) * route_pitch(K) * sizeof(float);
     L.kn_off = off;
     off += (size_t)2 * ((K + 31) / 32) * 32 * sizeof(float);
     L.qs_off = off;
     // 16 bytes of padding put the query rows of one wave's lanes on different banks
     L.qs_pitch = dh2 * elem_bytes + 16;
-    off += (size_t)kRtRows * L.qs_pitch;
+    off += (size_t)(hp ? 2 : 1) * kRtRows * L.qs_pitch;
+    L.xch_off = off;
+    off += hp ? (size_t)kRtWaves * kWave * sizeof(uint64_t) : 0;
     L.total = off;
     return L;
 }
@@ -347,24 +352,35 @@ __device__ __forceinline__ uint64_t exact_key(const T* qh, const T* __restrict__
     return make_key(Elem<T>::round64(acc), (uint32_t)j);
 }
 
-template <typename T, int RPW>
-__global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
+// kHP (small batches): 2 kRtWaves waves, one row per wave and group of kRtWaves waves per
+// query half, so that the two halves' scoring, filter, exact chains and sorts run at the same
+// time; the second group hands its candidate lists to the first, which combines.  The
+// operations on each row are the same as in the one-group form, so the outputs are too.
+template <typename T, int RPW, bool kHP = false>
+__global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
                                                     const T* __restrict__ keys2, const float* __restrict__ key_norms,
                                                     int64_t rows, int dq, int K, int top_k, int kc,
                                                     T* __restrict__ out_gates, int32_t* __restrict__ out_ids) {
     using M = Mfma<T>;
     extern __shared__ __align__(16) unsigned char smem[];
     const int dh2 = dq / 2;
+    static_assert(!kHP || RPW == 1, "the half-parallel form takes one row per wave");
+    constexpr int kThreads = (kHP ? 2 : 1) * kRtWaves * 64;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // hw: this wave's query half (kHP; else both, in turn); wv: its index within its group
+    const int hw = kHP ? wave / kRtWaves : 0, wv = kHP ? wave % kRtWaves : wave;
+    const int gtid = kHP ? tid % (kRtWaves * 64) : tid;
     const int lrow = lane & 31, lk = (lane >> 5) * M::kKL;
-    const RouteSmem L = route_smem_layout(K, dh2, (int)sizeof(T));
+    const RouteSmem L = route_smem_layout(K, dh2, (int)sizeof(T), kHP);
     const int pitch = route_pitch(K);
     const int kpad = ((K + 31) / 32) * 32;
-    float* S = reinterpret_cast<float*>(smem + L.s_off);
+    constexpr int kRowsWG = kRtWaves * RPW;  // rows of this workgroup (<= kRtRows)
+    // this group's score rows and staged query tile
+    float* S = reinterpret_cast<float*>(smem + L.s_off) + (kHP ? (size_t)hw * kRowsWG * pitch : 0);
+    unsigned char* const qsb = smem + L.qs_off + (kHP ? (size_t)hw * kRtRows * L.qs_pitch : 0);
     float* kn = reinterpret_cast<float*>(smem + L.kn_off);
     // lst[rr][half]: the canonical top-k_cand list of this wave's row rr and query half,
     // entry i held by lane i
-    constexpr int kRowsWG = kRtWaves * RPW;  // rows of this workgroup (<= kRtRows)
     // key vectors in flight per exact chain (one row per wave leaves registers for more)
     constexpr int kExG = RPW == 1 ? 8 : 2;
     using LK = ListKey<T>;
@@ -377,7 +393,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
     const float gamma = (float)(dh2 + 16) * 0x1p-22f * 1.01f;
 
     // Sub-key norms (upper bounds) for both tables.
-    for (int e = tid; e < 2 * kpad; e += kRtWaves * 64) {
+    for (int e = tid; e < 2 * kpad; e += kThreads) {
         const int half = e / kpad, j = e - half * kpad;
         float nrm = 0.0f;
         if (j < K) {
@@ -397,29 +413,30 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
     }
 
     const int qs_ld = L.qs_pitch / (int)sizeof(T);  // staged query row pitch (elements)
-    for (int half = 0; half < 2; ++half) {
+    for (int hh = 0; hh < (kHP ? 1 : 2); ++hh) {
+        const int half = kHP ? hw : hh;
         const T* keys = half ? keys2 : keys1;
         // 0. stage the query halves of the tile's rows in LDS, one 16-byte vector per
         //    thread and step; rows past the batch or past this workgroup's rows are zero
         {
             constexpr int kV = 16 / (int)sizeof(T);
             const int vpr = dh2 / kV;
-            for (int e = tid; e < kRtRows * vpr; e += kRtWaves * 64) {
+            for (int e = gtid; e < kRtRows * vpr; e += kRtWaves * 64) {
                 const int lr = e / vpr, c = e - lr * vpr;
                 const int64_t r = row0 + lr;
                 uint4 v = make_uint4(0u, 0u, 0u, 0u);
                 if (lr < kRowsWG && r < rows) v = *reinterpret_cast<const uint4*>(q + r * dq + half * dh2 + c * kV);
-                *reinterpret_cast<uint4*>(smem + L.qs_off + (size_t)lr * L.qs_pitch + (size_t)c * 16) = v;
+                *reinterpret_cast<uint4*>(qsb + (size_t)lr * L.qs_pitch + (size_t)c * 16) = v;
             }
         }
         __syncthreads();
-        const T* qtile = reinterpret_cast<const T*>(smem + L.qs_off);
+        const T* qtile = reinterpret_cast<const T*>(qsb);
 
         // 1. approximate scores for the 32-row tile: wave w takes key blocks w, w + 8, ...
         //    The key fragments of kU reduction steps are loaded before their MFMAs, so
         //    their L2 latencies overlap.
         constexpr int kU = sizeof(T) == 2 ? (RPW == 1 ? 4 : 1) : (RPW == 1 ? 16 : 8);
-        for (int kb0 = wave; kb0 < nkb; kb0 += 2 * kRtWaves) {
+        for (int kb0 = wv; kb0 < nkb; kb0 += 2 * kRtWaves) {
             f32x16_t acc[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c) acc[c] = f32x16_zero();
@@ -451,7 +468,9 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
                 const int kb = kb0 + kRtWaves * c;
                 if (kb < nkb) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) S[mfma32_row(i, lane) * pitch + kb * 32 + lrow] = acc[c][i];
+                    for (int i = 0; i < 16; ++i)
+                        if (!kHP || mfma32_row(i, lane) < kRowsWG)  // (kHP: only the live rows have storage)
+                            S[mfma32_row(i, lane) * pitch + kb * 32 + lrow] = acc[c][i];
                 }
             }
         }
@@ -501,8 +520,8 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             constexpr int kLPR = kWave / RPW;
             constexpr int kN = QVecF<T>::kN;
             static_assert(RPW == 1 || RPW == 4, "row groups of 64 or 16 lanes");
-            const int lr = wave * RPW + lane / kLPR;
-            const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
+            const int lr = wv * RPW + lane / kLPR;
+            const T* qs = reinterpret_cast<const T*>(qsb + (size_t)lr * L.qs_pitch);
             for (int i = (lane % kLPR) * kN; i < dh2; i += kLPR * kN) {
                 float v[kN];
                 QVecF<T>::load(qs + i, v);
@@ -520,7 +539,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         }
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) {
-            const int lr = wave * RPW + rr;
+            const int lr = wv * RPW + rr;
             const int64_t r = row0 + lr;
             if (r >= rows) break;
             // bound the norm of the staged query half (the 2^-12 slack covers the fp32
@@ -629,9 +648,9 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
                             start = p_end[t];
                         }
                     }
-                    const int lr = wave * RPW + rr;
+                    const int lr = wv * RPW + rr;
                     const uint32_t e = reinterpret_cast<const uint32_t*>(S + lr * pitch + kRtPendOff)[idx - start];
-                    const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
+                    const T* qs = reinterpret_cast<const T*>(qsb + (size_t)lr * L.qs_pitch);
                     reinterpret_cast<uint64_t*>(S + lr * pitch)[e & 0xffu] = exact_key<T, kExG>(qs, keys, dh2, (int)(e >> 8));
                 }
             }
@@ -641,7 +660,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
         // 4. canonical top-k_cand list of each row
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) {
-            const int lr = wave * RPW + rr;
+            const int lr = wv * RPW + rr;
             const int64_t r = row0 + lr;
             if (r >= rows) break;
             const int n = n_cand[rr];
@@ -652,7 +671,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             } else {
                 uint64_t run = 0;
                 const int32_t* cand = reinterpret_cast<const int32_t*>(S + lr * pitch);
-                const T* qs = reinterpret_cast<const T*>(smem + L.qs_off + (size_t)lr * L.qs_pitch);
+                const T* qs = reinterpret_cast<const T*>(qsb + (size_t)lr * L.qs_pitch);
                 for (int c0 = 0; c0 < n; c0 += kWave) {
                     const int idx = c0 + lane;
                     uint64_t key = idx < n ? exact_key<T, kExG>(qs, keys, dh2, cand[idx]) : 0ull;
@@ -665,6 +684,14 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
             else lst[rr][1] = run_l;
         }
         __syncthreads();
+    }
+    if constexpr (kHP) {
+        // the second group's lists to the first group's waves (row wv), which combine
+        typename LK::type* xch = reinterpret_cast<typename LK::type*>(smem + L.xch_off);
+        if (hw == 1) xch[wv * kWave + lane] = lst[0][1];
+        __syncthreads();
+        if (hw == 1) return;
+        lst[0][1] = xch[wv * kWave + lane];
     }
 
     // Combine the two candidate lists of each row and take the canonical top-k.
@@ -706,7 +733,7 @@ __global__ __launch_bounds__(kRtWaves * 64, 4) void route_kernel(const T* __rest
     }
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
-        const int lr = wave * RPW + rr;
+        const int lr = wv * RPW + rr;
         const int64_t r = row0 + lr;
         if (r >= rows) break;
         const uint64_t L1 = LK::unpack(lst[rr][0]), L2 = LK::unpack(lst[rr][1]);
@@ -775,9 +802,12 @@ int launch_route(const void* q, const void* k1, const void* k2, const float* key
     const bool small = rows <= kRtSmallRows;
     const int per_wg = kRtWaves * (small ? 1 : 4);
     dim3 grid((unsigned)((rows + per_wg - 1) / per_wg));
+    // small batches: one row per wave, the two query halves in parallel
+    const size_t smem_hp = route_smem_layout(K, dh2, dtype == kBF16 ? 2 : 4, true).total;
+    const dim3 block_hp(2 * kRtWaves * 64);
     if (dtype == kBF16) {
         if (small)
-            hipLaunchKernelGGL((route_kernel<uint16_t, 1>), grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
+            hipLaunchKernelGGL((route_kernel<uint16_t, 1, true>), grid, block_hp, smem_hp, stream, (const uint16_t*)q,
                                (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
                                (uint16_t*)gates, ids);
         else
@@ -786,7 +816,7 @@ int launch_route(const void* q, const void* k1, const void* k2, const float* key
                                (uint16_t*)gates, ids);
     } else {
         if (small)
-            hipLaunchKernelGGL((route_kernel<float, 1>), grid, dim3(kRtWaves * 64), smem, stream, (const float*)q,
+            hipLaunchKernelGGL((route_kernel<float, 1, true>), grid, block_hp, smem_hp, stream, (const float*)q,
                                (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
         else
             hipLaunchKernelGGL((route_kernel<float, 4>), grid, dim3(kRtWaves * 64), smem, stream, (const float*)q,
