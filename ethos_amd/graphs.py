@@ -47,11 +47,11 @@ class CapturedLayer:
         self.overlap_token_proj = overlap_token_proj
         self.warmup = max(1, int(warmup))
         self.input = torch.zeros((self.n_tok, layer.d_model), dtype=self.dtype, device=self.device)
-        self._watch = [t for t in list(layer.parameters()) + list(layer.buffers()) if t.is_floating_point()]
         self._capture()
 
     def _state(self):
-        return tuple((t.data_ptr(), t._version) for t in self._watch)
+        # looked up afresh on every call: a parameter replaced by a new object counts as a change
+        return tuple((t.data_ptr(), t._version) for t in self.layer._param_sources() if t is not None)
 
     def _capture(self) -> None:
         layer = self.layer

@@ -319,6 +319,15 @@ class EthosExpertLayer(nn.Module):
         self._gen_key = None
         self._gen = None
 
+    def _param_sources(self) -> list:
+        """Every tensor a forward reads (router parameters and BatchNorm buffers, latents and
+        both generator weights), looked up afresh through the modules' dicts, so that a
+        replaced parameter object is seen too."""
+        gen = self._modules["generation_network"]._modules["net"]._modules
+        return self._modules["router"]._packed_sources() + [
+            self._modules["expert_latents"]._parameters["weight"], gen["0"]._parameters["weight"],
+            gen["2"]._parameters["weight"]]
+
     def _generator_params(self, dtype, device):
         """(latents, W1, W2, W_u^T): the generator weights in the layer dtype on the device,
         and (bf16) the transpose of W2's first d_model rows, cached until a weight changes."""

@@ -60,6 +60,15 @@ def test_captured_layer_recaptures_after_a_parameter_change():
     torch.cuda.synchronize()
     assert cap.graph is not graph
     assert torch.equal(got, want) and not torch.equal(got, before)
+    # a parameter replaced by a new object (no version change on the old one) is seen too
+    graph = cap.graph
+    lat = m.expert_latents.weight
+    m.expert_latents.weight = torch.nn.Parameter(lat.detach() * 3.0)
+    with torch.no_grad():
+        want = m.forward_flat(x)
+    got = cap(x)
+    torch.cuda.synchronize()
+    assert cap.graph is not graph and torch.equal(got, want)
 
 
 @pytest.mark.gpu
