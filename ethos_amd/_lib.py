@@ -37,6 +37,8 @@ SIGNATURES = {
     "ethos_sort_workspace_bytes": (_sz, [_i64, _i64]),
     "ethos_sort_segment": (ctypes.c_int, [_vp, _i64, _i64, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ethos_sort_segment_noalloc": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ethos_sort_segment_token_proj": (ctypes.c_int, [_vp, _i64, _i64, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                     _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp]),
     "ethos_generate": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "ethos_apply_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "ethos_apply_scatter": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,

@@ -251,6 +251,41 @@ int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, v
                       "ethos_sort_segment");
 }
 
+int ethos_sort_segment_token_proj(const int32_t* ids, int64_t n_pairs, int64_t n_experts, void* workspace,
+                                  size_t workspace_bytes, int32_t* perm, int32_t* uniq_ids, int32_t* seg_off,
+                                  int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique, const void* x,
+                                  const void* w2, const void* wut, int64_t n_tok, int32_t d_model, int32_t d_hidden,
+                                  int32_t dtype, void* xp_out, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_sort_segment_token_proj: unknown dtype %d", dtype);
+    const int vec = dtype == ETHOS_BF16 ? 8 : 4;
+    if (n_pairs < 0 || n_experts <= 0 || n_experts > INT32_MAX || n_pairs > INT32_MAX || n_tok < 0 ||
+        n_tok > INT32_MAX || d_model <= 0 || d_hidden <= 0)
+        return fail(ETHOS_ESIZE, "ethos_sort_segment_token_proj: bad sizes");
+    if (d_model % vec || d_hidden % vec)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_sort_segment_token_proj: d_model and d_hidden must be multiples of %d",
+                    vec);
+    if (!seg_off || !n_unique) return fail(ETHOS_ENULL, "ethos_sort_segment_token_proj: null pointer");
+    if (n_tok > 0 && (!x || !w2 || !xp_out)) return fail(ETHOS_ENULL, "ethos_sort_segment_token_proj: null pointer");
+    if (n_tok > 0 && (!aligned16(x) || !aligned16(w2) || (wut && !aligned16(wut)) || !aligned16(xp_out)))
+        return fail(ETHOS_EALIGN, "ethos_sort_segment_token_proj: x, w2, wut and xp_out must be 16-byte aligned");
+    if (n_pairs > 0) {
+        if (!ids || !perm || !uniq_ids || !pair_slot || !sorted_slot)
+            return fail(ETHOS_ENULL, "ethos_sort_segment_token_proj: null pointer");
+        if (n_tok > 0 && dtype == ETHOS_BF16) {
+            const int rc = ethos::launch_sort_segment_tp(ids, n_pairs, n_experts, perm, uniq_ids, seg_off, pair_slot,
+                                                         sorted_slot, n_unique, x, wut, n_tok, d_model, d_hidden,
+                                                         xp_out, (hipStream_t)stream);
+            if (rc >= 0) return hip_status(rc, "ethos_sort_segment_token_proj");
+        }
+    }
+    // not one launch: the sort, then the projection
+    int rc = ethos_sort_segment(ids, n_pairs, n_experts, workspace, workspace_bytes, perm, uniq_ids, seg_off, pair_slot,
+                                sorted_slot, n_unique, stream);
+    if (rc != 0) return rc;
+    return ethos_token_proj(x, w2, wut, n_tok, d_model, d_hidden, dtype, xp_out, stream);
+}
+
 int ethos_sort_segment_noalloc(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* perm,
                                int32_t* uniq_ids, int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot,
                                int32_t* n_unique, void* stream) {

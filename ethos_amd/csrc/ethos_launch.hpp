@@ -52,6 +52,12 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
                         int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
                         hipStream_t stream);
 int launch_sort_empty(int32_t* seg_off, int32_t* n_unique, hipStream_t stream);
+// The sort with the bf16 token projection xp = RN(x W_u) (W_u^T given) in the same launch,
+// for batches the single-workgroup sort takes; -1 (nothing launched) otherwise.
+int launch_sort_segment_tp(const int32_t* ids, int64_t n, int64_t n_experts, int32_t* perm, int32_t* uniq,
+                           int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
+                           const void* x, const void* wut, int64_t n_tok, int d, int dh, void* xp,
+                           hipStream_t stream);
 
 size_t generate_smem_bytes(int dl, int dh, int dtype);
 int launch_generate(const void* latents, int64_t n_experts, const int32_t* uniq, const int32_t* n_unique,

@@ -36,6 +36,7 @@
 
 #include "ethos_common.hpp"
 #include "ethos_launch.hpp"
+#include "ethos_tp.hpp"
 
 namespace ethos {
 
@@ -655,20 +656,22 @@ constexpr int kSmallMax = 16384;
 constexpr int kSmallChunks = kSmallMax / 64;                 // 256
 constexpr int kSmallPer = kSmallChunks / kSmallWaves;        // chunks per wave at most
 
-__global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int32_t* __restrict__ ids, int n,
-                                                                      int key_bits_, int vb, int passes,
-                                                                      int32_t* __restrict__ perm,
-                                                                      int32_t* __restrict__ uniq,
-                                                                      int32_t* __restrict__ seg_off,
-                                                                      int32_t* __restrict__ pair_slot,
-                                                                      int32_t* __restrict__ sorted_slot,
-                                                                      int32_t* __restrict__ n_unique,
-                                                                      int32_t max_unique) {
-    __shared__ uint32_t buf[2][kSmallMax];
-    __shared__ uint16_t cnt[kSmallWaves][kRadix];  // per-wave digit counts, then bases (< 2^14)
-    __shared__ uint64_t cmask[kSmallChunks];       // head flags per chunk
-    __shared__ uint32_t cbase[kSmallChunks];       // heads before each chunk
-    __shared__ uint32_t wsum[kSmallWaves];
+// LDS of the small sort: the words twice, per-wave digit counts (then bases, < 2^14), head
+// flags per chunk, heads before each chunk, wave sums.
+constexpr size_t kSmallBufB = 2 * (size_t)kSmallMax * 4, kSmallCntB = (size_t)kSmallWaves * kRadix * 2;
+constexpr size_t kSmallLds = kSmallBufB + kSmallCntB + (size_t)kSmallChunks * 8 + (size_t)kSmallChunks * 4 +
+                             (size_t)kSmallWaves * 4;
+
+__device__ __forceinline__ void sort_small_body(unsigned char* lds, const int32_t* __restrict__ ids, int n,
+                                                int key_bits_, int vb, int passes, int32_t* __restrict__ perm,
+                                                int32_t* __restrict__ uniq, int32_t* __restrict__ seg_off,
+                                                int32_t* __restrict__ pair_slot, int32_t* __restrict__ sorted_slot,
+                                                int32_t* __restrict__ n_unique, int32_t max_unique) {
+    uint32_t (*buf)[kSmallMax] = reinterpret_cast<uint32_t (*)[kSmallMax]>(lds);
+    uint16_t (*cnt)[kRadix] = reinterpret_cast<uint16_t (*)[kRadix]>(lds + kSmallBufB);
+    uint64_t* cmask = reinterpret_cast<uint64_t*>(lds + kSmallBufB + kSmallCntB);
+    uint32_t* cbase = reinterpret_cast<uint32_t*>(lds + kSmallBufB + kSmallCntB + kSmallChunks * 8);
+    uint32_t* wsum = reinterpret_cast<uint32_t*>(lds + kSmallBufB + kSmallCntB + kSmallChunks * 12);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t kmax = (1u << key_bits_) - 1u;
     const int n_chunks = (n + 63) / 64;
@@ -809,6 +812,60 @@ __global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int3
         *n_unique = u_clamped;
         seg_off[u_clamped] = n;
     }
+}
+
+__global__ __launch_bounds__(kSmallWaves * 64) void sort_small_kernel(const int32_t* __restrict__ ids, int n,
+                                                                      int key_bits_, int vb, int passes,
+                                                                      int32_t* __restrict__ perm,
+                                                                      int32_t* __restrict__ uniq,
+                                                                      int32_t* __restrict__ seg_off,
+                                                                      int32_t* __restrict__ pair_slot,
+                                                                      int32_t* __restrict__ sorted_slot,
+                                                                      int32_t* __restrict__ n_unique,
+                                                                      int32_t max_unique) {
+    __shared__ __align__(16) unsigned char lds[kSmallLds];
+    sort_small_body(lds, ids, n, key_bits_, vb, passes, perm, uniq, seg_off, pair_slot, sorted_slot, n_unique,
+                    max_unique);
+}
+
+// The small sort in workgroup 0 and the bf16 token projection xp = RN(x W_u) in the
+// others (tile b - 1: column tile (b - 1) % nct, token tile (b - 1) / nct), which needs
+// only x: the tiles run on CUs the single sorting workgroup leaves idle.
+static_assert(kSmallLds >= (size_t)kTpLds, "the projection tile's ring fits the sort's LDS");
+__global__ __launch_bounds__(kSmallWaves * 64) void sort_small_tp_kernel(
+    const int32_t* __restrict__ ids, int n, int key_bits_, int vb, int passes, int32_t* __restrict__ perm,
+    int32_t* __restrict__ uniq, int32_t* __restrict__ seg_off, int32_t* __restrict__ pair_slot,
+    int32_t* __restrict__ sorted_slot, int32_t* __restrict__ n_unique, int32_t max_unique,
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wut, int n_tok, int d, int dh, int nct,
+    uint16_t* __restrict__ xp) {
+    __shared__ __align__(16) unsigned char lds[kSmallLds];
+    if (blockIdx.x == 0) {
+        sort_small_body(lds, ids, n, key_bits_, vb, passes, perm, uniq, seg_off, pair_slot, sorted_slot, n_unique,
+                        max_unique);
+    } else {
+        const int b = (int)blockIdx.x - 1;
+        token_proj_bf16_tile(lds, x, wut, n_tok, d, dh, xp, (b % nct) * kTpCols, (b / nct) * kTpRows);
+    }
+}
+
+int launch_sort_segment_tp(const int32_t* ids, int64_t n, int64_t n_experts, int32_t* perm, int32_t* uniq,
+                           int32_t* seg_off, int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique,
+                           const void* x, const void* wut, int64_t n_tok, int d, int dh, void* xp,
+                           hipStream_t stream) {
+    const int bits = sort_key_bits(n_experts);
+    const int passes = sort_passes(n_experts);
+    int vb = 0;
+    while (vb < 31 && ((int64_t)1 << vb) < n) ++vb;
+    const int32_t max_unique = (int32_t)(n < n_experts ? n : n_experts);
+    if (!(n <= kSmallMax && bits + vb <= 32) || wut == nullptr || d % kTpK || dh % 8 || n_tok < 1 ||
+        n_tok > INT32_MAX)
+        return -1;  // not the single-workgroup sort, or not the MFMA projection: two launches
+    const int nct = (dh + kTpCols - 1) / kTpCols;
+    const int64_t tiles = (int64_t)nct * ((n_tok + kTpRows - 1) / kTpRows);
+    hipLaunchKernelGGL(sort_small_tp_kernel, dim3((unsigned)(1 + tiles)), dim3(kSmallWaves * 64), 0, stream, ids,
+                       (int)n, bits, vb, passes, perm, uniq, seg_off, pair_slot, sorted_slot, n_unique, max_unique,
+                       (const uint16_t*)x, (const uint16_t*)wut, (int)n_tok, d, dh, nct, (uint16_t*)xp);
+    return (int)hipGetLastError();
 }
 
 size_t sort_workspace_bytes(int64_t n, int64_t n_experts) {

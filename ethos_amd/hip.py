@@ -163,6 +163,50 @@ def sort_segment(ids: torch.Tensor, n_experts: int) -> dict:
     return r
 
 
+# Pairs up to which the sort runs as one workgroup (and ethos_sort_segment_token_proj runs the
+# bf16 token projection in the same launch).
+SMALL_SORT_MAX = 16384
+
+
+def sort_segment_token_proj(ids: torch.Tensor, n_experts: int, x: torch.Tensor, w2: torch.Tensor,
+                            wut: torch.Tensor | None) -> tuple[dict, torch.Tensor]:
+    """sort_segment(ids, n_experts) and token_proj(x, w2, wut) in one library call: one
+    launch for bf16 batches of at most SMALL_SORT_MAX pairs with wut given, the two in turn
+    otherwise.  Returns (the sort's dict, x_proj)."""
+    _need(ids, "ids", torch.int32)
+    _need(x, "x", dim=2)
+    _need(w2, "w2", x.dtype, 2)
+    n = ids.numel()
+    dev = ids.device
+    n_tok, d = x.shape
+    dh = w2.shape[1]
+    if w2.shape[0] != 2 * d:
+        raise RuntimeError("sort_segment_token_proj: w2 must be [2 d_model, d_hidden]")
+    if wut is not None:
+        _need(wut, "wut", x.dtype, 2)
+        if wut.shape != (dh, d):
+            raise RuntimeError("sort_segment_token_proj: wut must be [d_hidden, d_model]")
+    max_u = max(1, min(n, n_experts))
+    ws, ws_bytes = workspace(load().ethos_sort_workspace_bytes(n, n_experts), dev)
+    r = dict(
+        perm=torch.empty(n, dtype=torch.int32, device=dev),
+        uniq=torch.empty(max_u, dtype=torch.int32, device=dev),
+        seg_off=torch.empty(max_u + 1, dtype=torch.int32, device=dev),
+        pair_slot=torch.empty(n, dtype=torch.int32, device=dev),
+        sorted_slot=torch.empty(n, dtype=torch.int32, device=dev),
+        n_unique=torch.empty(1, dtype=torch.int32, device=dev),
+        max_unique=max_u,
+    )
+    xp = torch.empty((n_tok, dh), dtype=x.dtype, device=x.device)
+    rc = load().ethos_sort_segment_token_proj(
+        ids.data_ptr(), n, n_experts, ws.data_ptr(), ws_bytes, r["perm"].data_ptr(), r["uniq"].data_ptr(),
+        r["seg_off"].data_ptr(), r["pair_slot"].data_ptr(), r["sorted_slot"].data_ptr(), r["n_unique"].data_ptr(),
+        x.data_ptr(), w2.data_ptr(), wut.data_ptr() if wut is not None else None, n_tok, d, dh, dtype_code(x.dtype),
+        xp.data_ptr(), _stream())
+    check(rc, "ethos_sort_segment_token_proj")
+    return r, xp
+
+
 def generate(latents: torch.Tensor, uniq: torch.Tensor, n_unique: torch.Tensor, max_unique: int, w1: torch.Tensor,
              w2: torch.Tensor, with_v: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Hidden rows h [max_unique, d_hidden] and v rows [max_unique, d] of the unique experts

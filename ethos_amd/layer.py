@@ -387,10 +387,16 @@ class EthosExpertLayer(nn.Module):
                 with torch.cuda.stream(side_stream):
                     hip.token_proj(x_flat, w2, wut, out=xp)
             gates, ids = self.router.route(x_flat, mark)
-            seg = hip.sort_segment(ids.view(-1), self.num_experts)
+            if xp is None and ids.numel() <= hip.SMALL_SORT_MAX and x_flat.dtype == torch.bfloat16:
+                # small batches: the token projection runs in the sort's launch, beside its
+                # single workgroup
+                _, _, w2, wut = self._generator_params(x_flat.dtype, x_flat.device)
+                seg, xp = hip.sort_segment_token_proj(ids.view(-1), self.num_experts, x_flat, w2, wut)
+            else:
+                seg = hip.sort_segment(ids.view(-1), self.num_experts)
             if mark is not None:
                 mark("sort_segment")
-            if xp is not None:
+            if side_stream is not None:
                 cur.wait_stream(side_stream)
             out, _ = self._expert_stages(x_flat, gates, seg, xp=xp)
         return out

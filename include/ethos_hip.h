@@ -10,6 +10,7 @@
  *   ethos_query_proj     per-head query projection + eval BatchNorm
  *   ethos_route_topk     sub-key scoring, top-k_cand per half, combination, top-k, softmax
  *   ethos_sort_segment   reordering of (token, head, k) pairs by expert id
+ *   ethos_sort_segment_token_proj  the same with the token projection x W_u beside it
  *   ethos_generate       hypernetwork expert generation over the unique experts
  *   ethos_apply_scatter  per-pair activation and weighted scatter-back into tokens
  *   ethos_apply_hidden   the same, by hidden-space reordering (no v rows)
@@ -153,6 +154,23 @@ size_t ethos_sort_workspace_bytes(int64_t n_pairs, int64_t n_experts);
 int ethos_sort_segment(const int32_t* ids, int64_t n_pairs, int64_t n_experts, void* workspace,
                        size_t workspace_bytes, int32_t* perm, int32_t* uniq_ids, int32_t* seg_off,
                        int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique, void* stream);
+
+/*
+ * ethos_sort_segment and ethos_token_proj in one call: the reordering of the pairs and the
+ * token projection x_proj = RN_T(x W_u) are independent (the projection needs only x).  For
+ * bf16 batches the single-workgroup sort takes (n_pairs <= 16384) with W_u^T given, both run
+ * in one launch, the projection's tiles in the workgroups beside the sort's one; otherwise it
+ * is the two calls in turn.  No counterpart in the reference (its pair loop forms x_proj per
+ * pair, model.py:326); for callers of ethos_expert_forward that pass xp.  Arguments and
+ * outputs are those of ethos_sort_segment (ids .. n_unique) and ethos_token_proj (x .. xp_out);
+ * the outputs are bit-identical to theirs.  The workspace is needed only when the two run in
+ * turn; it may be NULL for a single launch.
+ */
+int ethos_sort_segment_token_proj(const int32_t* ids, int64_t n_pairs, int64_t n_experts, void* workspace,
+                                  size_t workspace_bytes, int32_t* perm, int32_t* uniq_ids, int32_t* seg_off,
+                                  int32_t* pair_slot, int32_t* sorted_slot, int32_t* n_unique, const void* x,
+                                  const void* w2, const void* wut, int64_t n_tok, int32_t d_model, int32_t d_hidden,
+                                  int32_t dtype, void* xp_out, void* stream);
 
 /*
  * ethos_sort_segment without a caller workspace, for callers that cannot allocate device

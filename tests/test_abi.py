@@ -101,6 +101,25 @@ def test_route_rejects_top_k_above_32():
     assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 4096, 40, 32, 1, 16, 16, None) == -6
 
 
+def test_sort_segment_token_proj_argument_errors():
+    """Checked before any HIP call, so no GPU is needed."""
+    L = _lib.load()
+    ok = [16, 100, 262144, 16, 1 << 20, 16, 16, 16, 16, 16, 16, 16, 16, 16, 10, 64, 32, 1, 16, None]
+    bad_dtype = list(ok)
+    bad_dtype[17] = 5
+    assert L.ethos_sort_segment_token_proj(*bad_dtype) == -1
+    bad_width = list(ok)
+    bad_width[15] = 60  # d_model not a multiple of 8 (bf16)
+    assert L.ethos_sort_segment_token_proj(*bad_width) == -6
+    no_x = list(ok)
+    no_x[11] = None
+    assert L.ethos_sort_segment_token_proj(*no_x) == -3
+    misaligned = list(ok)
+    misaligned[18] = 18
+    assert L.ethos_sort_segment_token_proj(*misaligned) == -4
+    assert b"ethos_sort_segment_token_proj" in L.ethos_last_error()
+
+
 def test_sort_noalloc_rejects_pairs_beyond_its_static_workspace():
     """The no-allocation sort takes at most NOALLOC_MAX_PAIRS pairs (checked before any
     HIP call, so no GPU is needed), and validates like ethos_sort_segment."""

@@ -629,3 +629,30 @@ def test_stage_events_recorded_in_expert_forward():
     gaps = [a.elapsed_time(b) for a, b in zip(marks, marks[1:])]
     assert all(t >= 0 for t in gaps), gaps
     assert sum(gaps[:-1]) > 0
+
+
+@pytest.mark.parametrize("n_tok,H,k,d,dh,E,dt", [(64, 8, 16, 1024, 512, 262144, "bf16"),   # one launch
+                                                 (5, 2, 3, 256, 128, 300, "bf16"),         # one launch, one tile
+                                                 (64, 2, 4, 96, 64, 300, "bf16"),          # d % 64: two launches
+                                                 (1100, 8, 16, 256, 128, 262144, "bf16"),  # tiled sort: two launches
+                                                 (33, 2, 4, 128, 96, 300, "fp32")])
+def test_sort_segment_token_proj_matches_separate_calls(n_tok, H, k, d, dh, E, dt):
+    """The sort with the token projection beside it gives the outputs of sort_segment and
+    token_proj bit for bit, whether it runs as one launch (small bf16 batches) or as the two
+    in turn."""
+    rng = np.random.default_rng(n_tok + d)
+    enc = (lambda a: O.f32_to_bf16_bits(a)) if dt == "bf16" else (lambda a: a.astype(np.float32))
+    x = to_dev(enc(rng.standard_normal((n_tok, d)).astype(np.float32)))
+    w2 = to_dev(enc((rng.uniform(-1, 1, (2 * d, dh)) / np.sqrt(d)).astype(np.float32)))
+    wut = w2[:d].t().contiguous() if dt == "bf16" else None
+    ids = to_dev(rng.integers(0, E, n_tok * H * k).astype(np.int32))
+    seg, xp = hip.sort_segment_token_proj(ids, E, x, w2, wut)
+    seg_ref = hip.sort_segment(ids, E)
+    xp_ref = hip.token_proj(x, w2, wut)
+    torch.cuda.synchronize()
+    U = int(seg_ref["n_unique"].item())
+    assert int(seg["n_unique"].item()) == U
+    for key in ("perm", "pair_slot", "sorted_slot"):
+        assert torch.equal(seg[key], seg_ref[key]), key
+    assert torch.equal(seg["uniq"][:U], seg_ref["uniq"][:U]) and torch.equal(seg["seg_off"][:U + 1], seg_ref["seg_off"][:U + 1])
+    assert torch.equal(xp, xp_ref)
