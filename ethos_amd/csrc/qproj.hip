@@ -280,8 +280,10 @@ __device__ __forceinline__ QColFmt qp_col(const QRowMeta& m, uint16_t bias, floa
 // units of P) are integers of magnitude at most B = sum_i (|F_i| + 2^15)(|G_i| + 2^15) <=
 // 2^42 H', where in units of 2^(E_x + E_w) H' = A' + 2^-6 (|x|_1 + |w|_1) + d 2^-12 and A'
 // bounds sum |x_i w_i|.  Below 2^53 (H' < 2^11) P's fp64 form is exact; otherwise its
-// roundings add at most 2^-51 H' to the error.
-__device__ __forceinline__ bool qp_certify(double Pd, float4 xf, int2 xi, const QColFmt& cf, int d, uint16_t* out) {
+// roundings add at most 2^-51 H' to the error.  Branch-free: *out always receives bits,
+// which are the element's value when the result is true (a provisional value otherwise).
+__device__ __forceinline__ bool qp_certify_bits(double Pd, float4 xf, int2 xi, const QColFmt& cf, int d,
+                                                uint16_t* out) {
     const float dscale = (float)d * 0x1p-52f;  // chain rounding: d 2^-52 A'
     const float dterm = (float)d * 0x1p-12f;
     const double V = ldexp(Pd, xi.x + cf.ew - 42);
@@ -294,13 +296,33 @@ __device__ __forceinline__ bool qp_certify(double Pd, float4 xf, int2 xi, const 
     const bool exact = (xi.y | cf.nw) == 0 && Hs < 2047.0f;
     const float Es =
         1.01f * (__builtin_fmaf(dscale, As, __builtin_fmaf(xf.z, cf.aw, cf.mw * xf.x)) + 0x1p-51f * Hs);
-    const double E = exact ? 0.0 : ldexp((double)Es, xi.x + cf.ew) + 0x1p-50 * (fabs(V) + fabs(cf.b)) + 0x1p-1074;
-    const double sv = V + cf.b;
-    const uint16_t lo = Elem<uint16_t>::from_f64(sv - E);
-    const uint16_t hi = exact ? lo : Elem<uint16_t>::from_f64(sv + E);
-    if (!(xi.y >= 0 && cf.nw >= 0 && lo == hi)) return false;
-    *out = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32(lo), cf.al, cf.be));
-    return true;
+    const double Ed = ldexp((double)Es, xi.x + cf.ew) + 0x1p-50 * (fabs(V) + fabs(cf.b)) + 0x1p-1074;
+    const double E = exact ? 0.0 : Ed;
+    const double sv = V + cf.b;  // the element lies in [sv - E, sv + E] (E = 0: it is sv)
+    // The interval test in fp32, one paired conversion for both ends.  f = RN_f32(sv) is
+    // within 2^-24 |f| of sv for 2^-100 <= |f| <= 2^100; E32 = RN_f32(E) >= E (1 - 2^-23) -
+    // 2^-126 (flushed below 2^-126); so Ef, rounded twice, is >= E + |f| 2^-21 (1 - 2^-23).
+    // With Ef <= |f| / 2 the ends f -+ Ef are normal and their fp32 roundings (at most
+    // 1.5 |f| 2^-24 each) stay outside [sv - E, sv + E]; when RN_bf16 gives both ends the
+    // same bits it is constant on the interval (rounding is monotone), so that is the
+    // element's value.  An exact zero (E = 0, sv = +-0) is its own value.
+    const float f = (float)sv;
+    const float af = fabsf(f);
+    const float Ef = __builtin_fmaf((float)E, 1.0f + 0x1p-20f, __builtin_fmaf(af, 0x1p-21f, 0x1p-125f));
+    const uint32_t ends = pack_bf16x2(f - Ef, f + Ef);
+    const bool zero = exact && sv == 0.0;
+    const uint32_t lo = zero ? __float_as_uint(f) >> 16 : ends & 0xffffu;
+    const bool sure = ((ends >> 16) == (ends & 0xffffu) && af >= 0x1p-100f && af <= 0x1p100f && Ef <= 0.5f * af) ||
+                      zero;
+    *out = f32_to_bf16_bits(__builtin_fmaf(bf16_bits_to_f32((uint16_t)lo), cf.al, cf.be));
+    return sure && xi.y >= 0 && cf.nw >= 0;
+}
+// The same, writing *out only for a certified element.
+__device__ __forceinline__ bool qp_certify(double Pd, float4 xf, int2 xi, const QColFmt& cf, int d, uint16_t* out) {
+    uint16_t o;
+    const bool sure = qp_certify_bits(Pd, xf, xi, cf, d, &o);
+    if (sure) *out = o;
+    return sure;
 }
 
 // Queue the lanes' uncertain elements e (queue true) on the exact-chain list.
@@ -532,30 +554,39 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
         }
         return;
     }
-    // Certify each element; store it or queue it for the exact chain.
+    // Certify each element and store it; queue the uncertain ones for the exact chain (which
+    // overwrites their provisional values).  No branches per element, so that the compiler
+    // can overlap the elements' dependent chains: the stores go through a buffer descriptor
+    // over the tile's rows, with an out-of-range offset for the lanes past the last column
+    // or token (dropped by the hardware).
+    const __amdgpu_buffer_rsrc_t qrs =
+        __builtin_amdgcn_make_buffer_rsrc(q + (int64_t)t0 * ncols, 0, max(0, min(kQiRows, n_tok - t0)) * ncols * 2,
+                                          0x00020000);
 #pragma unroll
   for (int cb = 0; cb < kCB; ++cb) {
     const int c = c0 + wc * 32 * kCB + cb * 32 + l32;
     const bool col_ok = c < ncols;
     const QColFmt cf = qp_col(cmeta[cb], cbias[cb], calpha[cb], cbeta[cb]);
+    uint32_t unsure = 0;  // bit i: element i is live and uncertain
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int tl = wr * 32 + mfma32_row(i, lane);
-        const int t = t0 + tl;
-        const bool live = col_ok && t < n_tok;
-        bool sure = false;
-        if (live) {
-            // P by an fp64 Horner chain on the int32 sums (exact below 2^53, else four roundings)
-            double Pd = (double)acc[cb][0][i];
-            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][1][i]);
-            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][2][i]);
-            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][3][i]);
-            Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][4][i]);
-            uint16_t o;
-            sure = qp_certify(Pd, xpf[tl], xpi[tl], cf, d, &o);
-            if (sure) q[(int64_t)t * ncols + c] = o;
-        }
-        qp_queue(live && !sure, t * ncols + c, lane, count, list);
+        const bool live = col_ok && t0 + tl < n_tok;
+        // P by an fp64 Horner chain on the int32 sums (exact below 2^53, else four roundings)
+        double Pd = (double)acc[cb][0][i];
+        Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][1][i]);
+        Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][2][i]);
+        Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][3][i]);
+        Pd = __builtin_fma(Pd, 128.0, (double)acc[cb][4][i]);
+        uint16_t o;
+        const bool sure = qp_certify_bits(Pd, xpf[tl], xpi[tl], cf, d, &o);
+        __builtin_amdgcn_raw_buffer_store_b16(o, qrs, live ? (tl * ncols + c) * 2 : -1, 0, 0);
+        unsure |= (uint32_t)(live && !sure) << i;
+    }
+    while (__ballot(unsure != 0u)) {  // (rare) one uncertain element per lane and pass
+        const int i = __builtin_ctz(unsure | 0x10000u);
+        qp_queue(unsure != 0u, (t0 + wr * 32 + mfma32_row(i, lane)) * ncols + c, lane, count, list);
+        unsure &= unsure - 1u;
     }
   }
 }
