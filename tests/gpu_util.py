@@ -3,6 +3,7 @@ import numpy as np
 import torch
 
 from oracle import oracle as O
+from torch_reference import apply_from_routing
 
 
 def to_dev(a: np.ndarray, dt: str | None = None) -> torch.Tensor:
@@ -39,3 +40,18 @@ def check_out(out: np.ndarray, ref: np.ndarray, dt: str, signal: bool = False, n
         assert not bad.any(), f"{bad.sum()} bf16 elements out of tolerance, max |d|/max|ref| {(d / m).max():.3e}"
         nerr = np.linalg.norm(d) / max(np.linalg.norm(ref), 1e-30)
         assert nerr <= nerr_max, f"normalised error {nerr:.3e} > {nerr_max}"
+
+
+# Every token's output against the float32 expert stages (model.py:312-341) on the same
+# routing, measured against the size of the token's terms: the bf16 roundings of the
+# contract stay below this; a dropped pair or a pair on the wrong expert is ~1/sqrt(H k).
+ALL_TOKENS_BF16 = 2e-2
+
+
+def check_all_tokens(m, x, gates, ids, y, label):
+    with torch.no_grad():
+        yr, scale = apply_from_routing(m.state_dict(), x, gates, ids, m.num_heads)
+    err = (y.float() - yr).norm(dim=1) / scale.clamp_min(1e-3 * float(scale.max()))
+    print(f"{label}: all {err.numel()} tokens against the float32 expert stages: error / term size "
+          f"median {float(err.median()):.2e}, max {float(err.max()):.2e}", flush=True)
+    assert bool(torch.isfinite(y).all()) and float(err.max()) < ALL_TOKENS_BF16

@@ -8,7 +8,7 @@ import ethos_amd
 from ethos_amd import hip
 from ethos_amd.workloads import SHAPES, make_inputs
 from golden_util import load
-from gpu_util import check_out, to_dev, to_host
+from gpu_util import check_all_tokens, check_out, to_dev, to_host
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -154,6 +154,7 @@ def test_layer_cfg2_full_size():
     sub = np.arange(0, sh.n_tok, 8)
     r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub, q=qh)
     check_out(O.to_f32(to_host(y), "bf16")[sub], r["out"], "bf16", nerr_max=2e-3)
+    check_all_tokens(m, xd, gates, ids, y, "cfg2")
 
 
 def test_layer_cfg4_zipf_full_size():
@@ -199,6 +200,7 @@ def test_layer_cfg4_zipf_full_size():
     # output for a token subset
     r = O.layer_forward(xs, P, sh.num_heads, sh.top_k, "bf16", tokens=sub[::8], q=qh)
     check_out(O.to_f32(to_host(y), "bf16")[sub[::8]], r["out"], "bf16", nerr_max=2e-3)
+    check_all_tokens(m, xd, gates, ids, y, "cfg4")
 
 
 def test_router_rejects_cpu_and_bad_shapes():

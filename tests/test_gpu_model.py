@@ -20,7 +20,7 @@ from ethos_amd.layer import EthosExpertLayer
 from ethos_amd.model import CompressedMoEModel, init_random_, lm_config
 from ethos_amd.workloads import make_lm_inputs
 from golden_util import GOLDEN
-from gpu_util import check_out, to_host
+from gpu_util import check_all_tokens, check_out, to_host
 from oracle import oracle as O
 from torch_reference import lm_forward
 
@@ -140,3 +140,4 @@ def test_lm_whole_model_workload_full_size():
         r = O.layer_forward(xs, P, cfg.num_routing_heads, cfg.top_k, "bf16", tokens=y_sub, q=qh,
                             routed=(g_ref, ids_ref))
         check_out(O.to_f32(to_host(y), "bf16")[y_sub], r["out"], "bf16", nerr_max=2e-3)
+        check_all_tokens(layer, xf, gates, ids_l, y, f"block {i}")

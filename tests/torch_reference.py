@@ -65,6 +65,32 @@ def layer_forward(P: dict, x: torch.Tensor, n_heads: int, top_k: int, bn_batch_s
     return y, e
 
 
+def apply_from_routing(P: dict, x: torch.Tensor, gates: torch.Tensor, ids: torch.Tensor, n_heads: int,
+                       chunk: int = 2048):
+    """The expert stages of model.py:312-341 in float32 for a given routing (gates and ids
+    [n, H, k]), on x's device: y [n, d], and each token's scale sqrt(sum_p |a_p|^2 |v_p|^2) / H,
+    the size of its terms (an error measured against it does not grow where the terms cancel).
+    The hidden rows and v rows are computed once per distinct expert; the pairs in token chunks."""
+    n, d = x.shape
+    W1 = P["generation_network.net.0.weight"].float()
+    W2 = P["generation_network.net.2.weight"].float()
+    uniq, inv = torch.unique(ids.reshape(-1).long(), return_inverse=True)
+    hid = F.gelu(P["expert_latents.weight"][uniq].float() @ W1.t())   # [U, dh]
+    v = hid @ W2[d:].t()                                               # [U, d]
+    vn = v.norm(dim=1)
+    xp = x.float() @ W2[:d]                                            # [n, dh]
+    inv = inv.view(ids.shape)
+    y = torch.empty((n, d), dtype=torch.float32, device=x.device)
+    scale = torch.empty(n, dtype=torch.float32, device=x.device)
+    for t0 in range(0, n, chunk):
+        sl = inv[t0:t0 + chunk]
+        c = (hid[sl] * xp[t0:t0 + chunk, None, None, :]).sum(-1)
+        a = F.gelu(c) * gates[t0:t0 + chunk].float()
+        y[t0:t0 + chunk] = (a.unsqueeze(-1) * v[sl]).sum(dim=(1, 2)) / n_heads
+        scale[t0:t0 + chunk] = torch.sqrt(((a * vn[sl]) ** 2).sum(dim=(1, 2))) / n_heads
+    return y, scale
+
+
 # ----------------------------------------------------------------- whole language model
 def _rms(x, w, eps):
     xf = x.float()
