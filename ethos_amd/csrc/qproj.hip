@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void qproj_kernel(const T* __restrict__ x, con
 // non-finite value and sums within the bound of a rounding boundary are queued and
 // recomputed with the exact chain.
 // ---------------------------------------------------------------------------------
-constexpr int kQiKC = 64;               // reduction chunk (bytes of a digit row) staged in LDS
+constexpr int kQiPad = 64;              // digit rows are padded to a multiple of this many bytes
 constexpr int kQiMaxD = 16384;          // int32 digit-product sums cannot overflow below this
 
 struct QRowMeta {
@@ -123,7 +123,7 @@ struct QprojWs {
     int64_t* part;    // [kQiSplit][n_tok][ncols] partial sums (n_tok <= kQiSplitMaxTok only)
 };
 
-__host__ __device__ inline int qproj_dpad(int d) { return (d + kQiKC - 1) / kQiKC * kQiKC; }
+__host__ __device__ inline int qproj_dpad(int d) { return (d + kQiPad - 1) / kQiPad * kQiPad; }
 
 __host__ __device__ inline size_t qproj_align(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -339,32 +339,40 @@ __device__ __forceinline__ void qp_queue(bool queue, int e, int lane, int32_t* _
 }
 
 // Tile configuration: kWaves waves in kWaves / 2 rows x 2 columns, each wave 32 rows x
-// 32 kCB columns; kStages chunk buffers in LDS (kStages - 1 chunks in flight).
-template <int Waves, int CB, int Stages>
+// 32 kCB columns; reduction chunks of kKC bytes of every digit row; kStages chunk buffers in
+// LDS (kStages - 1 chunks in flight).  A chunk's copies are 1 KB blocks of kBR rows, dealt
+// to the waves in turn.
+template <int Waves, int CB, int Stages, int KC>
 struct QiCfg {
-    static constexpr int kWaves = Waves, kCB = CB, kStages = Stages;
+    static constexpr int kWaves = Waves, kCB = CB, kStages = Stages, kKC = KC;
     static constexpr int kRows = 16 * kWaves;  // = 32 (kWaves / 2)
     static constexpr int kCols = 64 * kCB;
-    static constexpr int kXB = kRows / (16 * kWaves);  // 16-row blocks each wave copies per x plane
-    static constexpr int kWB = kCols / (16 * kWaves);  // ... per w plane
-    static constexpr int kCopies = 3 * (kXB + kWB);    // 1 KB copies per wave per chunk
-    static constexpr int kStage = 3 * (kRows + kCols) * kQiKC;  // bytes of one chunk buffer
+    static constexpr int kSl = kKC / 16;      // 16-byte slots per staged row
+    static constexpr int kBR = 1024 / kKC;    // rows per 1 KB copy block
+    static constexpr int kXBlk = kRows / kBR, kWBlk = kCols / kBR;  // blocks per x / w plane
+    static constexpr int kCopies = 3 * (kXBlk + kWBlk) / kWaves;    // 1 KB copies per wave per chunk
+    static constexpr int kStage = 3 * (kRows + kCols) * kKC;        // bytes of one chunk buffer
     static constexpr size_t kTiles = (size_t)kStages * kStage;
     static constexpr size_t kSmem = kTiles + kRows * (sizeof(float4) + sizeof(int2));
-    static_assert(kXB == 1 && kWB >= 1 && kCols == 16 * kWaves * kWB, "copy blocks");
+    static_assert((kKC == 32 || kKC == 64) && kQiPad % kKC == 0, "chunk width");
+    static_assert(kRows % kBR == 0 && kCols % kBR == 0 && 3 * (kXBlk + kWBlk) % kWaves == 0, "copy blocks");
 };
-using QiLaunch = QiCfg<4, 1, 2>;
+using QiLaunch = QiCfg<4, 1, 2, 64>;
 
 // s_waitcnt with vmcnt(n) and no expcnt / lgkmcnt wait (gfx9 encoding: vmcnt bits [3:0]
 // and [15:14], expcnt [6:4], lgkmcnt [11:8])
 constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
 
-// LDS chunk buffer layout: x digit planes 0-2 (kRows rows of 64 bytes each), then w digit
-// planes 0-2 (kCols rows each); each row's four 16-byte slots XOR-swizzled with bits 2-3 of
-// the row so that the MFMA fragment reads (16 lanes on 16 consecutive rows, one slot) hit 64
-// distinct banks.  The chunk buffers form a ring: the copies of the next kStages - 1 chunks
-// are in flight while one chunk is multiplied.
-__device__ __forceinline__ int qi_slot(int row, int piece) { return piece ^ ((row >> 2) & 3); }
+// LDS chunk buffer layout: x digit planes 0-2 (kRows rows of kKC bytes each), then w digit
+// planes 0-2 (kCols rows each); each row's 16-byte slots XOR-swizzled (64-byte rows: with
+// bits 2-3 of the row; 32-byte rows: with bit 3) so that the MFMA fragment reads (16 lanes
+// on 16 consecutive rows, one slot) hit 64 distinct banks.  The chunk buffers form a ring:
+// the copies of the next kStages - 1 chunks are in flight while one chunk is multiplied.
+template <int KC>
+__device__ __forceinline__ int qi_slot(int row, int piece) {
+    if constexpr (KC == 64) return piece ^ ((row >> 2) & 3);
+    else return piece ^ ((row >> 3) & 1);
+}
 
 // Tile order of the i8 product kernel, for the per-XCD L2s (workgroup b runs on XCD
 // b % 8): the tiles are ordered by column group of kQiColGroup column tiles, then row
@@ -389,7 +397,7 @@ __device__ __forceinline__ bool qi_tile_t(int n_tok, int ncols, int* t0, int* c0
     return true;
 }
 
-template <int kWaves, int kCB, int kStages, bool kSplit>
+template <int kWaves, int kCB, int kStages, int kKC, bool kSplit>
 __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __restrict__ xdig,
                                                                  const int8_t* __restrict__ wdig,
                                                                  const QRowMeta* __restrict__ xmeta,
@@ -400,7 +408,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
                                                                  int ncols, int32_t* __restrict__ count,
                                                                  int32_t* __restrict__ list,
                                                                  uint16_t* __restrict__ q, int64_t* __restrict__ part) {
-    using C = QiCfg<kWaves, kCB, kStages>;
+    using C = QiCfg<kWaves, kCB, kStages, kKC>;
     constexpr int kQiRows = C::kRows, kQiCols = C::kCols;
     auto qi_tile = [](int n, int nc, int* t, int* c) { return qi_tile_t<kQiRows, kQiCols>(n, nc, t, c); };
     extern __shared__ __align__(16) unsigned char qsm[];
@@ -408,7 +416,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     // x row formats, scaled by 2^-E_x: {max|x| 2^-E, |x|_1 2^-E, n_inex 2^-21} and {E, n_inex}
     float4* xpf = reinterpret_cast<float4*>(qsm + C::kTiles);
     int2* xpi = reinterpret_cast<int2*>(qsm + C::kTiles + kQiRows * sizeof(float4));
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int wr = wave >> 1, wc = wave & 1;  // rows 32 wr .., columns 32 kCB wc ..
     int t0, c0;
@@ -416,7 +424,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     const int dpad = qproj_dpad(d);
     // the chunks this workgroup reduces: all of them, or (kSplit) range blockIdx.y of
     // gridDim.y ranges (possibly empty: its partial sums are then zero)
-    const int nch = dpad / kQiKC;
+    const int nch = dpad / kKC;
     int k_lo = 0, k_hi = nch;
     if constexpr (kSplit) {
         const int cps = (nch + (int)gridDim.y - 1) / (int)gridDim.y;
@@ -425,10 +433,11 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     }
     const int64_t xplane = (int64_t)n_tok * dpad, wplane = (int64_t)ncols * dpad;
 
-    // Copies: wave w moves 16-row block w of every x plane and blocks w, w + kWaves, ... of
-    // every w plane, 1 KB each; lane l writes block bytes 16 l .. 16 l + 15 = block row
-    // l / 4, slot l % 4, so it loads the piece that the swizzle puts in that slot.  Buffer
-    // descriptors bounded by the tile's live rows return zeros past the last token / column.
+    // Copies: the chunk's 1 KB blocks (x planes 0-2, then w planes 0-2, each plane's blocks of
+    // kBR rows in order) go to the waves in turn, block b to wave b % kWaves; lane l writes
+    // block bytes 16 l .. 16 l + 15 = block row l / kSl, slot l % kSl, so it loads the piece
+    // that the swizzle puts in that slot.  Buffer descriptors bounded by the tile's live rows
+    // return zeros past the last token / column.
     const int xrows = max(0, min(kQiRows, n_tok - t0)), wrows = max(0, min(kQiCols, ncols - c0));
     i32x4_t rs[6];
 #pragma unroll
@@ -440,29 +449,35 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     for (int r = 0; r < 6; ++r)
 #pragma unroll
         for (int j = 0; j < 4; ++j) rs[r][j] = __builtin_amdgcn_readfirstlane(rs[r][j]);
-    auto xplane_lds = [&](int stage, int p) { return tiles + (size_t)stage * C::kStage + p * kQiRows * kQiKC; };
+    auto xplane_lds = [&](int stage, int p) { return tiles + (size_t)stage * C::kStage + p * kQiRows * kKC; };
     auto wplane_lds = [&](int stage, int p) {
-        return tiles + (size_t)stage * C::kStage + (3 * kQiRows + p * kQiCols) * kQiKC;
+        return tiles + (size_t)stage * C::kStage + (3 * kQiRows + p * kQiCols) * kKC;
     };
-    const int xrow = 16 * wave + lane / 4;
-    const int xvoff = xrow * dpad + 16 * qi_slot(xrow, lane % 4);
+    // this wave's blocks: descriptor, LDS offset within a chunk buffer and lane offset
+    i32x4_t brs[C::kCopies];
+    int blds[C::kCopies], bvoff[C::kCopies];
+#pragma unroll
+    for (int j = 0; j < C::kCopies; ++j) {
+        const int b = wave + kWaves * j;  // wave-uniform
+        const bool isw = b >= 3 * C::kXBlk;
+        const int bb = isw ? b - 3 * C::kXBlk : b, nb = isw ? C::kWBlk : C::kXBlk;
+        const int p = bb / nb, rb = bb - p * nb;
+        const int row = rb * C::kBR + lane / C::kSl;
+        brs[j] = rs[(isw ? 3 : 0) + p];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) brs[j][q] = __builtin_amdgcn_readfirstlane(brs[j][q]);  // (scalar operands)
+        blds[j] = __builtin_amdgcn_readfirstlane((isw ? 3 * kQiRows + p * kQiCols : p * kQiRows) * kKC + rb * 1024);
+        bvoff[j] = row * dpad + 16 * qi_slot<kKC>(row, lane % C::kSl);
+    }
     auto issue = [&](int k0, int stage) {
 #pragma unroll
-        for (int p = 0; p < 3; ++p) lds_dma16(rs[p], xvoff, k0, lds_addr(xplane_lds(stage, p) + wave * 1024));
-#pragma unroll
-        for (int j = 0; j < C::kWB; ++j) {
-            const int blk = wave + kWaves * j;
-            const int wrow = 16 * blk + lane / 4;
-            const int wvoff = wrow * dpad + 16 * qi_slot(wrow, lane % 4);
-#pragma unroll
-            for (int p = 0; p < 3; ++p)
-                lds_dma16(rs[3 + p], wvoff, k0, lds_addr(wplane_lds(stage, p) + blk * 1024));
-        }
+        for (int j = 0; j < C::kCopies; ++j)
+            lds_dma16(brs[j], bvoff[j], k0, lds_addr(tiles + (size_t)stage * C::kStage + blds[j]));
     };
     static_assert(kStages >= 2 && kStages <= 4, "waits cover at most two chunks in flight past the current one");
 
     // the first chunk's copies go out before the metadata loads, so that one wait covers both
-    if (k_lo < k_hi) issue(k_lo * kQiKC, 0);
+    if (k_lo < k_hi) issue(k_lo * kKC, 0);
     if (!kSplit && tid < kQiRows && t0 + tid < n_tok) {
         const QRowMeta m = xmeta[t0 + tid];
         xpf[tid] = qp_xf(m);
@@ -495,7 +510,7 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
     const int arow = wr * 32 + l32;
 #pragma unroll
     for (int j = 1; j < kStages - 1; ++j)
-        if (k_lo + j < k_hi) issue((k_lo + j) * kQiKC, j);
+        if (k_lo + j < k_hi) issue((k_lo + j) * kKC, j);
     for (int kc = k_lo; kc < k_hi; ++kc) {
         const int stage = (kc - k_lo) % kStages;
         // this wave's copies of chunk kc have landed once at most those of the chunks after
@@ -509,18 +524,18 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * C::kCopies));
         __syncthreads();  // every wave's copies of chunk kc landed; chunk kc - 1 fully read
         const int kn = kc + kStages - 1;
-        if (kn < k_hi) issue(kn * kQiKC, (kn - k_lo) % kStages);  // into chunk kc - 1's buffer
+        if (kn < k_hi) issue(kn * kKC, (kn - k_lo) % kStages);  // into chunk kc - 1's buffer
 #pragma unroll
-        for (int s = 0; s < kQiKC; s += 32) {
+        for (int s = 0; s < kKC; s += 32) {
             const int piece = s / 16 + h;
             i32x4_t a[3], b[kCB][3];
-            const int aoff = arow * kQiKC + 16 * qi_slot(arow, piece);
+            const int aoff = arow * kKC + 16 * qi_slot<kKC>(arow, piece);
 #pragma unroll
             for (int p = 0; p < 3; ++p) a[p] = *reinterpret_cast<const i32x4_t*>(xplane_lds(stage, p) + aoff);
 #pragma unroll
             for (int cb = 0; cb < kCB; ++cb) {
                 const int brow = wc * 32 * kCB + cb * 32 + l32;
-                const int boff = brow * kQiKC + 16 * qi_slot(brow, piece);
+                const int boff = brow * kKC + 16 * qi_slot<kKC>(brow, piece);
 #pragma unroll
                 for (int p = 0; p < 3; ++p) b[cb][p] = *reinterpret_cast<const i32x4_t*>(wplane_lds(stage, p) + boff);
             }
@@ -757,7 +772,7 @@ int launch_qproj(const void* x, const void* w, const void* prepared, const void*
         const int64_t tiles = (int64_t)((ncols + C::kCols - 1) / C::kCols) * ((n_tok + C::kRows - 1) / C::kRows);
         const unsigned tgrid = (unsigned)(8 * ((tiles + 7) / 8));  // qi_tile_t: XCD-grouped tile order
         if (W.part != nullptr) {
-            hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, true>), dim3(tgrid, kQiSplit),
+            hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, C::kKC, true>), dim3(tgrid, kQiSplit),
                                dim3(C::kWaves * 64), C::kSmem, stream, W.xdig, wdig, W.meta, wmeta,
                                (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q,
                                W.part);
@@ -766,7 +781,7 @@ int launch_qproj(const void* x, const void* w, const void* prepared, const void*
                                (const int64_t*)W.part, (const QRowMeta*)W.meta, wmeta, (const uint16_t*)b, alpha, beta,
                                (int)n_tok, d, ncols, kQiSplit, W.count, W.list, (uint16_t*)q);
         } else {
-            hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, false>), dim3(tgrid),
+            hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, C::kKC, false>), dim3(tgrid),
                                dim3(C::kWaves * 64), C::kSmem, stream, W.xdig, wdig, W.meta, wmeta,
                                (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q,
                                (int64_t*)nullptr);
