@@ -325,91 +325,137 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats(const uint32_t* __restr
     }
 }
 
-// One wave per digit: exclusive prefix of the digit's tile counts over the tiles (in
+// One workgroup per digit: exclusive prefix of the digit's tile counts over the tiles (in
 // place), the total to tot[d].  Last pass (kLast): also the lower bits of the last key of
 // the digit in earlier tiles, as llo + 1 (0: none; in place of llo), by a prefix maximum
 // (the keys of one digit do not decrease over the tiles), and the exclusive prefix of the
 // new distinct keys, dist - [the tile's first key equals that last key] (in place of dist),
-// its total to stot[d].
+// its total to stot[d].  Thread i takes 4 consecutive tiles per round of 1,024 (16-byte
+// loads: rows start at multiples of 8 words), the waves' totals meet in LDS.
+constexpr int kScanThreads = 256, kScanPer = 4, kScanRound = kScanThreads * kScanPer;
+
+// Inclusive scan over the workgroup's threads in order of a sum and a maximum, returning
+// the exclusive prefixes; *tot_c / *tot_m get the workgroup's totals.  Ends with a barrier,
+// so sh can be used again at once.
+__device__ __forceinline__ void scan_block_sum_max(uint32_t c, uint32_t m, uint32_t* sh, uint32_t* ex_c,
+                                                   uint32_t* ex_m, uint32_t* tot_c, uint32_t* tot_m) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t ic = c, im = m;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t u = __shfl_up(ic, off, 64), w = __shfl_up(im, off, 64);
+        if (lane >= off) {
+            ic += u;
+            im = max(im, w);
+        }
+    }
+    if (lane == 63) {
+        sh[wave] = ic;
+        sh[4 + wave] = im;
+    }
+    __syncthreads();
+    uint32_t pc = 0, pm = 0, tc = 0, tm = 0;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+        const uint32_t a = sh[w], b = sh[4 + w];
+        if (w < wave) {
+            pc += a;
+            pm = max(pm, b);
+        }
+        tc += a;
+        tm = max(tm, b);
+    }
+    *ex_c = pc + ic - c;
+    const uint32_t pmw = __shfl_up(im, 1, 64);
+    *ex_m = max(pm, lane == 0 ? 0u : pmw);
+    *tot_c = tc;
+    *tot_m = tm;
+    __syncthreads();
+}
+
 template <bool kLast>
-__global__ __launch_bounds__(256) void tsort_scan(uint32_t* __restrict__ cnt, uint32_t* __restrict__ dist,
-                                                  const uint32_t* __restrict__ flo, uint32_t* __restrict__ llo,
-                                                  int n_tiles, uint32_t* __restrict__ tot,
-                                                  uint32_t* __restrict__ stot) {
-    const int lane = threadIdx.x & 63;
-    const int d = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (d >= kRadix) return;
+__global__ __launch_bounds__(kScanThreads) void tsort_scan(uint32_t* __restrict__ cnt, uint32_t* __restrict__ dist,
+                                                           const uint32_t* __restrict__ flo,
+                                                           uint32_t* __restrict__ llo, int n_tiles,
+                                                           uint32_t* __restrict__ tot, uint32_t* __restrict__ stot) {
+    __shared__ uint32_t sh[8];
+    const int d = blockIdx.x;
     const int64_t pitch = sort_tile_pitch(n_tiles);
     uint32_t* crow = cnt + (int64_t)d * pitch;
     uint32_t* drow = dist + (int64_t)d * pitch;
     const uint32_t* frow = flo + (int64_t)d * pitch;
     uint32_t* lrow = llo + (int64_t)d * pitch;
     uint32_t carry_c = 0, carry_s = 0, carry_l = 0;
-    constexpr int kPer = 8;
-    for (int t0 = 0; t0 < n_tiles; t0 += 64 * kPer) {
-        uint32_t c[kPer], ds[kPer], fl[kPer], le[kPer];
-        uint32_t sc = 0, ml = 0;
+    for (int t0 = 0; t0 < n_tiles; t0 += kScanRound) {
+        const int tb = t0 + kScanPer * (int)threadIdx.x;
+        // a row holds pitch >= n_tiles words, pitch % 8 == 0: the 16-byte load at tb < n_tiles
+        // stays in the row; tiles from n_tiles on count as empty
+        uint4 c4 = make_uint4(0u, 0u, 0u, 0u), d4 = c4, f4 = c4, l4 = c4;
+        if (tb < n_tiles) {
+            c4 = *reinterpret_cast<const uint4*>(crow + tb);
+            if (kLast) {
+                d4 = *reinterpret_cast<const uint4*>(drow + tb);
+                f4 = *reinterpret_cast<const uint4*>(frow + tb);
+                l4 = *reinterpret_cast<const uint4*>(lrow + tb);
+            }
+        }
+        uint32_t c[kScanPer] = {c4.x, c4.y, c4.z, c4.w}, ds[kScanPer] = {d4.x, d4.y, d4.z, d4.w};
+        const uint32_t fl[kScanPer] = {f4.x, f4.y, f4.z, f4.w}, lv[kScanPer] = {l4.x, l4.y, l4.z, l4.w};
+        uint32_t sc = 0, ml = 0, le[kScanPer];
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int t = t0 + lane * kPer + j;
-            const bool v = t < n_tiles;
-            c[j] = v ? crow[t] : 0u;
+        for (int j = 0; j < kScanPer; ++j) {
+            if (tb + j >= n_tiles) c[j] = ds[j] = 0u;
             sc += c[j];
-            if (kLast) {
-                ds[j] = v ? drow[t] : 0u;
-                fl[j] = v ? frow[t] : 0u;
-                const uint32_t l = v ? lrow[t] : 0u;  // loaded with the others, used when c[j] > 0
-                le[j] = c[j] ? l + 1u : 0u;
-                ml = max(ml, le[j]);
-            }
+            le[j] = c[j] ? lv[j] + 1u : 0u;
+            ml = max(ml, le[j]);
         }
-        // inclusive wave scans of the lane totals (sum of counts; max of the last keys)
-        uint32_t ic = sc, il = ml;
+        uint32_t ex_c, ex_l, tc, tl;
+        scan_block_sum_max(sc, kLast ? ml : 0u, sh, &ex_c, &ex_l, &tc, &tl);
+        uint32_t run_c = carry_c + ex_c, run_l = max(carry_l, ex_l);
+        uint32_t oc[kScanPer], ol[kScanPer], nd[kScanPer], sn = 0;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t u = __shfl_up(ic, off, 64);
-            const uint32_t w = __shfl_up(il, off, 64);
-            if (lane >= off) {
-                ic += u;
-                il = max(il, w);
-            }
-        }
-        uint32_t run_c = carry_c + ic - sc;
-        uint32_t run_l = max(carry_l, (uint32_t)__shfl_up(il, 1, 64));
-        if (lane == 0) run_l = carry_l;
-        uint32_t nd[kPer], sn = 0;
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int t = t0 + lane * kPer + j;
-            if (t < n_tiles) crow[t] = run_c;
+        for (int j = 0; j < kScanPer; ++j) {
+            oc[j] = run_c;
             run_c += c[j];
-            if (kLast) {
-                nd[j] = ds[j] - (c[j] && run_l != 0u && fl[j] + 1u == run_l ? 1u : 0u);
-                sn += nd[j];
-                if (t < n_tiles) lrow[t] = run_l;
-                run_l = max(run_l, le[j]);
-            }
+            nd[j] = ds[j] - (c[j] && run_l != 0u && fl[j] + 1u == run_l ? 1u : 0u);
+            sn += nd[j];
+            ol[j] = run_l;
+            run_l = max(run_l, le[j]);
         }
-        carry_c += __shfl(ic, 63, 64);
+        uint32_t os[kScanPer];
         if (kLast) {
-            uint32_t is = sn;
+            uint32_t ex_s, ts, unused_m, unused_t;
+            scan_block_sum_max(sn, 0u, sh, &ex_s, &unused_m, &ts, &unused_t);
+            uint32_t run_s = carry_s + ex_s;
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t u = __shfl_up(is, off, 64);
-                if (lane >= off) is += u;
-            }
-            uint32_t run_s = carry_s + is - sn;
-#pragma unroll
-            for (int j = 0; j < kPer; ++j) {
-                const int t = t0 + lane * kPer + j;
-                if (t < n_tiles) drow[t] = run_s;
+            for (int j = 0; j < kScanPer; ++j) {
+                os[j] = run_s;
                 run_s += nd[j];
             }
-            carry_s += __shfl(is, 63, 64);
-            carry_l = max(carry_l, __shfl(il, 63, 64));
+            carry_s += ts;
+            carry_l = max(carry_l, tl);
+        }
+        carry_c += tc;
+        if (tb + kScanPer <= n_tiles) {
+            *reinterpret_cast<uint4*>(crow + tb) = make_uint4(oc[0], oc[1], oc[2], oc[3]);
+            if (kLast) {
+                *reinterpret_cast<uint4*>(drow + tb) = make_uint4(os[0], os[1], os[2], os[3]);
+                *reinterpret_cast<uint4*>(lrow + tb) = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j) {
+                if (tb + j < n_tiles) {
+                    crow[tb + j] = oc[j];
+                    if (kLast) {
+                        drow[tb + j] = os[j];
+                        lrow[tb + j] = ol[j];
+                    }
+                }
+            }
         }
     }
-    if (lane == 0) {
+    if (threadIdx.x == 0) {
         tot[d] = carry_c;
         if (kLast) stot[d] = carry_s;
     }
@@ -901,7 +947,7 @@ int launch_sort_segment(const int32_t* ids, int64_t n, int64_t n_experts, void* 
     int32_t* table = sort_table_words(n, n_experts) ? reinterpret_cast<int32_t*>(stot + kRadix + 64) : nullptr;
     // keys compare on the bits the passes sort (those of ids below n_experts)
     const uint32_t mkmask = kRadixBits * passes >= 32 ? 0xffffffffu : (1u << (kRadixBits * passes)) - 1u;
-    const dim3 tg(tsort_grid(n_tiles)), tb(kTThreads), sg((unsigned)(kRadix / 4)), sb(256);
+    const dim3 tg(tsort_grid(n_tiles)), tb(kTThreads), sg((unsigned)kRadix), sb(kScanThreads);
     for (int p = 0; p < passes; ++p) {
         const uint32_t* kin = p == 0 ? reinterpret_cast<const uint32_t*>(ids) : kbuf[(p - 1) & 1];
         const uint32_t* vin = p == 0 ? nullptr : vbuf[(p - 1) & 1];

@@ -105,7 +105,8 @@ def test_route_ties_break_to_lowest_index():
                                          (300000, 2 ** 21, "same"), (300000, 2 ** 21, "skew"),
                                          (300000, 2 ** 21, "hot3d"), (2 ** 20, 262144, "same"),
                                          (2 ** 20 + 1, 262144, "same"), (2 ** 21 + 7, 262144, "hot2d"),
-                                         (2 ** 20 + 3, 7, "rand"), (2 ** 20 + 5, 2 ** 21, "skew")])
+                                         (2 ** 20 + 3, 7, "rand"), (2 ** 20 + 5, 2 ** 21, "skew"),
+                                         (4096 * 1024 + 4097, 262144, "rand"), (4096 * 1024 + 4097, 262144, "skew")])
 def test_sort_segment_exact(n, E, pattern):
     """The sort against the oracle's counting sort: one pass (E = 7), two (4,096 and 262,144
     experts) and three (2^21) over tiles of 4,096 pairs; batches up to 16,384 pairs take the
@@ -113,7 +114,8 @@ def test_sort_segment_exact(n, E, pattern):
     expert -> slot table for pair_slot.  Patterns: uniform ids, one id everywhere (one segment spanning
     every tile), Zipf-skewed ids, half the pairs on the largest id, and ids whose two
     9-bit digits (or, with 2^21 experts, all three digits) are Zipf-skewed (hot experts
-    whose segments cross tile boundaries, in the three-pass path too)."""
+    whose segments cross tile boundaries, in the three-pass path too).  Above 1,024 tiles the
+    per-digit scans over the tiles take more than one round."""
     rng = np.random.default_rng(n + E)
     if pattern == "hot3d":
         a = np.minimum(rng.zipf(1.1, n), 512) - 1
