@@ -228,9 +228,11 @@ __global__ __launch_bounds__(kTThreads) void tsort_count(const uint32_t* __restr
 // Per-tile statistics of the last pass (keys sorted by their lower bits lo = key & lomask),
 // for each digit d of the tile: cnt (keys), dist (distinct keys), flo / llo (lower bits of
 // the digit's first and last key in the tile's order, i.e. the smallest and largest).
-// Keys of at most 18 bits (two passes): distinct keys counted with a bitmap of all keys in
-// LDS (a key's bit is set by one of its copies first, whichever), flo / llo by atomic
-// min / max.
+// Keys of at most 18 bits (two passes): every key sets its bit in a bitmap of all keys in
+// LDS; with shift = 9 a digit's keys are the 512 bits [512 d, 512 d + 512) of it, so its
+// distinct keys are their population count and flo / llo the lowest and highest set bit
+// (two threads per digit, 256 bits each); with shift = 0 (one pass) a digit is one key.
+// The only atomics per key are the count and the (no-return) bit set.
 __global__ __launch_bounds__(kTThreads) void tsort_stats_map(const uint32_t* __restrict__ keys, int64_t n, int shift,
                                                              uint32_t mkmask, int n_tiles, uint32_t* __restrict__ cnt,
                                                              uint32_t* __restrict__ dist, uint32_t* __restrict__ flo,
@@ -238,40 +240,56 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats_map(const uint32_t* __r
     const int tile = tsort_tile(n_tiles);
     if (tile < 0) return;
     constexpr int kMapWords = (1 << (2 * kRadixBits)) / 32;
+    static_assert(kTThreads == 2 * kRadix, "two threads per digit");
     __shared__ uint4 seen[kMapWords / 4];
-    __shared__ uint32_t c[kRadix], dc[kRadix], mn[kRadix], mx[kRadix];
+    __shared__ uint32_t c[kRadix];
     const int tid = threadIdx.x;
     const int64_t base = (int64_t)tile * kTile + tid;
     uint32_t k[kTPer];
 #pragma unroll
     for (int j = 0; j < kTPer; ++j) k[j] = base + j * kTThreads < n ? keys[base + j * kTThreads] & mkmask : 0u;
     for (int e = tid; e < kMapWords / 4; e += kTThreads) seen[e] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid < kRadix) {
-        c[tid] = dc[tid] = mx[tid] = 0u;
-        mn[tid] = 0xffffffffu;
-    }
+    if (tid < kRadix) c[tid] = 0u;
     __syncthreads();
     uint32_t* sw = reinterpret_cast<uint32_t*>(seen);
-    const uint32_t lomask = (1u << shift) - 1u;
 #pragma unroll
     for (int j = 0; j < kTPer; ++j) {
         if (base + j * kTThreads < n) {
-            const uint32_t d = (k[j] >> shift) & (kRadix - 1), lo = k[j] & lomask;
-            const uint32_t bit = 1u << (k[j] & 31u);
-            atomicAdd(&c[d], 1u);
-            atomicMin(&mn[d], lo);
-            atomicMax(&mx[d], lo);
-            if (!(atomicOr(&sw[(k[j] >> 5) & (kMapWords - 1)], bit) & bit)) atomicAdd(&dc[d], 1u);
+            atomicAdd(&c[(k[j] >> shift) & (kRadix - 1)], 1u);
+            __hip_atomic_fetch_or(&sw[(k[j] >> 5) & (kMapWords - 1)], 1u << (k[j] & 31u), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
     __syncthreads();
-    if (tid < kRadix) {
-        const int64_t o = (int64_t)tid * sort_tile_pitch(n_tiles) + tile;
-        const uint32_t cc = c[tid];
+    // digit d = tid / 2; this thread's half of the digit's 512 bits: words 16 d + 8 h .. + 7
+    const int d = tid >> 1, h = tid & 1;
+    uint32_t pc = 0, lo_b = 0xffffffffu, hi_b = 0u;
+    if (shift != 0) {
+        const uint4 a = seen[4 * d + 2 * h], b = seen[4 * d + 2 * h + 1];
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 7; i >= 0; --i) {
+            pc += __popc(w[i]);
+            if (w[i]) lo_b = 256u * h + 32u * i + __builtin_ctz(w[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (w[i]) hi_b = 256u * h + 32u * i + 31u - __builtin_clz(w[i]);
+    }
+    const uint32_t pc_o = __shfl_xor(pc, 1, 64), lo_o = __shfl_xor(lo_b, 1, 64), hi_o = __shfl_xor(hi_b, 1, 64);
+    if (h == 0) {
+        const int64_t o = (int64_t)d * sort_tile_pitch(n_tiles) + tile;
+        const uint32_t cc = c[d];
         cnt[o] = cc;
-        dist[o] = dc[tid];
-        flo[o] = cc ? mn[tid] : 0u;
-        llo[o] = cc ? mx[tid] : 0u;
+        if (shift != 0) {
+            dist[o] = pc + pc_o;
+            flo[o] = cc ? min(lo_b, lo_o) : 0u;
+            llo[o] = cc ? (hi_o ? hi_o : hi_b) : 0u;
+        } else {
+            dist[o] = cc ? 1u : 0u;
+            flo[o] = 0u;
+            llo[o] = 0u;
+        }
     }
 }
 
