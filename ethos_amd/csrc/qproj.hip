@@ -115,8 +115,6 @@ constexpr int kQiSplit = 8;
 constexpr int64_t kQiSplitMaxTok = 128;
 
 struct QprojWs {
-    int32_t* count;   // [1]   uncertain elements
-    int32_t* list;    // [n_tok * ncols]
     int8_t* xdig;     // [3][n_tok][dpad]
     int8_t* wdig;     // [3][ncols][dpad]
     QRowMeta* meta;   // [n_tok + ncols]: x rows, then Wq rows
@@ -130,18 +128,13 @@ __host__ __device__ inline size_t qproj_align(size_t b) { return (b + 255) & ~(s
 __host__ __device__ inline size_t qproj_ws_bytes(int64_t n_tok, int ncols, int d) {
     const size_t rows = (size_t)n_tok + (size_t)ncols;
     const size_t part = n_tok <= kQiSplitMaxTok ? (size_t)kQiSplit * (size_t)n_tok * (size_t)ncols * 8 : 0;
-    return 256 + qproj_align(4 * (size_t)n_tok * ncols) + qproj_align(3 * rows * (size_t)qproj_dpad(d)) +
-           qproj_align(sizeof(QRowMeta) * rows) + qproj_align(part);
+    return qproj_align(3 * rows * (size_t)qproj_dpad(d)) + qproj_align(sizeof(QRowMeta) * rows) + qproj_align(part);
 }
 
 __host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols, int d) {
     unsigned char* p = reinterpret_cast<unsigned char*>(ws);
     const size_t dpad = (size_t)qproj_dpad(d);
     QprojWs w;
-    w.count = reinterpret_cast<int32_t*>(p);
-    p += 256;
-    w.list = reinterpret_cast<int32_t*>(p);
-    p += qproj_align(4 * (size_t)n_tok * ncols);
     w.xdig = reinterpret_cast<int8_t*>(p);
     w.wdig = w.xdig + 3 * (size_t)n_tok * dpad;
     p += qproj_align(3 * ((size_t)n_tok + ncols) * dpad);
@@ -154,14 +147,12 @@ __host__ __device__ inline QprojWs qproj_ws(void* ws, int64_t n_tok, int ncols, 
 __device__ __forceinline__ uint32_t qp_wave_max_u32(uint32_t v) { return (uint32_t)wave_max_u64((uint64_t)v); }
 
 // One wave per row of x (rows < n_tok) or Wq (the n_rows - n_tok rows after them): digit
-// planes and the row's format.  The first thread also resets the uncertain-element count,
-// if given (read by the kernels after this one on the same stream).
+// planes and the row's format.
 __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ w, int n_tok, int ncols,
                                                            int64_t n_rows, int d, int8_t* __restrict__ xdig,
                                                            int8_t* __restrict__ wdig, QRowMeta* __restrict__ xmeta,
-                                                           QRowMeta* __restrict__ wmeta, int32_t* __restrict__ count) {
-    if (count != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *count = 0;
+                                                           QRowMeta* __restrict__ wmeta) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n_rows) return;
@@ -325,16 +316,82 @@ __device__ __forceinline__ bool qp_certify(double Pd, float4 xf, int2 xi, const 
     return sure;
 }
 
-// Queue the lanes' uncertain elements e (queue true) on the exact-chain list.
-__device__ __forceinline__ void qp_queue(bool queue, int e, int lane, int32_t* __restrict__ count,
-                                         int32_t* __restrict__ list) {
-    const uint64_t bal = __ballot(queue);
-    if (bal) {
-        const int leader = __builtin_ctzll(bal);
-        int base = 0;
-        if (lane == leader) base = atomicAdd(count, (int)__popcll(bal));
-        base = __shfl(base, leader, 64);
-        if (queue) list[base + (int)__popcll(bal & ((1ull << lane) - 1ull))] = e;
+// The exact fp64 chain of one element e = t ncols + c (index order, as the contract defines),
+// computed by the whole wave (every lane calls with the same e); lane 0 stores the element.
+// A bf16 x bf16 product is exact in fp64 (16 significant bits, exponents within [-266,
+// 256]), so fma(x_i, w_i, acc) == acc + x_i w_i bit for bit.  Exactness test: every product
+// is an integer multiple of 2^L, L the smallest lowest-bit exponent of the non-zero products
+// (a bf16 value with biased exponent b is a multiple of 2^(max(b, 1) - 134)), and so is every
+// partial sum, in any order, of magnitude at most S = sum |x_i w_i|.  When S < 2^(L + 53)
+// every such sum is exact in fp64: the chain never rounds and equals the wave's sum in any
+// order.  (S is taken with a factor-2 margin for the rounding of its own sum; a non-finite
+// product makes S non-finite and fails the test.)  Otherwise the lanes write the products of
+// `chunk` indices at a time (a multiple of 8) to the wave's LDS scratch pw and lane 0 adds
+// them in order.
+__device__ __forceinline__ void qp_exact_element(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                              const uint16_t* __restrict__ bias, const float* __restrict__ alpha,
+                                              const float* __restrict__ beta, int d, int ncols, int64_t e,
+                                              double* pw, int chunk, uint16_t* __restrict__ q) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = e / ncols;
+    const int c = (int)(e - t * ncols);
+    const uint16_t* xr = x + t * d;
+    const uint16_t* wr = w + (int64_t)c * d;
+    double ls = 0.0, la = 0.0;
+    int lmin = 0x7fffffff;
+    for (int g = lane; g < d / 8; g += kWave) {
+        const uint4 xa = *reinterpret_cast<const uint4*>(xr + 8 * g);
+        const uint4 wa = *reinterpret_cast<const uint4*>(wr + 8 * g);
+        const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
+        const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t xb = (xv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+            const uint32_t wb = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+            const double pj = (double)__uint_as_float(xb << 16) * (double)__uint_as_float(wb << 16);
+            if (pj != 0.0) {
+                const int lx = max((int)((xb >> 7) & 0xffu), 1) - 134;
+                const int lw = max((int)((wb >> 7) & 0xffu), 1) - 134;
+                lmin = min(lmin, lx + lw);
+            }
+            ls += pj;
+            la += fabs(pj);
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        ls += __shfl_xor(ls, m, kWave);
+        la += __shfl_xor(la, m, kWave);
+        lmin = min(lmin, __shfl_xor(lmin, m, kWave));
+    }
+    double acc = ls;
+    if (!(lmin == 0x7fffffff || la < ldexp(1.0, lmin + 52))) {
+        acc = 0.0;
+        for (int k0 = 0; k0 < d; k0 += chunk) {
+            const int len = min(chunk, d - k0);  // a multiple of 8
+            for (int g = lane; g < len / 8; g += kWave) {
+                const uint4 xa = *reinterpret_cast<const uint4*>(xr + k0 + 8 * g);
+                const uint4 wa = *reinterpret_cast<const uint4*>(wr + k0 + 8 * g);
+                const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
+                const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    pw[8 * g + 2 * j] = (double)__uint_as_float(xv[j] << 16) * (double)__uint_as_float(wv[j] << 16);
+                    pw[8 * g + 2 * j + 1] =
+                        (double)__uint_as_float(xv[j] & 0xffff0000u) * (double)__uint_as_float(wv[j] & 0xffff0000u);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) {
+#pragma unroll 8
+                for (int i = 0; i < len; ++i) acc = acc + pw[i];
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    if (lane == 0) {
+        const float ql = Elem<uint16_t>::round64(acc + (double)bf16_bits_to_f32(bias[c]));
+        q[e] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
     }
 }
 
@@ -405,8 +462,8 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
                                                                  const uint16_t* __restrict__ bias,
                                                                  const float* __restrict__ alpha,
                                                                  const float* __restrict__ beta, int n_tok, int d,
-                                                                 int ncols, int32_t* __restrict__ count,
-                                                                 int32_t* __restrict__ list,
+                                                                 int ncols, const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w,
                                                                  uint16_t* __restrict__ q, int64_t* __restrict__ part) {
     using C = QiCfg<kWaves, kCB, kStages, kKC>;
     constexpr int kQiRows = C::kRows, kQiCols = C::kCols;
@@ -569,11 +626,17 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
         }
         return;
     }
-    // Certify each element and store it; queue the uncertain ones for the exact chain (which
-    // overwrites their provisional values).  No branches per element, so that the compiler
-    // can overlap the elements' dependent chains: the stores go through a buffer descriptor
-    // over the tile's rows, with an out-of-range offset for the lanes past the last column
-    // or token (dropped by the hardware).
+    // Certify each element and store it; the uncertain ones then take the exact chain, one at
+    // a time per wave (which overwrites their provisional values).  No branches per element,
+    // so that the compiler can overlap the elements' dependent chains: the stores go through
+    // a buffer descriptor over the tile's rows, with an out-of-range offset for the lanes past
+    // the last column or token (dropped by the hardware).  The exact chains use the chunk
+    // buffer of the second-to-last chunk as scratch: every wave finished reading it before the
+    // barrier of the last chunk, and no copy goes into it after that barrier.
+    constexpr int kPwChunk = (int)(C::kStage / (kWaves * sizeof(double))) / 8 * 8;
+    static_assert(kPwChunk >= 64, "exact-chain scratch");
+    const int free_stage = k_hi - k_lo >= 2 ? (k_hi - k_lo - 2) % kStages : 1;
+    double* const pw = reinterpret_cast<double*>(tiles + (size_t)free_stage * C::kStage) + (size_t)wave * kPwChunk;
     const __amdgpu_buffer_rsrc_t qrs =
         __builtin_amdgcn_make_buffer_rsrc(q + (int64_t)t0 * ncols, 0, max(0, min(kQiRows, n_tok - t0)) * ncols * 2,
                                           0x00020000);
@@ -598,25 +661,32 @@ __global__ __launch_bounds__(kWaves * 64) void qproj_i8_kernel(const int8_t* __r
         __builtin_amdgcn_raw_buffer_store_b16(o, qrs, live ? (tl * ncols + c) * 2 : -1, 0, 0);
         unsure |= (uint32_t)(live && !sure) << i;
     }
-    while (__ballot(unsure != 0u)) {  // (rare) one uncertain element per lane and pass
-        const int i = __builtin_ctz(unsure | 0x10000u);
-        qp_queue(unsure != 0u, (t0 + wr * 32 + mfma32_row(i, lane)) * ncols + c, lane, count, list);
-        unsure &= unsure - 1u;
+    // (rare) the wave's uncertain elements, lowest lane first
+    for (uint64_t pend = __ballot(unsure != 0u); pend != 0; pend = __ballot(unsure != 0u)) {
+        const int lead = __builtin_ctzll(pend);
+        const int i = __builtin_ctz(__builtin_amdgcn_readlane(unsure, lead));
+        const int tl = wr * 32 + mfma32_row(i, lead);
+        const int cl = c0 + wc * 32 * kCB + cb * 32 + (lead & 31);
+        qp_exact_element(x, w, bias, alpha, beta, d, ncols, (int64_t)(t0 + tl) * ncols + cl, pw, kPwChunk, q);
+        if (lane == lead) unsure &= unsure - 1u;
     }
   }
 }
 
 // Split reductions: element e = t ncols + c (one thread each) adds the kQiSplit partial sums
 // of the ranges (int64, exact), converts once to fp64 (exact below 2^53) and is certified
-// as in the product kernel.
+// as in the product kernel; a wave's uncertain elements take the exact chain in turn.
 __global__ __launch_bounds__(256) void qproj_split_finish_kernel(const int64_t* __restrict__ part,
                                                                  const QRowMeta* __restrict__ xmeta,
                                                                  const QRowMeta* __restrict__ wmeta,
                                                                  const uint16_t* __restrict__ bias,
                                                                  const float* __restrict__ alpha,
                                                                  const float* __restrict__ beta, int n_tok, int d,
-                                                                 int ncols, int n_split, int32_t* __restrict__ count,
-                                                                 int32_t* __restrict__ list, uint16_t* __restrict__ q) {
+                                                                 int ncols, int n_split, const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 uint16_t* __restrict__ q) {
+    constexpr int kFinChunk = 512;
+    __shared__ __align__(16) double scratch_pw[4][kFinChunk];
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t n_el = (int64_t)n_tok * ncols;
     const bool live = e < n_el;
@@ -631,99 +701,12 @@ __global__ __launch_bounds__(256) void qproj_split_finish_kernel(const int64_t* 
         sure = qp_certify((double)P, qp_xf(xm), qp_xi(xm), cf, d, &o);
         if (sure) q[e] = o;
     }
-    qp_queue(live && !sure, (int)e, threadIdx.x & 63, count, list);
-}
-
-// Exact fp64 chain for the queued elements (index order, as the contract defines).  A
-// bf16 x bf16 product is exact in fp64 (16 significant bits, exponents within
-// [-266, 256]), so fma(x_i, w_i, acc) == acc + x_i w_i bit for bit: one wave per element
-// loads both rows with coalesced 16-byte loads, its 64 lanes write the products to LDS
-// (1024 per pass), and the first lane runs the dependent additions in index order.
-constexpr int kFixChunk = 1024;
-
-__global__ __launch_bounds__(256) void qproj_fixup_kernel(const uint16_t* __restrict__ x,
-                                                          const uint16_t* __restrict__ w,
-                                                          const uint16_t* __restrict__ bias,
-                                                          const float* __restrict__ alpha,
-                                                          const float* __restrict__ beta, int d, int ncols,
-                                                          const int32_t* __restrict__ count,
-                                                          const int32_t* __restrict__ list, uint16_t* __restrict__ q) {
-    __shared__ __align__(16) double prod[4][kFixChunk];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    double* pw = prod[wave];
-    const int n = *count;
-    for (int idx = blockIdx.x * 4 + wave; idx < n; idx += gridDim.x * 4) {
-        const int e = list[idx];
-        const int t = e / ncols, c = e - t * ncols;
-        const uint16_t* xr = x + (int64_t)t * d;
-        const uint16_t* wr = w + (int64_t)c * d;
-        // Exactness test.  Every product is an integer multiple of 2^L, L the smallest
-        // lowest-bit exponent of the non-zero products (a bf16 value with biased exponent
-        // b is a multiple of 2^(max(b, 1) - 134)), and so is every partial sum, in any
-        // order, of magnitude at most S = sum |x_i w_i|.  When S < 2^(L + 53) every such
-        // sum is exact in fp64: the chain never rounds and equals the wave's sum in any
-        // order.  (S is taken with a factor-2 margin for the rounding of its own sum;
-        // a non-finite product makes S non-finite and fails the test.)
-        double ls = 0.0, la = 0.0;
-        int lmin = 0x7fffffff;
-        for (int g = lane; g < d / 8; g += kWave) {
-            const uint4 xa = *reinterpret_cast<const uint4*>(xr + 8 * g);
-            const uint4 wa = *reinterpret_cast<const uint4*>(wr + 8 * g);
-            const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
-            const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t xb = (xv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-                const uint32_t wb = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-                const double pj = (double)__uint_as_float(xb << 16) * (double)__uint_as_float(wb << 16);
-                if (pj != 0.0) {
-                    const int lx = max((int)((xb >> 7) & 0xffu), 1) - 134;
-                    const int lw = max((int)((wb >> 7) & 0xffu), 1) - 134;
-                    lmin = min(lmin, lx + lw);
-                }
-                ls += pj;
-                la += fabs(pj);
-            }
-        }
-#pragma unroll
-        for (int m = 1; m < kWave; m <<= 1) {
-            ls += __shfl_xor(ls, m, kWave);
-            la += __shfl_xor(la, m, kWave);
-            lmin = min(lmin, __shfl_xor(lmin, m, kWave));
-        }
-        if (lmin == 0x7fffffff || la < ldexp(1.0, lmin + 52)) {
-            if (lane == 0) {
-                const float ql = Elem<uint16_t>::round64(ls + (double)bf16_bits_to_f32(bias[c]));
-                q[e] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
-            }
-            continue;
-        }
-        double acc = 0.0;
-        for (int k0 = 0; k0 < d; k0 += kFixChunk) {
-            const int len = min(kFixChunk, d - k0);  // a multiple of 8
-            for (int g = lane; g < len / 8; g += kWave) {
-                const uint4 xa = *reinterpret_cast<const uint4*>(xr + k0 + 8 * g);
-                const uint4 wa = *reinterpret_cast<const uint4*>(wr + k0 + 8 * g);
-                const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
-                const uint32_t wv[4] = {wa.x, wa.y, wa.z, wa.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    pw[8 * g + 2 * j] = (double)__uint_as_float(xv[j] << 16) * (double)__uint_as_float(wv[j] << 16);
-                    pw[8 * g + 2 * j + 1] =
-                        (double)__uint_as_float(xv[j] & 0xffff0000u) * (double)__uint_as_float(wv[j] & 0xffff0000u);
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-            if (lane == 0) {
-#pragma unroll 16
-                for (int i = 0; i < len; ++i) acc = acc + pw[i];
-            }
-            __builtin_amdgcn_wave_barrier();
-        }
-        if (lane == 0) {
-            const float ql = Elem<uint16_t>::round64(acc + (double)bf16_bits_to_f32(bias[c]));
-            q[e] = f32_to_bf16_bits(__builtin_fmaf(ql, alpha[c], beta[c]));
-        }
+    bool unsure = live && !sure;
+    for (uint64_t pend = __ballot(unsure); pend != 0; pend = __ballot(unsure)) {
+        const int lead = __builtin_ctzll(pend);
+        const int64_t el = (int64_t)blockIdx.x * 256 + (threadIdx.x & ~63) + lead;
+        qp_exact_element(x, w, bias, alpha, beta, d, ncols, el, scratch_pw[threadIdx.x >> 6], kFinChunk, q);
+        if ((int)(threadIdx.x & 63) == lead) unsure = false;
     }
 }
 
@@ -751,7 +734,7 @@ int launch_qproj_prepare(const void* w, int ncols, int d, int dtype, void* prepa
     prepared_parts(prepared, ncols, d, &wdig, &wmeta);
     hipLaunchKernelGGL(qproj_digits_kernel, dim3((unsigned)((ncols + 3) / 4)), dim3(256), 0, stream, nullptr,
                        (const uint16_t*)w, 0, ncols, (int64_t)ncols, d, nullptr, const_cast<int8_t*>(wdig), nullptr,
-                       const_cast<QRowMeta*>(wmeta), nullptr);
+                       const_cast<QRowMeta*>(wmeta));
     return (int)hipGetLastError();
 }
 
@@ -767,31 +750,25 @@ int launch_qproj(const void* x, const void* w, const void* prepared, const void*
         if (prepared) prepared_parts(prepared, ncols, d, &wdig, &wmeta);
         hipLaunchKernelGGL(qproj_digits_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream,
                            (const uint16_t*)x, (const uint16_t*)w, (int)n_tok, ncols, rows, d, W.xdig, W.wdig, W.meta,
-                           W.meta + n_tok, W.count);
+                           W.meta + n_tok);
         using C = QiLaunch;
         const int64_t tiles = (int64_t)((ncols + C::kCols - 1) / C::kCols) * ((n_tok + C::kRows - 1) / C::kRows);
         const unsigned tgrid = (unsigned)(8 * ((tiles + 7) / 8));  // qi_tile_t: XCD-grouped tile order
         if (W.part != nullptr) {
             hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, C::kKC, true>), dim3(tgrid, kQiSplit),
                                dim3(C::kWaves * 64), C::kSmem, stream, W.xdig, wdig, W.meta, wmeta,
-                               (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q,
-                               W.part);
+                               (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, (const uint16_t*)x,
+                               (const uint16_t*)w, (uint16_t*)q, W.part);
             const int64_t n_el = n_tok * (int64_t)ncols;
             hipLaunchKernelGGL(qproj_split_finish_kernel, dim3((unsigned)((n_el + 255) / 256)), dim3(256), 0, stream,
                                (const int64_t*)W.part, (const QRowMeta*)W.meta, wmeta, (const uint16_t*)b, alpha, beta,
-                               (int)n_tok, d, ncols, kQiSplit, W.count, W.list, (uint16_t*)q);
+                               (int)n_tok, d, ncols, kQiSplit, (const uint16_t*)x, (const uint16_t*)w, (uint16_t*)q);
         } else {
             hipLaunchKernelGGL((qproj_i8_kernel<C::kWaves, C::kCB, C::kStages, C::kKC, false>), dim3(tgrid),
                                dim3(C::kWaves * 64), C::kSmem, stream, W.xdig, wdig, W.meta, wmeta,
-                               (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, W.count, W.list, (uint16_t*)q,
-                               (int64_t*)nullptr);
+                               (const uint16_t*)b, alpha, beta, (int)n_tok, d, ncols, (const uint16_t*)x,
+                               (const uint16_t*)w, (uint16_t*)q, (int64_t*)nullptr);
         }
-        // one wave per queued element, at most one per element of the batch
-        const int64_t fix_wg = (n_tok * (int64_t)ncols + 3) / 4;
-        const unsigned fgrid = (unsigned)(fix_wg < (int64_t)num_cus * 4 ? fix_wg : (int64_t)num_cus * 4);
-        hipLaunchKernelGGL(qproj_fixup_kernel, dim3(fgrid), dim3(256), 0, stream, (const uint16_t*)x,
-                           (const uint16_t*)w, (const uint16_t*)b, alpha, beta, d, ncols, W.count, W.list,
-                           (uint16_t*)q);
         return (int)hipGetLastError();
     }
     dim3 grid((ncols + kQpTN - 1) / kQpTN, (unsigned)((n_tok + kQpTM - 1) / kQpTM));
