@@ -703,32 +703,40 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
     // win the tie on its expert id).  So: rank the staircase, then merge in the rare
     // outside pairs equal to theta.
     // Staircase pair t of this lane: entry lane + 64 t of the list of (a, b), a-major, with
-    // b < nb(a) = min(top_k / (a + 1), kc).  nb(a) does not increase with a, so one
-    // wave-uniform pass finds it without divisions.
+    // b < nb(a) = min(top_k / (a + 1), kc).  Lane a (< kc) holds nb(a) and its exclusive
+    // prefix cum(a) (a wave scan); an entry's row is the last a with nb(a) > 0 and
+    // cum(a) <= its index (nb does not increase with a).
     int st_a[kRtStSlots], st_b[kRtStSlots];
-#pragma unroll
-    for (int t = 0; t < kRtStSlots; ++t) {
-        st_a[t] = -1;
-        st_b[t] = 0;
-    }
     // fr_b: the first column outside the staircase in row a = lane (a <= top_k, a < kc), or
     // -1 when the row has none: the largest pair of the row outside the staircase
-    int fr_b = -1;
+    int fr_b;
     {
-        int nb = top_k < kc ? top_k : kc, cum = 0;
-        for (int a = 0; a < kc; ++a) {
-            while (nb > 0 && nb * (a + 1) > top_k) --nb;
-            if (lane == a && nb < kc) fr_b = nb;
-            if (nb == 0) break;
+        const int nbl = lane < kc ? min(top_k / (lane + 1), kc) : 0;
+        int incl = nbl;
 #pragma unroll
-            for (int t = 0; t < kRtStSlots; ++t) {
-                const int idx = lane + t * kWave;
-                if (idx >= cum && idx < cum + nb) {
-                    st_a[t] = a;
-                    st_b[t] = idx - cum;
-                }
-            }
-            cum += nb;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int v = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += v;
+        }
+        const int cuml = incl - nbl;
+        const int total = __shfl(incl, kWave - 1, kWave);  // (lanes from kc on add 0)
+        fr_b = lane < kc && lane <= top_k && nbl < kc ? nbl : -1;
+        int arow[kRtStSlots];
+#pragma unroll
+        for (int t = 0; t < kRtStSlots; ++t) arow[t] = 0;
+        for (int a = 1; a < kc; ++a) {
+            const int nba = __builtin_amdgcn_readlane(nbl, a), ca = __builtin_amdgcn_readlane(cuml, a);
+            if (nba == 0) break;
+#pragma unroll
+            for (int t = 0; t < kRtStSlots; ++t)
+                if (ca <= lane + t * kWave) arow[t] = a;
+        }
+#pragma unroll
+        for (int t = 0; t < kRtStSlots; ++t) {
+            const int idx = lane + t * kWave;
+            const int ca = __shfl(cuml, arow[t], kWave);
+            st_a[t] = idx < total ? arow[t] : -1;
+            st_b[t] = idx < total ? idx - ca : 0;
         }
     }
 #pragma unroll
