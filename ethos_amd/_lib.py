@@ -34,6 +34,10 @@ SIGNATURES = {
     "ethos_query_proj_prepared": (ctypes.c_int, [_vp, _vp, _vp, _sz, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp,
                                                  _sz, _vp, _vp]),
     "ethos_route_topk": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "ethos_route_keys_bytes": (_sz, [_i32, _i32, _i32]),
+    "ethos_route_prepare_keys": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "ethos_route_topk_prepared": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _i32, _i32,
+                                                 _vp, _vp, _vp]),
     "ethos_sort_workspace_bytes": (_sz, [_i64, _i64]),
     "ethos_sort_segment": (ctypes.c_int, [_vp, _i64, _i64, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ethos_sort_segment_noalloc": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

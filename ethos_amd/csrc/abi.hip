@@ -193,36 +193,82 @@ int ethos_query_proj_prepared(const void* x, const void* wq, const void* prepare
                            n_heads, d_query, dtype, workspace, workspace_bytes, q_out, stream);
 }
 
+static int route_checks(const char* name, int64_t n_rows, int32_t d_query, int32_t n_sub_keys, int32_t top_k,
+                        int32_t k_cand, int32_t dtype) {
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "%s: unknown dtype %d", name, dtype);
+    if (n_rows < 0 || d_query <= 0 || (d_query & 1) || n_sub_keys <= 0 || top_k <= 0 || k_cand <= 0)
+        return fail(ETHOS_ESIZE, "%s: bad sizes rows=%lld d_query=%d K=%d top_k=%d k_cand=%d", name,
+                    (long long)n_rows, d_query, n_sub_keys, top_k, k_cand);
+    if (k_cand > n_sub_keys) return fail(ETHOS_ESIZE, "%s: k_cand=%d exceeds the %d sub-keys", name, k_cand, n_sub_keys);
+    if (top_k > k_cand * k_cand) return fail(ETHOS_ESIZE, "%s: top_k=%d exceeds k_cand^2=%d", name, top_k, k_cand * k_cand);
+    if (k_cand > 32 || top_k > 32)
+        return fail(ETHOS_EUNSUPPORTED, "%s: k_cand=%d / top_k=%d above 32 are not supported", name, k_cand, top_k);
+    if ((int64_t)n_sub_keys * n_sub_keys > INT32_MAX)
+        return fail(ETHOS_EUNSUPPORTED, "%s: %d sub-keys give expert ids beyond int32", name, n_sub_keys);
+    if (!ethos::route_supported(n_sub_keys, d_query / 2, dtype))
+        return fail(ETHOS_EUNSUPPORTED,
+                    "%s: needs n_sub_keys <= 512, d_query/2 <= 256 and d_query/2 %% %d == 0 (got %d, %d)", name,
+                    dtype == ETHOS_BF16 ? 16 : 4, n_sub_keys, d_query);
+    return 0;
+}
+
 int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, const float* key_norms,
                      int64_t n_rows, int32_t d_query, int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype,
                      void* out_scores, int32_t* out_ids, void* stream) {
     g_err[0] = 0;
-    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_route_topk: unknown dtype %d", dtype);
-    if (n_rows < 0 || d_query <= 0 || (d_query & 1) || n_sub_keys <= 0 || top_k <= 0 || k_cand <= 0)
-        return fail(ETHOS_ESIZE, "ethos_route_topk: bad sizes rows=%lld d_query=%d K=%d top_k=%d k_cand=%d",
-                    (long long)n_rows, d_query, n_sub_keys, top_k, k_cand);
-    if (k_cand > n_sub_keys)
-        return fail(ETHOS_ESIZE, "ethos_route_topk: k_cand=%d exceeds the %d sub-keys", k_cand, n_sub_keys);
-    if (top_k > k_cand * k_cand)
-        return fail(ETHOS_ESIZE, "ethos_route_topk: top_k=%d exceeds k_cand^2=%d", top_k, k_cand * k_cand);
-    if (k_cand > 32 || top_k > 32)
-        return fail(ETHOS_EUNSUPPORTED, "ethos_route_topk: k_cand=%d / top_k=%d above 32 are not supported", k_cand,
-                    top_k);
-    if ((int64_t)n_sub_keys * n_sub_keys > INT32_MAX)
-        return fail(ETHOS_EUNSUPPORTED, "ethos_route_topk: %d sub-keys give expert ids beyond int32", n_sub_keys);
-    const int dh2 = d_query / 2;
-    if (!ethos::route_supported(n_sub_keys, dh2, dtype))
-        return fail(ETHOS_EUNSUPPORTED,
-                    "ethos_route_topk: needs n_sub_keys <= 512, d_query/2 <= 256 and d_query/2 %% %d == 0 "
-                    "(got %d, %d)", dtype == ETHOS_BF16 ? 16 : 4, n_sub_keys, d_query);
+    if (const int rc = route_checks("ethos_route_topk", n_rows, d_query, n_sub_keys, top_k, k_cand, dtype)) return rc;
     if (n_rows == 0) return 0;
     if (!q || !sub_keys_1 || !sub_keys_2 || !out_scores || !out_ids)
         return fail(ETHOS_ENULL, "ethos_route_topk: null pointer");
     if (!aligned16(q) || !aligned16(sub_keys_1) || !aligned16(sub_keys_2))
         return fail(ETHOS_EALIGN, "ethos_route_topk: q and sub-key tables must be 16-byte aligned");
-    return hip_status(ethos::launch_route(q, sub_keys_1, sub_keys_2, key_norms, n_rows, d_query, n_sub_keys, top_k,
-                                          k_cand, dtype, out_scores, out_ids, (hipStream_t)stream),
+    return hip_status(ethos::launch_route(q, sub_keys_1, sub_keys_2, key_norms, nullptr, n_rows, d_query, n_sub_keys,
+                                          top_k, k_cand, dtype, out_scores, out_ids, (hipStream_t)stream),
                       "ethos_route_topk");
+}
+
+size_t ethos_route_keys_bytes(int32_t n_sub_keys, int32_t d_query, int32_t dtype) {
+    if (!dtype_ok(dtype) || n_sub_keys <= 0 || d_query <= 0 || (d_query & 1) ||
+        !ethos::route_supported(n_sub_keys, d_query / 2, dtype))
+        return 0;
+    return ethos::route_keys_bytes(n_sub_keys, d_query / 2, dtype);
+}
+
+int ethos_route_prepare_keys(const void* sub_keys_1, const void* sub_keys_2, int32_t n_sub_keys, int32_t d_query,
+                             int32_t dtype, void* prepared, size_t prepared_bytes, void* stream) {
+    g_err[0] = 0;
+    if (!dtype_ok(dtype)) return fail(ETHOS_EDTYPE, "ethos_route_prepare_keys: unknown dtype %d", dtype);
+    const size_t need = ethos_route_keys_bytes(n_sub_keys, d_query, dtype);
+    if (need == 0)
+        return fail(ETHOS_EUNSUPPORTED, "ethos_route_prepare_keys: unsupported sizes K=%d d_query=%d", n_sub_keys,
+                    d_query);
+    if (!sub_keys_1 || !sub_keys_2 || !prepared) return fail(ETHOS_ENULL, "ethos_route_prepare_keys: null pointer");
+    if (prepared_bytes < need)
+        return fail(ETHOS_ESIZE, "ethos_route_prepare_keys: prepared holds %zu bytes, needs %zu", prepared_bytes, need);
+    if (!aligned16(prepared)) return fail(ETHOS_EALIGN, "ethos_route_prepare_keys: prepared must be 16-byte aligned");
+    return hip_status(ethos::launch_route_prepare_keys(sub_keys_1, sub_keys_2, n_sub_keys, d_query, dtype, prepared,
+                                                       (hipStream_t)stream),
+                      "ethos_route_prepare_keys");
+}
+
+int ethos_route_topk_prepared(const void* q, const void* sub_keys_1, const void* sub_keys_2, const float* key_norms,
+                              const void* prepared, size_t prepared_bytes, int64_t n_rows, int32_t d_query,
+                              int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype, void* out_scores,
+                              int32_t* out_ids, void* stream) {
+    g_err[0] = 0;
+    if (const int rc = route_checks("ethos_route_topk_prepared", n_rows, d_query, n_sub_keys, top_k, k_cand, dtype))
+        return rc;
+    if (n_rows == 0) return 0;
+    if (!q || !sub_keys_1 || !sub_keys_2 || !prepared || !out_scores || !out_ids)
+        return fail(ETHOS_ENULL, "ethos_route_topk_prepared: null pointer");
+    if (prepared_bytes < ethos::route_keys_bytes(n_sub_keys, d_query / 2, dtype))
+        return fail(ETHOS_ESIZE, "ethos_route_topk_prepared: prepared holds %zu bytes, needs %zu", prepared_bytes,
+                    ethos::route_keys_bytes(n_sub_keys, d_query / 2, dtype));
+    if (!aligned16(q) || !aligned16(sub_keys_1) || !aligned16(sub_keys_2) || !aligned16(prepared))
+        return fail(ETHOS_EALIGN, "ethos_route_topk_prepared: q, sub-key tables and prepared must be 16-byte aligned");
+    return hip_status(ethos::launch_route(q, sub_keys_1, sub_keys_2, key_norms, prepared, n_rows, d_query, n_sub_keys,
+                                          top_k, k_cand, dtype, out_scores, out_ids, (hipStream_t)stream),
+                      "ethos_route_topk_prepared");
 }
 
 size_t ethos_sort_workspace_bytes(int64_t n_pairs, int64_t n_experts) {

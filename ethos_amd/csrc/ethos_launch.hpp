@@ -20,8 +20,11 @@ int launch_qproj(const void* x, const void* w, const void* prepared, const void*
 
 size_t route_smem_bytes(int K, int dh2, int elem_bytes);
 bool route_supported(int K, int dh2, int dtype);
-int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, int64_t rows, int dq, int K,
-                 int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream);
+int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, const void* kfrag,
+                 int64_t rows, int dq, int K, int top_k, int kc, int dtype, void* gates, int32_t* ids,
+                 hipStream_t stream);
+size_t route_keys_bytes(int K, int dh2, int dtype);
+int launch_route_prepare_keys(const void* k1, const void* k2, int K, int dq, int dtype, void* out, hipStream_t stream);
 
 // The sort's workspace: keys and values twice (4 n words), then per (digit, tile of
 // kSortTileKeys keys) four counters (rows of sort_tile_pitch words: the tile count rounded

@@ -360,7 +360,8 @@ template <typename T, int RPW, bool kHP = false>
 __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
                                                     const T* __restrict__ keys2, const float* __restrict__ key_norms,
                                                     int64_t rows, int dq, int K, int top_k, int kc,
-                                                    T* __restrict__ out_gates, int32_t* __restrict__ out_ids) {
+                                                    T* __restrict__ out_gates, int32_t* __restrict__ out_ids,
+                                                    const T* __restrict__ kfrag) {
     using M = Mfma<T>;
     extern __shared__ __align__(16) unsigned char smem[];
     const int dh2 = dq / 2;
@@ -447,8 +448,14 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
                     const int kk = k0 + u * M::kK;
 #pragma unroll
                     for (int c = 0; c < 2; ++c) {
-                        const int j = (kb0 + kRtWaves * c) * 32 + lrow;
-                        b[c][u] = kk < dh2 && j < K ? M::load(keys + (int64_t)j * dh2 + kk + lk) : M::zero();
+                        const int kb = kb0 + kRtWaves * c, j = kb * 32 + lrow;
+                        if (kfrag != nullptr)  // fragment-major copy: one contiguous 64-lane block
+                            b[c][u] = kk < dh2 && kb < nkb
+                                          ? M::load(kfrag + ((((int64_t)half * nkb + kb) * (dh2 / M::kK) + kk / M::kK) * kWave +
+                                                             lane) * M::kKL)
+                                          : M::zero();
+                        else
+                            b[c][u] = kk < dh2 && j < K ? M::load(keys + (int64_t)j * dh2 + kk + lk) : M::zero();
                     }
                 }
 #pragma unroll
@@ -798,13 +805,55 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
 
 size_t route_smem_bytes(int K, int dh2, int elem_bytes) { return route_smem_layout(K, dh2, elem_bytes).total; }
 
+// Fragment-major copy of both sub-key tables for the scoring MFMAs: block (half, key block kb
+// of 32 keys, k-step s) holds, for lane l of the wave, the M::kKL elements that lane loads as
+// its B fragment, keys[32 kb + l % 32][s kK + (l / 32) kKL ..] (zero past the last key), so
+// that each fragment load of a wave reads one contiguous block instead of 32 key rows.
+size_t route_keys_bytes(int K, int dh2, int dtype) {
+    const int kpad = (K + 31) / 32 * 32;
+    return (size_t)2 * kpad * dh2 * (dtype == kBF16 ? 2 : 4);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void route_keys_kernel(const T* __restrict__ k1, const T* __restrict__ k2, int K,
+                                                         int dh2, T* __restrict__ out) {
+    using M = Mfma<T>;
+    const int nkb = (K + 31) / 32, nks = dh2 / M::kK;
+    const int64_t n = (int64_t)2 * nkb * nks * kWave;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n) return;
+    const int l = (int)(e % kWave);
+    const int64_t blk = e / kWave;
+    const int s = (int)(blk % nks), kb = (int)((blk / nks) % nkb), half = (int)(blk / ((int64_t)nks * nkb));
+    const T* keys = half ? k2 : k1;
+    const int j = kb * 32 + l % 32, k0 = s * M::kK + (l / 32) * M::kKL;
+#pragma unroll
+    for (int i = 0; i < M::kKL; ++i) out[e * M::kKL + i] = j < K ? keys[(int64_t)j * dh2 + k0 + i] : T{};
+}
+
+int launch_route_prepare_keys(const void* k1, const void* k2, int K, int dq, int dtype, void* out,
+                              hipStream_t stream) {
+    const int dh2 = dq / 2;
+    const int kk = dtype == kBF16 ? Mfma<uint16_t>::kK : Mfma<float>::kK;
+    const int64_t n = (int64_t)2 * ((K + 31) / 32) * (dh2 / kk) * kWave;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (dtype == kBF16)
+        hipLaunchKernelGGL(route_keys_kernel<uint16_t>, grid, dim3(256), 0, stream, (const uint16_t*)k1,
+                           (const uint16_t*)k2, K, dh2, (uint16_t*)out);
+    else
+        hipLaunchKernelGGL(route_keys_kernel<float>, grid, dim3(256), 0, stream, (const float*)k1, (const float*)k2, K,
+                           dh2, (float*)out);
+    return (int)hipGetLastError();
+}
+
 bool route_supported(int K, int dh2, int dtype) {
     const int kq = dtype == kBF16 ? 16 : 4;
     return K <= kRtMaxK && dh2 <= kRtMaxDh2 && dh2 % kq == 0 && route_smem_bytes(K, dh2, dtype == kBF16 ? 2 : 4) <= 160 * 1024;
 }
 
-int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, int64_t rows, int dq, int K,
-                 int top_k, int kc, int dtype, void* gates, int32_t* ids, hipStream_t stream) {
+int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, const void* kfrag,
+                 int64_t rows, int dq, int K, int top_k, int kc, int dtype, void* gates, int32_t* ids,
+                 hipStream_t stream) {
     const int dh2 = dq / 2;
     const size_t smem = route_smem_bytes(K, dh2, dtype == kBF16 ? 2 : 4);
     const bool small = rows <= kRtSmallRows;
@@ -817,18 +866,20 @@ int launch_route(const void* q, const void* k1, const void* k2, const float* key
         if (small)
             hipLaunchKernelGGL((route_kernel<uint16_t, 1, true>), grid, block_hp, smem_hp, stream, (const uint16_t*)q,
                                (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
-                               (uint16_t*)gates, ids);
+                               (uint16_t*)gates, ids, (const uint16_t*)kfrag);
         else
             hipLaunchKernelGGL((route_kernel<uint16_t, 4>), grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
                                (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
-                               (uint16_t*)gates, ids);
+                               (uint16_t*)gates, ids, (const uint16_t*)kfrag);
     } else {
         if (small)
             hipLaunchKernelGGL((route_kernel<float, 1, true>), grid, block_hp, smem_hp, stream, (const float*)q,
-                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
+                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids,
+                               (const float*)kfrag);
         else
             hipLaunchKernelGGL((route_kernel<float, 4>), grid, dim3(kRtWaves * 64), smem, stream, (const float*)q,
-                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids);
+                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids,
+                               (const float*)kfrag);
     }
     return (int)hipGetLastError();
 }

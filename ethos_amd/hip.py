@@ -113,10 +113,31 @@ def query_proj(x: torch.Tensor, wq: torch.Tensor, bq: torch.Tensor, bn_alpha: to
     return out
 
 
+def route_prepare_keys(sub_keys_1: torch.Tensor, sub_keys_2: torch.Tensor) -> torch.Tensor:
+    """Both sub-key tables [K, dq/2] in the scoring MFMAs' fragment order (a uint8 device
+    buffer) for route_topk(..., prepared_keys=...)."""
+    _need(sub_keys_1, "sub_keys_1", dim=2)
+    _need(sub_keys_2, "sub_keys_2", sub_keys_1.dtype, 2)
+    K, dh2 = sub_keys_1.shape
+    if sub_keys_2.shape != (K, dh2):
+        raise RuntimeError("route_prepare_keys: the two sub-key tables must have the same shape")
+    code = dtype_code(sub_keys_1.dtype)
+    n = load().ethos_route_keys_bytes(K, 2 * dh2, code)
+    if n == 0:
+        raise RuntimeError(f"route_prepare_keys: unsupported sub-key tables {tuple(sub_keys_1.shape)}")
+    buf = torch.empty(n, dtype=torch.uint8, device=sub_keys_1.device)
+    rc = load().ethos_route_prepare_keys(sub_keys_1.data_ptr(), sub_keys_2.data_ptr(), K, 2 * dh2, code,
+                                         buf.data_ptr(), n, _stream())
+    check(rc, "ethos_route_prepare_keys")
+    return buf
+
+
 def route_topk(q: torch.Tensor, sub_keys_1: torch.Tensor, sub_keys_2: torch.Tensor, top_k: int,
-               k_cand: int | None = None, key_norms: torch.Tensor | None = None):
+               k_cand: int | None = None, key_norms: torch.Tensor | None = None,
+               prepared_keys: torch.Tensor | None = None):
     """q [..., dq] -> (gates [..., top_k] q.dtype, expert ids [..., top_k] int32).
-    key_norms: optional fp32 [2, K] upper bounds of the sub-key row norms."""
+    key_norms: optional fp32 [2, K] upper bounds of the sub-key row norms; prepared_keys:
+    optional route_prepare_keys(sub_keys_1, sub_keys_2) (the same results, faster)."""
     _need(q, "q")
     _need(sub_keys_1, "sub_keys_1", q.dtype, 2)
     _need(sub_keys_2, "sub_keys_2", q.dtype, 2)
@@ -132,10 +153,17 @@ def route_topk(q: torch.Tensor, sub_keys_1: torch.Tensor, sub_keys_2: torch.Tens
         _need(key_norms, "key_norms", torch.float32)
         if key_norms.numel() != 2 * K:
             raise RuntimeError("route_topk: key_norms must hold 2 * K values")
-    rc = load().ethos_route_topk(q.data_ptr(), sub_keys_1.data_ptr(), sub_keys_2.data_ptr(),
-                                 key_norms.data_ptr() if key_norms is not None else None, rows, dq, K, top_k, kc,
-                                 dtype_code(q.dtype), gates.data_ptr(), ids.data_ptr(), _stream())
-    check(rc, "ethos_route_topk")
+    kn = key_norms.data_ptr() if key_norms is not None else None
+    if prepared_keys is not None:
+        _need(prepared_keys, "prepared_keys", torch.uint8)
+        rc = load().ethos_route_topk_prepared(q.data_ptr(), sub_keys_1.data_ptr(), sub_keys_2.data_ptr(), kn,
+                                              prepared_keys.data_ptr(), prepared_keys.numel(), rows, dq, K, top_k, kc,
+                                              dtype_code(q.dtype), gates.data_ptr(), ids.data_ptr(), _stream())
+        check(rc, "ethos_route_topk_prepared")
+    else:
+        rc = load().ethos_route_topk(q.data_ptr(), sub_keys_1.data_ptr(), sub_keys_2.data_ptr(), kn, rows, dq, K,
+                                     top_k, kc, dtype_code(q.dtype), gates.data_ptr(), ids.data_ptr(), _stream())
+        check(rc, "ethos_route_topk")
     return gates, ids
 
 

@@ -165,6 +165,7 @@ class ProductKeyRouter(nn.Module):
         self._cache_key = None
         self._cache = None
         self._key_norms = None
+        self._keys_prepared = None
         self._wq_prepared = None
 
     # -- parameter packing (cached until a parameter changes) ---------------------
@@ -194,6 +195,8 @@ class ProductKeyRouter(nn.Module):
             alpha = torch.from_numpy(np.stack(alpha)).contiguous().to(device)
             beta = torch.from_numpy(np.stack(beta)).contiguous().to(device)
             self._key_norms = hip.key_norm_bounds(k1, k2).to(device)
+            # the sub-keys in the scoring MFMAs' fragment order
+            self._keys_prepared = hip.route_prepare_keys(k1, k2) if k1.is_cuda else None
             # the projection weights' prepared form (bf16: digit planes), reused by every call
             # until a parameter changes
             self._wq_prepared = hip.query_proj_prepare(wq) if wq.is_cuda else None
@@ -238,7 +241,7 @@ class ProductKeyRouter(nn.Module):
         q = self.queries(x_flat, packed)
         if mark is not None:
             mark("query_proj")
-        out = hip.route_topk(q, k1, k2, self.top_k, key_norms=self._key_norms)
+        out = hip.route_topk(q, k1, k2, self.top_k, key_norms=self._key_norms, prepared_keys=self._keys_prepared)
         if mark is not None:
             mark("route")
         return out

@@ -9,6 +9,7 @@
  *
  *   ethos_query_proj     per-head query projection + eval BatchNorm
  *   ethos_route_topk     sub-key scoring, top-k_cand per half, combination, top-k, softmax
+ *                        (ethos_route_topk_prepared: with the sub-keys' prepared form)
  *   ethos_sort_segment   reordering of (token, head, k) pairs by expert id
  *   ethos_sort_segment_token_proj  the same with the token projection x W_u beside it
  *   ethos_generate       hypernetwork expert generation over the unique experts
@@ -38,7 +39,7 @@
 extern "C" {
 #endif
 
-#define ETHOS_ABI_VERSION 7
+#define ETHOS_ABI_VERSION 8
 
 #define ETHOS_F32 0
 #define ETHOS_BF16 1
@@ -134,6 +135,28 @@ int ethos_query_proj_prepared(const void* x, const void* wq, const void* prepare
 int ethos_route_topk(const void* q, const void* sub_keys_1, const void* sub_keys_2, const float* key_norms,
                      int64_t n_rows, int32_t d_query, int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype,
                      void* out_scores, int32_t* out_ids, void* stream);
+
+/*
+ * The same routing with the sub-keys' layout for the scoring MFMAs computed once.  The
+ * reference reads router.sub_keys_{1,2}.weight on every call (model.py:219-220); these
+ * split the reordering off for callers that keep the tables between calls (the module
+ * does, per parameter version).
+ *   ethos_route_keys_bytes: size of the prepared form (0 for unsupported sizes).
+ *   ethos_route_prepare_keys: writes both tables in fragment order (for each block of 32
+ *     keys and each MFMA reduction step, the 64 lanes' operand pieces back to back) into
+ *     `prepared` (>= that many bytes, 16-byte aligned).
+ *   ethos_route_topk_prepared: ethos_route_topk with `prepared` from the same tables;
+ *     bit-identical results.  The tables themselves are still read (exact rescoring).
+ */
+size_t ethos_route_keys_bytes(int32_t n_sub_keys, int32_t d_query, int32_t dtype);
+
+int ethos_route_prepare_keys(const void* sub_keys_1, const void* sub_keys_2, int32_t n_sub_keys, int32_t d_query,
+                             int32_t dtype, void* prepared, size_t prepared_bytes, void* stream);
+
+int ethos_route_topk_prepared(const void* q, const void* sub_keys_1, const void* sub_keys_2, const float* key_norms,
+                              const void* prepared, size_t prepared_bytes, int64_t n_rows, int32_t d_query,
+                              int32_t n_sub_keys, int32_t top_k, int32_t k_cand, int32_t dtype, void* out_scores,
+                              int32_t* out_ids, void* stream);
 
 /* Workspace size for ethos_sort_segment. */
 size_t ethos_sort_workspace_bytes(int64_t n_pairs, int64_t n_experts);

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().ethos_abi_version() == 7
+    assert _lib.load().ethos_abi_version() == 8
 
 
 def _rc(fn, *args):
@@ -99,6 +99,26 @@ def test_route_rejects_top_k_above_32():
     assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 1024, 4, 8, 1, 16, 16, None) == -6
     assert L.ethos_route_topk(18, 16, 16, None, 4, 32, 64, 4, 8, 1, 16, 16, None) == -4
     assert L.ethos_route_topk(16, 16, 16, None, 4, 32, 4096, 40, 32, 1, 16, 16, None) == -6
+
+
+def test_route_prepared_keys_argument_errors():
+    L = _lib.load()
+    n = L.ethos_route_keys_bytes(512, 256, 1)
+    assert n == 2 * 512 * 128 * 2
+    assert L.ethos_route_keys_bytes(200, 64, 0) == 2 * 224 * 32 * 4  # keys padded to blocks of 32
+    assert L.ethos_route_keys_bytes(1024, 256, 1) == 0 and L.ethos_route_keys_bytes(512, 250, 1) == 0
+    assert L.ethos_route_keys_bytes(512, 256, 7) == 0
+    assert L.ethos_route_prepare_keys(16, 16, 512, 256, 7, 16, n, None) == -1
+    assert L.ethos_route_prepare_keys(16, 16, 1024, 256, 1, 16, n, None) == -6
+    assert L.ethos_route_prepare_keys(16, None, 512, 256, 1, 16, n, None) == -3
+    assert L.ethos_route_prepare_keys(16, 16, 512, 256, 1, 16, n - 1, None) == -2
+    assert L.ethos_route_prepare_keys(16, 16, 512, 256, 1, 18, n, None) == -4
+    args = (16, 16, 16, None)
+    assert L.ethos_route_topk_prepared(*args, None, n, 4, 256, 512, 4, 8, 1, 16, 16, None) == -3
+    assert L.ethos_route_topk_prepared(*args, 16, n - 1, 4, 256, 512, 4, 8, 1, 16, 16, None) == -2
+    assert L.ethos_route_topk_prepared(*args, 18, n, 4, 256, 512, 4, 8, 1, 16, 16, None) == -4
+    assert L.ethos_route_topk_prepared(*args, 16, n, 4, 256, 512, 40, 32, 1, 16, 16, None) == -6
+    assert L.ethos_route_topk_prepared(*args, 16, n, 0, 256, 512, 4, 8, 1, 16, 16, None) == 0  # no rows: nothing to do
 
 
 def test_sort_segment_token_proj_argument_errors():

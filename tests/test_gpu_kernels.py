@@ -80,6 +80,27 @@ def test_route_partial_tiles_bit_exact(rows, dt):
     assert np.array_equal(O.to_f32(to_host(g), dt), O.to_f32(g_ref, dt))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "fp32"])
+@pytest.mark.parametrize("rows,K,dh2", [(200, 512, 128), (4123, 512, 128), (300, 200, 32), (5000, 100, 64),
+                                        (64, 16, 16)])
+def test_route_prepared_keys_bit_exact(rows, K, dh2, dt):
+    """Routing with the sub-keys in fragment order (ethos_route_topk_prepared) equals the
+    oracle and the unprepared call bit for bit, for both row layouts, key counts that are
+    not a multiple of the 32-key blocks, and several query widths."""
+    rng = np.random.default_rng(rows + K)
+    top_k = 16 if K >= 32 else 4
+    q, k1, k2 = _stress_case("zipf", rng, rows, K, dh2, dt)
+    g_ref, ids_ref = O.route(q, k1, k2, top_k, dt)
+    d1, d2 = to_dev(k1), to_dev(k2)
+    prep = hip.route_prepare_keys(d1, d2)
+    kn = hip.key_norm_bounds(d1, d2).cuda()
+    g, ids = hip.route_topk(to_dev(q), d1, d2, top_k, key_norms=kn, prepared_keys=prep)
+    g0, ids0 = hip.route_topk(to_dev(q), d1, d2, top_k, key_norms=kn)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(ids), ids_ref) and torch.equal(ids, ids0)
+    assert np.array_equal(O.to_f32(to_host(g), dt), O.to_f32(g_ref, dt)) and torch.equal(g, g0)
+
+
 def test_route_ties_break_to_lowest_index():
     """Duplicate sub-key rows force exact score ties in both halves."""
     sh, x, P = _setup("tiny")
