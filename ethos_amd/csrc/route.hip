@@ -356,7 +356,7 @@ __device__ __forceinline__ uint64_t exact_key(const T* qh, const T* __restrict__
 // query half, so that the two halves' scoring, filter, exact chains and sorts run at the same
 // time; the second group hands its candidate lists to the first, which combines.  The
 // operations on each row are the same as in the one-group form, so the outputs are too.
-template <typename T, int RPW, bool kHP = false>
+template <typename T, int RPW, bool kHP = false, bool kPrep = false>
 __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel(const T* __restrict__ q, const T* __restrict__ keys1,
                                                     const T* __restrict__ keys2, const float* __restrict__ key_norms,
                                                     int64_t rows, int dq, int K, int top_k, int kc,
@@ -449,7 +449,7 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
 #pragma unroll
                     for (int c = 0; c < 2; ++c) {
                         const int kb = kb0 + kRtWaves * c, j = kb * 32 + lrow;
-                        if (kfrag != nullptr)  // fragment-major copy: one contiguous 64-lane block
+                        if constexpr (kPrep)  // fragment-major copy: one contiguous 64-lane block
                             b[c][u] = kk < dh2 && kb < nkb
                                           ? M::load(kfrag + ((((int64_t)half * nkb + kb) * (dh2 / M::kK) + kk / M::kK) * kWave +
                                                              lane) * M::kKL)
@@ -851,35 +851,37 @@ bool route_supported(int K, int dh2, int dtype) {
     return K <= kRtMaxK && dh2 <= kRtMaxDh2 && dh2 % kq == 0 && route_smem_bytes(K, dh2, dtype == kBF16 ? 2 : 4) <= 160 * 1024;
 }
 
+template <typename T, bool kPrep>
+static void launch_route_t(const void* q, const void* k1, const void* k2, const float* key_norms, const void* kfrag,
+                           int64_t rows, int dq, int K, int top_k, int kc, void* gates, int32_t* ids,
+                           hipStream_t stream) {
+    const int dh2 = dq / 2;
+    const bool small = rows <= kRtSmallRows;
+    const int per_wg = kRtWaves * (small ? 1 : 4);
+    const dim3 grid((unsigned)((rows + per_wg - 1) / per_wg));
+    if (small)  // one row per wave, the two query halves in parallel
+        hipLaunchKernelGGL((route_kernel<T, 1, true, kPrep>), grid, dim3(2 * kRtWaves * 64),
+                           route_smem_layout(K, dh2, (int)sizeof(T), true).total, stream, (const T*)q, (const T*)k1,
+                           (const T*)k2, key_norms, rows, dq, K, top_k, kc, (T*)gates, ids, (const T*)kfrag);
+    else
+        hipLaunchKernelGGL((route_kernel<T, 4, false, kPrep>), grid, dim3(kRtWaves * 64),
+                           route_smem_bytes(K, dh2, (int)sizeof(T)), stream, (const T*)q, (const T*)k1, (const T*)k2,
+                           key_norms, rows, dq, K, top_k, kc, (T*)gates, ids, (const T*)kfrag);
+}
+
 int launch_route(const void* q, const void* k1, const void* k2, const float* key_norms, const void* kfrag,
                  int64_t rows, int dq, int K, int top_k, int kc, int dtype, void* gates, int32_t* ids,
                  hipStream_t stream) {
-    const int dh2 = dq / 2;
-    const size_t smem = route_smem_bytes(K, dh2, dtype == kBF16 ? 2 : 4);
-    const bool small = rows <= kRtSmallRows;
-    const int per_wg = kRtWaves * (small ? 1 : 4);
-    dim3 grid((unsigned)((rows + per_wg - 1) / per_wg));
-    // small batches: one row per wave, the two query halves in parallel
-    const size_t smem_hp = route_smem_layout(K, dh2, dtype == kBF16 ? 2 : 4, true).total;
-    const dim3 block_hp(2 * kRtWaves * 64);
     if (dtype == kBF16) {
-        if (small)
-            hipLaunchKernelGGL((route_kernel<uint16_t, 1, true>), grid, block_hp, smem_hp, stream, (const uint16_t*)q,
-                               (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
-                               (uint16_t*)gates, ids, (const uint16_t*)kfrag);
+        if (kfrag)
+            launch_route_t<uint16_t, true>(q, k1, k2, key_norms, kfrag, rows, dq, K, top_k, kc, gates, ids, stream);
         else
-            hipLaunchKernelGGL((route_kernel<uint16_t, 4>), grid, dim3(kRtWaves * 64), smem, stream, (const uint16_t*)q,
-                               (const uint16_t*)k1, (const uint16_t*)k2, key_norms, rows, dq, K, top_k, kc,
-                               (uint16_t*)gates, ids, (const uint16_t*)kfrag);
+            launch_route_t<uint16_t, false>(q, k1, k2, key_norms, kfrag, rows, dq, K, top_k, kc, gates, ids, stream);
     } else {
-        if (small)
-            hipLaunchKernelGGL((route_kernel<float, 1, true>), grid, block_hp, smem_hp, stream, (const float*)q,
-                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids,
-                               (const float*)kfrag);
+        if (kfrag)
+            launch_route_t<float, true>(q, k1, k2, key_norms, kfrag, rows, dq, K, top_k, kc, gates, ids, stream);
         else
-            hipLaunchKernelGGL((route_kernel<float, 4>), grid, dim3(kRtWaves * 64), smem, stream, (const float*)q,
-                               (const float*)k1, (const float*)k2, key_norms, rows, dq, K, top_k, kc, (float*)gates, ids,
-                               (const float*)kfrag);
+            launch_route_t<float, false>(q, k1, k2, key_norms, kfrag, rows, dq, K, top_k, kc, gates, ids, stream);
     }
     return (int)hipGetLastError();
 }
