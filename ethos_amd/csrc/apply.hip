@@ -67,11 +67,25 @@ __global__ __launch_bounds__(256) void transpose_wu_kernel(const uint16_t* __res
     }
 }
 
+// Tiles for the per-XCD L2s (workgroup b runs on XCD b % 8): row block r goes to XCD r % 8,
+// its nct column tiles to consecutive slots there, so that each block of x is read from HBM by
+// one XCD; the grid is 8 nct ceil(row blocks / 8), and the padding workgroups return.
 __global__ __launch_bounds__(256) void token_proj_bf16_kernel(const uint16_t* __restrict__ x,
                                                               const uint16_t* __restrict__ wut, int n_tok, int d,
-                                                              int dh, uint16_t* __restrict__ xp) {
+                                                              int dh, uint16_t* __restrict__ xp, int nct, int nrb) {
     __shared__ __align__(16) unsigned char ring[kTpLds];
-    token_proj_bf16_tile(ring, x, wut, n_tok, d, dh, xp, blockIdx.x * kTpCols, blockIdx.y * kTpRows);
+    const int xcd = (int)(blockIdx.x & 7), j = (int)(blockIdx.x >> 3);
+    const int rb = (j / nct) * 8 + xcd, ct = j % nct;
+    if (rb >= nrb) return;
+    token_proj_bf16_tile(ring, x, wut, n_tok, d, dh, xp, ct * kTpCols, rb * kTpRows);
+}
+
+// x [n_tok, K] times the [N, K] operand, output [n_tok, N], by the tile kernel above.
+static void launch_tp_bf16(const uint16_t* x, const uint16_t* w, int64_t n_tok, int K, int N, uint16_t* out,
+                           hipStream_t stream) {
+    const int nct = (N + kTpCols - 1) / kTpCols, nrb = (int)((n_tok + kTpRows - 1) / kTpRows);
+    hipLaunchKernelGGL(token_proj_bf16_kernel, dim3((unsigned)(8 * nct * ((nrb + 7) / 8))), dim3(256), 0, stream, x,
+                       w, (int)n_tok, K, N, out, nct, nrb);
 }
 
 // Any shape and dtype: fp64 accumulation in index order, rounded once to T.
@@ -763,10 +777,7 @@ static void launch_token_proj(const void* x, const void* w2, const void* wut_in,
                                dim3(256), 0, stream, (const uint16_t*)w2, d, dh, w);
             wut = w;
         }
-        hipLaunchKernelGGL(token_proj_bf16_kernel,
-                           dim3((unsigned)((dh + kTpCols - 1) / kTpCols), (unsigned)((n_tok + kTpRows - 1) / kTpRows)),
-                           dim3(256), 0, stream, (const uint16_t*)x, (const uint16_t*)wut, (int)n_tok, d, dh,
-                           (uint16_t*)xp);
+        launch_tp_bf16((const uint16_t*)x, (const uint16_t*)wut, n_tok, d, dh, (uint16_t*)xp, stream);
     } else if (dtype == kBF16)
         hipLaunchKernelGGL(token_proj_kernel<uint16_t>, tgrid, dim3(256), 0, stream, (const uint16_t*)x,
                            (const uint16_t*)w2, (int)n_tok, d, dh, (uint16_t*)xp);
@@ -867,10 +878,7 @@ static int launch_hidden_tail(const void* w2, const void* hid, const int32_t* pa
     // projection kernels (K = dh, N = d)
     const unsigned char* wv = static_cast<const unsigned char*>(w2) + (size_t)d * dh * eb;
     if (hidden_proj_mfma(d, dh, dtype)) {
-        hipLaunchKernelGGL(token_proj_bf16_kernel,
-                           dim3((unsigned)((d + kTpCols - 1) / kTpCols), (unsigned)((n_tok + kTpRows - 1) / kTpRows)),
-                           dim3(256), 0, stream, (const uint16_t*)hs, (const uint16_t*)wv, (int)n_tok, dh, d,
-                           (uint16_t*)out);
+        launch_tp_bf16((const uint16_t*)hs, (const uint16_t*)wv, n_tok, dh, d, (uint16_t*)out, stream);
         return (int)hipGetLastError();
     }
     // generic: W_v as [dh, d] row-major (the token_proj_kernel operand layout), then the
