@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
                                                         float* __restrict__ act) {
     typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     const int64_t n_chunks = (n_pairs + 63) / 64;
     for (int64_t chunk = wave_id; chunk < n_chunks; chunk += n_waves) {
@@ -169,8 +169,8 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
                 const int j = j0 + q < cnt ? j0 + q : cnt - 1;  // a tail group repeats the last pair
                 const int s = __builtin_amdgcn_readlane(my_s, j);
                 pq[q] = __builtin_amdgcn_readlane(my_p, j);
-                load_raw<T, CH>(hid + (int64_t)s * dh, dh, lane, ur[q]);
-                load_raw<T, CH>(xp + (int64_t)(pq[q] / hk) * dh, dh, lane, xr[q]);
+                load_raw_buf<T, CH>(hid + (int64_t)s * dh, dh, lane, ur[q]);
+                load_raw_buf<T, CH>(xp + (int64_t)(pq[q] / hk) * dh, dh, lane, xr[q]);
             }
             float part[kActGroup];
 #pragma unroll
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     __shared__ float dots[kAct8Waves][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int part = lane & 7, slot = lane >> 3;
     const int64_t wave_id = (int64_t)blockIdx.x * kAct8Waves + wave;
     const int64_t n_waves = (int64_t)gridDim.x * kAct8Waves;
@@ -319,6 +319,26 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
 
 constexpr int kScatterUnroll = 8;  // v rows in flight per wave
 
+// Pairs are read a chunk of up to 64 at a time, lane j holding pair p0 + j's slot and
+// activation (one vector load each instead of a scalar load per pair, whose latency the
+// pair's row load would wait behind); a group of U pairs j0 .. j0 + U - 1 of the chunk is then
+// taken by lane reads.  A group past the chunk's last pair repeats that pair (its row is
+// loaded again and not used), so that the group's row loads issue with no branch between them.
+__device__ __forceinline__ void load_pair_chunk(const int32_t* __restrict__ pair_slot, const float* __restrict__ act,
+                                                int64_t p0, int cnt, int lane, int& sl, float& a) {
+    sl = lane < cnt ? pair_slot[p0 + lane] : 0;
+    a = lane < cnt ? act[p0 + lane] : 0.0f;
+}
+template <int U>
+__device__ __forceinline__ void pair_group(int csl, float cac, int j0, int cn, int (&sl)[U], float (&a)[U]) {
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+        const int j = j0 + q < cn ? j0 + q : cn - 1;
+        sl[q] = __builtin_amdgcn_readlane(csl, j);
+        a[q] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(cac), j));
+    }
+}
+
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict__ vr_,
                                                             const int32_t* __restrict__ pair_slot,
@@ -327,42 +347,49 @@ __global__ __launch_bounds__(256) void apply_scatter_kernel(const T* __restrict_
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     const float inv_h_div = (float)H;
     for (int64_t t = wave_id; t < n_tok; t += n_waves) {
         float o[CH * N];
 #pragma unroll
         for (int e = 0; e < CH * N; ++e) o[e] = 0.0f;
+        // chunks of a head's pairs, each loaded one chunk ahead (the next head's first after a
+        // head's last)
+        const int64_t tb = t * H * k;
+        int nsl;
+        float nac;
+        load_pair_chunk(pair_slot, act, tb, k < 64 ? k : 64, lane, nsl, nac);
         for (int h = 0; h < H; ++h) {
             float hacc[CH * N];
 #pragma unroll
             for (int e = 0; e < CH * N; ++e) hacc[e] = 0.0f;
-            const int64_t pbase = (t * H + h) * k;
-            for (int j0 = 0; j0 < k; j0 += kScatterUnroll) {
-                Raw vr[kScatterUnroll][CH];
-                float a[kScatterUnroll];
+            for (int c0 = 0; c0 < k; c0 += 64) {
+                const int csl = nsl, cn = k - c0 < 64 ? k - c0 : 64;
+                const float cac = nac;
+                const int nh = c0 + 64 < k ? h : h + 1, nc0 = c0 + 64 < k ? c0 + 64 : 0;
+                if (nh < H) load_pair_chunk(pair_slot, act, tb + (int64_t)nh * k + nc0, k - nc0 < 64 ? k - nc0 : 64, lane, nsl, nac);
+                for (int j0 = 0; j0 < cn; j0 += kScatterUnroll) {
+                    Raw vr[kScatterUnroll][CH];
+                    float a[kScatterUnroll];
+                    int sl[kScatterUnroll];
+                    pair_group<kScatterUnroll>(csl, cac, j0, cn, sl, a);
 #pragma unroll
-                for (int q = 0; q < kScatterUnroll; ++q) {
-                    if (j0 + q < k) {
-                        const int s = pair_slot[pbase + j0 + q];
-                        a[q] = act[pbase + j0 + q];
-                        load_raw<T, CH>(vr_ + (int64_t)s * d, d, lane, vr[q]);
-                    }
-                }
+                    for (int q = 0; q < kScatterUnroll; ++q) load_raw_buf<T, CH>(vr_ + (int64_t)sl[q] * d, d, lane, vr[q]);
 #pragma unroll
-                for (int q = 0; q < kScatterUnroll; ++q) {
-                    if (j0 + q < k) {
+                    for (int q = 0; q < kScatterUnroll; ++q) {
+                        if (j0 + q < cn) {
 #pragma unroll
-                        for (int c = 0; c < CH; ++c) {
-                            float vf[N];
-                            Vec16<T>::unpack(vr[q][c], vf);
+                            for (int c = 0; c < CH; ++c) {
+                                float vf[N];
+                                Vec16<T>::unpack(vr[q][c], vf);
 #pragma unroll
-                            for (int v = 0; v < N; v += 2) {
-                                float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
-                                Elem<T>::round32x2(p0, p1);  // RN_T(a v)
-                                hacc[c * N + v] += p0;
-                                hacc[c * N + v + 1] += p1;
+                                for (int v = 0; v < N; v += 2) {
+                                    float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
+                                    Elem<T>::round32x2(p0, p1);  // RN_T(a v)
+                                    hacc[c * N + v] += p0;
+                                    hacc[c * N + v + 1] += p1;
+                                }
                             }
                         }
                     }
@@ -403,7 +430,7 @@ __global__ __launch_bounds__(256) void apply_hacc_kernel(const T* __restrict__ h
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     const int np = H * k;
     for (int64_t t = wave_id; t < n_tok; t += n_waves) {
@@ -411,26 +438,31 @@ __global__ __launch_bounds__(256) void apply_hacc_kernel(const T* __restrict__ h
 #pragma unroll
         for (int e = 0; e < CH * N; ++e) acc[e] = 0.0f;
         const int64_t pbase = t * np;
-        for (int j0 = 0; j0 < np; j0 += kScatterUnroll) {
-            Raw hr[kScatterUnroll][CH];
-            float a[kScatterUnroll];
+        // chunks of the token's pairs, each loaded one chunk ahead
+        int nsl;
+        float nac;
+        load_pair_chunk(pair_slot, act, pbase, np < 64 ? np : 64, lane, nsl, nac);
+        for (int c0 = 0; c0 < np; c0 += 64) {
+            const int csl = nsl, cn = np - c0 < 64 ? np - c0 : 64;
+            const float cac = nac;
+            if (c0 + 64 < np) load_pair_chunk(pair_slot, act, pbase + c0 + 64, np - c0 - 64 < 64 ? np - c0 - 64 : 64, lane, nsl, nac);
+            for (int j0 = 0; j0 < cn; j0 += kScatterUnroll) {
+                Raw hr[kScatterUnroll][CH];
+                float a[kScatterUnroll];
+                int sl[kScatterUnroll];
+                pair_group<kScatterUnroll>(csl, cac, j0, cn, sl, a);
 #pragma unroll
-            for (int q = 0; q < kScatterUnroll; ++q) {
-                if (j0 + q < np) {
-                    const int s = pair_slot[pbase + j0 + q];
-                    a[q] = act[pbase + j0 + q];
-                    load_raw<T, CH>(hid + (int64_t)s * dh, dh, lane, hr[q]);
-                }
-            }
+                for (int q = 0; q < kScatterUnroll; ++q) load_raw_buf<T, CH>(hid + (int64_t)sl[q] * dh, dh, lane, hr[q]);
 #pragma unroll
-            for (int q = 0; q < kScatterUnroll; ++q) {
-                if (j0 + q < np) {
+                for (int q = 0; q < kScatterUnroll; ++q) {
+                    if (j0 + q < cn) {
 #pragma unroll
-                    for (int c = 0; c < CH; ++c) {
-                        float hf[N];
-                        Vec16<T>::unpack(hr[q][c], hf);
+                        for (int c = 0; c < CH; ++c) {
+                            float hf[N];
+                            Vec16<T>::unpack(hr[q][c], hf);
 #pragma unroll
-                        for (int v = 0; v < N; ++v) acc[c * N + v] += a[q] * hf[v];  // float32 products
+                            for (int v = 0; v < N; ++v) acc[c * N + v] += a[q] * hf[v];  // float32 products
+                        }
                     }
                 }
             }
@@ -485,30 +517,32 @@ __device__ __forceinline__ void scatter_head_sum(const T* __restrict__ vr_, cons
     typedef typename Vec16<T>::raw Raw;
 #pragma unroll
     for (int e = 0; e < CH * N; ++e) hacc[e] = 0.0f;
-    for (int j0 = 0; j0 < k; j0 += U) {
-        Raw vr[U][CH];
-        float a[U];
+    for (int c0 = 0; c0 < k; c0 += 64) {
+        const int cn = k - c0 < 64 ? k - c0 : 64;
+        int csl;
+        float cac;
+        load_pair_chunk(pair_slot, act, pbase + c0, cn, lane, csl, cac);
+        for (int j0 = 0; j0 < cn; j0 += U) {
+            Raw vr[U][CH];
+            float a[U];
+            int sl[U];
+            pair_group<U>(csl, cac, j0, cn, sl, a);
 #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            if (j0 + q < k) {
-                const int s = pair_slot[pbase + j0 + q];
-                a[q] = act[pbase + j0 + q];
-                load_raw<T, CH>(vr_ + (int64_t)s * d, d, lane, vr[q]);
-            }
-        }
+            for (int q = 0; q < U; ++q) load_raw_buf<T, CH>(vr_ + (int64_t)sl[q] * d, d, lane, vr[q]);
 #pragma unroll
-        for (int q = 0; q < U; ++q) {
-            if (j0 + q < k) {
+            for (int q = 0; q < U; ++q) {
+                if (j0 + q < cn) {
 #pragma unroll
-                for (int c = 0; c < CH; ++c) {
-                    float vf[N];
-                    Vec16<T>::unpack(vr[q][c], vf);
+                    for (int c = 0; c < CH; ++c) {
+                        float vf[N];
+                        Vec16<T>::unpack(vr[q][c], vf);
 #pragma unroll
-                    for (int v = 0; v < N; v += 2) {
-                        float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
-                        Elem<T>::round32x2(p0, p1);  // RN_T(a v)
-                        hacc[c * N + v] += p0;
-                        hacc[c * N + v + 1] += p1;
+                        for (int v = 0; v < N; v += 2) {
+                            float p0 = a[q] * vf[v], p1 = a[q] * vf[v + 1];
+                            Elem<T>::round32x2(p0, p1);  // RN_T(a v)
+                            hacc[c * N + v] += p0;
+                            hacc[c * N + v + 1] += p1;
+                        }
                     }
                 }
             }
@@ -524,7 +558,7 @@ __global__ __launch_bounds__(256) void apply_scatter_head_kernel(const T* __rest
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     for (int64_t it = wave_id; it < n_items; it += n_waves) {  // item = t * H + head
         float hacc[CH * N];
@@ -549,7 +583,7 @@ __global__ __launch_bounds__(kTokWaves * 64) void apply_scatter_tok_kernel(const
     typedef typename Vec16<T>::raw Raw;
     extern __shared__ __align__(16) unsigned char tok_lds[];
     T* hb = reinterpret_cast<T*>(tok_lds);  // [H][d]
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t t = blockIdx.x;
     for (int h = wave; h < H; h += kTokWaves) {
         float hacc[CH * N];
@@ -590,7 +624,7 @@ __global__ __launch_bounds__(256) void apply_head_sum_kernel(const T* __restrict
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     const float hdiv = (float)H;
     for (int64_t t = wave_id; t < n_tok; t += n_waves) {

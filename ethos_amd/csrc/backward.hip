@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void expert_bwd_pairs_kernel(const T* __restri
     constexpr int N = Vec16<T>::kN;
     typedef typename Vec16<T>::raw Raw;
     const int lane = threadIdx.x & 63;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     for (int64_t t = wave_id; t < n_tok; t += n_waves) {
         float xr[CH * N], yr[CH * N], ha[CH * N], dx[CH * N];
@@ -70,14 +70,12 @@ __global__ __launch_bounds__(256) void expert_bwd_pairs_kernel(const T* __restri
         for (int j0 = 0; j0 < hk; j0 += kBwdUnroll) {
             Raw hr[kBwdUnroll][CH];
             int sq[kBwdUnroll];
+            // slots first, then every row with no branch between the loads (past the last pair
+            // the last pair's row again, unused)
 #pragma unroll
-            for (int q = 0; q < kBwdUnroll; ++q) {
-                sq[q] = 0;
-                if (j0 + q < hk) {
-                    sq[q] = pair_slot[pbase + j0 + q];
-                    load_raw<T, CH>(hid + (int64_t)sq[q] * dh, dh, lane, hr[q]);
-                }
-            }
+            for (int q = 0; q < kBwdUnroll; ++q) sq[q] = pair_slot[pbase + (j0 + q < hk ? j0 + q : hk - 1)];
+#pragma unroll
+            for (int q = 0; q < kBwdUnroll; ++q) load_raw_buf<T, CH>(hid + (int64_t)sq[q] * dh, dh, lane, hr[q]);
 #pragma unroll
             for (int q = 0; q < kBwdUnroll; ++q) {
                 if (j0 + q >= hk) continue;
@@ -145,7 +143,7 @@ __global__ __launch_bounds__(256) void expert_bwd_sums_kernel(const float* __res
                                                               float* __restrict__ head, float* __restrict__ tail) {
     const int lane = threadIdx.x & 63;
     const int64_t n_blocks = (n_pairs + kBwdBlock - 1) / kBwdBlock;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     for (int64_t blk = wave_id; blk < n_blocks; blk += n_waves) {
         const int64_t b0 = blk * kBwdBlock;
@@ -204,7 +202,7 @@ __global__ __launch_bounds__(256) void expert_bwd_join_kernel(const int32_t* __r
                                                               float* __restrict__ dhs) {
     const int lane = threadIdx.x & 63;
     const int64_t n_blocks = (n_pairs + kBwdBlock - 1) / kBwdBlock;
-    const int64_t wave_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t wave_id = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n_waves = (int64_t)gridDim.x * 4;
     for (int64_t blk = wave_id; blk < n_blocks; blk += n_waves) {
         const int64_t b0 = blk * kBwdBlock, last = b0 + kBwdBlock - 1;

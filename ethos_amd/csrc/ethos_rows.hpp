@@ -115,4 +115,18 @@ __device__ __forceinline__ void load_raw(const T* __restrict__ row, int d, int l
     }
 }
 
+// The same slices through a buffer descriptor over the row's d elements: lanes past the row
+// read zeros without a per-lane branch, and for a wave-uniform row pointer the descriptor and
+// its address arithmetic stay in scalar registers.
+template <typename T, int CH>
+__device__ __forceinline__ void load_raw_buf(const T* row, int d, int lane, typename Vec16<T>::raw (&r)[CH]) {
+    constexpr int N = Vec16<T>::kN;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row), (short)0, d * (int)sizeof(T), 0x00020000);
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+        r[c] = __builtin_bit_cast(typename Vec16<T>::raw,
+                                  __builtin_amdgcn_raw_buffer_load_b128(rs, (c * 64 * N + lane * N) * (int)sizeof(T), 0, 0));
+}
+
 }  // namespace ethos

@@ -35,7 +35,7 @@ constexpr int kTpLds = kTpStages * kTpStage;               // LDS of one tile's 
 __device__ __forceinline__ void token_proj_bf16_tile(unsigned char* ring, const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ wut, int n_tok, int d, int dh,
                                                      uint16_t* __restrict__ xp, int c0, int t0) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const bool active = wave < 4;
     const int h = lane >> 5, l32 = lane & 31;
     const int wr = (wave & 3) >> 1, wc = wave & 1;

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void generate_kernel(const T* __restrict__ lat
     const int zp = dl + kGenPad, hp = dh + kGenPad;
     T* zs = reinterpret_cast<T*>(smem);
     T* hs = zs + R * zp;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lrow = lane & 31, lk = (lane >> 5) * M::kKL;
     // uniq, h and v hold max_unique rows
     const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
     __shared__ int32_t ids_s[kHsMaxTiles][kHsRows];
     __shared__ float dsm[kAct ? kWaves : 1][64];  // per-wave dot products of the activations
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
     const int n_tiles = (U + kHsRows - 1) / kHsRows;
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(kG2Waves * 64) __attribute__((amdgpu_waves_per_eu(1
     // row holds its 16-byte group q at slot q ^ (r % 8).
     __shared__ u32x4_t stg[kG2Waves][kG2MB * 32 * 8];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);
     const int n_tiles = (U + kG2Rows - 1) / kG2Rows;
@@ -633,7 +633,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // row holds its 16-byte group q at slot q ^ (r % 8).
     __shared__ u32x4_t stg[4][kWsRows * 8];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int h = lane >> 5, l32 = lane & 31;
     // the h and v outputs hold max_unique rows
     const int U = (int)((int64_t)*n_unique < max_unique ? (int64_t)*n_unique : max_unique);

@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
                                                            int8_t* __restrict__ wdig, QRowMeta* __restrict__ xmeta,
                                                            QRowMeta* __restrict__ wmeta) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= n_rows) return;
     const bool is_x = row < n_tok;
     const int64_t r = is_x ? row : row - n_tok;

@@ -88,7 +88,7 @@ static unsigned tsort_grid(int n_tiles) { return 64u * (unsigned)(((n_tiles + 7)
 template <int NV>
 __device__ __forceinline__ void scan512(const uint32_t (&v)[NV], uint32_t (&ex)[NV], uint32_t (&tot)[NV],
                                         uint32_t* wsum) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint32_t inc[NV];
 #pragma unroll
     for (int c = 0; c < NV; ++c) inc[c] = v[c];
@@ -126,7 +126,7 @@ __device__ __forceinline__ void scan512(const uint32_t (&v)[NV], uint32_t (&ex)[
 // Exclusive scan of one value per thread over the workgroup's 1024 threads; tot gets the
 // sum.  wsum: kTW words of LDS.
 __device__ __forceinline__ uint32_t scan1024(uint32_t v, uint32_t* wsum, uint32_t& tot) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint32_t inc = v;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -156,7 +156,7 @@ __device__ __forceinline__ uint32_t scan1024(uint32_t v, uint32_t* wsum, uint32_
 template <bool kFirst>
 __device__ __forceinline__ void tile_load(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
                                           int64_t n, int tile, uint32_t (&key)[kTC], uint32_t (&val)[kTC]) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int64_t base = (int64_t)tile * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
@@ -168,7 +168,7 @@ __device__ __forceinline__ void tile_load(const uint32_t* __restrict__ keys, con
 }
 __device__ __forceinline__ void tile_rank(int64_t n, int tile, int shift, uint32_t (*wcnt)[kRadix],
                                           const uint32_t (&key)[kTC], uint32_t (&rank)[kTC]) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int64_t base = (int64_t)tile * kTile + wave * (kTC * 64);
 #pragma unroll
     for (int j = 0; j < kTC; ++j) {
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats(const uint32_t* __restr
     __shared__ uint32_t wcnt[kTW][kRadix];
     __shared__ uint32_t sk[kTile];
     __shared__ uint32_t lstart[kRadix], dcnt[kRadix], wsum[8];
-    const int tid = threadIdx.x, wave = tid >> 6;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint32_t key[kTC], val[kTC], rank[kTC];
     tile_load<true>(keys, nullptr, n, tile, key, val);
     zero_wcnt(wcnt);
@@ -357,7 +357,7 @@ constexpr int kScanThreads = 256, kScanPer = 4, kScanRound = kScanThreads * kSca
 // so sh can be used again at once.
 __device__ __forceinline__ void scan_block_sum_max(uint32_t c, uint32_t m, uint32_t* sh, uint32_t* ex_c,
                                                    uint32_t* ex_m, uint32_t* tot_c, uint32_t* tot_m) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint32_t ic = c, im = m;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_down(const uint32_t* __restri
     __shared__ uint32_t gbase[kRadix], lstart[kRadix], wsum[2 * 8];
     const int tile = tsort_tile(n_tiles);
     if (tile < 0) return;
-    const int tid = threadIdx.x, wave = tid >> 6;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t my_pre = tid < kRadix ? pre[(int64_t)tid * sort_tile_pitch(n_tiles) + tile] : 0u;
     uint32_t tv[2] = {tid < kRadix ? tot[tid] : 0u, 0u};
     uint32_t key[kTC], val[kTC], rank[kTC];
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(kTThreads) void tsort_down_last(
     __shared__ uint32_t wsum[3 * 8];
     const int tile = tsort_tile(n_tiles);
     if (tile < 0) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int64_t o = (int64_t)tid * sort_tile_pitch(n_tiles) + tile;
     const bool dl = tid < kRadix;
     const uint32_t my_pre = dl ? pre[o] : 0u, my_spre = dl ? spre[o] : 0u, my_plast = dl ? plast[o] : 0u;
@@ -736,7 +736,7 @@ __device__ __forceinline__ void sort_small_body(unsigned char* lds, const int32_
     uint64_t* cmask = reinterpret_cast<uint64_t*>(lds + kSmallBufB + kSmallCntB);
     uint32_t* cbase = reinterpret_cast<uint32_t*>(lds + kSmallBufB + kSmallCntB + kSmallChunks * 8);
     uint32_t* wsum = reinterpret_cast<uint32_t*>(lds + kSmallBufB + kSmallCntB + kSmallChunks * 12);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const uint32_t kmax = (1u << key_bits_) - 1u;
     const int n_chunks = (n + 63) / 64;
     const int cpw = (n_chunks + kSmallWaves - 1) / kSmallWaves;  // chunks per wave (<= kSmallPer)
