@@ -367,7 +367,7 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
     const int dh2 = dq / 2;
     static_assert(!kHP || RPW == 1, "the half-parallel form takes one row per wave");
     constexpr int kThreads = (kHP ? 2 : 1) * kRtWaves * 64;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     // hw: this wave's query half (kHP; else both, in turn); wv: its index within its group
     const int hw = kHP ? wave / kRtWaves : 0, wv = kHP ? wave % kRtWaves : wave;
     const int gtid = kHP ? tid % (kRtWaves * 64) : tid;
@@ -585,25 +585,19 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
             __builtin_amdgcn_wave_barrier();
             uint64_t* ck = reinterpret_cast<uint64_t*>(S + lr * pitch);
             int32_t* cand = reinterpret_cast<int32_t*>(S + lr * pitch);
-            bool f[kRtSlots];
-            uint64_t fb[kRtSlots];
+            // the survivors, counted and (the first 64, in slot order) written as they are found
             int n = 0;
 #pragma unroll
             for (int m = 0; m < kRtSlots; ++m) {
                 const int j = lane + m * kWave;
-                f[m] = j < K && __builtin_fmaf(gq, knr[m], sv[m]) >= cut;
-                fb[m] = ballot(f[m]);
-                n += (int)__popcll(fb[m]);
+                const bool f = j < K && __builtin_fmaf(gq, knr[m], sv[m]) >= cut;
+                const uint64_t fb = ballot(f);
+                const int pos = n + count_below(fb);
+                if (f && pos < kWave) ck[pos] = ((uint64_t)__float_as_uint(sv[m]) << 32) | (uint32_t)j;
+                n += (int)__popcll(fb);
             }
             n_cand[rr] = n;
             if (n <= kWave) {
-                int pos = 0;
-#pragma unroll
-                for (int m = 0; m < kRtSlots; ++m) {
-                    if (f[m])
-                        ck[pos + count_below(fb[m])] = ((uint64_t)__float_as_uint(sv[m]) << 32) | (uint32_t)(lane + m * kWave);
-                    pos += (int)__popcll(fb[m]);
-                }
                 __builtin_amdgcn_wave_barrier();
                 // certify each survivor; certified ones become final keys, the others join
                 // the pending list as (sub-key << 8 | slot)
@@ -626,11 +620,16 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
                 }
                 n_pend[rr] = (int)__popcll(bal);
             } else {
+                // (rare) every survivor's sub-key, over the keys written above
+                __builtin_amdgcn_wave_barrier();
                 int pos = 0;
 #pragma unroll
                 for (int m = 0; m < kRtSlots; ++m) {
-                    if (f[m]) cand[pos + count_below(fb[m])] = lane + m * kWave;
-                    pos += (int)__popcll(fb[m]);
+                    const int j = lane + m * kWave;
+                    const bool f = j < K && __builtin_fmaf(gq, knr[m], sv[m]) >= cut;
+                    const uint64_t fb = ballot(f);
+                    if (f) cand[pos + count_below(fb)] = j;
+                    pos += (int)__popcll(fb);
                 }
                 slow_rows |= 1u << rr;
             }
