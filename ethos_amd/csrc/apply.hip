@@ -205,7 +205,9 @@ __global__ __launch_bounds__(256) void apply_act_kernel(const T* __restrict__ xp
 constexpr int kAct8Waves = 4;
 constexpr int64_t kActSmallPairs = 65536;  // batches up to this many pairs take 16-pair token-order units
 
-template <typename T, int P>
+// kFull: the row is exactly 8 P pieces of 16 bytes, so every lane's pieces are in range and
+// the row loads need no per-lane test (a masked load is a branch of its own).
+template <typename T, int P, bool kFull>
 __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __restrict__ xp, const T* __restrict__ hid,
                                                                      const int32_t* __restrict__ perm,
                                                                      const int32_t* __restrict__ sorted_slot,
@@ -236,14 +238,16 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
             const int j0 = (int)(u - t * cpt) * upairs;
             const int cnt = hk - j0 < upairs ? hk - j0 : upairs;
             const int64_t pbase = t * hk + j0;
-            const int my_s = lane < cnt ? pair_slot[pbase + lane] : 0;
-            const T my_g = lane < cnt ? gates[pbase + lane] : T{};
+            // (lanes past the unit load its last pair: no select waits on these loads)
+            const int lc = lane < cnt ? lane : cnt - 1;
+            const int my_s = pair_slot[pbase + lc];
+            const T my_g = gates[pbase + lc];
             const T* xr = xp + t * dh;
             Raw xv[P];
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 const int e = (part + 8 * i) * N;
-                xv[i] = e < dh ? *reinterpret_cast<const Raw*>(xr + e) : Raw{};
+                xv[i] = kFull || e < dh ? *reinterpret_cast<const Raw*>(xr + e) : Raw{};
             }
             const int ng = (cnt + 7) / 8;
             for (int g0 = 0; g0 < ng; g0 += 2) {
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
 #pragma unroll
                     for (int i = 0; i < P; ++i) {
                         const int e = (part + 8 * i) * N;
-                        hv[b][i] = e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
+                        hv[b][i] = kFull || e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
                     }
                 }
 #pragma unroll
@@ -301,8 +305,8 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 const int e = (part + 8 * i) * N;
-                hv[i] = e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
-                xv[i] = e < dh ? *reinterpret_cast<const Raw*>(xr + e) : Raw{};
+                hv[i] = kFull || e < dh ? *reinterpret_cast<const Raw*>(hr + e) : Raw{};
+                xv[i] = kFull || e < dh ? *reinterpret_cast<const Raw*>(xr + e) : Raw{};
             }
             float acc = 0.0f;
 #pragma unroll
@@ -703,9 +707,14 @@ static void launch_act8_t(const void* xp, const void* hid, const int32_t* perm, 
     const int64_t cap = (int64_t)num_cus * 16;
     int64_t g1 = ((n_pairs + upairs - 1) / upairs + kAct8Waves - 1) / kAct8Waves;
     g1 = g1 > cap ? cap : (g1 < 1 ? 1 : g1);
-    hipLaunchKernelGGL((apply_act8_kernel<T, P>), dim3((unsigned)g1), dim3(kAct8Waves * 64), 0, stream, (const T*)xp,
-                       (const T*)hid, perm, sorted_slot, pair_slot, n_unique, seg_off, (const T*)gates, n_pairs, hk, dh,
-                       upairs, act);
+    if (dh == 8 * P * Vec16<T>::kN)
+        hipLaunchKernelGGL((apply_act8_kernel<T, P, true>), dim3((unsigned)g1), dim3(kAct8Waves * 64), 0, stream,
+                           (const T*)xp, (const T*)hid, perm, sorted_slot, pair_slot, n_unique, seg_off, (const T*)gates,
+                           n_pairs, hk, dh, upairs, act);
+    else
+        hipLaunchKernelGGL((apply_act8_kernel<T, P, false>), dim3((unsigned)g1), dim3(kAct8Waves * 64), 0, stream,
+                           (const T*)xp, (const T*)hid, perm, sorted_slot, pair_slot, n_unique, seg_off, (const T*)gates,
+                           n_pairs, hk, dh, upairs, act);
 }
 
 // Per-pair activations a_p (phase 1): 8 lanes per pair for rows of up to 64 pieces of 16
