@@ -245,9 +245,10 @@ __global__ __launch_bounds__(kTThreads) void tsort_stats_map(const uint32_t* __r
     __shared__ uint32_t c[kRadix];
     const int tid = threadIdx.x;
     const int64_t base = (int64_t)tile * kTile + tid;
+    // (positions past the batch load its last key, unused: no load waits on a branch)
     uint32_t k[kTPer];
 #pragma unroll
-    for (int j = 0; j < kTPer; ++j) k[j] = base + j * kTThreads < n ? keys[base + j * kTThreads] & mkmask : 0u;
+    for (int j = 0; j < kTPer; ++j) k[j] = keys[base + j * kTThreads < n ? base + j * kTThreads : n - 1] & mkmask;
     for (int e = tid; e < kMapWords / 4; e += kTThreads) seen[e] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < kRadix) c[tid] = 0u;
     __syncthreads();
@@ -686,12 +687,17 @@ __global__ __launch_bounds__(kPsThreads) void tsort_pair_slot(const uint32_t* __
                                                               const int32_t* __restrict__ slot_table,
                                                               int32_t* __restrict__ pair_slot) {
     const int64_t base = (int64_t)blockIdx.x * (kPsThreads * kPsPer) + threadIdx.x;
+    // every id, then every table entry, loaded before any store (positions past the batch
+    // repeat its last pair, not stored): no load waits on a branch or on another's use
     uint32_t k[kPsPer];
+    int32_t v[kPsPer];
 #pragma unroll
-    for (int j = 0; j < kPsPer; ++j) k[j] = base + j * kPsThreads < n ? ids[base + j * kPsThreads] & mkmask : 0u;
+    for (int j = 0; j < kPsPer; ++j) k[j] = ids[base + j * kPsThreads < n ? base + j * kPsThreads : n - 1] & mkmask;
+#pragma unroll
+    for (int j = 0; j < kPsPer; ++j) v[j] = slot_table[k[j]];
 #pragma unroll
     for (int j = 0; j < kPsPer; ++j)
-        if (base + j * kPsThreads < n) pair_slot[base + j * kPsThreads] = slot_table[k[j]];
+        if (base + j * kPsThreads < n) pair_slot[base + j * kPsThreads] = v[j];
 }
 
 __global__ void seg_empty(int32_t* __restrict__ seg_off, int32_t* __restrict__ n_unique) {
