@@ -693,10 +693,15 @@ __global__ __launch_bounds__(256) void qproj_split_finish_kernel(const int64_t* 
     bool sure = false;
     if (live) {
         const int t = (int)(e / ncols), c = (int)(e - (int64_t)t * ncols);
-        int64_t P = 0;
-        for (int s = 0; s < n_split; ++s) P += part[(int64_t)s * n_el + e];
         const QRowMeta xm = xmeta[t];
         const QColFmt cf = qp_col(wmeta[c], bias[c], alpha[c], beta[c]);
+        // every partial sum requested before any is added (integers: exact in any order)
+        int64_t pv[kQiSplit];
+#pragma unroll
+        for (int s = 0; s < kQiSplit; ++s) pv[s] = s < n_split ? part[(int64_t)s * n_el + e] : 0;
+        int64_t P = 0;
+#pragma unroll
+        for (int s = 0; s < kQiSplit; ++s) P += pv[s];
         uint16_t o;
         sure = qp_certify((double)P, qp_xf(xm), qp_xi(xm), cf, d, &o);
         if (sure) q[e] = o;
