@@ -165,16 +165,24 @@ __device__ __forceinline__ uint32_t pk_lshl_b16(uint32_t a, uint32_t sh) {  // s
 // clamp(|x|bits - 0x3a7f, 0, hi) + base with hi = 1537 / 1793 and base = 0 / 1538.
 constexpr int kGeluMcPos = 1538;               // entries for x >= +0
 constexpr int kGeluMcSize = kGeluMcPos + 1794;  // and for x <= -0
-__device__ __forceinline__ f32x2_t gelu_mc_entry(int i, const uint16_t* lut16) {
+// Entry i in two steps, so that a caller can request every table value it needs before
+// building any entry: the table index entry i reads (a valid index for every i below
+// kGeluMcSize; entries that are a closed form ignore the value), then the entry from it.
+__device__ __forceinline__ int gelu_mc_lut_index(int i) {
+    if (i < kGeluMcPos) return i == 0 || i == kGeluMcPos - 1 ? 0 : i - 1;
+    const int j = i - kGeluMcPos;
+    return j == 0 || j == 1793 ? 0 : 1536 + j - 1;
+}
+__device__ __forceinline__ f32x2_t gelu_mc_entry_from(int i, uint16_t v) {
     if (i < kGeluMcPos) {
         if (i == 0) return f32x2_t{0.5f, 0.0f};
         if (i == kGeluMcPos - 1) return f32x2_t{1.0f, 0.0f};
-        return f32x2_t{0.0f, __uint_as_float((uint32_t)lut16[i - 1] << 16)};
+        return f32x2_t{0.0f, __uint_as_float((uint32_t)v << 16)};
     }
     const int j = i - kGeluMcPos;
     if (j == 0) return f32x2_t{0.5f, -0.0f};
     if (j == 1793) return f32x2_t{0.0f, -0.0f};
-    return f32x2_t{0.0f, __uint_as_float((uint32_t)lut16[1536 + j - 1] << 16)};
+    return f32x2_t{0.0f, __uint_as_float((uint32_t)v << 16)};
 }
 __device__ __forceinline__ uint32_t gelu_bf16x2_mc(uint32_t pk, uint32_t mc_bytes) {
     const uint32_t a = pk & 0x7fff7fffu;

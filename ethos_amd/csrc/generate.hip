@@ -214,17 +214,37 @@ __global__ __launch_bounds__(DH) void hidden_ws_bf16_kernel(const uint16_t* __re
     // activations here unless the token order applies (few hidden-row bytes)
     const bool act_on = kAct && (int64_t)U * DH * (int64_t)sizeof(uint16_t) > kActTokenOrderMaxHBytes;
 
-    // the GELU table and this workgroup's tile ids (-1 past U or for ids outside the table)
-    for (int e = tid; e < kGeluMcSize; e += DH) gmc[e] = gelu_mc_entry(e, kGeluLut);
-    for (int e = tid; e < kHsMaxTiles * kHsRows; e += DH) {
-        const int i = e / kHsRows, r = e % kHsRows;
-        const int64_t u = ((int64_t)blockIdx.x + (int64_t)i * G) * kHsRows + r;
-        int id = -1;
-        if (u < U) {
-            const int v = uniq[u];
-            id = v >= 0 && v < n_experts ? v : -1;
+    // the GELU table and this workgroup's tile ids (-1 past U or for ids outside the table);
+    // every value is requested before any is used (positions past the end read a valid
+    // element, unused), so the loads share one round trip
+    {
+        constexpr int kGIt = (kGeluMcSize + DH - 1) / DH, kIIt = kHsMaxTiles * kHsRows / DH;
+        static_assert(kHsMaxTiles * kHsRows % DH == 0, "id table loop");
+        uint16_t gv[kGIt];
+        int iv[kIIt];
+#pragma unroll
+        for (int it = 0; it < kGIt; ++it) {
+            const int e = tid + it * DH;
+            gv[it] = kGeluLut[gelu_mc_lut_index(e < kGeluMcSize ? e : 0)];
         }
-        ids_s[i][r] = id;
+#pragma unroll
+        for (int it = 0; it < kIIt; ++it) {
+            const int e = tid + it * DH, i = e / kHsRows, r = e % kHsRows;
+            const int64_t u = ((int64_t)blockIdx.x + (int64_t)i * G) * kHsRows + r;
+            iv[it] = U > 0 ? uniq[u < U ? u : 0] : -1;  // (no unique expert: nothing to read)
+        }
+#pragma unroll
+        for (int it = 0; it < kGIt; ++it) {
+            const int e = tid + it * DH;
+            if (e < kGeluMcSize) gmc[e] = gelu_mc_entry_from(e, gv[it]);
+        }
+#pragma unroll
+        for (int it = 0; it < kIIt; ++it) {
+            const int e = tid + it * DH, i = e / kHsRows, r = e % kHsRows;
+            const int64_t u = ((int64_t)blockIdx.x + (int64_t)i * G) * kHsRows + r;
+            const int v = iv[it];
+            ids_s[i][r] = u < U && v >= 0 && v < n_experts ? v : -1;
+        }
     }
     const uint32_t mc_bytes = lds_addr(gmc);
     // the wave's W1 rows: A fragment (cb, s) = W1[hid0 + 32 cb + l32][16 s + 8 h ..]
