@@ -393,14 +393,26 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
     const int nkb = kpad / 32;
     const float gamma = (float)(dh2 + 16) * 0x1p-22f * 1.01f;
 
-    // Sub-key norms (upper bounds) for both tables.
-    for (int e = tid; e < 2 * kpad; e += kThreads) {
-        const int half = e / kpad, j = e - half * kpad;
-        float nrm = 0.0f;
-        if (j < K) {
-            if (key_norms) {
-                nrm = key_norms[half * K + j];
-            } else {
+    // Sub-key norms (upper bounds) for both tables: given ones all requested before any is
+    // stored (positions past the tables read entry 0, unused)
+    if (key_norms != nullptr) {
+        constexpr int kKnIt = (2 * kRtMaxK + kThreads - 1) / kThreads;
+        float kv[kKnIt];
+#pragma unroll
+        for (int it = 0; it < kKnIt; ++it) {
+            const int e = tid + it * kThreads, half = e / kpad, j = e - half * kpad;
+            kv[it] = key_norms[e < 2 * kpad && j < K ? half * K + j : 0];
+        }
+#pragma unroll
+        for (int it = 0; it < kKnIt; ++it) {
+            const int e = tid + it * kThreads, half = e / kpad, j = e - half * kpad;
+            if (e < 2 * kpad) kn[e] = j < K ? kv[it] : 0.0f;
+        }
+    } else {
+        for (int e = tid; e < 2 * kpad; e += kThreads) {
+            const int half = e / kpad, j = e - half * kpad;
+            float nrm = 0.0f;
+            if (j < K) {
                 const T* kr = (half ? keys2 : keys1) + (int64_t)j * dh2;
                 double s2 = 0.0;
                 for (int i = 0; i < dh2; ++i) {
@@ -409,8 +421,8 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
                 }
                 nrm = (float)(sqrt(s2) * (1.0 + 0x1p-20));
             }
+            kn[e] = nrm;
         }
-        kn[e] = nrm;
     }
 
     const int qs_ld = L.qs_pitch / (int)sizeof(T);  // staged query row pitch (elements)
