@@ -164,12 +164,22 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
     int8_t* dst = (is_x ? xdig : wdig) + r * dpad;
     const int ng = d / 8, npad = dpad / 8;
 
+    // The row's first kDigCache groups of 8 per lane (rows of up to 2048 elements entirely)
+    // are loaded once, all before any is used, and serve both passes; groups past the row
+    // load group 0 again, unused.
+    constexpr int kDigCache = 4;
+    uint4 cv[kDigCache];
+#pragma unroll
+    for (int c = 0; c < kDigCache; ++c) {
+        const int g = lane + c * kWave;
+        cv[c] = *reinterpret_cast<const uint4*>(src + 8 * (g < ng ? g : 0));
+    }
+
     // pass 1: largest biased exponent, inf / NaN, |.|_1 and max |.|
     uint32_t emax = 0, amax_bits = 0;
     bool bad = false;
     float l1 = 0.0f;
-    for (int g = lane; g < ng; g += kWave) {
-        const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * g);
+    auto scan = [&](const uint4 v) {
         const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -180,7 +190,11 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
             amax_bits = max(amax_bits, bits);
             l1 += __uint_as_float(bits << 16);
         }
-    }
+    };
+#pragma unroll
+    for (int c = 0; c < kDigCache; ++c)
+        if (lane + c * kWave < ng) scan(cv[c]);
+    for (int g = lane + kDigCache * kWave; g < ng; g += kWave) scan(*reinterpret_cast<const uint4*>(src + 8 * g));
     emax = qp_wave_max_u32(emax);
     bad = __ballot(bad) != 0;
     // subnormal floor: the bounds stay upper bounds even if fp32 arithmetic flushes them
@@ -190,10 +204,9 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
 
     // pass 2: F = trunc(v 2^(21 - E)) from the bit fields, split into three digits
     int n_inex = 0;
-    for (int g = lane; g < npad; g += kWave) {
+    auto digits = [&](int g, const uint4 v, bool live) {
         uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
-        if (g < ng && !bad) {
-            const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * g);
+        if (live) {
             const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -222,6 +235,15 @@ __global__ __launch_bounds__(256) void qproj_digits_kernel(const uint16_t* __res
         *reinterpret_cast<uint2*>(dst + 8 * g) = make_uint2(p0[0], p0[1]);
         *reinterpret_cast<uint2*>(dst + plane + 8 * g) = make_uint2(p1[0], p1[1]);
         *reinterpret_cast<uint2*>(dst + 2 * plane + 8 * g) = make_uint2(p2[0], p2[1]);
+    };
+#pragma unroll
+    for (int c = 0; c < kDigCache; ++c) {
+        const int g = lane + c * kWave;
+        if (g < npad) digits(g, cv[c], g < ng && !bad);
+    }
+    for (int g = lane + kDigCache * kWave; g < npad; g += kWave) {
+        const bool live = g < ng && !bad;
+        digits(g, live ? *reinterpret_cast<const uint4*>(src + 8 * g) : make_uint4(0u, 0u, 0u, 0u), live);
     }
     const int total_inex = (int)wave_sum((float)n_inex);
     if (lane == 0) {
