@@ -327,11 +327,14 @@ constexpr int kScatterUnroll = 8;  // v rows in flight per wave
 // activation (one vector load each instead of a scalar load per pair, whose latency the
 // pair's row load would wait behind); a group of U pairs j0 .. j0 + U - 1 of the chunk is then
 // taken by lane reads.  A group past the chunk's last pair repeats that pair (its row is
-// loaded again and not used), so that the group's row loads issue with no branch between them.
+// loaded again and not used), so that the group's row loads issue with no branch between them;
+// likewise lanes past the chunk (cnt >= 1) load its last pair, so that no branch's join waits
+// for the chunk's loads.
 __device__ __forceinline__ void load_pair_chunk(const int32_t* __restrict__ pair_slot, const float* __restrict__ act,
                                                 int64_t p0, int cnt, int lane, int& sl, float& a) {
-    sl = lane < cnt ? pair_slot[p0 + lane] : 0;
-    a = lane < cnt ? act[p0 + lane] : 0.0f;
+    const int64_t p = p0 + (lane < cnt ? lane : cnt - 1);
+    sl = pair_slot[p];
+    a = act[p];
 }
 template <int U>
 __device__ __forceinline__ void pair_group(int csl, float cac, int j0, int cn, int (&sl)[U], float (&a)[U]) {
