@@ -383,7 +383,7 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
     // lst[rr][half]: the canonical top-k_cand list of this wave's row rr and query half,
     // entry i held by lane i
     // key vectors in flight per exact chain (one row per wave leaves registers for more)
-    constexpr int kExG = RPW == 1 ? 8 : 2;
+    constexpr int kExG = RPW == 1 ? 8 : 4;
     using LK = ListKey<T>;
     typename LK::type lst[RPW][2];
 #pragma unroll
