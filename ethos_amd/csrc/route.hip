@@ -448,7 +448,7 @@ __global__ __launch_bounds__((kHP ? 2 : 1) * kRtWaves * 64, 4) void route_kernel
         // 1. approximate scores for the 32-row tile: wave w takes key blocks w, w + 8, ...
         //    The key fragments of kU reduction steps are loaded before their MFMAs, so
         //    their L2 latencies overlap.
-        constexpr int kU = sizeof(T) == 2 ? (RPW == 1 ? 4 : 1) : (RPW == 1 ? 16 : 8);
+        constexpr int kU = sizeof(T) == 2 ? (RPW == 1 ? 4 : 2) : (RPW == 1 ? 16 : 8);
         for (int kb0 = wv; kb0 < nkb; kb0 += 2 * kRtWaves) {
             f32x16_t acc[2];
 #pragma unroll
