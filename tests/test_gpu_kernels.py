@@ -269,6 +269,35 @@ def test_apply_shapes(n_tok, d, dh, dt):
     check_out(got, ref, dt, signal=True, nerr_max=2e-3)
 
 
+@pytest.mark.parametrize("n_tok,dt", [(1100, "bf16"), (40, "bf16"), (1100, "fp32")])
+def test_apply_long_pair_lists(n_tok, dt):
+    """More than 64 pairs per (token, head) and per token: the gathers take a head's or a
+    token's pairs in chunks of 64, the next chunk loaded while one is summed, so a head's
+    second chunk and the next head's first must follow in order.  Both orders of the apply,
+    above 1,024 tokens (one wave per token) and below (one workgroup per token), against
+    the oracle."""
+    rng = np.random.default_rng(n_tok + 7)
+    d, dh, H, k, E = 256, 128, 2, 70, 5000
+    enc = (lambda a: O.f32_to_bf16_bits(a)) if dt == "bf16" else (lambda a: a.astype(np.float32))
+    x = enc(rng.standard_normal((n_tok, d)).astype(np.float32))
+    w2 = enc((rng.uniform(-1, 1, (2 * d, dh)) * 4 / np.sqrt(d)).astype(np.float32))
+    ids = rng.integers(0, E, (n_tok, H, k)).astype(np.int32)
+    g = enc(rng.uniform(0, 1, (n_tok, H, k)).astype(np.float32))
+    seg = hip.sort_segment(to_dev(ids.reshape(-1)), E)
+    U = int(seg["n_unique"].item())
+    h = enc(rng.standard_normal((seg["max_unique"], dh)).astype(np.float32) * 0.3)
+    v = enc(rng.standard_normal((seg["max_unique"], d)).astype(np.float32))
+    out = hip.apply_scatter(to_dev(x), to_dev(w2), to_dev(h), to_dev(v), seg, to_dev(g), H, k)
+    out_h = hip.apply_hidden(to_dev(x), to_dev(w2), to_dev(h), seg, to_dev(g), H, k)
+    torch.cuda.synchronize()
+    xp = O.token_proj(x, w2, dt)
+    slot = to_host(seg["pair_slot"])
+    ref = O.apply(xp, O.to_f32(h, dt)[:U], O.to_f32(v, dt)[:U], slot, g, H, k, dt)
+    check_out(O.to_f32(to_host(out), dt), ref, dt, signal=True, nerr_max=2e-3)
+    ref_h = O.apply_hidden(xp, O.to_f32(h, dt)[:U], w2, slot, g, H, k, dt)
+    check_out(O.to_f32(to_host(out_h), dt), ref_h, dt, signal=True, nerr_max=2e-3)
+
+
 @pytest.mark.parametrize("d,dh,H,dt", [(1024, 128, 8, "bf16"), (4096, 64, 2, "bf16"), (256, 64, 3, "fp32")])
 def test_scatter_paths_bit_identical(d, dh, H, dt):
     """The scatter-back's three forms give the same bits: up to 1,024 tokens one workgroup
