@@ -284,13 +284,14 @@ __global__ __launch_bounds__(kAct8Waves * 64) void apply_act8_kernel(const T* __
     for (int64_t chunk = wave_id; chunk < n_chunks; chunk += n_waves) {
         const int64_t i0 = chunk * 64;
         const int cnt = (int)min((int64_t)64, n_pairs - i0);
-        const int my_s = lane < cnt ? sorted_slot[i0 + lane] : 0;
+        // (lanes past the chunk read its last position, unused: no load waits on a branch)
+        const int my_s = sorted_slot[i0 + (lane < cnt ? lane : cnt - 1)];
         bool mine = lane < cnt;
-        if (seg_off != nullptr && mine) {
+        if (seg_off != nullptr) {
             // pairs of tiles within the cap were done by the hidden-row kernel
             const int t0 = my_s - my_s % kActTileRows;
             const int t1 = t0 + kActTileRows < U ? t0 + kActTileRows : U;
-            mine = (int64_t)seg_off[t1] - (int64_t)seg_off[t0] > kActFusedCap;
+            mine = mine && (int64_t)seg_off[t1] - (int64_t)seg_off[t0] > kActFusedCap;
         }
         if (ballot(mine) == 0) continue;
         const int my_p = mine ? perm[i0 + lane] : 0;
