@@ -118,8 +118,8 @@ def test_lm_whole_model_workload_full_size():
     del logits2
     assert len(inputs) == cfg.num_layers
     n = ids.numel()
-    q_sub = np.arange(0, n, 64)    # 128 tokens for the query projection
-    y_sub = np.arange(7, n, 256)   # 32 tokens for the layer output
+    q_sub = np.arange(0, n, 4)     # 2,048 tokens for the query projection
+    y_sub = np.arange(7, n, 64)    # 128 tokens for the layer output
     for i, x in sorted(inputs.items()):
         layer = m.layers[i].mlp
         xf = x.reshape(-1, cfg.d_model).contiguous()
